@@ -1,0 +1,184 @@
+"""GPU parity of the fused W4A16 GEMV (xqhip_gemv_w4a16 / _argmax) against the
+oracle's restatement of gemvW4A16Neon / gemvW4A16ArgmaxNeon
+(customlib/kernels/generated/arm64_neon/xq_gemv_w4a16_neon.cpp:259-348).
+
+Tolerance (fp16/fp32 outputs): |gpu - oracle| <= 1e-2 + 1e-3 * |oracle|.
+Greedy ids: bit-exact whenever the oracle's top-2 margin exceeds 1e-2.
+"""
+import numpy as np
+import pytest
+
+import oracle_bind as ob
+import xqbind as xb
+from synth import f16_vector, w4_matrix
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-2, 1e-3
+
+
+def assert_close(got, want, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bound = ATOL + RTOL * np.abs(want)
+    bad = np.nonzero(err > bound)[0]
+    assert bad.size == 0, (f"{what}: {bad.size} of {want.size} outside tolerance; worst idx {bad[np.argmax(err[bad])]} "
+                           f"got {got[bad[0]]} want {want[bad[0]]}; max err {err.max():.3g}")
+
+
+def run_gemv(q, x, x_type=xb.F16, y_type=xb.F32, norm_w=None, eps=1e-6, epi=xb.EPI_STORE, y_init=None):
+    w = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols, q.group, q.affine)
+    xd = xb.DeviceBuffer.from_array(x)
+    nd = xb.DeviceBuffer.from_array(norm_w.astype(np.float32)) if norm_w is not None else None
+    out_n = q.rows // 2 if epi == xb.EPI_SILU_PAIR else q.rows
+    ydt = np.float16 if y_type == xb.F16 else np.float32
+    yd = xb.DeviceBuffer(out_n * np.dtype(ydt).itemsize)
+    if y_init is not None:
+        yd.upload(y_init.astype(ydt))
+    xb.ck(xb.hip().xqhip_gemv_w4a16(w.ref, xd.ptr, x_type, nd.ptr if nd else None, eps, yd.ptr, y_type, epi, None))
+    xb.ck(xb.hip().xqhip_device_synchronize())
+    return yd.download(ydt, out_n).astype(np.float32), w
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(4096, 4096, 0), (12288, 4096, 1), (4096, 12288, 2), (1000, 1024, 3),
+                                            (130, 4160, 4), (8, 64, 5), (1, 8192, 6)])
+def test_gemv_fp16_in_matches_oracle(rows, cols, seed):
+    q = w4_matrix(rows, cols, seed)
+    x = f16_vector(cols, seed + 100)
+    want = ob.gemv(q, x.astype(np.float32))
+    got, w = run_gemv(q, x, xb.F16, xb.F32)
+    assert w.w.layout == xb.LAYOUT_TILED64 and w.w.inexact_meta == 0
+    assert_close(got, want, f"gemv {rows}x{cols}")
+
+
+def test_gemv_config0_fp16_out():
+    q = w4_matrix(4096, 4096, 11)
+    x = f16_vector(4096, 12)
+    want = ob.gemv(q, x.astype(np.float32))
+    got, _ = run_gemv(q, x, xb.F16, xb.F16)
+    assert_close(got, want, "gemv 4096^2 fp16 out")
+
+
+def test_gemv_fp32_in_affine_v2():
+    q = w4_matrix(2048, 4096, 21, affine=1)
+    x = np.random.default_rng(22).normal(0, 1, 4096).astype(np.float32)
+    want = ob.gemv(q, x)
+    got, _ = run_gemv(q, x, xb.F32, xb.F32)
+    assert_close(got, want, "affine gemv")
+
+
+def test_gemv_fused_rmsnorm():
+    q = w4_matrix(4096, 4096, 31)
+    rng = np.random.default_rng(32)
+    h = rng.normal(0, 3.0, 4096).astype(np.float32)
+    nw = rng.normal(1.0, 0.1, 4096).astype(np.float32)
+    normed = np.empty(4096, np.float32)
+    ob.oracle().orc_rmsnorm(ob.p(h), ob.p(nw), 4096, 1e-6, ob.p(normed))
+    want = ob.gemv(q, normed)
+    got, _ = run_gemv(q, h, xb.F32, xb.F32, norm_w=nw)
+    assert_close(got, want, "rmsnorm+gemv")
+
+
+def test_gemv_residual_add_epilogue():
+    q = w4_matrix(4096, 12288, 41)
+    x = np.random.default_rng(42).normal(0, 1, 12288).astype(np.float32)
+    h0 = np.random.default_rng(43).normal(0, 10, 4096).astype(np.float32)
+    want = h0 + ob.gemv(q, x)
+    got, _ = run_gemv(q, x, xb.F32, xb.F32, epi=xb.EPI_ADD, y_init=h0)
+    assert_close(got, want, "gemv+residual")
+
+
+def test_gemv_silu_pair_epilogue():
+    inter, hidden = 2048, 4096
+    g = w4_matrix(inter, hidden, 51)
+    u = w4_matrix(inter, hidden, 52)
+    # interleave rows: (gate_0, up_0, gate_1, up_1, ...)
+    rb, gpr = hidden // 2, hidden // 64
+    packed = np.stack([g.packed.reshape(inter, rb), u.packed.reshape(inter, rb)], 1).reshape(-1)
+    scales = np.stack([g.scales.reshape(inter, gpr), u.scales.reshape(inter, gpr)], 1).reshape(-1)
+    zeros = np.stack([g.zeros.reshape(inter, gpr), u.zeros.reshape(inter, gpr)], 1).reshape(-1)
+    q = ob.Quantized(packed, scales, zeros, 2 * inter, hidden)
+    x = np.random.default_rng(53).normal(0, 1, hidden).astype(np.float32)
+    gy, uy = ob.gemv(g, x), ob.gemv(u, x)
+    want = np.array([ob.oracle().orc_silu(float(a)) for a in gy], np.float32) * uy
+    got, _ = run_gemv(q, x, xb.F32, xb.F32, epi=xb.EPI_SILU_PAIR)
+    assert_close(got, want, "gate/up silu")
+
+
+@pytest.mark.parametrize("rows,cols,group", [(7, 24, 8), (8, 4, 4), (33, 100, 10), (64, 4096, 128)])
+def test_gemv_generic_layout(rows, cols, group):
+    """Group sizes other than 64 take the generic kernel (reference tiny-model shapes)."""
+    w = np.sin(np.arange(rows * cols, dtype=np.float32) * np.float32(0.17)) * np.float32(0.7)
+    q = ob.quantize_lowbit(w, rows, cols, 4, group)
+    x = np.cos(np.arange(cols, dtype=np.float32) * np.float32(0.11)).astype(np.float32)
+    want = ob.gemv(q, x)
+    got, dw = run_gemv(q, x, xb.F32, xb.F32)
+    assert dw.w.layout == xb.LAYOUT_GENERIC
+    # fp32 activations and metadata: only the summation order differs from the oracle
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4)
+
+
+def run_argmax(q, x, x_type=xb.F32, norm_w=None, calls=1):
+    w = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols, q.group, q.affine)
+    xd = xb.DeviceBuffer.from_array(x)
+    nd = xb.DeviceBuffer.from_array(norm_w.astype(np.float32)) if norm_w is not None else None
+    ws = xb.DeviceBuffer(xb.hip().xqhip_argmax_workspace_bytes(q.rows))
+    ws.zero()
+    idx = xb.DeviceBuffer(4)
+    val = xb.DeviceBuffer(4)
+    res = []
+    for _ in range(calls):
+        xb.ck(xb.hip().xqhip_gemv_w4a16_argmax(w.ref, xd.ptr, x_type, nd.ptr if nd else None, 1e-6, ws.ptr,
+                                               idx.ptr, val.ptr, None))
+        xb.ck(xb.hip().xqhip_device_synchronize())
+        res.append((int(idx.download(np.int32, 1)[0]), float(val.download(np.float32, 1)[0])))
+    return res
+
+
+def top2_margin(v):
+    s = np.sort(v.astype(np.float64))
+    return s[-1] - s[-2]
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(50000, 4096, 61), (248320, 4096, 62), (4099, 1024, 63)])
+def test_argmax_matches_oracle(rows, cols, seed):
+    q = w4_matrix(rows, cols, seed)
+    x = np.random.default_rng(seed + 1).normal(0, 1, cols).astype(np.float32)
+    want_idx, want_val = ob.gemv_argmax(q, x)
+    logits = ob.gemv(q, x)
+    assert want_idx == int(np.argmax(logits))
+    for got_idx, got_val in run_argmax(q, x, calls=3):  # repeated calls: the kernel re-arms its counter
+        assert abs(got_val - want_val) <= ATOL + RTOL * abs(want_val)
+        if top2_margin(logits) > 1e-2:
+            assert got_idx == want_idx
+
+
+def test_argmax_ties_pick_lowest_row():
+    base = w4_matrix(1, 4096, 71)
+    rows = 9000
+    packed = np.tile(base.packed, rows)
+    scales = np.tile(base.scales, rows) * 0.5
+    zeros = np.tile(base.zeros, rows)
+    # rows 3000.. are identical copies; make earlier rows smaller so the max is tied across 3000..8999
+    scales = scales.reshape(rows, -1)
+    scales[:3000] *= 0.25
+    q = ob.Quantized(packed, scales.reshape(-1), zeros, rows, 4096)
+    x = np.abs(np.random.default_rng(72).normal(0, 1, 4096)).astype(np.float32)
+    want_idx, _ = ob.gemv_argmax(q, x)
+    got = run_argmax(q, x)[0]
+    assert want_idx == got[0] == (3000 if ob.gemv(q, x)[3000] > 0 else 0)
+
+
+def test_argmax_fused_final_norm():
+    q = w4_matrix(30000, 4096, 81)
+    rng = np.random.default_rng(82)
+    h = rng.normal(0, 1, 4096).astype(np.float32)
+    nw = rng.normal(1.0, 0.1, 4096).astype(np.float32)
+    normed = np.empty(4096, np.float32)
+    ob.oracle().orc_rmsnorm(ob.p(h), ob.p(nw), 4096, 1e-6, ob.p(normed))
+    want_idx, want_val = ob.gemv_argmax(q, normed)
+    got_idx, got_val = run_argmax(q, h, norm_w=nw)[0]
+    assert abs(got_val - want_val) <= ATOL + RTOL * abs(want_val)
+    if top2_margin(ob.gemv(q, normed)) > 1e-2:
+        assert got_idx == want_idx

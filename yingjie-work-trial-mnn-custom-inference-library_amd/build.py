@@ -1,0 +1,111 @@
+"""Builds the two shared libraries of the MI355X decode path, in-tree.
+
+  lib/libxqhip.so    hand-written gfx950 HIP kernels + the thin C ABI of include/xqhip.h
+  lib/libxqwen35.so  C++ host runtime (Session / model / XQ4 reader) exporting the
+                     reference C ABI of include/xqwen35.h; links libxqhip.so
+
+Usage: python build.py [--jobs N] [--only hip|host]
+Compiles every time it is called (hipcc cross-compiles for gfx950 without a GPU).
+"""
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+INCLUDE = os.path.join(ROOT, "include")
+HIP_SRC = os.path.join(HERE, "csrc", "hip")
+HOST_SRC = os.path.join(HERE, "csrc", "host")
+LIB = os.path.join(HERE, "lib")
+OBJ = os.path.join(HERE, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    # packed fp32 VALU ops are disabled for all device code on this target
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
+    "-I", INCLUDE, "-I", HIP_SRC,
+]
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
+              "-fvisibility=hidden", "-I", INCLUDE, "-I", HOST_SRC, "-DXQWEN35_BUILD=1"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("build step failed:\n" + " ".join(cmd) + "\n" + r.stdout)
+    return r.stdout
+
+
+def _compile_many(jobs, tasks):
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for out in ex.map(_run, tasks):
+            if out.strip():
+                sys.stderr.write(out)
+
+
+def build_hip(jobs):
+    srcs = sorted(f for f in os.listdir(HIP_SRC) if f.endswith(".hip"))
+    objs, tasks = [], []
+    for f in srcs:
+        o = os.path.join(OBJ, "hip", f[:-4] + ".o")
+        objs.append(o)
+        tasks.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(HIP_SRC, f), "-o", o])
+    os.makedirs(os.path.join(OBJ, "hip"), exist_ok=True)
+    _compile_many(jobs, tasks)
+    out = os.path.join(LIB, "libxqhip.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", tmp, *objs,
+          "-Wl,-soname,libxqhip.so"])
+    os.replace(tmp, out)
+    return out
+
+
+def build_host(jobs):
+    if not os.path.isdir(HOST_SRC):
+        return None
+    srcs = sorted(f for f in os.listdir(HOST_SRC) if f.endswith(".cpp"))
+    if not srcs:
+        return None
+    objs, tasks = [], []
+    for f in srcs:
+        o = os.path.join(OBJ, "host", f[:-4] + ".o")
+        objs.append(o)
+        tasks.append(["g++", *HOST_FLAGS, "-c", os.path.join(HOST_SRC, f), "-o", o])
+    os.makedirs(os.path.join(OBJ, "host"), exist_ok=True)
+    _compile_many(jobs, tasks)
+    out = os.path.join(LIB, "libxqwen35.so")
+    tmp = out + ".tmp"
+    _run(["g++", "-shared", "-o", tmp, *objs, "-L", LIB, "-lxqhip", "-Wl,-rpath,$ORIGIN",
+          "-Wl,-soname,libxqwen35.so", "-lpthread"])
+    os.replace(tmp, out)
+    return out
+
+
+def build(jobs=None, only=None):
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    os.makedirs(LIB, exist_ok=True)
+    built = []
+    if only in (None, "hip"):
+        built.append(build_hip(jobs))
+    if only in (None, "host"):
+        h = build_host(jobs)
+        if h:
+            built.append(h)
+    shutil.rmtree(OBJ, ignore_errors=True)
+    return built
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--only", choices=["hip", "host"], default=None)
+    a = ap.parse_args()
+    for p in build(a.jobs, a.only):
+        print(p)

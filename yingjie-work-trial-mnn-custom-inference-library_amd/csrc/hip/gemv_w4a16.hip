@@ -1,0 +1,463 @@
+// gemv_w4a16.hip - batch-1 W4A16 group-64 GEMV for gfx950 (CDNA4, wave64).
+//
+// Replaces gemvW4A16Neon / gemvW4A16ArgmaxNeon
+// (customlib/kernels/generated/arm64_neon/xq_gemv_w4a16_neon.cpp:259-348).
+// The reference factorises each group g of a row as
+//     acc += s_g * (sum_c q_c x_c  -  z_g * sum_c x_c)          (version 1)
+//     acc += s_g * sum_c q_c x_c  +  z_g * sum_c x_c            (version 2)
+// and so do these kernels: the per-group sums of x are computed once per block
+// and the inner loop is a pure code-times-activation dot product.
+//
+// Inner loop (TILED64 layout).  One lane owns one 64-column group of a row per
+// 4096-column chunk: it streams the group's 32 bytes of nibbles with two 16-byte
+// loads (a wave's load instruction covers 1 KiB contiguous) and one u32 of
+// (fp16 scale, fp16 zero).  Each u32 of 8 nibbles becomes four fp16 pairs with
+// one v_and_or_b32 each (0x6400 | q = 1024 + q, 0x6400 | q<<4 = 1024 + 16q, exact)
+// and one shift per word.
+//
+// Activations are carried at ~22-bit precision as x = hi + lo * 2^-11 with hi, lo
+// fp16 (lo is the fp32 rounding residual of hi, scaled up so it stays normal).
+// Both are staged once per block in LDS as the fp16 pairs matching the nibble
+// order (odd columns pre-divided by 16, exact), with the per-group constants
+// 1024 * sum(staged) that remove the 1024 offsets; each pair of codes then costs
+// two v_dot2_f32_f16 (hi and lo), so a word of 8 weights is 13 VALU ops and the
+// dot products are accurate to fp32 level.  The staged activations of a lane's
+// groups live in registers for the whole block.
+//
+// Columns beyond 4096 are split over the waves of a block (one 4096-column chunk
+// per wave), whose partial row sums are combined through LDS in a fixed order.
+#include "xqhip_common.hpp"
+#include "xqhip_kernels.hpp"
+
+namespace xqhip {
+
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
+
+constexpr int kGroupLdsBytes = 272;  // 128 B hi pairs + 128 B lo pairs + 16 B pad (spreads LDS banks)
+
+__device__ __forceinline__ float load_act(const void* x, int x_f16, int i) {
+    if (x_f16) return static_cast<float>(static_cast<const _Float16*>(x)[i]);
+    return static_cast<const float*>(x)[i];
+}
+
+// RMSNorm factor of ref_rmsnorm.cpp:8-17 over the block: 1/sqrt(mean(x^2)+eps).
+__device__ float block_rms_inv(const void* x, int x_f16, int n, float eps, float* red) {
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < n; c += blockDim.x) {
+        const float v = load_act(x, x_f16, c);
+        ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+}
+
+// Stage x (optionally RMS-normalised) for the dot2 inner loop.
+// Per group (kGroupLdsBytes): 8 x uint4 of hi pairs, then 8 x uint4 of lo pairs;
+// word j of a group holds, for columns 8j..8j+7, the fp16 pairs
+// (x0,x4) (x1/16,x5/16) (x2,x6) (x3/16,x7/16).
+// gc[g] = (sum of the effective x of the group, 1024*sum(hi staged), 1024*sum(lo staged), 0).
+__device__ void stage_activations(const void* x, int x_f16, const float* norm_w, float inv, int groups,
+                                  unsigned char* xs_bytes, float4* gc) {
+    for (int it = threadIdx.x; it < groups * 4; it += blockDim.x) {
+        const int g = it >> 2, qtr = it & 3;
+        float gsum = 0.0f, st_hi = 0.0f, st_lo = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int w = qtr * 2 + j;
+            const int c0 = g * 64 + w * 8;
+            _Float16 sh[8], sl[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float v = load_act(x, x_f16, c0 + i);
+                if (norm_w) v = v * inv * norm_w[c0 + i];
+                const _Float16 hi = static_cast<_Float16>(v);
+                const float lo = (v - static_cast<float>(hi)) * 2048.0f;
+                const float sc = (i & 1) ? 0.0625f : 1.0f;
+                sh[i] = static_cast<_Float16>(static_cast<float>(hi) * sc);
+                sl[i] = static_cast<_Float16>(lo * sc);
+            }
+            unsigned char* gb = xs_bytes + static_cast<size_t>(g) * kGroupLdsBytes + w * 16;
+            uint4 word;
+            word.x = as_u32(h2{sh[0], sh[4]});
+            word.y = as_u32(h2{sh[1], sh[5]});
+            word.z = as_u32(h2{sh[2], sh[6]});
+            word.w = as_u32(h2{sh[3], sh[7]});
+            *reinterpret_cast<uint4*>(gb) = word;
+            word.x = as_u32(h2{sl[0], sl[4]});
+            word.y = as_u32(h2{sl[1], sl[5]});
+            word.z = as_u32(h2{sl[2], sl[6]});
+            word.w = as_u32(h2{sl[3], sl[7]});
+            *reinterpret_cast<uint4*>(gb + 128) = word;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float a = static_cast<float>(sh[i]), b = static_cast<float>(sl[i]);
+                st_hi += a;
+                st_lo += b;
+                const float eff = a + b * (1.0f / 2048.0f);
+                gsum += (i & 1) ? 16.0f * eff : eff;
+            }
+        }
+#pragma unroll
+        for (int m = 1; m <= 2; m <<= 1) {
+            gsum += __shfl_xor(gsum, m, kWave);
+            st_hi += __shfl_xor(st_hi, m, kWave);
+            st_lo += __shfl_xor(st_lo, m, kWave);
+        }
+        if (qtr == 0) gc[g] = make_float4(gsum, 1024.0f * st_hi, 1024.0f * st_lo, 0.0f);
+    }
+}
+
+// m_lo = 0x000F000F, m_hi = 0x00F000F0 and magic = kMagic2 are passed in so
+// they stay in VGPRs across the loop.
+__device__ __forceinline__ void dot8(uint32_t w, uint4 xh, uint4 xl, float& dh, float& dl, uint32_t m_lo,
+                                     uint32_t m_hi, uint32_t magic) {
+    const uint32_t w8 = w >> 8;
+    const h2 p0 = as_h2(and_or(w, m_lo, magic)), p1 = as_h2(and_or(w, m_hi, magic));
+    const h2 p2 = as_h2(and_or(w8, m_lo, magic)), p3 = as_h2(and_or(w8, m_hi, magic));
+    dh = dot2(p0, as_h2(xh.x), dh);
+    dl = dot2(p0, as_h2(xl.x), dl);
+    dh = dot2(p1, as_h2(xh.y), dh);
+    dl = dot2(p1, as_h2(xl.y), dl);
+    dh = dot2(p2, as_h2(xh.z), dh);
+    dl = dot2(p2, as_h2(xl.z), dl);
+    dh = dot2(p3, as_h2(xh.w), dh);
+    dl = dot2(p3, as_h2(xl.w), dl);
+}
+
+// Final argmax over per-block partial keys; run by the last block to finish.
+__device__ void finish_argmax(uint64_t block_best, uint64_t* partial, uint32_t* counter, int32_t* out_idx,
+                              float* out_val, uint64_t* lds_keys) {
+    __shared__ int is_last;
+    if (threadIdx.x == 0) {
+        partial[blockIdx.x] = block_best;
+        __threadfence();
+        const uint32_t ticket = atomicAdd(counter, 1u);
+        is_last = (ticket == gridDim.x - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < static_cast<int>(gridDim.x); i += blockDim.x)
+        best = u64_max(best, __hip_atomic_load(&partial[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    best = wave_max_u64(best);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) lds_keys[wid] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = 0;
+        for (int i = 0; i < static_cast<int>(blockDim.x / kWave); ++i) b = u64_max(b, lds_keys[i]);
+        *out_idx = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(b));
+        *out_val = float_from_order_key(static_cast<uint32_t>(b >> 32));
+        *counter = 0u;  // ready for the next call (no host-side clear needed)
+    }
+}
+
+// ---------------------------------------------------------------------------
+// TILED64 kernel.  NCH = number of 4096-column chunks (the last may be partial);
+// a block has RG row groups x NCH waves, wave (rg, c) owns chunk c for the rows
+// of row group rg; R = rows per wave iteration.
+// ---------------------------------------------------------------------------
+template <int NCH, int RG, int R, int EPI>
+__global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
+    const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
+    const void* __restrict__ x, int x_f16, const float* __restrict__ norm_w, float eps, void* __restrict__ y,
+    int y_f16, uint64_t* __restrict__ partial, uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
+    float* __restrict__ out_val) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int G = cols >> 6;
+    unsigned char* xs = smem;
+    float4* gc = reinterpret_cast<float4*>(smem + static_cast<size_t>(G) * kGroupLdsBytes);
+    float* red = reinterpret_cast<float*>(gc + G);                   // 32 floats
+    uint64_t* lds_keys = reinterpret_cast<uint64_t*>(red + 32);      // 16 keys
+    float* part = reinterpret_cast<float*>(lds_keys + 16);           // [RG][NCH][R]
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int c = wid % NCH;
+    const int rg = wid / NCH;
+
+    float inv = 1.0f;
+    if (norm_w) inv = block_rms_inv(x, x_f16, cols, eps, red);
+    stage_activations(x, x_f16, norm_w, inv, G, xs, gc);
+    __syncthreads();
+
+    const int g = c * 64 + lane;
+    const bool has_group = g < G;
+    const int gcnt = min(64, G - c * 64);
+    uint4 xh[8], xl[8];
+    float4 gk = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        xh[j] = make_uint4(0, 0, 0, 0);
+        xl[j] = make_uint4(0, 0, 0, 0);
+    }
+    if (has_group) {
+        const unsigned char* gb = xs + static_cast<size_t>(g) * kGroupLdsBytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            xh[j] = *reinterpret_cast<const uint4*>(gb + j * 16);
+            xl[j] = *reinterpret_cast<const uint4*>(gb + 128 + j * 16);
+        }
+        gk = gc[g];
+    }
+
+    const size_t row_bytes = static_cast<size_t>(cols) >> 1;
+    const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = kMagic2;
+    uint64_t best = 0;
+    for (int base = blockIdx.x * RG; base * R < rows; base += gridDim.x * RG) {
+        const int r0 = (base + rg) * R;
+        float acc[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+        if (r0 < rows) {
+            uint4 wa[R], wb[R];
+            uint32_t mt[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int row = min(r0 + i, rows - 1);
+                if (has_group) {
+                    const uint8_t* rowp = nib + static_cast<size_t>(row) * row_bytes + c * 2048;
+                    wa[i] = load_nt16(rowp + lane * 16);
+                    wb[i] = load_nt16(rowp + gcnt * 16 + lane * 16);
+                    mt[i] = __builtin_nontemporal_load(meta + static_cast<size_t>(row) * G + g);
+                } else {
+                    wa[i] = make_uint4(0, 0, 0, 0);
+                    wb[i] = make_uint4(0, 0, 0, 0);
+                    mt[i] = 0u;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                float dh = 0.0f, dl = 0.0f;
+                dot8(wa[i].x, xh[0], xl[0], dh, dl, m_lo, m_hi, magic);
+                dot8(wa[i].y, xh[1], xl[1], dh, dl, m_lo, m_hi, magic);
+                dot8(wa[i].z, xh[2], xl[2], dh, dl, m_lo, m_hi, magic);
+                dot8(wa[i].w, xh[3], xl[3], dh, dl, m_lo, m_hi, magic);
+                dot8(wb[i].x, xh[4], xl[4], dh, dl, m_lo, m_hi, magic);
+                dot8(wb[i].y, xh[5], xl[5], dh, dl, m_lo, m_hi, magic);
+                dot8(wb[i].z, xh[6], xl[6], dh, dl, m_lo, m_hi, magic);
+                dot8(wb[i].w, xh[7], xl[7], dh, dl, m_lo, m_hi, magic);
+                // sum_c q_c x_c of the group, with the 1024 offsets removed per part
+                const float t = fmaf(dl - gk.z, 1.0f / 2048.0f, dh - gk.y);
+                const float s = half_lo(mt[i]);
+                const float z = half_hi(mt[i]);
+                acc[i] = affine ? fmaf(s, t, z * gk.x) : s * fmaf(-z, gk.x, t);
+                acc[i] = wave_sum(acc[i]);
+            }
+        }
+        if constexpr (NCH > 1) {
+            if (lane < R) {
+                float v = acc[0];
+#pragma unroll
+                for (int i = 1; i < R; ++i)
+                    if (lane == i) v = acc[i];
+                part[(rg * NCH + c) * R + lane] = v;
+            }
+            __syncthreads();
+            if (c == 0) {
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int cc = 0; cc < NCH; ++cc) t += part[(rg * NCH + cc) * R + i];
+                    acc[i] = t;
+                }
+            }
+            __syncthreads();
+        }
+        if (c != 0 || r0 >= rows) continue;
+        if constexpr (EPI == EPI_ARGMAX) {
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+                if (r0 + i < rows) best = u64_max(best, argmax_key(acc[i], static_cast<uint32_t>(r0 + i)));
+        } else if constexpr (EPI == EPI_SILU) {
+            float gv = acc[0], uv = acc[1];
+#pragma unroll
+            for (int i = 1; i < R / 2; ++i)
+                if (lane == i) {
+                    gv = acc[2 * i];
+                    uv = acc[2 * i + 1];
+                }
+            const int orow = (r0 >> 1) + lane;
+            if (lane < R / 2 && 2 * orow < rows) static_cast<float*>(y)[orow] = silu_dev(gv) * uv;
+        } else {
+            float v = acc[0];
+#pragma unroll
+            for (int i = 1; i < R; ++i)
+                if (lane == i) v = acc[i];
+            const int row = r0 + lane;
+            if (lane < R && row < rows) {
+                if constexpr (EPI == EPI_ADD) {
+                    static_cast<float*>(y)[row] += v;
+                } else {
+                    if (y_f16)
+                        static_cast<_Float16*>(y)[row] = static_cast<_Float16>(v);
+                    else
+                        static_cast<float*>(y)[row] = v;
+                }
+            }
+        }
+    }
+    if constexpr (EPI == EPI_ARGMAX) {
+        if (lane == 0) lds_keys[wid] = (c == 0) ? best : 0;
+        __syncthreads();
+        uint64_t b = 0;
+        if (threadIdx.x == 0)
+            for (int i = 0; i < NCH * RG; ++i) b = u64_max(b, lds_keys[i]);
+        __syncthreads();
+        finish_argmax(b, partial, counter, out_idx, out_val, lds_keys);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GENERIC kernel: any group size, reference row-major layout, fp32 metadata.
+// One wave per unit (a row, or a (gate, up) row pair for EPI_SILU); it follows
+// the reference's per-group factorisation directly.  Used for tiny shapes only.
+// ---------------------------------------------------------------------------
+template <int EPI>
+__global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict__ nib,
+                                                       const float* __restrict__ scales,
+                                                       const float* __restrict__ zeros, int rows, int cols,
+                                                       int group, int affine, const void* __restrict__ x, int x_f16,
+                                                       const float* __restrict__ norm_w, float eps,
+                                                       void* __restrict__ y, int y_f16,
+                                                       uint64_t* __restrict__ partial,
+                                                       uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
+                                                       float* __restrict__ out_val) {
+    __shared__ float red[32];
+    __shared__ uint64_t lds_keys[16];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    float inv = 1.0f;
+    if (norm_w) inv = block_rms_inv(x, x_f16, cols, eps, red);
+    const int G = (cols + group - 1) / group;
+    const size_t row_bytes = (static_cast<size_t>(cols) + 1) >> 1;
+    const int per_unit = (EPI == EPI_SILU) ? 2 : 1;
+    const int units = (rows + per_unit - 1) / per_unit;
+    uint64_t best = 0;
+    for (int u = blockIdx.x * nw + wid; u < units; u += gridDim.x * nw) {
+        float res[2] = {0.0f, 0.0f};
+        for (int k = 0; k < per_unit; ++k) {
+            const int row = u * per_unit + k;
+            if (row >= rows) break;
+            float a = 0.0f;
+            for (int g = lane; g < G; g += kWave) {
+                const int c0 = g * group;
+                const int n = min(group, cols - c0);
+                float cd = 0.0f, gs = 0.0f;
+                for (int c = c0; c < c0 + n; ++c) {
+                    const uint8_t b = nib[static_cast<size_t>(row) * row_bytes + (c >> 1)];
+                    const float q = static_cast<float>((c & 1) ? (b >> 4) : (b & 0x0f));
+                    float xv = load_act(x, x_f16, c);
+                    if (norm_w) xv = xv * inv * norm_w[c];
+                    cd += q * xv;
+                    gs += xv;
+                }
+                const size_t mi = static_cast<size_t>(row) * G + g;
+                if (affine)
+                    a += scales[mi] * cd + zeros[mi] * gs;
+                else
+                    a += scales[mi] * (cd - zeros[mi] * gs);
+            }
+            res[k] = wave_sum(a);
+        }
+        if (lane == 0) {
+            if constexpr (EPI == EPI_ARGMAX) {
+                best = u64_max(best, argmax_key(res[0], static_cast<uint32_t>(u)));
+            } else if constexpr (EPI == EPI_SILU) {
+                static_cast<float*>(y)[u] = silu_dev(res[0]) * res[1];
+            } else if constexpr (EPI == EPI_ADD) {
+                static_cast<float*>(y)[u] += res[0];
+            } else {
+                if (y_f16)
+                    static_cast<_Float16*>(y)[u] = static_cast<_Float16>(res[0]);
+                else
+                    static_cast<float*>(y)[u] = res[0];
+            }
+        }
+    }
+    if constexpr (EPI == EPI_ARGMAX) {
+        if (lane == 0) lds_keys[wid] = best;
+        __syncthreads();
+        uint64_t b = 0;
+        if (threadIdx.x == 0)
+            for (int i = 0; i < nw; ++i) b = u64_max(b, lds_keys[i]);
+        __syncthreads();
+        finish_argmax(b, partial, counter, out_idx, out_val, lds_keys);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host-side launch
+// ---------------------------------------------------------------------------
+
+constexpr int kThreads = 256;
+
+template <int NCH, int R, int EPI>
+static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
+    constexpr int RG = NCH == 1 ? 4 : (NCH == 4 ? 1 : 2);
+    const int G = p.cols >> 6;
+    const size_t lds = static_cast<size_t>(G) * (kGroupLdsBytes + sizeof(float4)) + 32 * sizeof(float) + 16 * 8 +
+                       RG * NCH * R * sizeof(float);
+    const int batches = (p.rows + R - 1) / R;
+    int blocks = (batches + RG - 1) / RG;
+    if (blocks > p.max_blocks) blocks = p.max_blocks;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
+                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.norm_w, p.eps,
+                       p.y, p.y_f16, p.partial, p.counter, p.out_idx, p.out_val);
+    return hipGetLastError();
+}
+
+template <int NCH>
+static hipError_t launch_tiled_nch(const GemvLaunch& p, hipStream_t s) {
+    switch (p.epi) {
+        case EPI_STORE: return launch_tiled_t<NCH, 2, EPI_STORE>(p, s);
+        case EPI_ADD: return launch_tiled_t<NCH, 2, EPI_ADD>(p, s);
+        case EPI_SILU: return launch_tiled_t<NCH, 2, EPI_SILU>(p, s);
+        case EPI_ARGMAX: return launch_tiled_t<NCH, 2, EPI_ARGMAX>(p, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int EPI>
+static hipError_t launch_generic_t(const GemvLaunch& p, hipStream_t s) {
+    const int per_unit = (EPI == EPI_SILU) ? 2 : 1;
+    const int units = (p.rows + per_unit - 1) / per_unit;
+    const int nw = kThreads / kWave;
+    int blocks = (units + nw - 1) / nw;
+    if (blocks > p.max_blocks) blocks = p.max_blocks;
+    if (blocks < 1) blocks = 1;
+    const float* sc = static_cast<const float*>(p.meta);
+    const int G = (p.cols + p.group - 1) / p.group;
+    const float* zr = sc + static_cast<size_t>(p.rows) * G;
+    hipLaunchKernelGGL((gemv_w4_generic<EPI>), dim3(blocks), dim3(kThreads), 0, s, p.nib, sc, zr, p.rows, p.cols,
+                       p.group, p.affine, p.x, p.x_f16, p.norm_w, p.eps, p.y, p.y_f16, p.partial, p.counter,
+                       p.out_idx, p.out_val);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s) {
+    if (p.layout == 0) {
+        const int G = p.cols >> 6;
+        const int nch = (G + 63) / 64;
+        switch (nch) {
+            case 1: return launch_tiled_nch<1>(p, s);
+            case 2: return launch_tiled_nch<2>(p, s);
+            case 3: return launch_tiled_nch<3>(p, s);
+            case 4: return launch_tiled_nch<4>(p, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    switch (p.epi) {
+        case EPI_STORE: return launch_generic_t<EPI_STORE>(p, s);
+        case EPI_ADD: return launch_generic_t<EPI_ADD>(p, s);
+        case EPI_SILU: return launch_generic_t<EPI_SILU>(p, s);
+        case EPI_ARGMAX: return launch_generic_t<EPI_ARGMAX>(p, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace xqhip

@@ -1,0 +1,125 @@
+// xqhip_common.hpp - shared device helpers for the gfx950 (CDNA4, wave64) kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xqhip {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Streaming (non-temporal) 16-byte load: weights are read once per token and
+// should not displace activations or the KV cache from the caches.
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// fp16 bit pattern 0x6400 is 1024.0; OR-ing a 4-bit code into mantissa bits
+// 0-3 gives 1024+q exactly, into bits 4-7 gives 1024+16q exactly.
+constexpr uint32_t kMagic2 = 0x64006400u;
+
+// (a & mask) | bits in one v_and_or_b32.  Written as inline asm because VOP3
+// cannot encode literal constants on gfx9-family targets and the compiler would
+// otherwise split it into v_and_b32 + v_or_b32 with literals; with the two
+// constants held in VGPRs (hoisted out of the loop) it is one instruction.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+    return r;
+}
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// v_dot2_f32_f16: a.x*b.x + a.y*b.y + c with fp32 accumulation (products of two
+// fp16 values are exact in fp32).
+__device__ __forceinline__ float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+__device__ __forceinline__ float half_lo(uint32_t u) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u & 0xffffu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t u) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16)));
+}
+
+// Butterfly sum over the 64 lanes of a wave; every lane ends with the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Sum over all threads of a block (blockDim.x a multiple of 64, <= 1024).
+// `red` is __shared__ scratch of at least 16 floats.  Every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int nw = (blockDim.x + kWave - 1) / kWave;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float sigmoid_dev(float x) {
+    if (x >= 0.0f) {
+        const float e = expf(-x);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(x);
+    return e / (1.0f + e);
+}
+
+__device__ __forceinline__ float softplus_dev(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return expf(x);
+    return log1pf(expf(x));
+}
+
+// Order-preserving map of a float to uint32 (larger float -> larger key);
+// NaN maps below -inf so it never wins an argmax.
+__device__ __forceinline__ uint32_t float_order_key(float v) {
+    if (v != v) return 0u;
+    const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);  // -0 ties with +0, as in a float compare
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float float_from_order_key(uint32_t k) {
+    const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(b);
+}
+
+// (value, index) packed so that the numeric max of the key is the largest value
+// and, among equal values, the lowest index.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    return (static_cast<uint64_t>(float_order_key(v)) << 32) | static_cast<uint64_t>(0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint64_t u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
+        v = u64_max(v, (static_cast<uint64_t>(hi) << 32) | lo);
+    }
+    return v;
+}
+
+}  // namespace xqhip
