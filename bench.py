@@ -85,11 +85,13 @@ def bench_mlp(args):
     h = xb.DeviceBuffer.from_array(inp["h"])
     ffn = xb.DeviceBuffer(inter * 4)
     hip = xb.hip()
+    pro = xb.prologue(xb.PRO_RMS, nw, eps=1e-6)
+    pro_ref = ctypes.byref(pro)
 
     def step(i):
         gu, dn = copies[i % ncopy]
-        xb.ck(hip.xqhip_gemv_w4a16(gu.ref, h.ptr, xb.F32, nw.ptr, 1e-6, ffn.ptr, xb.F32, xb.EPI_SILU_PAIR, None))
-        xb.ck(hip.xqhip_gemv_w4a16(dn.ref, ffn.ptr, xb.F32, None, 0.0, h.ptr, xb.F32, xb.EPI_ADD, None))
+        xb.ck(hip.xqhip_gemv_w4a16(gu.ref, h.ptr, xb.F32, pro_ref, ffn.ptr, xb.F32, xb.EPI_SILU_PAIR, None))
+        xb.ck(hip.xqhip_gemv_w4a16(dn.ref, ffn.ptr, xb.F32, None, h.ptr, xb.F32, xb.EPI_ADD, None))
 
     for i in range(args.warmup):
         step(i)
@@ -113,9 +115,9 @@ def bench_mlp(args):
             fn(i)
         return ev.stop_ms() / n
 
-    t_gu = time_kernel(lambda i: xb.ck(hip.xqhip_gemv_w4a16(copies[i % ncopy][0].ref, h.ptr, xb.F32, nw.ptr, 1e-6,
+    t_gu = time_kernel(lambda i: xb.ck(hip.xqhip_gemv_w4a16(copies[i % ncopy][0].ref, h.ptr, xb.F32, pro_ref,
                                                             ffn.ptr, xb.F32, xb.EPI_SILU_PAIR, None)))
-    t_dn = time_kernel(lambda i: xb.ck(hip.xqhip_gemv_w4a16(copies[i % ncopy][1].ref, ffn.ptr, xb.F32, None, 0.0,
+    t_dn = time_kernel(lambda i: xb.ck(hip.xqhip_gemv_w4a16(copies[i % ncopy][1].ref, ffn.ptr, xb.F32, None,
                                                             h.ptr, xb.F32, xb.EPI_ADD, None)))
     log(f"[bench] mlp step {ms_per_step * 1e3:.1f} us (wall {wall / args.steps * 1e3:.1f} us); "
         f"gate/up {t_gu * 1e3:.1f} us = {bytes_gu / t_gu / 1e6:.0f} GB/s; down {t_dn * 1e3:.1f} us = "

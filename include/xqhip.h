@@ -79,6 +79,12 @@ XQHIP_API int xqhip_free(void* ptr);
 XQHIP_API int xqhip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 XQHIP_API int xqhip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 XQHIP_API int xqhip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Asynchronous copies (no synchronisation); host memory should be pinned. */
+XQHIP_API int xqhip_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+XQHIP_API int xqhip_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream);
+/* Pinned host memory (hipHostMalloc). */
+XQHIP_API int xqhip_host_alloc(void** ptr, size_t bytes);
+XQHIP_API int xqhip_host_free(void* ptr);
 /* Byte fill done by a kernel (safe inside captured graphs). */
 XQHIP_API int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream);
 XQHIP_API int xqhip_stream_synchronize(void* stream);
@@ -100,25 +106,98 @@ XQHIP_API int xqhip_w4_free(xqhip_w4* w);
 XQHIP_API uint64_t xqhip_w4_weight_bytes(const xqhip_w4* w);
 
 /* ---- fused dequant GEMV ------------------------------------------------ */
+/* Normalisation applied to the GEMV input inside the kernel prologue. */
+enum {
+    XQHIP_PRO_NONE = 0,
+    XQHIP_PRO_RMS = 1,        /* x * inv * weight[c], inv = 1/sqrt(mean(x^2) + eps)
+                                 (rmsnormReference, ref_rmsnorm.cpp:8-17)          */
+    XQHIP_PRO_GATED_HEAD = 2  /* per head of head_dim values:
+                                 x * inv_h * weight[c % head_dim] * silu(gate[c])
+                                 (applyGatedHeadRms, custom_model.cpp:329-349)     */
+};
+typedef struct xqhip_prologue {
+    int32_t mode;
+    int32_t head_dim;     /* GATED_HEAD only                                      */
+    const float* weight;  /* device: RMS [cols], GATED_HEAD [head_dim]             */
+    const float* gate;    /* device: GATED_HEAD [cols]                             */
+    float eps;
+} xqhip_prologue;
+
 /* y = W x, replacing gemvW4A16Neon
  * (customlib/kernels/generated/arm64_neon/xq_gemv_w4a16_neon.cpp:259-291).
- * x: `cols` values of x_type.  If norm_w != NULL the kernel first applies the
- * RMSNorm of ref_rmsnorm.cpp:8-17 to x (x * inv * norm_w, eps) in its prologue.
+ * x: `cols` values of x_type, optionally normalised by `pro` (NULL = none).
  * y: `rows` values of y_type (EPI_SILU_PAIR: rows/2 values).  Inputs must not
  * alias outputs. */
-XQHIP_API int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const float* norm_w, float eps,
-                               void* y, int y_type, int epilogue, void* stream);
+XQHIP_API int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro, void* y,
+                               int y_type, int epilogue, void* stream);
 
 /* Workspace bytes xqhip_gemv_w4a16_argmax needs for a matrix of `rows` rows. */
 XQHIP_API size_t xqhip_argmax_workspace_bytes(int rows);
 /* Greedy lm_head: argmax_r (W x)[r] without materialising logits, ties to the
- * lowest row, replacing gemvW4A16ArgmaxNeon (xq_gemv_w4a16_neon.cpp:293-348).
- * Block-level argmax, then the last block to finish reduces the partials.
- * workspace: device memory of xqhip_argmax_workspace_bytes(rows), zeroed once
- * before first use (the kernel leaves it ready for the next call).
- * out_index / out_value: device int32 / float. */
-XQHIP_API int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const float* norm_w, float eps,
+ * lowest row, replacing gemvW4A16ArgmaxNeon (xq_gemv_w4a16_neon.cpp:293-348)
+ * and sampleGreedy (custom_model.cpp:1281-1338).  Block-level argmax, then the
+ * last block to finish reduces the partials.  workspace: device memory of
+ * xqhip_argmax_workspace_bytes(rows), zero-filled once before first use (the
+ * kernel leaves it ready for the next call).  out_index / out_value: device. */
+XQHIP_API int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
                                       void* workspace, int32_t* out_index, float* out_value, void* stream);
+
+/* ---- decode-step ops (all device pointers; `pos` is a device int32) ----- */
+/* out[hidden] = bf16 table row of *token as fp32; ids outside [0, vocab) wrap
+ * to |id| % vocab (loadEmbeddingRow, custom_model.cpp:569-608). */
+XQHIP_API int xqhip_embed_bf16(const uint16_t* table, int vocab, int hidden, const int32_t* token, float* out,
+                               void* stream);
+
+/* Host helper: the RoPE (cos, sin) table [max_pos][rotary_dim/2] for
+ * applyRopeVector (custom_model.cpp:351-370), computed with the host libm in
+ * the reference's float operation order: inv_freq = powf(theta, -2i/rd),
+ * angle = pos * inv_freq, (cosf(angle), sinf(angle)).  out: host floats,
+ * 2 * max_pos * (rotary_dim/2) of them. */
+XQHIP_API int xqhip_rope_table(float theta, int rotary_dim, int max_pos, float* out);
+
+/* Full-attention head preparation for position *pos: per query head, split
+ * the gated q_proj output into (q, gate) (custom_model.cpp:740-753), per-head
+ * RMSNorm of q and k (custom_model.cpp:301-313, weights already +1), partial
+ * RoPE from rope_cs (device copy of xqhip_rope_table), then k and v appended
+ * as fp16 at cache slot *pos of the [t][kv_head][head_dim] caches
+ * (appendKv, custom_model.cpp:673-733).  q_out, gate_out: nq*head_dim fp32
+ * (gate_out is 0 when gated == 0, matching custom_model.cpp:750-753). */
+XQHIP_API int xqhip_attn_prep(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
+                              int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
+                              const float* rope_cs, const int32_t* pos, float* q_out, float* gate_out, void* k_cache,
+                              void* v_cache, void* stream);
+
+/* GQA decode over the fp16 caches for context *pos + 1 (scores, softmax and
+ * V reduction of custom_model.cpp:840-928) followed by the sigmoid output gate
+ * (custom_model.cpp:929-951): out = softmax(q k^T / sqrt(d)) v * sigmoid(gate).
+ * workspace: xqhip_gqa_workspace_bytes(), zero-filled once before first use. */
+XQHIP_API size_t xqhip_gqa_workspace_bytes(int nq, int nkv, int head_dim);
+XQHIP_API int xqhip_gqa_decode(const float* q, const void* k_cache, const void* v_cache, const float* gate, int nq,
+                               int nkv, int head_dim, int max_ctx, const int32_t* pos, float* out, void* workspace,
+                               void* stream);
+
+/* Linear attention: conv1d + SiLU over the mixed q|k|v channels with the
+ * [channels][ksize-1] history updated in place, then L2-normalised q and k
+ * heads (custom_model.cpp:961-1047).  out: conv_dim fp32. */
+XQHIP_API int xqhip_linear_conv(const float* mixed, float* conv_state, const float* conv_w, int lk_n, int lk_hd,
+                                int lv_n, int lv_hd, int ksize, float* out, void* stream);
+/* Gated delta rule per value head on the fp32 state [lv_n][lk_hd][lv_hd]
+ * (custom_model.cpp:1074-1096, gatedDeltaDecodeReference ref_delta.cpp:8-41),
+ * with beta = sigmoid(b), g = -exp(a_log) * softplus(a + dt_bias).
+ * conv: output of xqhip_linear_conv; out: lv_n * lv_hd fp32. */
+XQHIP_API int xqhip_gated_delta(const float* conv, const float* a, const float* b, const float* a_log,
+                                const float* dt_bias, float* state, int lk_n, int lv_n, int lk_hd, int lv_hd,
+                                float* out, void* stream);
+/* y = x * inv * w (rmsnormReference, ref_rmsnorm.cpp:8-17). */
+XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream);
+
+/* ---- streams and graphs ------------------------------------------------ */
+XQHIP_API int xqhip_stream_create(void** stream);
+XQHIP_API int xqhip_stream_destroy(void* stream);
+XQHIP_API int xqhip_graph_begin(void* stream);
+XQHIP_API int xqhip_graph_end(void* stream, void** graph_exec);
+XQHIP_API int xqhip_graph_launch(void* graph_exec, void* stream);
+XQHIP_API int xqhip_graph_destroy(void* graph_exec);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,227 @@
+"""GPU parity of the non-GEMV decode kernels against the oracle restatements of
+customlib/runtime/custom_model.cpp (embedding :569-608, q/gate split :740-753,
+head RMSNorm :301-313, partial RoPE :351-370, KV append :673-733, GQA decode
+:840-928, output gate :929-951, conv1d :961-1010, L2 norm :315-327, gated delta
+:1074-1096 / ref_delta.cpp:8-41).
+
+Shapes follow the one-layer decode workloads at position 511: 32 query heads,
+8 KV heads, head_dim 128, rotary 32, theta 1e7, a seeded fp16 KV cache of 511
+tokens ~N(0,1) plus the appended one; linear attention with 16 key heads and
+32 value heads of 128, fp32 state ~N(0, 0.1), decay in (0,1), beta ~U(0,1).
+Tolerance for fp32/fp16 outputs: |gpu - oracle| <= 1e-2 + 1e-3 |oracle|;
+index and layout checks are exact.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle_bind as ob
+import xqbind as xb
+
+pytestmark = pytest.mark.gpu
+O = ob.oracle
+ATOL, RTOL = 1e-2, 1e-3
+
+
+def close(got, want, what, atol=ATOL, rtol=RTOL):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bad = err > atol + rtol * np.abs(want)
+    assert not bad.any(), f"{what}: {bad.sum()} / {bad.size} bad, max err {err.max():.3g}"
+
+
+def dev(a):
+    return xb.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def bf16_bits(x):
+    return (np.asarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_embedding_rows_and_wrap():
+    vocab, hidden = 1000, 4096
+    rng = np.random.default_rng(0)
+    table = bf16_bits(rng.normal(0, 1, vocab * hidden).astype(np.float32))
+    td = dev(table)
+    out = xb.DeviceBuffer(hidden * 4)
+    tok = xb.DeviceBuffer(4)
+    for t in (0, 17, 999, -5, 1003, -2000):
+        tok.upload(np.array([t], np.int32))
+        xb.ck(xb.hip().xqhip_embed_bf16(td.ptr, vocab, hidden, tok.ptr, out.ptr, None))
+        got = out.download(np.float32, hidden)
+        row = t if 0 <= t < vocab else abs(t) % vocab
+        want = (table[row * hidden:(row + 1) * hidden].astype(np.uint32) << 16).view(np.float32)
+        assert np.array_equal(got, want), t
+
+
+def test_rope_table_matches_oracle_libm():
+    rd, theta, npos = 32, 1e7, 600
+    tab = np.empty(npos * rd, np.float32)
+    xb.ck(xb.hip().xqhip_rope_table(theta, rd, npos, xb.ptr(tab)))
+    tab = tab.reshape(npos, rd // 2, 2)
+    # rotate unit vectors with the oracle: (1,0) -> (cos, sin)
+    for pos in (0, 1, 511, 599):
+        x = np.zeros(rd, np.float32)
+        x[: rd // 2] = 1.0
+        O().orc_rope_partial(ob.p(x), 1, rd, rd, pos, theta)
+        assert np.array_equal(x[: rd // 2], tab[pos, :, 0]) and np.array_equal(x[rd // 2:], tab[pos, :, 1])
+
+
+def attn_layer_inputs(nq=32, nkv=8, hd=128, ctx_before=511, seed=5, gated=True):
+    rng = np.random.default_rng(seed)
+    qsrc = rng.normal(0, 1, nq * hd * (2 if gated else 1)).astype(np.float32)
+    k = rng.normal(0, 1, nkv * hd).astype(np.float32)
+    v = rng.normal(0, 1, nkv * hd).astype(np.float32)
+    qn = rng.normal(1, 0.1, hd).astype(np.float32)
+    kn = rng.normal(1, 0.1, hd).astype(np.float32)
+    kc = rng.normal(0, 1, (ctx_before, nkv, hd)).astype(np.float16)
+    vc = rng.normal(0, 1, (ctx_before, nkv, hd)).astype(np.float16)
+    return qsrc, k, v, qn, kn, kc, vc
+
+
+@pytest.mark.parametrize("gated", [True, False])
+def test_attention_prep_and_gqa_decode_pos511(gated):
+    nq, nkv, hd, rd, theta, pos, eps = 32, 8, 128, 32, 1e7, 511, 1e-6
+    max_ctx = 1024
+    qsrc, k, v, qn, kn, kc, vc = attn_layer_inputs(gated=gated)
+    # ---- oracle (custom_model.cpp:740-951 order) ----
+    if gated:
+        qq = qsrc.reshape(nq, 2, hd)[:, 0].reshape(-1).copy()
+        gate = qsrc.reshape(nq, 2, hd)[:, 1].reshape(-1).copy()
+    else:
+        qq, gate = qsrc.copy(), np.zeros(nq * hd, np.float32)
+    kk = k.copy()
+    O().orc_head_rms(ob.p(qq), ob.p(qn), nq, hd, eps)
+    O().orc_head_rms(ob.p(kk), ob.p(kn), nkv, hd, eps)
+    O().orc_rope_partial(ob.p(qq), nq, hd, rd, pos, theta)
+    O().orc_rope_partial(ob.p(kk), nkv, hd, rd, pos, theta)
+    # ---- device ----
+    tab = np.empty(max_ctx * rd, np.float32)
+    xb.ck(xb.hip().xqhip_rope_table(theta, rd, max_ctx, xb.ptr(tab)))
+    kcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    vcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    kcache[:pos], vcache[:pos] = kc, vc
+    kd, vd = dev(kcache), dev(vcache)
+    qs_d, k_d, v_d = dev(qsrc), dev(k), dev(v)
+    qn_d, kn_d, tab_d = dev(qn), dev(kn), dev(tab)
+    pos_d = dev(np.array([pos], np.int32))
+    qo, go = xb.DeviceBuffer(nq * hd * 4), xb.DeviceBuffer(nq * hd * 4)
+    xb.ck(xb.hip().xqhip_attn_prep(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr, kn_d.ptr, eps,
+                                   tab_d.ptr, pos_d.ptr, qo.ptr, go.ptr, kd.ptr, vd.ptr, None))
+    q_got = qo.download(np.float32, nq * hd)
+    close(q_got, qq, "q after norm+rope", atol=1e-5, rtol=1e-5)
+    assert np.array_equal(go.download(np.float32, nq * hd), gate)
+    kc_got = kd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+    vc_got = vd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+    assert np.array_equal(kc_got[:pos], kc) and np.array_equal(vc_got[:pos], vc)  # earlier slots untouched
+    assert np.array_equal(vc_got[pos].reshape(-1), v.astype(np.float16))          # slot layout [t][kvh][d]
+    close(kc_got[pos].reshape(-1).astype(np.float32), kk, "appended k", atol=2e-3, rtol=1e-3)
+    # ---- attention over the fp16 cache (the oracle sees the same fp16 values) ----
+    ctx = pos + 1
+    kf = kc_got[:ctx].astype(np.float32).reshape(-1)
+    vf = vc_got[:ctx].astype(np.float32).reshape(-1)
+    att = np.empty(nq * hd, np.float32)
+    O().orc_attention_model(ob.p(qq), ob.p(kf), ob.p(vf), ctx, nkv, nq, hd, ob.p(att))
+    sig = np.array([O().orc_sigmoid(float(g)) for g in gate], np.float32)
+    want = att * sig
+    ws = xb.DeviceBuffer(xb.hip().xqhip_gqa_workspace_bytes(nq, nkv, hd))
+    ws.zero()
+    out = xb.DeviceBuffer(nq * hd * 4)
+    for _ in range(2):  # the combine counters re-arm themselves
+        xb.ck(xb.hip().xqhip_gqa_decode(qo.ptr, kd.ptr, vd.ptr, go.ptr, nq, nkv, hd, max_ctx, pos_d.ptr, out.ptr,
+                                        ws.ptr, None))
+        close(out.download(np.float32, nq * hd), want, "gqa decode + gate")
+
+
+@pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 100])
+def test_gqa_short_contexts(ctx):
+    nq, nkv, hd = 4, 2, 8
+    rng = np.random.default_rng(ctx)
+    q = rng.normal(0, 1, nq * hd).astype(np.float32)
+    kc = rng.normal(0, 1, (ctx, nkv, hd)).astype(np.float16)
+    vc = rng.normal(0, 1, (ctx, nkv, hd)).astype(np.float16)
+    gate = rng.normal(0, 1, nq * hd).astype(np.float32)
+    att = np.empty(nq * hd, np.float32)
+    O().orc_attention_model(ob.p(q), ob.p(kc.astype(np.float32).reshape(-1)), ob.p(vc.astype(np.float32).reshape(-1)),
+                            ctx, nkv, nq, hd, ob.p(att))
+    want = att * np.array([O().orc_sigmoid(float(g)) for g in gate], np.float32)
+    ws = xb.DeviceBuffer(xb.hip().xqhip_gqa_workspace_bytes(nq, nkv, hd))
+    ws.zero()
+    out = xb.DeviceBuffer(nq * hd * 4)
+    xb.ck(xb.hip().xqhip_gqa_decode(dev(q).ptr, dev(kc).ptr, dev(vc).ptr, dev(gate).ptr, nq, nkv, hd, 128,
+                                    dev(np.array([ctx - 1], np.int32)).ptr, out.ptr, ws.ptr, None))
+    close(out.download(np.float32, nq * hd), want, f"gqa ctx={ctx}")
+
+
+def linear_inputs(lk_n=16, lv_n=32, lk_hd=128, lv_hd=128, ks=4, seed=9):
+    rng = np.random.default_rng(seed)
+    conv_dim = 2 * lk_n * lk_hd + lv_n * lv_hd
+    mixed = rng.normal(0, 1, conv_dim).astype(np.float32)
+    state = rng.normal(0, 0.5, conv_dim * (ks - 1)).astype(np.float32)
+    w = rng.normal(0, 0.5, conv_dim * ks).astype(np.float32)
+    return mixed, state, w
+
+
+@pytest.mark.parametrize("shape", [(16, 32, 128, 128, 4), (1, 2, 2, 2, 2), (3, 6, 64, 32, 3)])
+def test_linear_conv_and_gated_delta(shape):
+    lk_n, lv_n, lk_hd, lv_hd, ks = shape
+    mixed, cstate, cw = linear_inputs(lk_n, lv_n, lk_hd, lv_hd, ks)
+    conv_dim = mixed.size
+    # oracle conv + l2 norm (custom_model.cpp:986-1047)
+    st_o = cstate.copy()
+    conv_o = np.empty(conv_dim, np.float32)
+    O().orc_conv1d_step(ob.p(mixed), ob.p(st_o), ob.p(cw), conv_dim, ks, ob.p(conv_o))
+    qv = conv_o[: lk_n * lk_hd].copy()
+    kv = conv_o[lk_n * lk_hd: 2 * lk_n * lk_hd].copy()
+    O().orc_l2norm_heads(ob.p(qv), lk_n, lk_hd)
+    O().orc_l2norm_heads(ob.p(kv), lk_n, lk_hd)
+    conv_o[: lk_n * lk_hd] = qv
+    conv_o[lk_n * lk_hd: 2 * lk_n * lk_hd] = kv
+    # device conv
+    md, sd, wd = dev(mixed), dev(cstate), dev(cw)
+    cout = xb.DeviceBuffer(conv_dim * 4)
+    xb.ck(xb.hip().xqhip_linear_conv(md.ptr, sd.ptr, wd.ptr, lk_n, lk_hd, lv_n, lv_hd, ks, cout.ptr, None))
+    conv_g = cout.download(np.float32, conv_dim)
+    close(conv_g, conv_o, "conv1d+silu+l2norm", atol=1e-5, rtol=1e-5)
+    assert np.array_equal(sd.download(np.float32, cstate.size), st_o)  # history shift is exact
+    # gated delta: decay in (0,1), beta ~U(0,1)
+    rng = np.random.default_rng(11)
+    beta_t = rng.uniform(0, 1, lv_n)
+    b = np.log(beta_t / (1 - beta_t)).astype(np.float32)
+    a = rng.normal(0, 1, lv_n).astype(np.float32)
+    a_log = rng.normal(-1, 0.5, lv_n).astype(np.float32)
+    dt = rng.normal(0, 0.5, lv_n).astype(np.float32)
+    S0 = rng.normal(0, 0.1, lv_n * lk_hd * lv_hd).astype(np.float32)
+    S_o = S0.copy()
+    out_o = np.zeros(lv_n * lv_hd, np.float32)
+    factor = max(1, lv_n // max(1, lk_n))
+    for vh in range(lv_n):
+        kh = min(lk_n - 1, vh // factor)
+        beta = O().orc_sigmoid(float(b[vh]))
+        gate = np.float32(-np.exp(np.float32(a_log[vh]))) * np.float32(O().orc_softplus(float(a[vh] + dt[vh])))
+        qh = np.ascontiguousarray(conv_o[kh * lk_hd:(kh + 1) * lk_hd])
+        khv = np.ascontiguousarray(conv_o[lk_n * lk_hd + kh * lk_hd: lk_n * lk_hd + (kh + 1) * lk_hd])
+        vv = np.ascontiguousarray(conv_o[2 * lk_n * lk_hd + vh * lv_hd: 2 * lk_n * lk_hd + (vh + 1) * lv_hd])
+        Sv = S_o[vh * lk_hd * lv_hd:(vh + 1) * lk_hd * lv_hd]
+        ov = np.zeros(lv_hd, np.float32)
+        O().orc_gated_delta(ob.p(qh), ob.p(khv), ob.p(vv), beta, float(gate), lk_hd, lv_hd, ob.p(Sv), ob.p(ov))
+        S_o[vh * lk_hd * lv_hd:(vh + 1) * lk_hd * lv_hd] = Sv
+        out_o[vh * lv_hd:(vh + 1) * lv_hd] = ov
+    Sd = dev(S0)
+    od = xb.DeviceBuffer(lv_n * lv_hd * 4)
+    xb.ck(xb.hip().xqhip_gated_delta(dev(conv_o).ptr, dev(a).ptr, dev(b).ptr, dev(a_log).ptr, dev(dt).ptr, Sd.ptr,
+                                     lk_n, lv_n, lk_hd, lv_hd, od.ptr, None))
+    close(od.download(np.float32, lv_n * lv_hd), out_o, "gated delta out", atol=1e-4, rtol=1e-4)
+    close(Sd.download(np.float32, S0.size), S_o, "gated delta state", atol=1e-5, rtol=1e-4)
+
+
+def test_rmsnorm_kernel():
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 5, 4096).astype(np.float32)
+    w = rng.normal(1, 0.1, 4096).astype(np.float32)
+    want = np.empty_like(x)
+    O().orc_rmsnorm(ob.p(x), ob.p(w), 4096, 1e-6, ob.p(want))
+    y = xb.DeviceBuffer(4096 * 4)
+    xb.ck(xb.hip().xqhip_rmsnorm(dev(x).ptr, dev(w).ptr, 4096, 1e-6, y.ptr, None))
+    close(y.download(np.float32, 4096), want, "rmsnorm", atol=1e-5, rtol=1e-5)

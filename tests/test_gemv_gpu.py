@@ -5,6 +5,8 @@ oracle's restatement of gemvW4A16Neon / gemvW4A16ArgmaxNeon
 Tolerance (fp16/fp32 outputs): |gpu - oracle| <= 1e-2 + 1e-3 * |oracle|.
 Greedy ids: bit-exact whenever the oracle's top-2 margin exceeds 1e-2.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -36,7 +38,9 @@ def run_gemv(q, x, x_type=xb.F16, y_type=xb.F32, norm_w=None, eps=1e-6, epi=xb.E
     yd = xb.DeviceBuffer(out_n * np.dtype(ydt).itemsize)
     if y_init is not None:
         yd.upload(y_init.astype(ydt))
-    xb.ck(xb.hip().xqhip_gemv_w4a16(w.ref, xd.ptr, x_type, nd.ptr if nd else None, eps, yd.ptr, y_type, epi, None))
+    pro = xb.prologue(xb.PRO_RMS, nd, eps=eps) if nd else None
+    xb.ck(xb.hip().xqhip_gemv_w4a16(w.ref, xd.ptr, x_type, ctypes.byref(pro) if pro else None, yd.ptr, y_type, epi,
+                                    None))
     xb.ck(xb.hip().xqhip_device_synchronize())
     return yd.download(ydt, out_n).astype(np.float32), w
 
@@ -129,7 +133,8 @@ def run_argmax(q, x, x_type=xb.F32, norm_w=None, calls=1):
     val = xb.DeviceBuffer(4)
     res = []
     for _ in range(calls):
-        xb.ck(xb.hip().xqhip_gemv_w4a16_argmax(w.ref, xd.ptr, x_type, nd.ptr if nd else None, 1e-6, ws.ptr,
+        pro = xb.prologue(xb.PRO_RMS, nd, eps=1e-6) if nd else None
+        xb.ck(xb.hip().xqhip_gemv_w4a16_argmax(w.ref, xd.ptr, x_type, ctypes.byref(pro) if pro else None, ws.ptr,
                                                idx.ptr, val.ptr, None))
         xb.ck(xb.hip().xqhip_device_synchronize())
         res.append((int(idx.download(np.int32, 1)[0]), float(val.download(np.float32, 1)[0])))
@@ -182,3 +187,23 @@ def test_argmax_fused_final_norm():
     assert abs(got_val - want_val) <= ATOL + RTOL * abs(want_val)
     if top2_margin(ob.gemv(q, normed)) > 1e-2:
         assert got_idx == want_idx
+
+
+def test_gemv_gated_head_prologue():
+    """out_proj input of the linear-attention layer: per-head gated RMSNorm fused
+    into the GEMV prologue (applyGatedHeadRms, custom_model.cpp:329-349)."""
+    heads, hd, hidden = 32, 128, 4096
+    q = w4_matrix(hidden, heads * hd, 91)
+    rng = np.random.default_rng(92)
+    o = rng.normal(0, 0.3, heads * hd).astype(np.float32)
+    z = rng.normal(0, 1, heads * hd).astype(np.float32)
+    w = rng.normal(1, 0.1, hd).astype(np.float32)
+    normed = np.empty_like(o)
+    ob.oracle().orc_gated_head_rms(ob.p(o), ob.p(w), ob.p(z), heads, hd, 1e-6, ob.p(normed))
+    want = ob.gemv(q, normed)
+    dw = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols)
+    od, zd, wd = xb.DeviceBuffer.from_array(o), xb.DeviceBuffer.from_array(z), xb.DeviceBuffer.from_array(w)
+    yd = xb.DeviceBuffer(hidden * 4)
+    pro = xb.prologue(xb.PRO_GATED_HEAD, wd, zd, head_dim=hd, eps=1e-6)
+    xb.ck(xb.hip().xqhip_gemv_w4a16(dw.ref, od.ptr, xb.F32, ctypes.byref(pro), yd.ptr, xb.F32, xb.EPI_STORE, None))
+    assert_close(yd.download(np.float32, hidden), want, "gated-head prologue gemv")

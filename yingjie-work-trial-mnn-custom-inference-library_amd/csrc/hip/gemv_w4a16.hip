@@ -40,15 +40,43 @@ __device__ __forceinline__ float load_act(const void* x, int x_f16, int i) {
     return static_cast<const float*>(x)[i];
 }
 
-// RMSNorm factor of ref_rmsnorm.cpp:8-17 over the block: 1/sqrt(mean(x^2)+eps).
-__device__ float block_rms_inv(const void* x, int x_f16, int n, float eps, float* red) {
-    float ss = 0.0f;
-    for (int c = threadIdx.x; c < n; c += blockDim.x) {
-        const float v = load_act(x, x_f16, c);
-        ss += v * v;
+// Normalisation prologues fused into the GEMV (computed by every block from x):
+//   PRO_RMS   x * inv * w[c], inv = 1/sqrt(mean(x^2)+eps)        (ref_rmsnorm.cpp:8-17)
+//   PRO_GATED per head h of head_dim values: x * inv_h * w[c % head_dim] * silu(z[c])
+//             (applyGatedHeadRms, custom_model.cpp:329-349)
+// inv_lds receives inv (PRO_RMS) or inv_h for every head (PRO_GATED).
+__device__ void prologue_factors(const void* x, int x_f16, int n, const Prologue& pro, float* inv_lds, float* red) {
+    if (pro.mode == PRO_RMS) {
+        float ss = 0.0f;
+        for (int c = threadIdx.x; c < n; c += blockDim.x) {
+            const float v = load_act(x, x_f16, c);
+            ss += v * v;
+        }
+        ss = block_sum(ss, red);
+        if (threadIdx.x == 0) inv_lds[0] = 1.0f / sqrtf(ss / static_cast<float>(n) + pro.eps);
+    } else if (pro.mode == PRO_GATED) {
+        const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = blockDim.x / kWave;
+        const int heads = n / pro.head_dim;
+        for (int h = wid; h < heads; h += nw) {
+            float ss = 0.0f;
+            for (int d = lane; d < pro.head_dim; d += kWave) {
+                const float v = load_act(x, x_f16, h * pro.head_dim + d);
+                ss += v * v;
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) inv_lds[h] = 1.0f / sqrtf(ss / static_cast<float>(pro.head_dim) + pro.eps);
+        }
     }
-    ss = block_sum(ss, red);
-    return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+    __syncthreads();
+}
+
+__device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& pro, const float* inv_lds) {
+    if (pro.mode == PRO_RMS) return v * inv_lds[0] * pro.w[c];
+    if (pro.mode == PRO_GATED) {
+        const int h = c / pro.head_dim;
+        return v * inv_lds[h] * pro.w[c - h * pro.head_dim] * silu_dev(pro.z[c]);
+    }
+    return v;
 }
 
 // Stage x (optionally RMS-normalised) for the dot2 inner loop.
@@ -56,7 +84,7 @@ __device__ float block_rms_inv(const void* x, int x_f16, int n, float eps, float
 // word j of a group holds, for columns 8j..8j+7, the fp16 pairs
 // (x0,x4) (x1/16,x5/16) (x2,x6) (x3/16,x7/16).
 // gc[g] = (sum of the effective x of the group, 1024*sum(hi staged), 1024*sum(lo staged), 0).
-__device__ void stage_activations(const void* x, int x_f16, const float* norm_w, float inv, int groups,
+__device__ void stage_activations(const void* x, int x_f16, const Prologue& pro, const float* inv_lds, int groups,
                                   unsigned char* xs_bytes, float4* gc) {
     for (int it = threadIdx.x; it < groups * 4; it += blockDim.x) {
         const int g = it >> 2, qtr = it & 3;
@@ -68,8 +96,7 @@ __device__ void stage_activations(const void* x, int x_f16, const float* norm_w,
             _Float16 sh[8], sl[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                float v = load_act(x, x_f16, c0 + i);
-                if (norm_w) v = v * inv * norm_w[c0 + i];
+                const float v = prologue_apply(load_act(x, x_f16, c0 + i), c0 + i, pro, inv_lds);
                 const _Float16 hi = static_cast<_Float16>(v);
                 const float lo = (v - static_cast<float>(hi)) * 2048.0f;
                 const float sc = (i & 1) ? 0.0625f : 1.0f;
@@ -161,7 +188,7 @@ __device__ void finish_argmax(uint64_t block_best, uint64_t* partial, uint32_t* 
 template <int NCH, int RG, int R, int EPI>
 __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
-    const void* __restrict__ x, int x_f16, const float* __restrict__ norm_w, float eps, void* __restrict__ y,
+    const void* __restrict__ x, int x_f16, Prologue pro, void* __restrict__ y,
     int y_f16, uint64_t* __restrict__ partial, uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
     float* __restrict__ out_val) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -171,15 +198,15 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     float* red = reinterpret_cast<float*>(gc + G);                   // 32 floats
     uint64_t* lds_keys = reinterpret_cast<uint64_t*>(red + 32);      // 16 keys
     float* part = reinterpret_cast<float*>(lds_keys + 16);           // [RG][NCH][R]
+    float* inv_lds = part + RG * NCH * R;                            // [kMaxNormHeads]
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = threadIdx.x / kWave;
     const int c = wid % NCH;
     const int rg = wid / NCH;
 
-    float inv = 1.0f;
-    if (norm_w) inv = block_rms_inv(x, x_f16, cols, eps, red);
-    stage_activations(x, x_f16, norm_w, inv, G, xs, gc);
+    prologue_factors(x, x_f16, cols, pro, inv_lds, red);
+    stage_activations(x, x_f16, pro, inv_lds, G, xs, gc);
     __syncthreads();
 
     const int g = c * 64 + lane;
@@ -320,18 +347,17 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
                                                        const float* __restrict__ scales,
                                                        const float* __restrict__ zeros, int rows, int cols,
                                                        int group, int affine, const void* __restrict__ x, int x_f16,
-                                                       const float* __restrict__ norm_w, float eps,
-                                                       void* __restrict__ y, int y_f16,
+                                                       Prologue pro, void* __restrict__ y, int y_f16,
                                                        uint64_t* __restrict__ partial,
                                                        uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
                                                        float* __restrict__ out_val) {
     __shared__ float red[32];
     __shared__ uint64_t lds_keys[16];
+    __shared__ float inv_lds[kMaxNormHeads];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = threadIdx.x / kWave;
     const int nw = blockDim.x / kWave;
-    float inv = 1.0f;
-    if (norm_w) inv = block_rms_inv(x, x_f16, cols, eps, red);
+    prologue_factors(x, x_f16, cols, pro, inv_lds, red);
     const int G = (cols + group - 1) / group;
     const size_t row_bytes = (static_cast<size_t>(cols) + 1) >> 1;
     const int per_unit = (EPI == EPI_SILU) ? 2 : 1;
@@ -350,8 +376,7 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
                 for (int c = c0; c < c0 + n; ++c) {
                     const uint8_t b = nib[static_cast<size_t>(row) * row_bytes + (c >> 1)];
                     const float q = static_cast<float>((c & 1) ? (b >> 4) : (b & 0x0f));
-                    float xv = load_act(x, x_f16, c);
-                    if (norm_w) xv = xv * inv * norm_w[c];
+                    const float xv = prologue_apply(load_act(x, x_f16, c), c, pro, inv_lds);
                     cd += q * xv;
                     gs += xv;
                 }
@@ -400,13 +425,18 @@ static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     constexpr int RG = NCH == 1 ? 4 : (NCH == 4 ? 1 : 2);
     const int G = p.cols >> 6;
     const size_t lds = static_cast<size_t>(G) * (kGroupLdsBytes + sizeof(float4)) + 32 * sizeof(float) + 16 * 8 +
-                       RG * NCH * R * sizeof(float);
+                       (RG * NCH * R + kMaxNormHeads) * sizeof(float);
     const int batches = (p.rows + R - 1) / R;
     int blocks = (batches + RG - 1) / RG;
     if (blocks > p.max_blocks) blocks = p.max_blocks;
     if (blocks < 1) blocks = 1;
+    if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
-                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.norm_w, p.eps,
+                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro,
                        p.y, p.y_f16, p.partial, p.counter, p.out_idx, p.out_val);
     return hipGetLastError();
 }
@@ -434,7 +464,7 @@ static hipError_t launch_generic_t(const GemvLaunch& p, hipStream_t s) {
     const int G = (p.cols + p.group - 1) / p.group;
     const float* zr = sc + static_cast<size_t>(p.rows) * G;
     hipLaunchKernelGGL((gemv_w4_generic<EPI>), dim3(blocks), dim3(kThreads), 0, s, p.nib, sc, zr, p.rows, p.cols,
-                       p.group, p.affine, p.x, p.x_f16, p.norm_w, p.eps, p.y, p.y_f16, p.partial, p.counter,
+                       p.group, p.affine, p.x, p.x_f16, p.pro, p.y, p.y_f16, p.partial, p.counter,
                        p.out_idx, p.out_val);
     return hipGetLastError();
 }

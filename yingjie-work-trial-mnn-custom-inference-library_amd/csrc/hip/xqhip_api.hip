@@ -5,6 +5,7 @@
 #include "xqhip_kernels.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -112,6 +113,23 @@ int xqhip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     if (bytes == 0) return XQHIP_OK;
     return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)), "memcpy d2d");
 }
+
+int xqhip_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return XQHIP_OK;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)), "memcpy h2d async");
+}
+
+int xqhip_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return XQHIP_OK;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)), "memcpy d2h async");
+}
+
+int xqhip_host_alloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(XQHIP_EINVAL, "xqhip_host_alloc: null out pointer");
+    return check(hipHostMalloc(ptr, bytes == 0 ? 1 : bytes, hipHostMallocDefault), "hipHostMalloc");
+}
+
+int xqhip_host_free(void* ptr) { return ptr ? check(hipHostFree(ptr), "hipHostFree") : XQHIP_OK; }
 
 int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream) {
     if (bytes == 0) return XQHIP_OK;
@@ -226,16 +244,28 @@ static int validate_w4(const xqhip_w4* w, const char* who) {
     return XQHIP_OK;
 }
 
-int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const float* norm_w, float eps, void* y,
-                     int y_type, int epilogue, void* stream) {
-    if (int rc = validate_w4(w, "xqhip_gemv_w4a16")) return rc;
-    if (!x || !y) return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: null vector");
-    if (epilogue < XQHIP_EPI_STORE || epilogue > XQHIP_EPI_SILU_PAIR)
-        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: unknown epilogue %d", epilogue);
-    if (epilogue == XQHIP_EPI_SILU_PAIR && (w->rows % 2 != 0))
-        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: SILU_PAIR needs an even row count");
-    if (epilogue != XQHIP_EPI_STORE && y_type != XQHIP_F32)
-        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: ADD/SILU_PAIR write fp32");
+static xqhip::Prologue make_prologue(const xqhip_prologue* pro) {
+    xqhip::Prologue p{};
+    if (pro) {
+        p.mode = pro->mode;
+        p.w = pro->weight;
+        p.z = pro->gate;
+        p.head_dim = pro->head_dim;
+        p.eps = pro->eps;
+    }
+    return p;
+}
+
+static int validate_prologue(const xqhip_prologue* pro, int cols, const char* who) {
+    if (!pro || pro->mode == XQHIP_PRO_NONE) return XQHIP_OK;
+    if (pro->mode == XQHIP_PRO_RMS && pro->weight) return XQHIP_OK;
+    if (pro->mode == XQHIP_PRO_GATED_HEAD && pro->weight && pro->gate && pro->head_dim > 0 &&
+        cols % pro->head_dim == 0 && cols / pro->head_dim <= xqhip::kMaxNormHeads)
+        return XQHIP_OK;
+    return fail(XQHIP_EINVAL, "%s: bad prologue (mode %d)", who, pro->mode);
+}
+
+static xqhip::GemvLaunch base_launch(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro) {
     xqhip::GemvLaunch p{};
     p.nib = static_cast<const uint8_t*>(w->nib);
     p.meta = w->meta;
@@ -246,8 +276,22 @@ int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const float* 
     p.layout = w->layout;
     p.x = x;
     p.x_f16 = x_type == XQHIP_F16;
-    p.norm_w = norm_w;
-    p.eps = eps;
+    p.pro = make_prologue(pro);
+    return p;
+}
+
+int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro, void* y, int y_type,
+                     int epilogue, void* stream) {
+    if (int rc = validate_w4(w, "xqhip_gemv_w4a16")) return rc;
+    if (int rc = validate_prologue(pro, w->cols, "xqhip_gemv_w4a16")) return rc;
+    if (!x || !y) return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: null vector");
+    if (epilogue < XQHIP_EPI_STORE || epilogue > XQHIP_EPI_SILU_PAIR)
+        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: unknown epilogue %d", epilogue);
+    if (epilogue == XQHIP_EPI_SILU_PAIR && (w->rows % 2 != 0))
+        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: SILU_PAIR needs an even row count");
+    if (epilogue != XQHIP_EPI_STORE && y_type != XQHIP_F32)
+        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: ADD/SILU_PAIR write fp32");
+    xqhip::GemvLaunch p = base_launch(w, x, x_type, pro);
     p.y = y;
     p.y_f16 = y_type == XQHIP_F16;
     p.epi = epilogue;
@@ -260,30 +304,149 @@ size_t xqhip_argmax_workspace_bytes(int rows) {
     return 256 + sizeof(uint64_t) * kArgmaxMaxBlocks;
 }
 
-int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const float* norm_w, float eps,
-                            void* workspace, int32_t* out_index, float* out_value, void* stream) {
+int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro, void* workspace,
+                            int32_t* out_index, float* out_value, void* stream) {
     if (int rc = validate_w4(w, "xqhip_gemv_w4a16_argmax")) return rc;
+    if (int rc = validate_prologue(pro, w->cols, "xqhip_gemv_w4a16_argmax")) return rc;
     if (!x || !workspace || !out_index || !out_value)
         return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax: null argument");
-    xqhip::GemvLaunch p{};
-    p.nib = static_cast<const uint8_t*>(w->nib);
-    p.meta = w->meta;
-    p.rows = w->rows;
-    p.cols = w->cols;
-    p.group = w->group;
-    p.affine = w->affine;
-    p.layout = w->layout;
-    p.x = x;
-    p.x_f16 = x_type == XQHIP_F16;
-    p.norm_w = norm_w;
-    p.eps = eps;
+    xqhip::GemvLaunch p = base_launch(w, x, x_type, pro);
     p.epi = 3;
     p.counter = static_cast<uint32_t*>(workspace);
     p.partial = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(workspace) + 256);
     p.out_idx = out_index;
     p.out_val = out_value;
-    p.max_blocks = kArgmaxMaxBlocks;
+    p.max_blocks = std::min(kArgmaxMaxBlocks, gemv_block_cap());
     return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax launch");
+}
+
+int xqhip_embed_bf16(const uint16_t* table, int vocab, int hidden, const int32_t* token, float* out, void* stream) {
+    if (!table || !token || !out || vocab <= 0 || hidden <= 0) return fail(XQHIP_EINVAL, "xqhip_embed_bf16: bad args");
+    xqhip::EmbedLaunch p{table, vocab, hidden, token, out};
+    return check(xqhip::launch_embed(p, as_stream(stream)), "embed launch");
+}
+
+int xqhip_rope_table(float theta, int rotary_dim, int max_pos, float* out) {
+    if (!out || rotary_dim < 0 || max_pos <= 0) return fail(XQHIP_EINVAL, "xqhip_rope_table: bad args");
+    const int half = rotary_dim / 2;
+    for (int pos = 0; pos < max_pos; ++pos) {
+        for (int i = 0; i < half; ++i) {
+            const float inv_freq = std::pow(theta, -static_cast<float>(2 * i) / static_cast<float>(rotary_dim));
+            const float angle = static_cast<float>(pos) * inv_freq;
+            out[(static_cast<size_t>(pos) * half + i) * 2] = std::cos(angle);
+            out[(static_cast<size_t>(pos) * half + i) * 2 + 1] = std::sin(angle);
+        }
+    }
+    return XQHIP_OK;
+}
+
+int xqhip_attn_prep(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
+                    int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
+                    const float* rope_cs, const int32_t* pos, float* q_out, float* gate_out, void* k_cache,
+                    void* v_cache, void* stream) {
+    if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !pos || !q_out || !gate_out || !k_cache || !v_cache ||
+        nq <= 0 || nkv <= 0 || head_dim <= 0 || head_dim > 1024 || (rotary_dim > 0 && !rope_cs))
+        return fail(XQHIP_EINVAL, "xqhip_attn_prep: bad args");
+    const int active = std::max(0, std::min(head_dim, rotary_dim));
+    xqhip::QkPrepLaunch p{};
+    p.q_src = q_src;
+    p.k_src = k_src;
+    p.v_src = v_src;
+    p.gated = gated;
+    p.nq = nq;
+    p.nkv = nkv;
+    p.head_dim = head_dim;
+    p.rotary_dim = active;
+    p.rope_pairs = active / 2;
+    p.q_norm = q_norm;
+    p.k_norm = k_norm;
+    p.eps = eps;
+    p.rope_cs = rope_cs;
+    p.pos = pos;
+    p.q_out = q_out;
+    p.gate_out = gate_out;
+    p.k_cache = static_cast<_Float16*>(k_cache);
+    p.v_cache = static_cast<_Float16*>(v_cache);
+    return check(xqhip::launch_qk_prep(p, as_stream(stream)), "attn_prep launch");
+}
+
+size_t xqhip_gqa_workspace_bytes(int nq, int nkv, int head_dim) { return xqhip::gqa_workspace_bytes(nq, nkv, head_dim); }
+
+int xqhip_gqa_decode(const float* q, const void* k_cache, const void* v_cache, const float* gate, int nq, int nkv,
+                     int head_dim, int max_ctx, const int32_t* pos, float* out, void* workspace, void* stream) {
+    if (!q || !k_cache || !v_cache || !gate || !pos || !out || !workspace)
+        return fail(XQHIP_EINVAL, "xqhip_gqa_decode: null argument");
+    if (!xqhip::gqa_supported(nq, nkv, head_dim, max_ctx))
+        return fail(XQHIP_EINVAL, "xqhip_gqa_decode: unsupported shape nq=%d nkv=%d hd=%d ctx=%d", nq, nkv, head_dim,
+                    max_ctx);
+    xqhip::GqaLaunch p{};
+    p.q = q;
+    p.k_cache = static_cast<const _Float16*>(k_cache);
+    p.v_cache = static_cast<const _Float16*>(v_cache);
+    p.gate = gate;
+    p.nq = nq;
+    p.nkv = nkv;
+    p.head_dim = head_dim;
+    p.max_ctx = max_ctx;
+    p.pos = pos;
+    p.out = out;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    p.counters = reinterpret_cast<uint32_t*>(ws);
+    float* f = reinterpret_cast<float*>(ws + 256 + sizeof(uint32_t) * static_cast<size_t>(nkv));
+    p.part_ml = f;
+    p.part_o = f + static_cast<size_t>(nq) * 16 * 2;
+    return check(xqhip::launch_gqa(p, as_stream(stream)), "gqa launch");
+}
+
+int xqhip_linear_conv(const float* mixed, float* conv_state, const float* conv_w, int lk_n, int lk_hd, int lv_n,
+                      int lv_hd, int ksize, float* out, void* stream) {
+    if (!mixed || !conv_state || !conv_w || !out || lk_n <= 0 || lv_n <= 0 || ksize < 1 ||
+        !xqhip::conv_supported(lk_hd, lv_hd))
+        return fail(XQHIP_EINVAL, "xqhip_linear_conv: bad args");
+    xqhip::ConvLaunch p{mixed, conv_state, conv_w, lk_n, lk_hd, lv_n, lv_hd, ksize, out};
+    return check(xqhip::launch_conv(p, as_stream(stream)), "conv launch");
+}
+
+int xqhip_gated_delta(const float* conv, const float* a, const float* b, const float* a_log, const float* dt_bias,
+                      float* state, int lk_n, int lv_n, int lk_hd, int lv_hd, float* out, void* stream) {
+    if (!conv || !a || !b || !a_log || !dt_bias || !state || !out || lk_n <= 0 || lv_n <= 0 || lv_hd <= 0 ||
+        !xqhip::delta_supported(lk_hd))
+        return fail(XQHIP_EINVAL, "xqhip_gated_delta: bad args");
+    xqhip::DeltaLaunch p{conv, a, b, a_log, dt_bias, state, lk_n, lv_n, lk_hd, lv_hd, out};
+    return check(xqhip::launch_delta(p, as_stream(stream)), "delta launch");
+}
+
+int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream) {
+    if (!x || !w || !y || n <= 0) return fail(XQHIP_EINVAL, "xqhip_rmsnorm: bad args");
+    return check(xqhip::launch_rmsnorm(x, w, n, eps, y, as_stream(stream)), "rmsnorm launch");
+}
+
+int xqhip_stream_create(void** stream) {
+    hipStream_t s;
+    if (int rc = check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return rc;
+    *stream = s;
+    return XQHIP_OK;
+}
+int xqhip_stream_destroy(void* stream) { return check(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy"); }
+
+int xqhip_graph_begin(void* stream) {
+    return check(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+}
+int xqhip_graph_end(void* stream, void** graph_exec) {
+    hipGraph_t g;
+    if (int rc = check(hipStreamEndCapture(as_stream(stream), &g), "hipStreamEndCapture")) return rc;
+    hipGraphExec_t e;
+    const int rc = check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc) return rc;
+    *graph_exec = e;
+    return XQHIP_OK;
+}
+int xqhip_graph_launch(void* graph_exec, void* stream) {
+    return check(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)), "hipGraphLaunch");
+}
+int xqhip_graph_destroy(void* graph_exec) {
+    return check(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
 }
 
 }  // extern "C"

@@ -6,6 +6,18 @@
 
 namespace xqhip {
 
+enum { PRO_NONE = 0, PRO_RMS = 1, PRO_GATED = 2 };
+constexpr int kMaxNormHeads = 256;
+
+// Normalisation applied to the GEMV input inside the kernel prologue.
+struct Prologue {
+    int mode;          // PRO_*
+    const float* w;    // PRO_RMS: [cols]; PRO_GATED: [head_dim]
+    const float* z;    // PRO_GATED: gate [cols]
+    int head_dim;      // PRO_GATED
+    float eps;
+};
+
 // One fused-dequant GEMV launch (gemv_w4a16.hip).
 struct GemvLaunch {
     const uint8_t* nib;
@@ -13,8 +25,7 @@ struct GemvLaunch {
     int rows, cols, group, affine, layout;
     const void* x;
     int x_f16;
-    const float* norm_w;  // fused RMSNorm of x when non-null
-    float eps;
+    Prologue pro;
     void* y;
     int y_f16;
     int epi;  // 0 store, 1 add, 2 silu pair, 3 argmax
@@ -26,5 +37,72 @@ struct GemvLaunch {
 };
 
 hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s);
+
+// decode_ops.hip
+struct EmbedLaunch {
+    const uint16_t* table;
+    int vocab, hidden;
+    const int32_t* tok;
+    float* out;
+};
+hipError_t launch_embed(const EmbedLaunch& p, hipStream_t s);
+
+struct QkPrepLaunch {
+    const float* q_src;  // q_proj output (gated: per head [q | gate])
+    const float* k_src;
+    const float* v_src;
+    int gated, nq, nkv, head_dim, rotary_dim, rope_pairs;
+    const float* q_norm;
+    const float* k_norm;
+    float eps;
+    const float* rope_cs;  // [max_ctx][rope_pairs] (cos, sin)
+    const int32_t* pos;
+    float* q_out;
+    float* gate_out;
+    _Float16* k_cache;
+    _Float16* v_cache;
+};
+hipError_t launch_qk_prep(const QkPrepLaunch& p, hipStream_t s);
+
+struct GqaLaunch {
+    const float* q;
+    const _Float16* k_cache;
+    const _Float16* v_cache;
+    const float* gate;
+    int nq, nkv, head_dim, max_ctx;
+    const int32_t* pos;
+    float* out;
+    uint32_t* counters;
+    float* part_o;
+    float* part_ml;
+};
+size_t gqa_workspace_bytes(int nq, int nkv, int head_dim);
+bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx);
+hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s);
+
+struct ConvLaunch {
+    const float* mixed;
+    float* state;
+    const float* conv_w;
+    int lk_n, lk_hd, lv_n, lv_hd, ksize;
+    float* out;
+};
+bool conv_supported(int lk_hd, int lv_hd);
+hipError_t launch_conv(const ConvLaunch& p, hipStream_t s);
+
+struct DeltaLaunch {
+    const float* conv;  // normalised q | k | v
+    const float* a;
+    const float* b;
+    const float* a_log;
+    const float* dt_bias;
+    float* state;
+    int lk_n, lv_n, lk_hd, lv_hd;
+    float* out;
+};
+bool delta_supported(int lk_hd);
+hipError_t launch_delta(const DeltaLaunch& p, hipStream_t s);
+
+hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
 
 }  // namespace xqhip

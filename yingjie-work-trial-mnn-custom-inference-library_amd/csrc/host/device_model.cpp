@@ -1,0 +1,565 @@
+// device_model.cpp - see device_model.hpp.
+//
+// Op order per layer follows CustomModel::runLayer (custom_model.cpp:1138-1256);
+// fused kernels are named after every reference op they absorb, so the kernel
+// trace keeps the reference's row vocabulary.
+#include "device_model.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+
+namespace xqh {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+const char* kTraceBackend = "hip";
+
+double elapsed_ms(void* a, void* b) {
+    float ms = 0.0f;
+    if (xqhip_event_elapsed_ms(a, b, &ms) != 0) return 0.0;
+    return static_cast<double>(ms);
+}
+
+}  // namespace
+
+DeviceModel::~DeviceModel() {
+    if (stream_) xqhip_stream_synchronize(stream_);
+    if (g_prefill_) xqhip_graph_destroy(g_prefill_);
+    if (g_decode_) xqhip_graph_destroy(g_decode_);
+    for (xqhip_w4* m : matrices_) xqhip_w4_free(m);
+    for (void* p : allocations_) xqhip_free(p);
+    for (void* e : event_pool_) xqhip_event_destroy(e);
+    if (h_ctrl_) xqhip_host_free(h_ctrl_);
+    if (h_tok_) xqhip_host_free(h_tok_);
+    if (stream_) xqhip_stream_destroy(stream_);
+}
+
+bool DeviceModel::fail_hip(std::string* error, const char* what) {
+    *error = std::string(what) + ": " + xqhip_last_error();
+    return false;
+}
+
+template <typename T>
+bool DeviceModel::alloc(T** p, size_t count, std::string* error) {
+    void* q = nullptr;
+    if (xqhip_malloc(&q, std::max<size_t>(1, count * sizeof(T))) != 0) return fail_hip(error, "device allocation");
+    allocations_.push_back(q);
+    *p = static_cast<T*>(q);
+    return true;
+}
+
+bool DeviceModel::upload_vec(const std::vector<float>& v, float** out, std::string* error) {
+    if (!alloc(out, v.size(), error)) return false;
+    if (xqhip_memcpy_h2d(*out, v.data(), v.size() * sizeof(float), nullptr) != 0) return fail_hip(error, "upload");
+    return true;
+}
+
+bool DeviceModel::upload_matrix(const HostMatrix& m, xqhip_w4* out, std::string* error) {
+    if (xqhip_w4_upload(m.packed.data(), m.scales.data(), m.zeros.data(), m.rows, m.cols, m.group, m.affine ? 1 : 0,
+                        out) != 0)
+        return fail_hip(error, "weight upload");
+    matrices_.push_back(out);
+    weight_bytes_ += xqhip_w4_weight_bytes(out);
+    inexact_meta_ += out->inexact_meta;
+    return true;
+}
+
+static void add_one(std::vector<float>* v) {
+    for (float& x : *v) x += 1.0f;
+}
+
+bool DeviceModel::load_layer(int index, Layer* L, std::string* error) {
+    const std::string p = model_dir_ + "/layers_" + std::to_string(index) + "_";
+    std::vector<float> in_norm, post_norm;
+    HostMatrix gate, up, down;
+    if (!read_f32_file(p + "input_layernorm_weight.f32", hidden_, &in_norm, error) ||
+        !read_f32_file(p + "post_attention_layernorm_weight.f32", hidden_, &post_norm, error) ||
+        !read_xq4_file(p + "mlp_gate_proj_weight.xq4", &gate, error) ||
+        !read_xq4_file(p + "mlp_up_proj_weight.xq4", &up, error) ||
+        !read_xq4_file(p + "mlp_down_proj_weight.xq4", &down, error))
+        return false;
+    add_one(&in_norm);  // custom_model.cpp:524-525
+    add_one(&post_norm);
+    if (gate.rows != inter_ || up.rows != inter_ || gate.cols != hidden_ || down.cols != inter_ ||
+        down.rows != hidden_) {
+        *error = "layer " + std::to_string(index) + ": MLP shapes disagree with the manifest";
+        return false;
+    }
+    HostMatrix gu;
+    if (!interleave_rows(gate, up, &gu, error) || !upload_matrix(gu, &L->gate_up, error) ||
+        !upload_matrix(down, &L->down, error) || !upload_vec(in_norm, &L->in_norm, error) ||
+        !upload_vec(post_norm, &L->post_norm, error))
+        return false;
+
+    if (file_exists(p + "self_attn_q_proj_weight.xq4")) {  // custom_model.cpp:526
+        L->full = true;
+        HostMatrix q, k, v, o;
+        std::vector<float> qn, kn;
+        if (!read_xq4_file(p + "self_attn_q_proj_weight.xq4", &q, error) ||
+            !read_xq4_file(p + "self_attn_k_proj_weight.xq4", &k, error) ||
+            !read_xq4_file(p + "self_attn_v_proj_weight.xq4", &v, error) ||
+            !read_xq4_file(p + "self_attn_o_proj_weight.xq4", &o, error) ||
+            !read_f32_file(p + "self_attn_q_norm_weight.f32", hd_, &qn, error) ||
+            !read_f32_file(p + "self_attn_k_norm_weight.f32", hd_, &kn, error))
+            return false;
+        add_one(&qn);  // custom_model.cpp:536-537
+        add_one(&kn);
+        L->q_gated = q.rows >= nq_ * 2 * hd_;  // custom_model.cpp:742
+        const int q_rows = nq_ * hd_ * (L->q_gated ? 2 : 1);
+        if (q.rows != q_rows || k.rows != nkv_ * hd_ || v.rows != nkv_ * hd_ || q.cols != hidden_ ||
+            o.cols != nq_ * hd_ || o.rows != hidden_ || nq_ * hd_ > std::max(hidden_, lv_dim_)) {
+            *error = "layer " + std::to_string(index) + ": attention shapes disagree with the manifest";
+            return false;
+        }
+        HostMatrix qkv;
+        if (!concat_rows({&q, &k, &v}, &qkv, error) || !upload_matrix(qkv, &L->in_proj, error) ||
+            !upload_matrix(o, &L->out_proj, error) || !upload_vec(qn, &L->q_norm, error) ||
+            !upload_vec(kn, &L->k_norm, error))
+            return false;
+        const size_t kv = static_cast<size_t>(max_ctx_) * nkv_ * hd_;
+        uint16_t *kc = nullptr, *vc = nullptr;
+        if (!alloc(&kc, kv, error) || !alloc(&vc, kv, error)) return false;
+        L->k_cache = kc;
+        L->v_cache = vc;
+        return true;
+    }
+    L->full = false;
+    HostMatrix qkv, a, b, z, out;
+    std::vector<float> lin_norm, conv_w, a_log, dt_bias;
+    if (!read_xq4_file(p + "linear_attn_in_proj_qkv_weight.xq4", &qkv, error) ||
+        !read_xq4_file(p + "linear_attn_in_proj_a_weight.xq4", &a, error) ||
+        !read_xq4_file(p + "linear_attn_in_proj_b_weight.xq4", &b, error) ||
+        !read_xq4_file(p + "linear_attn_in_proj_z_weight.xq4", &z, error) ||
+        !read_xq4_file(p + "linear_attn_out_proj_weight.xq4", &out, error) ||
+        !read_f32_file(p + "linear_attn_norm_weight.f32", lv_hd_, &lin_norm, error) ||
+        !read_f32_file(p + "linear_attn_conv1d_weight.f32", conv_dim_ * ksize_, &conv_w, error) ||
+        !read_f32_file(p + "linear_attn_A_log.f32", lv_n_, &a_log, error) ||
+        !read_f32_file(p + "linear_attn_dt_bias.f32", lv_n_, &dt_bias, error))
+        return false;
+    if (qkv.rows != conv_dim_ || a.rows != lv_n_ || b.rows != lv_n_ || z.rows != lv_dim_ || qkv.cols != hidden_ ||
+        out.cols != lv_dim_ || out.rows != hidden_) {
+        *error = "layer " + std::to_string(index) + ": linear-attention shapes disagree with the manifest";
+        return false;
+    }
+    HostMatrix fused;
+    if (!concat_rows({&qkv, &a, &b, &z}, &fused, error) || !upload_matrix(fused, &L->in_proj, error) ||
+        !upload_matrix(out, &L->out_proj, error) || !upload_vec(lin_norm, &L->lin_norm, error) ||
+        !upload_vec(conv_w, &L->conv_w, error) || !upload_vec(a_log, &L->a_log, error) ||
+        !upload_vec(dt_bias, &L->dt_bias, error))
+        return false;
+    return alloc(&L->conv_state, static_cast<size_t>(conv_dim_) * std::max(0, ksize_ - 1), error) &&
+           alloc(&L->rec_state, static_cast<size_t>(lv_n_) * lk_hd_ * lv_hd_, error);
+}
+
+bool DeviceModel::load(const std::string& model_dir, const std::string& backend_request, int max_context,
+                       std::string* error) {
+    model_dir_ = model_dir;
+    backend_request_ = backend_request.empty() ? "cpu" : backend_request;
+    if (xqhip_device_count() < 1) {
+        *error = "no HIP device visible: this library runs the decode path on an MI355X and has no CPU path";
+        return false;
+    }
+    if (xqhip_set_device(0) != 0) return fail_hip(error, "select device");
+    char name[256] = {};
+    xqhip_device_name(name, sizeof(name));
+    device_name_ = name;
+
+    const std::string js = read_text(model_dir + "/xqwen35_manifest.json");  // custom_model.cpp:431-453
+    hidden_ = manifest_int(js, "hidden_size", hidden_);
+    inter_ = manifest_int(js, "intermediate_size", inter_);
+    vocab_ = manifest_int(js, "vocab_size", vocab_);
+    nq_ = manifest_int(js, "num_attention_heads", nq_);
+    nkv_ = manifest_int(js, "num_key_value_heads", nkv_);
+    hd_ = manifest_int(js, "head_dim", hd_);
+    const float prf = manifest_float(js, "partial_rotary_factor", 0.25f);
+    rot_ = std::max(2, static_cast<int>(std::round(static_cast<float>(hd_) * prf)));
+    if (rot_ & 1) --rot_;
+    lk_hd_ = manifest_int(js, "linear_key_head_dim", lk_hd_);
+    lv_hd_ = manifest_int(js, "linear_value_head_dim", lv_hd_);
+    lk_n_ = manifest_int(js, "linear_num_key_heads", lk_n_);
+    lv_n_ = manifest_int(js, "linear_num_value_heads", lv_n_);
+    ksize_ = manifest_int(js, "linear_conv_kernel_dim", ksize_);
+    lk_dim_ = lk_hd_ * lk_n_;
+    lv_dim_ = lv_hd_ * lv_n_;
+    conv_dim_ = 2 * lk_dim_ + lv_dim_;
+    eps_ = manifest_float(js, "rms_norm_eps", eps_);
+    theta_ = manifest_float(js, "rope_theta", theta_);
+    const int n_layers = manifest_int(js, "num_hidden_layers", 32);
+    // KV capacity: the reference grows its caches without bound; here they are
+    // allocated once, for at least 8192 positions and at most 16384.
+    max_ctx_ = std::min(16384, std::max(8192, max_context));
+    if (hidden_ <= 0 || vocab_ <= 0 || n_layers < 0 || nq_ <= 0 || nkv_ <= 0 || hd_ <= 0 || nq_ % nkv_ != 0) {
+        *error = "invalid model dimensions in xqwen35_manifest.json";
+        return false;
+    }
+
+    // embeddings (custom_model.cpp:454-464): whole table resident in HBM
+    {
+        std::ifstream f(model_dir + "/embeddings_bf16.bin", std::ios::binary | std::ios::ate);
+        if (!f) {
+            *error = "missing embeddings_bf16.bin";
+            return false;
+        }
+        const uint64_t want = static_cast<uint64_t>(vocab_) * hidden_ * 2;
+        if (static_cast<uint64_t>(f.tellg()) < want) {
+            *error = "short embeddings_bf16.bin";
+            return false;
+        }
+        std::vector<uint16_t> host(static_cast<size_t>(want / 2));
+        f.seekg(0);
+        f.read(reinterpret_cast<char*>(host.data()), static_cast<std::streamsize>(want));
+        if (!alloc(&embed_, host.size(), error)) return false;
+        if (xqhip_memcpy_h2d(embed_, host.data(), want, nullptr) != 0) return fail_hip(error, "embedding upload");
+    }
+    std::vector<float> fn;
+    if (!read_f32_file(model_dir + "/norm_weight.f32", hidden_, &fn, error)) return false;
+    add_one(&fn);  // custom_model.cpp:468
+    HostMatrix lm;
+    if (!upload_vec(fn, &final_norm_, error) || !read_xq4_file(model_dir + "/lm_head_weight.xq4", &lm, error) ||
+        !upload_matrix(lm, &lm_head_, error))
+        return false;
+    layers_.assign(static_cast<size_t>(n_layers), Layer());  // sized once: matrices_ keeps pointers into it
+    for (int i = 0; i < n_layers; ++i)
+        if (!load_layer(i, &layers_[i], error)) return false;
+    bool any_full = false, any_linear = false;
+    int max_proj = 1;
+    for (const Layer& L : layers_) {
+        any_full |= L.full;
+        any_linear |= !L.full;
+        max_proj = std::max(max_proj, L.in_proj.rows);
+    }
+    const int rot_active = std::max(0, std::min(hd_, rot_));
+    if (any_full && xqhip_gqa_workspace_bytes(nq_, nkv_, hd_) == 0) {
+        *error = "attention workspace";
+        return false;
+    }
+    const int attn_n = std::max({nq_ * hd_, lv_dim_, hidden_});
+    size_t ws_argmax = xqhip_argmax_workspace_bytes(lm_head_.rows);
+    size_t ws_gqa = any_full ? xqhip_gqa_workspace_bytes(nq_, nkv_, hd_) : 1;
+    uint8_t *wa = nullptr, *wg = nullptr;
+    if (!alloc(&resid_, hidden_, error) || !alloc(&normed_, hidden_, error) || !alloc(&proj_, max_proj, error) ||
+        !alloc(&q_rot_, static_cast<size_t>(nq_) * hd_, error) || !alloc(&gate_, static_cast<size_t>(nq_) * hd_, error) ||
+        !alloc(&attn_, attn_n, error) || !alloc(&conv_out_, std::max(1, conv_dim_), error) ||
+        !alloc(&ffn_, inter_, error) || !alloc(&best_val_, 1, error) || !alloc(&d_ctrl_, 4, error) ||
+        !alloc(&wa, ws_argmax, error) || !alloc(&wg, ws_gqa, error))
+        return false;
+    argmax_ws_ = wa;
+    gqa_ws_ = wg;
+    if (xqhip_stream_create(&stream_) != 0) return fail_hip(error, "stream");
+    xqhip_fill_u8(resid_, 0, sizeof(float) * hidden_, stream_);  // hidden_ starts at zero (custom_model.cpp:478)
+    xqhip_fill_u8(argmax_ws_, 0, ws_argmax, stream_);
+    xqhip_fill_u8(gqa_ws_, 0, ws_gqa, stream_);
+    xqhip_fill_u8(d_ctrl_, 0, 16, stream_);
+    if (any_full && rot_active > 0) {
+        std::vector<float> tab(static_cast<size_t>(max_ctx_) * (rot_active / 2) * 2);
+        xqhip_rope_table(theta_, rot_active, max_ctx_, tab.data());
+        if (!upload_vec(tab, &rope_cs_, error)) return false;
+    }
+    (void)any_linear;
+    void* pinned = nullptr;
+    if (xqhip_host_alloc(&pinned, 4 * sizeof(int32_t)) != 0) return fail_hip(error, "pinned memory");
+    h_tok_ = static_cast<int32_t*>(pinned);
+    reset_state();
+    return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "load sync");
+}
+
+void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past the position are never read)
+    for (Layer& L : layers_) {
+        if (L.full) continue;
+        xqhip_fill_u8(L.conv_state, 0, sizeof(float) * conv_dim_ * std::max(0, ksize_ - 1), stream_);
+        xqhip_fill_u8(L.rec_state, 0, sizeof(float) * lv_n_ * lk_hd_ * lv_hd_, stream_);
+    }
+    detail_prefill_ = detail_decode_ = true;
+}
+
+bool DeviceModel::op_begin(bool timed, const std::string& name, std::vector<std::string> extra, int split) {
+    if (!timed) return true;
+    while (event_pool_.size() < event_next_ + 2) {
+        void* e = nullptr;
+        if (xqhip_event_create(&e) != 0) return false;
+        event_pool_.push_back(e);
+    }
+    TimedOp op;
+    op.name = name;
+    op.extra_names = std::move(extra);
+    op.split = split;
+    op.ev0 = event_pool_[event_next_++];
+    op.ev1 = event_pool_[event_next_++];
+    xqhip_event_record(op.ev0, stream_);
+    ops_.push_back(std::move(op));
+    return true;
+}
+
+void DeviceModel::op_end(bool timed) {
+    if (timed && !ops_.empty()) xqhip_event_record(ops_.back().ev1, stream_);
+}
+
+void DeviceModel::flush_timed(KernelTrace* trace) {
+    for (const TimedOp& op : ops_) {
+        const double ms = elapsed_ms(op.ev0, op.ev1);
+        if (trace) {
+            trace->add(op.name, ms, kTraceBackend);
+            for (const std::string& e : op.extra_names) trace->add(e, ms / op.split, kTraceBackend);
+        }
+    }
+    ops_.clear();
+    event_next_ = 0;
+}
+
+#define XQ_CALL(expr, what) \
+    if ((expr) != 0) return fail_hip(error, what)
+
+bool DeviceModel::enqueue_embed(const int32_t* token_dev, bool timed, std::string* error) {
+    op_begin(timed, "embedding_bf16_row_read");
+    XQ_CALL(xqhip_embed_bf16(embed_, vocab_, hidden_, token_dev, resid_, stream_), "embedding");
+    op_end(timed);
+    return true;
+}
+
+bool DeviceModel::enqueue_lm_head(bool timed, std::string* error) {
+    xqhip_prologue fin{XQHIP_PRO_RMS, 0, final_norm_, nullptr, eps_};
+    op_begin(timed, "lm_head_custom(fused:rmsnorm_final,argmax)", {"sampling_greedy_custom"});
+    XQ_CALL(xqhip_gemv_w4a16_argmax(&lm_head_, resid_, XQHIP_F32, &fin, argmax_ws_, d_ctrl_ + 2, best_val_, stream_),
+            "lm_head argmax");
+    op_end(timed);
+    return true;
+}
+
+bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
+    const int32_t* pos = d_ctrl_;
+    for (Layer& L : layers_) {
+        xqhip_prologue rms_in{XQHIP_PRO_RMS, 0, L.in_norm, nullptr, eps_};
+        if (L.full) {
+            op_begin(timed, "linear_q_proj_w4a16(fused:k_proj,v_proj,rmsnorm_input)");
+            XQ_CALL(xqhip_gemv_w4a16(&L.in_proj, resid_, XQHIP_F32, &rms_in, proj_, XQHIP_F32, XQHIP_EPI_STORE, stream_),
+                    "qkv projection");
+            op_end(timed);
+            const float* k_src = proj_ + static_cast<size_t>(nq_) * hd_ * (L.q_gated ? 2 : 1);
+            const float* v_src = k_src + static_cast<size_t>(nkv_) * hd_;
+            op_begin(timed, "rope_qk_custom(fused:q_norm,k_norm,kv_append)", {"prefill_kv_build_custom"});
+            XQ_CALL(xqhip_attn_prep(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm, L.k_norm,
+                                    eps_, rope_cs_, pos, q_rot_, gate_, L.k_cache, L.v_cache, stream_),
+                    "attention prep");
+            op_end(timed);
+            op_begin(timed, "attention_gqa_decode_custom(fused:output_gate)",
+                     {"attention_score_custom", "attention_softmax_custom", "attention_v_reduce_custom"}, 3);
+            XQ_CALL(xqhip_gqa_decode(q_rot_, L.k_cache, L.v_cache, gate_, nq_, nkv_, hd_, max_ctx_, pos, attn_,
+                                     gqa_ws_, stream_),
+                    "gqa decode");
+            op_end(timed);
+            op_begin(timed, "linear_o_proj_w4a16(fused:residual_add_attention)");
+            XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, nullptr, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),
+                    "o projection");
+            op_end(timed);
+        } else {
+            op_begin(timed, "linear_attn_in_proj_qkv_w4a16(fused:in_proj_a,in_proj_b,in_proj_z,rmsnorm_input)");
+            XQ_CALL(xqhip_gemv_w4a16(&L.in_proj, resid_, XQHIP_F32, &rms_in, proj_, XQHIP_F32, XQHIP_EPI_STORE, stream_),
+                    "linear-attention in projection");
+            op_end(timed);
+            op_begin(timed, "linear_attention_conv1d_custom(fused:linear_attention_qk_l2norm)");
+            XQ_CALL(xqhip_linear_conv(proj_, L.conv_state, L.conv_w, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, conv_out_,
+                                      stream_),
+                    "conv1d");
+            op_end(timed);
+            const float* a = proj_ + conv_dim_;
+            const float* b = a + lv_n_;
+            const float* z = b + lv_n_;
+            op_begin(timed, "linear_attention_state_update_custom");
+            XQ_CALL(xqhip_gated_delta(conv_out_, a, b, L.a_log, L.dt_bias, L.rec_state, lk_n_, lv_n_, lk_hd_, lv_hd_,
+                                      attn_, stream_),
+                    "gated delta");
+            op_end(timed);
+            xqhip_prologue gated{XQHIP_PRO_GATED_HEAD, lv_hd_, L.lin_norm, z, eps_};
+            op_begin(timed, "linear_attn_out_proj_w4a16(fused:linear_attention_gated_rmsnorm,residual_add_attention)");
+            XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, &gated, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),
+                    "out projection");
+            op_end(timed);
+        }
+        xqhip_prologue rms_post{XQHIP_PRO_RMS, 0, L.post_norm, nullptr, eps_};
+        op_begin(timed, "linear_gate_proj_w4a16(fused:up_proj,rmsnorm_post_attention,silu_gate_mul)");
+        XQ_CALL(xqhip_gemv_w4a16(&L.gate_up, resid_, XQHIP_F32, &rms_post, ffn_, XQHIP_F32, XQHIP_EPI_SILU_PAIR, stream_),
+                "gate/up projection");
+        op_end(timed);
+        op_begin(timed, "linear_down_proj_w4a16(fused:residual_add_mlp)");
+        XQ_CALL(xqhip_gemv_w4a16(&L.down, ffn_, XQHIP_F32, nullptr, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),
+                "down projection");
+        op_end(timed);
+    }
+    return true;
+}
+
+bool DeviceModel::ensure_graphs(std::string* error) {
+    if (g_prefill_ && g_decode_) return true;
+    XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
+    bool ok = enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error);
+    void* g = nullptr;
+    if (xqhip_graph_end(stream_, &g) != 0 || !ok) return ok ? fail_hip(error, "graph instantiate") : false;
+    g_prefill_ = g;
+    XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
+    ok = enqueue_lm_head(false, error) && enqueue_embed(d_ctrl_ + 2, false, error) && enqueue_layers(false, error);
+    g = nullptr;
+    if (xqhip_graph_end(stream_, &g) != 0 || !ok) return ok ? fail_hip(error, "graph instantiate") : false;
+    g_decode_ = g;
+    return true;
+}
+
+bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace* trace, std::string* error) {
+    if (!token_ids || n_tokens == 0) {  // custom_model.cpp:611-614
+        *error = "custom prefill requires prompt tokens";
+        return false;
+    }
+    if (n_tokens > static_cast<size_t>(max_ctx_)) {
+        *error = "prompt longer than the KV capacity (" + std::to_string(max_ctx_) + " tokens)";
+        return false;
+    }
+    reset_state();
+    if (!ensure_graphs(error)) return false;
+    if (h_ctrl_cap_ < 2 * n_tokens) {
+        if (h_ctrl_) xqhip_host_free(h_ctrl_);
+        h_ctrl_ = nullptr;
+        void* p = nullptr;
+        XQ_CALL(xqhip_host_alloc(&p, sizeof(int32_t) * 2 * n_tokens), "pinned memory");
+        h_ctrl_ = static_cast<int32_t*>(p);
+        h_ctrl_cap_ = 2 * n_tokens;
+    }
+    const size_t op_events = 2 * (6 * layers_.size() + 4);
+    while (event_pool_.size() < n_tokens + 1 + op_events) {
+        void* e = nullptr;
+        XQ_CALL(xqhip_event_create(&e), "event");
+        event_pool_.push_back(e);
+    }
+    // per-token boundary events live at the top of the pool, op events at the bottom
+    auto tok_ev = [&](size_t i) { return event_pool_[event_pool_.size() - 1 - i]; };
+    xqhip_event_record(tok_ev(0), stream_);
+    for (size_t i = 0; i < n_tokens; ++i) {
+        h_ctrl_[2 * i] = static_cast<int32_t>(i);
+        h_ctrl_[2 * i + 1] = token_ids[i];
+        XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_ctrl_ + 2 * i, 2 * sizeof(int32_t), stream_), "control upload");
+        if (i == 0 && detail_prefill_) {
+            if (!enqueue_embed(d_ctrl_ + 1, true, error) || !enqueue_layers(true, error)) return false;
+        } else {
+            XQ_CALL(xqhip_graph_launch(g_prefill_, stream_), "prefill graph");
+        }
+        xqhip_event_record(tok_ev(i + 1), stream_);
+    }
+    XQ_CALL(xqhip_stream_synchronize(stream_), "prefill");
+    detail_prefill_ = false;
+    if (trace) {
+        for (size_t i = 0; i < n_tokens; ++i)
+            trace->add("prefill_token_custom", elapsed_ms(tok_ev(i), tok_ev(i + 1)), kTraceBackend);
+    }
+    flush_timed(trace);
+    detail_decode_ = true;
+    return true;
+}
+
+bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* trace, std::string* error) {
+    if (!token_id) {
+        *error = "decodeOne token output is null";
+        return false;
+    }
+    if (lm_head_.rows <= 0 || lm_head_.cols != hidden_) {  // custom_model.cpp:1282-1285
+        *error = "lm_head matrix is not loaded";
+        return false;
+    }
+    if (position >= static_cast<size_t>(max_ctx_)) {
+        *error = "context position " + std::to_string(position) + " exceeds the KV capacity (" +
+                 std::to_string(max_ctx_) + " tokens)";
+        return false;
+    }
+    if (!ensure_graphs(error)) return false;
+    h_tok_[0] = static_cast<int32_t>(position);
+    h_tok_[1] = 0;
+    XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
+    if (detail_decode_) {
+        if (!enqueue_lm_head(true, error) || !enqueue_embed(d_ctrl_ + 2, true, error) || !enqueue_layers(true, error))
+            return false;
+    } else {
+        op_begin(true, "decode_step_graph_custom");
+        XQ_CALL(xqhip_graph_launch(g_decode_, stream_), "decode graph");
+        op_end(true);
+    }
+    XQ_CALL(xqhip_memcpy_d2h_async(h_tok_ + 2, d_ctrl_ + 2, sizeof(int32_t), stream_), "token readback");
+    XQ_CALL(xqhip_stream_synchronize(stream_), "decode");
+    *token_id = h_tok_[2];
+    detail_decode_ = false;
+    flush_timed(trace);
+    return true;
+}
+
+std::string DeviceModel::coverage_summary() const {  // fields of custom_model.cpp:1358-1380
+    std::ostringstream o;
+    o << "custom_decode_loop;hotpath_replaced=true;full_custom_decode=true;"
+      << "backend_request=" << backend_request_ << ";device=hip:" << device_name_ << ";"
+      << "linear_backend=hip_gfx950_w4a16_dequant_gemv_dot2;"
+      << "linear=q_proj,k_proj,v_proj,o_proj,gate_proj,up_proj,down_proj,linear_attn_qkv_a_b_z_out,lm_head;"
+      << "rmsnorm=hip_fused_gemv_prologue;rope=hip_table_libm;attention=hip_gqa_decode_split_fp16_kv;"
+      << "attention_output_gate=hip_fused;linear_attention_state=hip_gated_delta_fp32_state;"
+      << "linear_attention_qk_norm=hip_fused_conv1d;linear_attention_gated_rmsnorm=hip_fused_gemv_prologue;"
+      << "sampling=hip_fused_lm_head_argmax;prefill_kv_build=hip_fp16_append;decode_step=hip_graph;"
+      << "weight_bytes_per_token=" << weight_bytes_ << ";fp16_meta_inexact=" << inexact_meta_
+      << ";kv_capacity=" << max_ctx_ << ";fallback_ops=none";
+    return o.str();
+}
+
+bool DeviceModel::copy_hidden(float* out_values, size_t value_capacity, size_t* out_size) {
+    if (out_size) *out_size = static_cast<size_t>(hidden_);
+    if (!out_values || value_capacity < static_cast<size_t>(hidden_)) return false;
+    if (xqhip_rmsnorm(resid_, final_norm_, hidden_, eps_, normed_, stream_) != 0) return false;
+    return xqhip_memcpy_d2h(out_values, normed_, sizeof(float) * hidden_, stream_) == 0;
+}
+
+std::string DeviceModel::debug_json(int top_k) {  // custom_model.cpp:1382-1436
+    const int k = std::max(1, std::min(top_k, 16));
+    std::vector<float> h(static_cast<size_t>(hidden_), 0.0f);
+    size_t n_h = 0;
+    copy_hidden(h.data(), h.size(), &n_h);
+    double sum = 0.0, sum_sq = 0.0;
+    float mn = h.empty() ? 0.0f : h[0], mx = mn;
+    int nonfinite = 0;
+    for (float v : h) {
+        if (!std::isfinite(v)) {
+            ++nonfinite;
+            continue;
+        }
+        sum += v;
+        sum_sq += static_cast<double>(v) * v;
+        mn = std::min(mn, v);
+        mx = std::max(mx, v);
+    }
+    const double n = static_cast<double>(h.size());
+    const double mean = n > 0 ? sum / n : 0.0;
+    const double var = n > 0 ? std::max(0.0, sum_sq / n - mean * mean) : 0.0;
+    std::vector<float> logits(static_cast<size_t>(std::max(0, lm_head_.rows)), 0.0f);
+    if (lm_head_.rows > 0 && lm_head_.cols == hidden_) {
+        std::string err;
+        if (!logits_) alloc(&logits_, lm_head_.rows, &err);
+        if (logits_ &&
+            xqhip_gemv_w4a16(&lm_head_, normed_, XQHIP_F32, nullptr, logits_, XQHIP_F32, XQHIP_EPI_STORE, stream_) == 0)
+            xqhip_memcpy_d2h(logits.data(), logits_, sizeof(float) * logits.size(), stream_);
+    }
+    std::vector<int> best;
+    for (int i = 0; i < static_cast<int>(logits.size()); ++i) {
+        size_t at = 0;
+        while (at < best.size() && logits[best[at]] >= logits[i]) ++at;
+        if (at < static_cast<size_t>(k)) {
+            best.insert(best.begin() + static_cast<std::ptrdiff_t>(at), i);
+            if (best.size() > static_cast<size_t>(k)) best.pop_back();
+        }
+    }
+    std::ostringstream o;
+    o << "{\"hidden\":{\"size\":" << h.size() << ",\"mean\":" << mean << ",\"std\":" << std::sqrt(var)
+      << ",\"min\":" << mn << ",\"max\":" << mx << ",\"l2\":" << std::sqrt(sum_sq) << ",\"nonfinite\":" << nonfinite
+      << "},\"lm_head_topk\":[";
+    for (size_t i = 0; i < best.size(); ++i)
+        o << (i ? "," : "") << "{\"token\":" << best[i] << ",\"logit\":" << logits[best[i]] << "}";
+    o << "]}";
+    return o.str();
+}
+
+}  // namespace xqh

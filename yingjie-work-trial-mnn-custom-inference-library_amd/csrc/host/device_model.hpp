@@ -1,0 +1,135 @@
+// device_model.hpp - the decode model resident on one MI355X.
+//
+// Replaces CustomModel (customlib/runtime/custom_model.hpp:38-146,
+// custom_model.cpp:423-1447) with the same load / prefill / decodeOne /
+// resetState / coverageSummary / debugJson / copyHidden behaviour.  All weights,
+// the fp16 KV cache, the fp32 recurrent state and every activation live in HBM;
+// the host only feeds (position, token) and reads back the sampled token.
+// Each token runs as one captured HIP graph (about six kernels per layer).
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "kernel_trace.hpp"
+#include "model_files.hpp"
+#include "xqhip.h"
+
+namespace xqh {
+
+class DeviceModel {
+public:
+    DeviceModel() = default;
+    ~DeviceModel();
+    DeviceModel(const DeviceModel&) = delete;
+    DeviceModel& operator=(const DeviceModel&) = delete;
+
+    bool load(const std::string& model_dir, const std::string& backend_request, int max_context, std::string* error);
+    bool prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace* trace, std::string* error);
+    bool decode_one(int32_t* token_id, size_t position, KernelTrace* trace, std::string* error);
+    void reset_state();
+
+    int hidden_size() const { return hidden_; }
+    int vocab_size() const { return vocab_; }
+    int layers() const { return static_cast<int>(layers_.size()); }
+    std::string coverage_summary() const;
+    std::string debug_json(int top_k);
+    bool copy_hidden(float* out_values, size_t value_capacity, size_t* out_size);
+    uint64_t weight_bytes_per_token() const { return weight_bytes_; }
+    const std::string& device_name() const { return device_name_; }
+
+private:
+    struct Layer {
+        bool full = false;
+        // norms (reference +1 already applied where the reference applies it)
+        float* in_norm = nullptr;
+        float* post_norm = nullptr;
+        float* q_norm = nullptr;
+        float* k_norm = nullptr;
+        float* lin_norm = nullptr;
+        float* conv_w = nullptr;
+        float* a_log = nullptr;
+        float* dt_bias = nullptr;
+        // weights: fused input projection, output projection, gate/up (interleaved), down
+        xqhip_w4 in_proj{};
+        xqhip_w4 out_proj{};
+        xqhip_w4 gate_up{};
+        xqhip_w4 down{};
+        bool q_gated = false;
+        // state
+        void* k_cache = nullptr;  // fp16 [max_ctx][nkv][hd]
+        void* v_cache = nullptr;
+        float* conv_state = nullptr;  // [conv_dim][ksize-1]
+        float* rec_state = nullptr;   // [lv_n][lk_hd][lv_hd]
+    };
+
+    struct TimedOp {
+        std::string name;
+        std::vector<std::string> extra_names;  // rows that share this op's time
+        int split = 1;                         // time divided over extra rows (fused attention)
+        void* ev0 = nullptr;
+        void* ev1 = nullptr;
+    };
+
+    bool upload_matrix(const HostMatrix& m, xqhip_w4* out, std::string* error);
+    bool upload_vec(const std::vector<float>& v, float** out, std::string* error);
+    template <typename T>
+    bool alloc(T** p, size_t count, std::string* error);
+    bool load_layer(int index, Layer* L, std::string* error);
+
+    // enqueue one token through all layers (reads pos from d_ctrl_[0])
+    bool enqueue_layers(bool timed, std::string* error);
+    bool enqueue_embed(const int32_t* token_dev, bool timed, std::string* error);
+    bool enqueue_lm_head(bool timed, std::string* error);
+    bool op_begin(bool timed, const std::string& name, std::vector<std::string> extra = {}, int split = 1);
+    void op_end(bool timed);
+    void flush_timed(KernelTrace* trace);
+    bool ensure_graphs(std::string* error);
+    bool fail_hip(std::string* error, const char* what);
+
+    // dimensions (defaults of custom_model.hpp:98-114)
+    int hidden_ = 4096, inter_ = 12288, vocab_ = 248320, nq_ = 16, nkv_ = 4, hd_ = 256, rot_ = 64;
+    int lk_hd_ = 128, lv_hd_ = 128, lk_n_ = 16, lv_n_ = 32, ksize_ = 4, lk_dim_ = 2048, lv_dim_ = 4096;
+    int conv_dim_ = 8192;
+    float eps_ = 1.0e-6f, theta_ = 10000000.0f;
+    int max_ctx_ = 8192;
+    std::string model_dir_, backend_request_, device_name_;
+    uint64_t weight_bytes_ = 0;
+    int inexact_meta_ = 0;
+
+    std::vector<Layer> layers_;
+    xqhip_w4 lm_head_{};
+    float* final_norm_ = nullptr;
+    uint16_t* embed_ = nullptr;
+    float* rope_cs_ = nullptr;
+
+    // activations / workspaces
+    float* resid_ = nullptr;     // fp32 residual stream (pre final-norm)
+    float* normed_ = nullptr;    // final-normed hidden (exposed hidden state)
+    float* proj_ = nullptr;      // fused input projection output
+    float* q_rot_ = nullptr;
+    float* gate_ = nullptr;
+    float* attn_ = nullptr;      // attention / delta output
+    float* conv_out_ = nullptr;
+    float* ffn_ = nullptr;
+    float* logits_ = nullptr;    // debug_json only
+    float* best_val_ = nullptr;
+    void* argmax_ws_ = nullptr;
+    void* gqa_ws_ = nullptr;
+    int32_t* d_ctrl_ = nullptr;  // [0] position, [1] input token, [2] sampled token
+    int32_t* h_ctrl_ = nullptr;  // pinned staging, 2 ints per queued token
+    size_t h_ctrl_cap_ = 0;
+    int32_t* h_tok_ = nullptr;   // pinned sampled-token readback
+    void* stream_ = nullptr;
+    void* g_prefill_ = nullptr;  // graph: embed(input token) + layers
+    void* g_decode_ = nullptr;   // graph: lm_head argmax -> embed(sampled) + layers
+    bool detail_prefill_ = true, detail_decode_ = true;
+    std::vector<TimedOp> ops_;
+    std::vector<void*> event_pool_;
+    size_t event_next_ = 0;
+    std::vector<void*> allocations_;
+    std::vector<xqhip_w4*> matrices_;
+};
+
+}  // namespace xqh
