@@ -31,8 +31,13 @@ def close(got, want, what, atol=ATOL, rtol=RTOL):
     assert not bad.any(), f"{what}: {bad.sum()} / {bad.size} bad, max err {err.max():.3g}"
 
 
+_keep = []  # device buffers stay alive until the module ends (no free before the kernel ran)
+
+
 def dev(a):
-    return xb.DeviceBuffer.from_array(np.ascontiguousarray(a))
+    b = xb.DeviceBuffer.from_array(np.ascontiguousarray(a))
+    _keep.append(b)
+    return b
 
 
 def bf16_bits(x):
@@ -143,8 +148,8 @@ def test_gqa_short_contexts(ctx):
     vc = rng.normal(0, 1, (ctx, nkv, hd)).astype(np.float16)
     gate = rng.normal(0, 1, nq * hd).astype(np.float32)
     att = np.empty(nq * hd, np.float32)
-    O().orc_attention_model(ob.p(q), ob.p(kc.astype(np.float32).reshape(-1)), ob.p(vc.astype(np.float32).reshape(-1)),
-                            ctx, nkv, nq, hd, ob.p(att))
+    kf, vf = kc.astype(np.float32).reshape(-1), vc.astype(np.float32).reshape(-1)
+    O().orc_attention_model(ob.p(q), ob.p(kf), ob.p(vf), ctx, nkv, nq, hd, ob.p(att))
     want = att * np.array([O().orc_sigmoid(float(g)) for g in gate], np.float32)
     ws = xb.DeviceBuffer(xb.hip().xqhip_gqa_workspace_bytes(nq, nkv, hd))
     ws.zero()
