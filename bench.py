@@ -2,6 +2,11 @@
 """Benchmark of the MI355X batch-1 W4A16 decode path (one GPU).
 
 Prints ONE JSON line.  Workloads (--workload):
+  decode (default) random-init 9B-shaped hybrid model (32 layers, 3 linear : 1
+         full attention, hidden 4096, MLP 12288, vocab 248320, W4A16 g64) run
+         through the xqwen35.h ABI: a 512-token prefill of random token ids,
+         then K greedy decode steps.  value = decode tokens/s (generated tokens
+         / decode wall time, as xq_metrics reports it).
   mlp    decode MLP block, hidden 4096 -> 12288 -> 4096, W4A16 g64: fused
          RMSNorm + gate/up GEMV + SiLU*up, then down GEMV + residual add.
          value = algorithmic HBM GB/s of the block (the GEMV bandwidth metric).
@@ -179,12 +184,151 @@ def cpu_baseline_mlp(inp, hidden, inter, step_bytes, seconds):
                       f"(reference worker pool, {threads} threads of {os.cpu_count()} host cores) + SiLU/residual"}
 
 
+# ---------------------------------------------------------------------------
+# workload: end-to-end batch-1 decode of the 9B-shaped model
+# ---------------------------------------------------------------------------
+MODEL_DIR = os.environ.get("XQ_BENCH_MODEL_DIR", "/tmp/xq_synth_9b_w4a16_g64")
+
+
+def ensure_model(path):
+    marker = os.path.join(path, ".complete")
+    if os.path.exists(marker):
+        return 0.0
+    t0 = time.perf_counter()
+    log(f"[bench] writing the synthetic 9B-shaped model to {path} ...")
+    xb.write_synth_model(path, threads=min(16, os.cpu_count() or 1))
+    open(marker, "w").write("ok")
+    dt = time.perf_counter() - t0
+    log(f"[bench] model written in {dt:.1f} s")
+    return dt
+
+
+def trace_rows(sess):
+    st, txt = sess.json("xq_get_kernel_trace_json", 1 << 22)
+    return {r["name"]: r for r in json.loads(txt)["rows"]} if st == 0 else {}
+
+
+def bench_decode(args):
+    prompt_len, hidden, inter = 512, 4096, 12288
+    gen_s = ensure_model(MODEL_DIR)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 248320, prompt_len, dtype=np.int32)
+    t0 = time.perf_counter()
+    sess = xb.Session(MODEL_DIR, xb.options(backend=b"hip", max_context=8192))
+    if not sess.ok():
+        raise RuntimeError(f"xq_create failed: {sess.status}")
+    load_s = time.perf_counter() - t0
+    log(f"[bench] model loaded in {load_s:.1f} s: {sess.json('xq_get_backend_info')[1][:300]}")
+    # warmup: one prefill + W decode steps (captures the step graphs)
+    st, m = sess.prefill(prompt)
+    for _ in range(args.warmup):
+        st, tok, m = sess.decode_one()
+        assert st == 0
+    # timed: fresh prefill (untimed), then exactly K decode steps
+    assert sess.lib.xq_reset(sess.h) == 0
+    st, m = sess.prefill(prompt)
+    assert st == 0, m.error
+    prefill_ms = m.prefill_ms
+    xb.ck(xb.hip().xqhip_device_synchronize())
+    toks = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        st, tok, m = sess.decode_one()
+        assert st == 0, m.error
+        toks.append(tok)
+    xb.ck(xb.hip().xqhip_device_synchronize())
+    wall = time.perf_counter() - t0
+    decode_ms = m.decode_total_ms
+    ms_per_step = wall * 1e3 / args.steps
+    tps = args.steps / wall
+    rows = trace_rows(sess)
+    gu = next((r for n, r in rows.items() if n.startswith("linear_gate_proj")), None)
+    dn = next((r for n, r in rows.items() if n.startswith("linear_down_proj")), None)
+    lm = next((r for n, r in rows.items() if n.startswith("lm_head_custom")), None)
+    step = rows.get("decode_step_graph_custom")
+    bytes_gu = w4_bytes(2 * inter, hidden) + hidden * 4 + inter * 4
+    bytes_dn = w4_bytes(hidden, inter) + inter * 4 + 2 * hidden * 4
+    bytes_lm = w4_bytes(248320, hidden) + hidden * 4
+    info = sess.json("xq_get_backend_info")[1]
+    wbytes = int(info.split("weight_bytes_per_token=")[1].split(";")[0]) if "weight_bytes_per_token=" in info else 0
+    ach = bytes_gu / (gu["mean_ms"] * 1e-3) / 1e9 if gu else None
+    step_ms = step["mean_ms"] if step else ms_per_step
+    log(f"[bench] decode {args.steps} steps: {ms_per_step:.3f} ms/token wall ({tps:.1f} tok/s), graph step "
+        f"{step_ms:.3f} ms, weights {wbytes / 1e9:.3f} GB/token -> {wbytes / (step_ms * 1e-3) / 1e9:.0f} GB/s; "
+        f"prefill {prefill_ms:.1f} ms ({prompt_len / prefill_ms * 1e3:.0f} tok/s)")
+    result = {
+        "metric": METRIC, "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u4xf16->f32", "data": "synthetic",
+        "config": {"workload": "batch-1 greedy decode, random-init 9B-shaped hybrid model (32 layers 3:1 linear:full, "
+                               "hidden 4096, MLP 12288, vocab 248320, 32q/8kv heads d128, W4A16 g64), "
+                               f"{prompt_len}-token prefill then {args.steps} decode steps",
+                   "prompt_tokens": prompt_len, "weight_bytes_per_token": wbytes,
+                   "graph_step_ms": round(step_ms, 4), "decode_total_ms_from_xq_metrics": round(decode_ms, 3),
+                   "weight_stream_GBps": round(wbytes / (step_ms * 1e-3) / 1e9, 1),
+                   "prefill_ms": round(prefill_ms, 2), "prefill_tokens_per_s": round(prompt_len / prefill_ms * 1e3, 1),
+                   "model_write_s": round(gen_s, 1), "load_s": round(load_s, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1) if ach else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4) if ach else None, "traffic": None,
+                     "kernel": "gemv_w4_tiled gate/up 24576x4096 (+RMSNorm prologue, SiLU*up epilogue), in-model",
+                     "bytes_per_launch": bytes_gu,
+                     "avg_launch_us": round(gu["mean_ms"] * 1e3, 2) if gu else None,
+                     "launches_timed": gu["calls"] if gu else 0,
+                     "down_proj": {"bytes_per_launch": bytes_dn,
+                                   "avg_launch_us": round(dn["mean_ms"] * 1e3, 2) if dn else None},
+                     "lm_head_argmax": {"bytes_per_launch": bytes_lm,
+                                        "avg_launch_us": round(lm["mean_ms"] * 1e3, 2) if lm else None}},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_decode(prompt, sess, args.cpu_seconds)
+    sess.close()
+    return result
+
+
+def cpu_baseline_decode(prompt, gpu_sess, seconds):
+    """The compiled reference customlib (oracle/_ref) on the same model files and
+    host cores, timed by its own xq_metrics; falls back to the oracle port.
+    Bounded sample: a short prompt and a few greedy steps.  The GPU session runs
+    the same sample so the greedy ids can be compared at full size."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_bind as ob
+    n_prompt, n_new = 8, 4
+    sample = prompt[:n_prompt]
+    threads = min(8, os.cpu_count() or 1)
+    st, gpu_toks, _ = gpu_sess.generate(sample, n_new)
+    if ob.ref_available():
+        ref = xb.bind_xq_abi(ctypes.CDLL(ob.REF_SO))
+        t0 = time.perf_counter()
+        rs = xb.Session(MODEL_DIR, xb.options(backend=b"cpu", threads=threads), lib=ref)
+        load_s = time.perf_counter() - t0
+        st, toks, m = rs.generate(sample, n_new)
+        rs.close()
+        kind, tps, pre = "reference", m.decode_tokens_per_second, m.prefill_tokens_per_second
+    else:
+        t0 = time.perf_counter()
+        om = ob.OracleModel(MODEL_DIR)
+        load_s = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        om.prefill(sample)
+        t2 = time.perf_counter()
+        toks = np.array([om.decode_one(n_prompt + i) for i in range(n_new)])
+        t3 = time.perf_counter()
+        kind, tps, pre = "port", n_new / (t3 - t2), n_prompt / (t2 - t1)
+    match = [int(a) == int(b) for a, b in zip(gpu_toks, toks)]
+    return {"value": round(tps, 4), "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"{n_prompt}-token prompt + {n_new} greedy decode steps on the same 9B-shaped model files "
+                      f"(reference worker pool {threads} threads of {os.cpu_count()} host cores; load {load_s:.1f} s; "
+                      f"prefill {pre:.3f} tok/s)",
+            "greedy_ids_gpu": [int(t) for t in gpu_toks], "greedy_ids_cpu": [int(t) for t in toks],
+            "greedy_ids_match": all(match)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="mlp", choices=["mlp"])
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", default="decode", choices=["decode", "mlp"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -199,7 +343,7 @@ def main():
     name = ctypes.create_string_buffer(256)
     xb.hip().xqhip_device_name(name, 256)
     log(f"[bench] device: {name.value.decode()}")
-    res = {"mlp": bench_mlp}[args.workload](args)
+    res = {"decode": bench_decode, "mlp": bench_mlp}[args.workload](args)
     print(json.dumps(res), flush=True)
 
 

@@ -9,6 +9,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <sstream>
@@ -393,7 +394,13 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
     return true;
 }
 
+static bool graphs_enabled() {
+    const char* v = std::getenv("XQ_DECODE_GRAPHS");
+    return !(v && v[0] == '0');
+}
+
 bool DeviceModel::ensure_graphs(std::string* error) {
+    if (!graphs_enabled()) return true;  // eager launches of the same kernels
     if (g_prefill_ && g_decode_) return true;
     XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
     bool ok = enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error);
@@ -440,8 +447,9 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
         h_ctrl_[2 * i] = static_cast<int32_t>(i);
         h_ctrl_[2 * i + 1] = token_ids[i];
         XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_ctrl_ + 2 * i, 2 * sizeof(int32_t), stream_), "control upload");
-        if (i == 0 && detail_prefill_) {
-            if (!enqueue_embed(d_ctrl_ + 1, true, error) || !enqueue_layers(true, error)) return false;
+        if ((i == 0 && detail_prefill_) || !g_prefill_) {
+            const bool timed = i == 0 && detail_prefill_;
+            if (!enqueue_embed(d_ctrl_ + 1, timed, error) || !enqueue_layers(timed, error)) return false;
         } else {
             XQ_CALL(xqhip_graph_launch(g_prefill_, stream_), "prefill graph");
         }
@@ -476,8 +484,9 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     h_tok_[0] = static_cast<int32_t>(position);
     h_tok_[1] = 0;
     XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
-    if (detail_decode_) {
-        if (!enqueue_lm_head(true, error) || !enqueue_embed(d_ctrl_ + 2, true, error) || !enqueue_layers(true, error))
+    if (detail_decode_ || !g_decode_) {
+        const bool timed = detail_decode_;
+        if (!enqueue_lm_head(timed, error) || !enqueue_embed(d_ctrl_ + 2, timed, error) || !enqueue_layers(timed, error))
             return false;
     } else {
         op_begin(true, "decode_step_graph_custom");
