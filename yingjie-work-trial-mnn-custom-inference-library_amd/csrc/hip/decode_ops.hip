@@ -17,6 +17,10 @@
 
 namespace xqhip {
 
+constexpr int kAttnSplits = 16;
+constexpr int kAttnMaxGroup = 8;
+constexpr int kAttnMaxSlice = 1024;  // tokens per split: context <= 16384
+
 // ---------------------------------------------------------------------------
 // embedding: bf16 row -> fp32 hidden (exact), token read from device memory.
 // ---------------------------------------------------------------------------
@@ -105,9 +109,96 @@ hipError_t launch_qk_prep(const QkPrepLaunch& p, hipStream_t s) {
 // of each kv head to finish merges the partials (rescaling by exp(m_s - m)),
 // applies the sigmoid output gate and writes the head outputs.
 // ---------------------------------------------------------------------------
-constexpr int kAttnSplits = 16;
-constexpr int kAttnMaxGroup = 8;
-constexpr int kAttnMaxSlice = 1024;  // tokens per split: context <= 16384
+
+// Partial softmax-attention of `group` query heads over tokens [t0, t0+n) of one
+// kv head.  Scores: 8 lanes per token, each lane owning HD/8 consecutive dims
+// (16-byte loads); the 8 partial dots of every query head are summed across the
+// 8 lanes.  V: each lane owns HD/64 dims of all heads for a quarter of the
+// tokens; the quarters are summed through LDS.  HD == 0: any head_dim
+// (scalar loads, tiny shapes).
+template <int HD>
+__device__ void gqa_slice(const GqaLaunch& p, int kh, int t0, int n, int group, int hd, float* qs, float* sc, float* ml,
+                          float* vpart) {
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
+    const int per_stride = blockDim.x / 8;  // tokens per pass
+    if constexpr (HD > 0) {
+        constexpr int DL = HD / 8;  // dims per lane
+        const int sub = threadIdx.x & 7;
+        for (int tt = threadIdx.x / 8; tt < ((n + per_stride - 1) / per_stride) * per_stride; tt += per_stride) {
+            const bool valid = tt < n;
+            float kv[DL];
+            if (valid) {
+                const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + tt) * p.nkv + kh) * HD + sub * DL;
+#pragma unroll
+                for (int u = 0; u < DL / 8; ++u) {
+                    const uint4 w = *reinterpret_cast<const uint4*>(krow + 8 * u);
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kv[8 * u + 2 * e] = half_lo(ww[e]);
+                        kv[8 * u + 2 * e + 1] = half_hi(ww[e]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int d = 0; d < DL; ++d) kv[d] = 0.0f;
+            }
+            for (int g = 0; g < group; ++g) {
+                const float* qv = qs + g * HD + sub * DL;
+                float dot = 0.0f;
+#pragma unroll
+                for (int d = 0; d < DL; ++d) dot += qv[d] * kv[d];
+                dot += __shfl_xor(dot, 1, kWave);
+                dot += __shfl_xor(dot, 2, kWave);
+                dot += __shfl_xor(dot, 4, kWave);
+                if (valid && sub == 0) sc[g * p.slice + tt] = dot * rscale;
+            }
+        }
+    } else {
+        for (int pr = threadIdx.x; pr < n * group; pr += blockDim.x) {
+            const int t = pr / group, g = pr % group;
+            const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; ++d) dot += qs[g * hd + d] * static_cast<float>(krow[d]);
+            sc[g * p.slice + t] = dot * rscale;
+        }
+    }
+    __syncthreads();
+    for (int g = wid; g < group; g += blockDim.x / kWave) {
+        float m = -INFINITY;
+        for (int t = lane; t < n; t += kWave) m = fmaxf(m, sc[g * p.slice + t]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int t = lane; t < n; t += kWave) {
+            const float e = expf(sc[g * p.slice + t] - m);
+            sc[g * p.slice + t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            ml[2 * g] = m;
+            ml[2 * g + 1] = l;
+        }
+    }
+    __syncthreads();
+    const int quarters = blockDim.x / kWave;  // token groups
+    for (int d0 = lane; d0 < hd; d0 += kWave) {  // this lane's dims: d0, d0 + 64, ...
+        float o[kAttnMaxGroup];
+#pragma unroll
+        for (int g = 0; g < kAttnMaxGroup; ++g) o[g] = 0.0f;
+        for (int t = wid; t < n; t += quarters) {
+            const float vv = static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d0]);
+#pragma unroll
+            for (int g = 0; g < kAttnMaxGroup; ++g)
+                if (g < group) o[g] += sc[g * p.slice + t] * vv;
+        }
+#pragma unroll
+        for (int g = 0; g < kAttnMaxGroup; ++g)
+            if (g < group) vpart[(wid * group + g) * hd + d0] = o[g];
+    }
+    __syncthreads();
+}
 
 __global__ void __launch_bounds__(256) gqa_decode_kernel(GqaLaunch p) {
     extern __shared__ float smem[];
@@ -118,55 +209,35 @@ __global__ void __launch_bounds__(256) gqa_decode_kernel(GqaLaunch p) {
     const int ctx = *p.pos + 1;
     const int per = (ctx + kAttnSplits - 1) / kAttnSplits;
     const int t0 = split * per;
-    const int t1 = min(ctx, t0 + per);
-    const int n = max(0, t1 - t0);
-    float* qs = smem;                       // [group][hd]
-    float* sc = qs + group * hd;            // [group][per]
-    float* ml = sc + group * per;           // [group][2]
+    const int n = max(0, min(ctx, t0 + per) - t0);
+    float* qs = smem;                              // [group][hd]
+    float* sc = qs + group * hd;                   // [group][slice]
+    float* ml = sc + group * p.slice;              // [group][2]
+    float* vpart = ml + 2 * group;                 // [4][group][hd]
     __shared__ int is_last;
 
     for (int i = threadIdx.x; i < group * hd; i += blockDim.x)
         qs[i] = p.q[static_cast<size_t>(kh * group + i / hd) * hd + (i % hd)];
     __syncthreads();
-    const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
-    for (int pr = threadIdx.x; pr < n * group; pr += blockDim.x) {
-        const int t = pr / group, g = pr % group;
-        const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * hd;
-        const float* qv = qs + g * hd;
-        float dot = 0.0f;
-        for (int d = 0; d < hd; ++d) dot += qv[d] * static_cast<float>(krow[d]);
-        sc[g * per + t] = dot * rscale;
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    for (int g = wid; g < group; g += nw) {
-        float m = -INFINITY;
-        for (int t = lane; t < n; t += kWave) m = fmaxf(m, sc[g * per + t]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int t = lane; t < n; t += kWave) {
-            const float e = (n > 0) ? expf(sc[g * per + t] - m) : 0.0f;
-            sc[g * per + t] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            ml[2 * g] = m;
-            ml[2 * g + 1] = l;
-        }
-    }
-    __syncthreads();
+    if (hd == 128)
+        gqa_slice<128>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
+    else if (hd == 256)
+        gqa_slice<256>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
+    else if (hd == 64)
+        gqa_slice<64>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
+    else
+        gqa_slice<0>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
     const int qh0 = kh * group;
+    const int quarters = blockDim.x / kWave;
     for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
         const int g = i / hd, d = i % hd;
         float o = 0.0f;
-        for (int t = 0; t < n; ++t)
-            o += sc[g * per + t] * static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d]);
+        for (int w = 0; w < quarters; ++w) o += vpart[(w * group + g) * hd + d];
         p.part_o[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * hd + d] = o;
     }
     for (int g = threadIdx.x; g < group; g += blockDim.x) {
         p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2] = ml[2 * g];
-        p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2 + 1] = ml[2 * g + 1];
+        p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2 + 1] = (n > 0) ? ml[2 * g + 1] : 0.0f;
     }
     __threadfence();
     __syncthreads();
@@ -205,22 +276,30 @@ size_t gqa_workspace_bytes(int nq, int nkv, int head_dim) {
            sizeof(float) * static_cast<size_t>(nq) * kAttnSplits * (head_dim + 2);
 }
 
-hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
+static size_t gqa_lds_bytes(int group, int head_dim, int slice) {
+    return sizeof(float) * (static_cast<size_t>(group) * head_dim + static_cast<size_t>(group) * slice + 2 * group +
+                            4 * static_cast<size_t>(group) * head_dim);
+}
+
+hipError_t launch_gqa(const GqaLaunch& p0, hipStream_t s) {
+    GqaLaunch p = p0;
     const int group = p.nq / p.nkv;
-    const int per_max = (p.max_ctx + kAttnSplits - 1) / kAttnSplits;
-    const size_t lds = sizeof(float) * (static_cast<size_t>(group) * p.head_dim + static_cast<size_t>(group) * per_max +
-                                        2 * group);
+    p.slice = (p.max_ctx + kAttnSplits - 1) / kAttnSplits;
+    const size_t lds = gqa_lds_bytes(group, p.head_dim, p.slice);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gqa_decode_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(gqa_decode_kernel, dim3(p.nkv, kAttnSplits), dim3(256), lds, s, p);
     return hipGetLastError();
 }
 
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx) {
-    if (nkv <= 0 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup) return false;
+    if (nkv <= 0 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || head_dim <= 0) return false;
     const int per_max = (max_ctx + kAttnSplits - 1) / kAttnSplits;
     if (per_max > kAttnMaxSlice) return false;
-    const size_t lds = sizeof(float) * (static_cast<size_t>(nq / nkv) * head_dim +
-                                        static_cast<size_t>(nq / nkv) * per_max + 2 * (nq / nkv));
-    return lds <= 64 * 1024 && head_dim > 0;
+    return gqa_lds_bytes(nq / nkv, head_dim, per_max) <= 160 * 1024;
 }
 
 // ---------------------------------------------------------------------------
@@ -299,28 +378,32 @@ __global__ void __launch_bounds__(256) gated_delta_kernel(DeltaLaunch p) {
     const float* q = p.conv + static_cast<size_t>(kh) * dk;
     const float* k = p.conv + static_cast<size_t>(p.lk_n) * dk + static_cast<size_t>(kh) * dk;
     const float* v = p.conv + 2 * static_cast<size_t>(p.lk_n) * dk + static_cast<size_t>(vh) * dv;
-    for (int i = threadIdx.x; i < dk; i += blockDim.x) {
-        qk[i] = q[i];
-        qk[256 + i] = k[i];
-    }
-    const float beta = sigmoid_dev(p.b[vh]);
-    const float gate = -expf(p.a_log[vh]) * softplus_dev(p.a[vh] + p.dt_bias[vh]);
-    const float decay = expf(gate);
-    __syncthreads();
-
     const int jl = threadIdx.x % kDeltaCols;
     const int ig = threadIdx.x / kDeltaCols;
     const int j = j0 + jl;
     const bool active = j < dv;
     float* S = p.state + static_cast<size_t>(vh) * dk * dv;
     float sreg[kDeltaMaxKPerThread];
+#pragma unroll
+    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {  // state loads first: they do not depend on q, k
+        const int i = ig + r * kDeltaIGroups;
+        sreg[r] = (active && i < dk) ? S[static_cast<size_t>(i) * dv + j] : 0.0f;
+    }
+    for (int i = threadIdx.x; i < dk; i += blockDim.x) {
+        qk[i] = q[i];
+        qk[256 + i] = k[i];
+    }
+    const float vj = active ? v[j] : 0.0f;
+    const float beta = sigmoid_dev(p.b[vh]);
+    const float gate = -expf(p.a_log[vh]) * softplus_dev(p.a[vh] + p.dt_bias[vh]);
+    const float decay = expf(gate);
+    __syncthreads();
     float pred = 0.0f;
 #pragma unroll
     for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
         const int i = ig + r * kDeltaIGroups;
-        sreg[r] = 0.0f;
         if (active && i < dk) {
-            sreg[r] = S[static_cast<size_t>(i) * dv + j] * decay;
+            sreg[r] *= decay;
             pred += sreg[r] * qk[256 + i];
         }
     }
@@ -332,7 +415,7 @@ __global__ void __launch_bounds__(256) gated_delta_kernel(DeltaLaunch p) {
     __syncthreads();
     pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
     __syncthreads();
-    const float delta = active ? beta * (v[j] - pred) : 0.0f;
+    const float delta = active ? beta * (vj - pred) : 0.0f;
     float o = 0.0f;
 #pragma unroll
     for (int r = 0; r < kDeltaMaxKPerThread; ++r) {

@@ -33,7 +33,6 @@ namespace xqhip {
 
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 
-constexpr int kGroupLdsBytes = 272;  // 128 B hi pairs + 128 B lo pairs + 16 B pad (spreads LDS banks)
 
 __device__ __forceinline__ float load_act(const void* x, int x_f16, int i) {
     if (x_f16) return static_cast<float>(static_cast<const _Float16*>(x)[i]);
@@ -79,42 +78,146 @@ __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& 
     return v;
 }
 
-// Stage x (optionally RMS-normalised) for the dot2 inner loop.
-// Per group (kGroupLdsBytes): 8 x uint4 of hi pairs, then 8 x uint4 of lo pairs;
-// word j of a group holds, for columns 8j..8j+7, the fp16 pairs
-// (x0,x4) (x1/16,x5/16) (x2,x6) (x3/16,x7/16).
-// gc[g] = (sum of the effective x of the group, 1024*sum(hi staged), 1024*sum(lo staged), 0).
-__device__ void stage_activations(const void* x, int x_f16, const Prologue& pro, const float* inv_lds, int groups,
-                                  unsigned char* xs_bytes, float4* gc) {
-    for (int it = threadIdx.x; it < groups * 4; it += blockDim.x) {
-        const int g = it >> 2, qtr = it & 3;
-        float gsum = 0.0f, st_hi = 0.0f, st_lo = 0.0f;
+// ---------------------------------------------------------------------------
+// Activation staging, once per GEMV launch (stage_x_kernel), into the
+// file-scope device buffer g_xstage that the GEMV blocks then copy to LDS.
+// Record of group g (kStageRecord uint4): 8 words of hi pairs, 8 words of lo
+// pairs, then (sum of the effective x of the group, 1024*sum(hi staged),
+// 1024*sum(lo staged), 0).  Word j holds, for columns 8j..8j+7 of the group,
+// the fp16 pairs (x0,x4) (x1/16,x5/16) (x2,x6) (x3/16,x7/16), matching the
+// nibble order produced by dot8.  Launches on one stream are ordered, so one
+// buffer per device serves every GEMV; GEMVs on different streams of one
+// device must not overlap.
+// ---------------------------------------------------------------------------
+constexpr int kStageRecord = 17;
+constexpr int kMaxStageGroups = 256;  // cols <= 16384
+__device__ uint4 g_xstage[kMaxStageGroups * kStageRecord];
+
+// One block of kStageThreads stages the whole vector: every thread owns the
+// (group, word) items t, t + kStageThreads, ... (8 consecutive columns each),
+// loads them once with 16-byte loads, and the norm factors come from the same
+// registers: the RMS over the vector by one block reduction, the per-head
+// factors of PRO_GATED by a lane butterfly over the head's consecutive items.
+constexpr int kStageThreads = 512;
+constexpr int kStageItems = 6;  // items per thread: cols <= 512 * 6 * 8 = 24576
+
+__device__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__device__ __forceinline__ void load8(const void* x, int x_f16, int c0, float* v) {
+    const void* p = x_f16 ? static_cast<const void*>(static_cast<const _Float16*>(x) + c0)
+                          : static_cast<const void*>(static_cast<const float*>(x) + c0);
+    if (!aligned16(p)) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int w = qtr * 2 + j;
-            const int c0 = g * 64 + w * 8;
+        for (int i = 0; i < 8; ++i) v[i] = load_act(x, x_f16, c0 + i);
+        return;
+    }
+    if (x_f16) {
+        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const _Float16*>(x) + c0);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = half_lo(w[i]);
+            v[2 * i + 1] = half_hi(w[i]);
+        }
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + c0);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + c0 + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+}
+
+__device__ __forceinline__ void load8f(const float* p, float* v) {
+    if (!aligned16(p)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = p[i];
+        return;
+    }
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__global__ void __launch_bounds__(kStageThreads) stage_x_kernel(const void* __restrict__ x, int x_f16, Prologue pro,
+                                                                int cols) {
+    __shared__ float red[32];
+    const int G = cols >> 6;
+    const int n_items = G * 8;
+    float v[kStageItems][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kStageItems; ++k) {
+        const int item = threadIdx.x + k * kStageThreads;
+        if (item < n_items) {
+            load8(x, x_f16, item * 8, v[k]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
+        }
+    }
+    if (pro.mode == PRO_RMS) {
+        ss = block_sum(ss, red);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + pro.eps);
+#pragma unroll
+        for (int k = 0; k < kStageItems; ++k) {
+            const int item = threadIdx.x + k * kStageThreads;
+            if (item < n_items) {
+                float w[8];
+                load8f(pro.w + item * 8, w);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * w[i];
+            }
+        }
+    } else if (pro.mode == PRO_GATED) {
+        // head_dim % 8 == 0 and head_dim / 8 a power of two <= 64: the items of a
+        // head are head_dim/8 consecutive lanes of one wave
+        const int per_head = pro.head_dim >> 3;
+#pragma unroll
+        for (int k = 0; k < kStageItems; ++k) {
+            const int item = threadIdx.x + k * kStageThreads;
+            float hs = 0.0f;
+            if (item < n_items)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) hs += v[k][i] * v[k][i];
+            for (int m = 1; m < per_head; m <<= 1) hs += __shfl_xor(hs, m, kWave);
+            if (item < n_items) {
+                const float inv = 1.0f / sqrtf(hs / static_cast<float>(pro.head_dim) + pro.eps);
+                const int c0 = item * 8;
+                const int d0 = c0 % pro.head_dim;
+                float w[8], z[8];
+                load8f(pro.w + d0, w);
+                load8f(pro.z + c0, z);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * w[i] * silu_dev(z[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kStageItems; ++k) {
+        const int item = threadIdx.x + k * kStageThreads;
+        const int g = item >> 3, w = item & 7;
+        float gsum = 0.0f, st_hi = 0.0f, st_lo = 0.0f;
+        if (item < n_items) {
             _Float16 sh[8], sl[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float v = prologue_apply(load_act(x, x_f16, c0 + i), c0 + i, pro, inv_lds);
-                const _Float16 hi = static_cast<_Float16>(v);
-                const float lo = (v - static_cast<float>(hi)) * 2048.0f;
+                const _Float16 hi = static_cast<_Float16>(v[k][i]);
+                const float lo = (v[k][i] - static_cast<float>(hi)) * 2048.0f;
                 const float sc = (i & 1) ? 0.0625f : 1.0f;
                 sh[i] = static_cast<_Float16>(static_cast<float>(hi) * sc);
                 sl[i] = static_cast<_Float16>(lo * sc);
             }
-            unsigned char* gb = xs_bytes + static_cast<size_t>(g) * kGroupLdsBytes + w * 16;
             uint4 word;
             word.x = as_u32(h2{sh[0], sh[4]});
             word.y = as_u32(h2{sh[1], sh[5]});
             word.z = as_u32(h2{sh[2], sh[6]});
             word.w = as_u32(h2{sh[3], sh[7]});
-            *reinterpret_cast<uint4*>(gb) = word;
+            g_xstage[g * kStageRecord + w] = word;
             word.x = as_u32(h2{sl[0], sl[4]});
             word.y = as_u32(h2{sl[1], sl[5]});
             word.z = as_u32(h2{sl[2], sl[6]});
             word.w = as_u32(h2{sl[3], sl[7]});
-            *reinterpret_cast<uint4*>(gb + 128) = word;
+            g_xstage[g * kStageRecord + 8 + w] = word;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float a = static_cast<float>(sh[i]), b = static_cast<float>(sl[i]);
@@ -125,13 +228,25 @@ __device__ void stage_activations(const void* x, int x_f16, const Prologue& pro,
             }
         }
 #pragma unroll
-        for (int m = 1; m <= 2; m <<= 1) {
+        for (int m = 1; m <= 4; m <<= 1) {  // the 8 words of a group are 8 consecutive lanes
             gsum += __shfl_xor(gsum, m, kWave);
             st_hi += __shfl_xor(st_hi, m, kWave);
             st_lo += __shfl_xor(st_lo, m, kWave);
         }
-        if (qtr == 0) gc[g] = make_float4(gsum, 1024.0f * st_hi, 1024.0f * st_lo, 0.0f);
+        if (item < n_items && w == 0) {
+            const float4 kk = make_float4(gsum, 1024.0f * st_hi, 1024.0f * st_lo, 0.0f);
+            g_xstage[g * kStageRecord + 16] = *reinterpret_cast<const uint4*>(&kk);
+        }
     }
+}
+
+bool stage_supported(int cols, const Prologue& pro) {
+    if (cols % 64 != 0 || cols / 8 > kStageThreads * kStageItems) return false;
+    if (pro.mode == PRO_GATED) {
+        const int per = pro.head_dim / 8;
+        return pro.head_dim % 8 == 0 && per >= 1 && per <= 64 && (per & (per - 1)) == 0;
+    }
+    return true;
 }
 
 // m_lo = 0x000F000F, m_hi = 0x00F000F0 and magic = kMagic2 are passed in so
@@ -183,93 +298,98 @@ __device__ void finish_argmax(uint64_t block_best, uint64_t* partial, uint32_t* 
 // ---------------------------------------------------------------------------
 // TILED64 kernel.  NCH = number of 4096-column chunks (the last may be partial);
 // a block has RG row groups x NCH waves, wave (rg, c) owns chunk c for the rows
-// of row group rg; R = rows per wave iteration.
+// of row group rg; R = rows per wave iteration.  The weights of the next row
+// batch are in flight while the current one is reduced (two register buffers),
+// and the first batch is requested before the staged activations are read.
 // ---------------------------------------------------------------------------
+template <int R>
+struct WBatch {
+    uint4 a[R], b[R];
+    uint32_t m[R];
+};
+
+template <int R>
+__device__ __forceinline__ void load_batch(WBatch<R>& wb, const uint8_t* __restrict__ nib,
+                                           const uint32_t* __restrict__ meta, int r0, int rows, size_t row_bytes,
+                                           int G, int c, int lane, int gcnt, bool has_group) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int row = min(r0 + i, rows - 1);
+        if (has_group) {
+            const uint8_t* rowp = nib + static_cast<size_t>(row) * row_bytes + c * 2048;
+            wb.a[i] = load_nt16(rowp + lane * 16);
+            wb.b[i] = load_nt16(rowp + gcnt * 16 + lane * 16);
+            wb.m[i] = __builtin_nontemporal_load(meta + static_cast<size_t>(row) * G + c * 64 + lane);
+        } else {
+            wb.a[i] = make_uint4(0, 0, 0, 0);
+            wb.b[i] = make_uint4(0, 0, 0, 0);
+            wb.m[i] = 0u;
+        }
+    }
+}
+
 template <int NCH, int RG, int R, int EPI>
 __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
-    const void* __restrict__ x, int x_f16, Prologue pro, void* __restrict__ y,
-    int y_f16, uint64_t* __restrict__ partial, uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
-    float* __restrict__ out_val) {
-    extern __shared__ __align__(16) unsigned char smem[];
+    void* __restrict__ y, int y_f16, uint64_t* __restrict__ partial, uint32_t* __restrict__ counter,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_val) {
+    extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
+    __shared__ float part[RG * NCH * R];
+    __shared__ uint64_t lds_keys[16];
     const int G = cols >> 6;
-    unsigned char* xs = smem;
-    float4* gc = reinterpret_cast<float4*>(smem + static_cast<size_t>(G) * kGroupLdsBytes);
-    float* red = reinterpret_cast<float*>(gc + G);                   // 32 floats
-    uint64_t* lds_keys = reinterpret_cast<uint64_t*>(red + 32);      // 16 keys
-    float* part = reinterpret_cast<float*>(lds_keys + 16);           // [RG][NCH][R]
-    float* inv_lds = part + RG * NCH * R;                            // [kMaxNormHeads]
-
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = threadIdx.x / kWave;
     const int c = wid % NCH;
     const int rg = wid / NCH;
-
-    prologue_factors(x, x_f16, cols, pro, inv_lds, red);
-    stage_activations(x, x_f16, pro, inv_lds, G, xs, gc);
-    __syncthreads();
-
     const int g = c * 64 + lane;
     const bool has_group = g < G;
     const int gcnt = min(64, G - c * 64);
+    const size_t row_bytes = static_cast<size_t>(cols) >> 1;
+    const int stride = gridDim.x * RG;
+
+    WBatch<R> buf0, buf1;
+    int base = blockIdx.x * RG;
+    if (base * R < rows) load_batch<R>(buf0, nib, meta, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+
+    for (int i = threadIdx.x; i < G * kStageRecord; i += blockDim.x) xs[i] = g_xstage[i];
+    __syncthreads();
     uint4 xh[8], xl[8];
     float4 gk = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        xh[j] = make_uint4(0, 0, 0, 0);
-        xl[j] = make_uint4(0, 0, 0, 0);
+        xh[j] = has_group ? xs[g * kStageRecord + j] : make_uint4(0, 0, 0, 0);
+        xl[j] = has_group ? xs[g * kStageRecord + 8 + j] : make_uint4(0, 0, 0, 0);
     }
     if (has_group) {
-        const unsigned char* gb = xs + static_cast<size_t>(g) * kGroupLdsBytes;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            xh[j] = *reinterpret_cast<const uint4*>(gb + j * 16);
-            xl[j] = *reinterpret_cast<const uint4*>(gb + 128 + j * 16);
-        }
-        gk = gc[g];
+        const uint4 k = xs[g * kStageRecord + 16];
+        gk = *reinterpret_cast<const float4*>(&k);
     }
 
-    const size_t row_bytes = static_cast<size_t>(cols) >> 1;
     const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = kMagic2;
     uint64_t best = 0;
-    for (int base = blockIdx.x * RG; base * R < rows; base += gridDim.x * RG) {
-        const int r0 = (base + rg) * R;
+
+    auto process = [&](WBatch<R>& cur, int bbase) {
+        const int r0 = (bbase + rg) * R;
         float acc[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) acc[i] = 0.0f;
         if (r0 < rows) {
-            uint4 wa[R], wb[R];
-            uint32_t mt[R];
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int row = min(r0 + i, rows - 1);
-                if (has_group) {
-                    const uint8_t* rowp = nib + static_cast<size_t>(row) * row_bytes + c * 2048;
-                    wa[i] = load_nt16(rowp + lane * 16);
-                    wb[i] = load_nt16(rowp + gcnt * 16 + lane * 16);
-                    mt[i] = __builtin_nontemporal_load(meta + static_cast<size_t>(row) * G + g);
-                } else {
-                    wa[i] = make_uint4(0, 0, 0, 0);
-                    wb[i] = make_uint4(0, 0, 0, 0);
-                    mt[i] = 0u;
-                }
-            }
 #pragma unroll
             for (int i = 0; i < R; ++i) {
                 float dh = 0.0f, dl = 0.0f;
-                dot8(wa[i].x, xh[0], xl[0], dh, dl, m_lo, m_hi, magic);
-                dot8(wa[i].y, xh[1], xl[1], dh, dl, m_lo, m_hi, magic);
-                dot8(wa[i].z, xh[2], xl[2], dh, dl, m_lo, m_hi, magic);
-                dot8(wa[i].w, xh[3], xl[3], dh, dl, m_lo, m_hi, magic);
-                dot8(wb[i].x, xh[4], xl[4], dh, dl, m_lo, m_hi, magic);
-                dot8(wb[i].y, xh[5], xl[5], dh, dl, m_lo, m_hi, magic);
-                dot8(wb[i].z, xh[6], xl[6], dh, dl, m_lo, m_hi, magic);
-                dot8(wb[i].w, xh[7], xl[7], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.a[i].x, xh[0], xl[0], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.a[i].y, xh[1], xl[1], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.a[i].z, xh[2], xl[2], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.a[i].w, xh[3], xl[3], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.b[i].x, xh[4], xl[4], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.b[i].y, xh[5], xl[5], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.b[i].z, xh[6], xl[6], dh, dl, m_lo, m_hi, magic);
+                dot8(cur.b[i].w, xh[7], xl[7], dh, dl, m_lo, m_hi, magic);
                 // sum_c q_c x_c of the group, with the 1024 offsets removed per part
                 const float t = fmaf(dl - gk.z, 1.0f / 2048.0f, dh - gk.y);
-                const float s = half_lo(mt[i]);
-                const float z = half_hi(mt[i]);
-                acc[i] = affine ? fmaf(s, t, z * gk.x) : s * fmaf(-z, gk.x, t);
+                const float sc = half_lo(cur.m[i]);
+                const float z = half_hi(cur.m[i]);
+                acc[i] = affine ? fmaf(sc, t, z * gk.x) : sc * fmaf(-z, gk.x, t);
                 acc[i] = wave_sum(acc[i]);
             }
         }
@@ -293,7 +413,7 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
             }
             __syncthreads();
         }
-        if (c != 0 || r0 >= rows) continue;
+        if (c != 0 || r0 >= rows) return;
         if constexpr (EPI == EPI_ARGMAX) {
 #pragma unroll
             for (int i = 0; i < R; ++i)
@@ -325,7 +445,20 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
                 }
             }
         }
+    };
+
+    // two batches per trip so each register buffer has a fixed name
+    while (base * R < rows) {
+        const int b1 = base + stride;
+        if (b1 * R < rows) load_batch<R>(buf1, nib, meta, (b1 + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        process(buf0, base);
+        if (b1 * R >= rows) break;
+        const int b2 = b1 + stride;
+        if (b2 * R < rows) load_batch<R>(buf0, nib, meta, (b2 + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        process(buf1, b1);
+        base = b2;
     }
+
     if constexpr (EPI == EPI_ARGMAX) {
         if (lane == 0) lds_keys[wid] = (c == 0) ? best : 0;
         __syncthreads();
@@ -424,30 +557,32 @@ template <int NCH, int R, int EPI>
 static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     constexpr int RG = NCH == 1 ? 4 : (NCH == 4 ? 1 : 2);
     const int G = p.cols >> 6;
-    const size_t lds = static_cast<size_t>(G) * (kGroupLdsBytes + sizeof(float4)) + 32 * sizeof(float) + 16 * 8 +
-                       (RG * NCH * R + kMaxNormHeads) * sizeof(float);
-    const int batches = (p.rows + R - 1) / R;
-    int blocks = (batches + RG - 1) / RG;
-    if (blocks > p.max_blocks) blocks = p.max_blocks;
-    if (blocks < 1) blocks = 1;
+    if (!stage_supported(p.cols, p.pro)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(stage_x_kernel, dim3(1), dim3(kStageThreads), 0, s, p.x, p.x_f16, p.pro, p.cols);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const size_t lds = static_cast<size_t>(G) * kStageRecord * sizeof(uint4);
     if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
     }
+    const int batches = (p.rows + R - 1) / R;
+    int blocks = (batches + RG - 1) / RG;
+    if (blocks > p.max_blocks) blocks = p.max_blocks;
+    if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
-                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro,
-                       p.y, p.y_f16, p.partial, p.counter, p.out_idx, p.out_val);
+                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.y, p.y_f16, p.partial,
+                       p.counter, p.out_idx, p.out_val);
     return hipGetLastError();
 }
 
 template <int NCH>
 static hipError_t launch_tiled_nch(const GemvLaunch& p, hipStream_t s) {
     switch (p.epi) {
-        case EPI_STORE: return launch_tiled_t<NCH, 2, EPI_STORE>(p, s);
-        case EPI_ADD: return launch_tiled_t<NCH, 2, EPI_ADD>(p, s);
-        case EPI_SILU: return launch_tiled_t<NCH, 2, EPI_SILU>(p, s);
-        case EPI_ARGMAX: return launch_tiled_t<NCH, 2, EPI_ARGMAX>(p, s);
+        case EPI_STORE: return launch_tiled_t<NCH, 4, EPI_STORE>(p, s);
+        case EPI_ADD: return launch_tiled_t<NCH, 4, EPI_ADD>(p, s);
+        case EPI_SILU: return launch_tiled_t<NCH, 4, EPI_SILU>(p, s);
+        case EPI_ARGMAX: return launch_tiled_t<NCH, 4, EPI_ARGMAX>(p, s);
     }
     return hipErrorInvalidValue;
 }

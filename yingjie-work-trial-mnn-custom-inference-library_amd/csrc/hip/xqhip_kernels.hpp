@@ -70,6 +70,7 @@ struct GqaLaunch {
     const _Float16* v_cache;
     const float* gate;
     int nq, nkv, head_dim, max_ctx;
+    int slice;  // LDS score row length (set by the launcher)
     const int32_t* pos;
     float* out;
     uint32_t* counters;
