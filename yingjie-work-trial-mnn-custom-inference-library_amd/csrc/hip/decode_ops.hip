@@ -239,15 +239,18 @@ __global__ void __launch_bounds__(256) gqa_decode_kernel(GqaLaunch p) {
         p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2] = ml[2 * g];
         p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2 + 1] = (n > 0) ? ml[2 * g + 1] : 0.0f;
     }
-    __threadfence();
+    // every wave's partial stores have completed at L2 before wave 0 releases
+    // them (one agent-scope fence per block: it writes back the XCD's L2)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const uint32_t ticket = atomicAdd(&p.counters[kh], 1u);
         is_last = ticket == kAttnSplits - 1;
+        if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
         const int g = i / hd, d = i % hd;
         const size_t base = static_cast<size_t>(qh0 + g) * kAttnSplits;

@@ -79,122 +79,132 @@ __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& 
 }
 
 // ---------------------------------------------------------------------------
-// Activation staging, once per GEMV launch (stage_x_kernel), into the
-// file-scope device buffer g_xstage that the GEMV blocks then copy to LDS.
-// Record of group g (kStageRecord uint4): 8 words of hi pairs, 8 words of lo
-// pairs, then (sum of the effective x of the group, 1024*sum(hi staged),
-// 1024*sum(lo staged), 0).  Word j holds, for columns 8j..8j+7 of the group,
-// the fp16 pairs (x0,x4) (x1/16,x5/16) (x2,x6) (x3/16,x7/16), matching the
-// nibble order produced by dot8.  Launches on one stream are ordered, so one
-// buffer per device serves every GEMV; GEMVs on different streams of one
-// device must not overlap.
+// Activation staging into LDS, done by every GEMV block while its first batch
+// of weights is in flight.  Record of group g (kStageRecord uint4): 8 words of
+// hi pairs, 8 words of lo pairs, then (sum of the effective x of the group,
+// 1024*sum(hi staged), 1024*sum(lo staged), 0).  Word j holds, for columns
+// 8j..8j+7 of the group, the fp16 pairs (x0,x4) (x1/16,x5/16) (x2,x6)
+// (x3/16,x7/16), matching the nibble order produced by dot8.
 // ---------------------------------------------------------------------------
 constexpr int kStageRecord = 17;
-constexpr int kMaxStageGroups = 256;  // cols <= 16384
-__device__ uint4 g_xstage[kMaxStageGroups * kStageRecord];
+constexpr int kMaxStageCols = 16384;
 
-// One block of kStageThreads stages the whole vector: every thread owns the
-// (group, word) items t, t + kStageThreads, ... (8 consecutive columns each),
-// loads them once with 16-byte loads, and the norm factors come from the same
-// registers: the RMS over the vector by one block reduction, the per-head
-// factors of PRO_GATED by a lane butterfly over the head's consecutive items.
-constexpr int kStageThreads = 512;
-constexpr int kStageItems = 6;  // items per thread: cols <= 512 * 6 * 8 = 24576
-
-__device__ __forceinline__ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-__device__ __forceinline__ void load8(const void* x, int x_f16, int c0, float* v) {
-    const void* p = x_f16 ? static_cast<const void*>(static_cast<const _Float16*>(x) + c0)
-                          : static_cast<const void*>(static_cast<const float*>(x) + c0);
-    if (!aligned16(p)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = load_act(x, x_f16, c0 + i);
-        return;
-    }
-    if (x_f16) {
-        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const _Float16*>(x) + c0);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[2 * i] = half_lo(w[i]);
-            v[2 * i + 1] = half_hi(w[i]);
-        }
-    } else {
-        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + c0);
-        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + c0 + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    }
-}
-
+// The block stages the whole vector: thread t owns the (group, word) items
+// t, t + THREADS, ... (8 consecutive columns each).  It first issues the
+// 16-byte loads of x and of the prologue vectors (x, the RMS weight and the
+// gate are 16-byte aligned, checked by the C ABI), then calls `prefetch`,
+// which issues the block's first weight loads, so the (cache-resident)
+// activations return first and the staging arithmetic below overlaps the
+// weight stream (vector loads return in issue order).  The norm factors come
+// from the same registers: the RMS over the vector by one block reduction, the
+// per-head factors of PRO_GATED by a lane butterfly over the head's
+// consecutive items.  ITEMS * THREADS * 8 must cover `cols`; the caller
+// synchronises the block before reading xs.  Prologue vectors are preloaded
+// only for <= 2 items per thread (the 4096-column launches): wider blocks load
+// them after the prefetch, to keep the register budget of the main loop.
 __device__ __forceinline__ void load8f(const float* p, float* v) {
-    if (!aligned16(p)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = p[i];
-        return;
-    }
     const float4 a = *reinterpret_cast<const float4*>(p);
     const float4 b = *reinterpret_cast<const float4*>(p + 4);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-__global__ void __launch_bounds__(kStageThreads) stage_x_kernel(const void* __restrict__ x, int x_f16, Prologue pro,
-                                                                int cols) {
-    __shared__ float red[32];
+// f16 x: the 8 halves stay packed in v[0..3] (as raw bits) until unpack8_f16.
+__device__ __forceinline__ void load8h_raw(const _Float16* p, float* v) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+}
+
+__device__ __forceinline__ void unpack8_f16(float* v) {
+    const uint32_t a = __float_as_uint(v[0]), b = __float_as_uint(v[1]), c = __float_as_uint(v[2]),
+                   d = __float_as_uint(v[3]);
+    v[0] = half_lo(a); v[1] = half_hi(a); v[2] = half_lo(b); v[3] = half_hi(b);
+    v[4] = half_lo(c); v[5] = half_hi(c); v[6] = half_lo(d); v[7] = half_hi(d);
+}
+
+template <int THREADS, int ITEMS, typename Prefetch>
+__device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f16, const Prologue& pro, int cols,
+                                            uint4* __restrict__ xs, float* red, Prefetch&& prefetch) {
+    constexpr bool kPre = ITEMS <= 2;
+    constexpr int kW = kPre ? ITEMS : 1;
     const int G = cols >> 6;
     const int n_items = G * 8;
-    float v[kStageItems][8];
-    float ss = 0.0f;
+    float v[ITEMS][8], wv[kW][8], zv[kW][8];
 #pragma unroll
-    for (int k = 0; k < kStageItems; ++k) {
-        const int item = threadIdx.x + k * kStageThreads;
-        if (item < n_items) {
-            load8(x, x_f16, item * 8, v[k]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
+    for (int k = 0; k < ITEMS; ++k) {
+        const int item = min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1);
+        if (x_f16)
+            load8h_raw(static_cast<const _Float16*>(x) + item * 8, v[k]);
+        else
+            load8f(static_cast<const float*>(x) + item * 8, v[k]);
+        if constexpr (kPre) {
+            if (pro.mode == PRO_RMS) {
+                load8f(pro.w + item * 8, wv[k]);
+            } else if (pro.mode == PRO_GATED) {
+                load8f(pro.w + (item * 8) % pro.head_dim, wv[k]);
+                load8f(pro.z + item * 8, zv[k]);
+            }
         }
     }
+    prefetch();
+    if (x_f16) {
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) unpack8_f16(v[k]);
+    }
     if (pro.mode == PRO_RMS) {
-        ss = block_sum(ss, red);
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const int item = threadIdx.x + k * THREADS;
+            if (item < n_items)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
+        }
+        ss = block_sum_t<THREADS / kWave>(ss, red);
         const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + pro.eps);
 #pragma unroll
-        for (int k = 0; k < kStageItems; ++k) {
-            const int item = threadIdx.x + k * kStageThreads;
-            if (item < n_items) {
-                float w[8];
-                load8f(pro.w + item * 8, w);
+        for (int k = 0; k < ITEMS; ++k) {
+            float wl[8];
+            if constexpr (kPre) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * w[i];
+                for (int i = 0; i < 8; ++i) wl[i] = wv[k][i];
+            } else {
+                const int item = min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1);
+                load8f(pro.w + item * 8, wl);
             }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i];
         }
     } else if (pro.mode == PRO_GATED) {
         // head_dim % 8 == 0 and head_dim / 8 a power of two <= 64: the items of a
         // head are head_dim/8 consecutive lanes of one wave
         const int per_head = pro.head_dim >> 3;
 #pragma unroll
-        for (int k = 0; k < kStageItems; ++k) {
-            const int item = threadIdx.x + k * kStageThreads;
+        for (int k = 0; k < ITEMS; ++k) {
             float hs = 0.0f;
-            if (item < n_items)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) hs += v[k][i] * v[k][i];
+            for (int i = 0; i < 8; ++i) hs += v[k][i] * v[k][i];
             for (int m = 1; m < per_head; m <<= 1) hs += __shfl_xor(hs, m, kWave);
-            if (item < n_items) {
-                const float inv = 1.0f / sqrtf(hs / static_cast<float>(pro.head_dim) + pro.eps);
-                const int c0 = item * 8;
-                const int d0 = c0 % pro.head_dim;
-                float w[8], z[8];
-                load8f(pro.w + d0, w);
-                load8f(pro.z + c0, z);
+            const float inv = 1.0f / sqrtf(hs / static_cast<float>(pro.head_dim) + pro.eps);
+            float wl[8], zl[8];
+            if constexpr (kPre) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * w[i] * silu_dev(z[i]);
+                for (int i = 0; i < 8; ++i) {
+                    wl[i] = wv[k][i];
+                    zl[i] = zv[k][i];
+                }
+            } else {
+                const int item = min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1);
+                load8f(pro.w + (item * 8) % pro.head_dim, wl);
+                load8f(pro.z + item * 8, zl);
             }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i] * silu_dev(zl[i]);
         }
     }
 #pragma unroll
-    for (int k = 0; k < kStageItems; ++k) {
-        const int item = threadIdx.x + k * kStageThreads;
+    for (int k = 0; k < ITEMS; ++k) {
+        const int item = threadIdx.x + k * THREADS;
         const int g = item >> 3, w = item & 7;
         float gsum = 0.0f, st_hi = 0.0f, st_lo = 0.0f;
         if (item < n_items) {
@@ -212,12 +222,12 @@ __global__ void __launch_bounds__(kStageThreads) stage_x_kernel(const void* __re
             word.y = as_u32(h2{sh[1], sh[5]});
             word.z = as_u32(h2{sh[2], sh[6]});
             word.w = as_u32(h2{sh[3], sh[7]});
-            g_xstage[g * kStageRecord + w] = word;
+            xs[g * kStageRecord + w] = word;
             word.x = as_u32(h2{sl[0], sl[4]});
             word.y = as_u32(h2{sl[1], sl[5]});
             word.z = as_u32(h2{sl[2], sl[6]});
             word.w = as_u32(h2{sl[3], sl[7]});
-            g_xstage[g * kStageRecord + 8 + w] = word;
+            xs[g * kStageRecord + 8 + w] = word;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float a = static_cast<float>(sh[i]), b = static_cast<float>(sl[i]);
@@ -235,13 +245,13 @@ __global__ void __launch_bounds__(kStageThreads) stage_x_kernel(const void* __re
         }
         if (item < n_items && w == 0) {
             const float4 kk = make_float4(gsum, 1024.0f * st_hi, 1024.0f * st_lo, 0.0f);
-            g_xstage[g * kStageRecord + 16] = *reinterpret_cast<const uint4*>(&kk);
+            xs[g * kStageRecord + 16] = *reinterpret_cast<const uint4*>(&kk);
         }
     }
 }
 
 bool stage_supported(int cols, const Prologue& pro) {
-    if (cols % 64 != 0 || cols / 8 > kStageThreads * kStageItems) return false;
+    if (cols % 64 != 0 || cols > kMaxStageCols) return false;
     if (pro.mode == PRO_GATED) {
         const int per = pro.head_dim / 8;
         return pro.head_dim % 8 == 0 && per >= 1 && per <= 64 && (per & (per - 1)) == 0;
@@ -270,15 +280,18 @@ __device__ __forceinline__ void dot8(uint32_t w, uint4 xh, uint4 xl, float& dh, 
 __device__ void finish_argmax(uint64_t block_best, uint64_t* partial, uint32_t* counter, int32_t* out_idx,
                               float* out_val, uint64_t* lds_keys) {
     __shared__ int is_last;
+    // One release (L2 write-back) per block and one acquire in the last block:
+    // an agent-scope fence costs a whole-L2 write-back/invalidate on this part,
+    // so it is issued by a single wave, never by every wave of the block.
     if (threadIdx.x == 0) {
         partial[blockIdx.x] = block_best;
-        __threadfence();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const uint32_t ticket = atomicAdd(counter, 1u);
         is_last = (ticket == gridDim.x - 1) ? 1 : 0;
+        if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     uint64_t best = 0;
     for (int i = threadIdx.x; i < static_cast<int>(gridDim.x); i += blockDim.x)
         best = u64_max(best, __hip_atomic_load(&partial[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -298,9 +311,17 @@ __device__ void finish_argmax(uint64_t block_best, uint64_t* partial, uint32_t* 
 // ---------------------------------------------------------------------------
 // TILED64 kernel.  NCH = number of 4096-column chunks (the last may be partial);
 // a block has RG row groups x NCH waves, wave (rg, c) owns chunk c for the rows
-// of row group rg; R = rows per wave iteration.  The weights of the next row
-// batch are in flight while the current one is reduced (two register buffers),
-// and the first batch is requested before the staged activations are read.
+// of row group rg; R = rows per wave iteration.  Two register buffers of
+// weights: a buffer is refilled with the batch two strides ahead as soon as it
+// is reduced, and the first two batches are requested before the activations
+// are staged.
+//
+// Weights are read through buffer resources: a load past the end of the
+// matrix (a row beyond `rows`, a lane beyond the last group of a partial
+// chunk) is dropped by the hardware range check and returns zeros, so every
+// load is issued unconditionally.  That keeps the number of loads in flight
+// the same on every path, which lets each wait cover exactly the buffer it
+// consumes (vector loads complete in issue order) instead of draining both.
 // ---------------------------------------------------------------------------
 template <int R>
 struct WBatch {
@@ -308,33 +329,50 @@ struct WBatch {
     uint32_t m[R];
 };
 
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9-family format
+constexpr int kLoadNT = 2;                    // non-temporal (streamed once)
+constexpr uint32_t kOutOfRange = 0x80000000u; // beyond every range (matrices < 2 GiB)
+
+struct WSrc {
+    __amdgpu_buffer_rsrc_t nib, meta;
+};
+
+__device__ __forceinline__ WSrc make_wsrc(const uint8_t* nib, const uint32_t* meta, int rows, int cols) {
+    const uint32_t nib_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 1);
+    const uint32_t meta_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 6) * 4u;
+    WSrc s;
+    s.nib = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(nib), 0, nib_bytes, kRsrcWord3);
+    s.meta = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(meta), 0, meta_bytes, kRsrcWord3);
+    return s;
+}
+
+__device__ __forceinline__ uint4 as_uint4(u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
 template <int R>
-__device__ __forceinline__ void load_batch(WBatch<R>& wb, const uint8_t* __restrict__ nib,
-                                           const uint32_t* __restrict__ meta, int r0, int rows, size_t row_bytes,
+__device__ __forceinline__ void load_batch(WBatch<R>& wb, const WSrc& src, int r0, int rows, uint32_t row_bytes,
                                            int G, int c, int lane, int gcnt, bool has_group) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-        const int row = min(r0 + i, rows - 1);
-        if (has_group) {
-            const uint8_t* rowp = nib + static_cast<size_t>(row) * row_bytes + c * 2048;
-            wb.a[i] = load_nt16(rowp + lane * 16);
-            wb.b[i] = load_nt16(rowp + gcnt * 16 + lane * 16);
-            wb.m[i] = __builtin_nontemporal_load(meta + static_cast<size_t>(row) * G + c * 64 + lane);
-        } else {
-            wb.a[i] = make_uint4(0, 0, 0, 0);
-            wb.b[i] = make_uint4(0, 0, 0, 0);
-            wb.m[i] = 0u;
-        }
+        const int row = r0 + i;
+        const bool ok = has_group && row < rows;
+        const uint32_t off = static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(c * 2048 + lane * 16);
+        const uint32_t moff = (static_cast<uint32_t>(row) * static_cast<uint32_t>(G) + c * 64 + lane) * 4u;
+        wb.a[i] = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off : kOutOfRange, 0, kLoadNT));
+        wb.b[i] = as_uint4(
+            __builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off + gcnt * 16 : kOutOfRange, 0, kLoadNT));
+        wb.m[i] = __builtin_amdgcn_raw_buffer_load_b32(src.meta, ok ? moff : kOutOfRange, 0, kLoadNT);
     }
 }
 
 template <int NCH, int RG, int R, int EPI>
 __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
-    void* __restrict__ y, int y_f16, uint64_t* __restrict__ partial, uint32_t* __restrict__ counter,
-    int32_t* __restrict__ out_idx, float* __restrict__ out_val) {
+    const void* __restrict__ x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
+    uint64_t* __restrict__ partial, uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
+    float* __restrict__ out_val) {
     extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
     __shared__ float part[RG * NCH * R];
+    __shared__ float red[32];
     __shared__ uint64_t lds_keys[16];
     const int G = cols >> 6;
     const int lane = threadIdx.x & (kWave - 1);
@@ -344,14 +382,18 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const int g = c * 64 + lane;
     const bool has_group = g < G;
     const int gcnt = min(64, G - c * 64);
-    const size_t row_bytes = static_cast<size_t>(cols) >> 1;
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) >> 1;
     const int stride = gridDim.x * RG;
+    const WSrc src = make_wsrc(nib, meta, rows, cols);
 
+    // activations first, then the first two weight batches, then the staging
+    // arithmetic while the weights stream in
     WBatch<R> buf0, buf1;
     int base = blockIdx.x * RG;
-    if (base * R < rows) load_batch<R>(buf0, nib, meta, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-
-    for (int i = threadIdx.x; i < G * kStageRecord; i += blockDim.x) xs[i] = g_xstage[i];
+    stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, [&]() {
+        load_batch<R>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+    });
     __syncthreads();
     uint4 xh[8], xl[8];
     float4 gk = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -447,16 +489,19 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         }
     };
 
-    // two batches per trip so each register buffer has a fixed name
-    while (base * R < rows) {
-        const int b1 = base + stride;
-        if (b1 * R < rows) load_batch<R>(buf1, nib, meta, (b1 + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+    // two batches per trip so each register buffer has a fixed name; a buffer
+    // is refilled with the batch two strides ahead as soon as it is reduced
+    // The trip count is the grid-wide maximum (uniform, so the loop has no
+    // early exit between the two buffers): batches past the end load nothing
+    // and are skipped by process().
+    const int units = (rows + R * RG - 1) / (R * RG);
+    const int trips = (units + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+    for (int t = 0; t < trips; t += 2) {
         process(buf0, base);
-        if (b1 * R >= rows) break;
-        const int b2 = b1 + stride;
-        if (b2 * R < rows) load_batch<R>(buf0, nib, meta, (b2 + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-        process(buf1, b1);
-        base = b2;
+        load_batch<R>(buf0, src, (base + 2 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        process(buf1, base + stride);
+        load_batch<R>(buf1, src, (base + 3 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        base += 2 * stride;
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
@@ -553,26 +598,46 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
 
 constexpr int kThreads = 256;
 
+// Blocks of `fn` resident on the current device at once (occupancy x CUs),
+// cached per kernel and device.
+static int resident_blocks(const void* fn, int threads, size_t lds, int* cache) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
+    if (cache[dev] > 0) return cache[dev];
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, threads, lds) != hipSuccess) return 0;
+    cache[dev] = (per > 0 ? per : 1) * cus;
+    return cache[dev];
+}
+
 template <int NCH, int R, int EPI>
 static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     constexpr int RG = NCH == 1 ? 4 : (NCH == 4 ? 1 : 2);
     const int G = p.cols >> 6;
     if (!stage_supported(p.cols, p.pro)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(stage_x_kernel, dim3(1), dim3(kStageThreads), 0, s, p.x, p.x_f16, p.pro, p.cols);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    // buffer-resource offsets are 32-bit and kOutOfRange must lie past the end
+    if (static_cast<uint64_t>(p.rows) * static_cast<uint64_t>(p.cols / 2) >= kOutOfRange) return hipErrorInvalidValue;
     const size_t lds = static_cast<size_t>(G) * kStageRecord * sizeof(uint4);
     if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
     }
-    const int batches = (p.rows + R - 1) / R;
-    int blocks = (batches + RG - 1) / RG;
-    if (blocks > p.max_blocks) blocks = p.max_blocks;
-    if (blocks < 1) blocks = 1;
+    // Every block stages x once, so launch no more blocks than are resident at
+    // once and balance the row trips: trips = ceil(units / cap), blocks =
+    // ceil(units / trips).
+    static int resident_cache[16] = {};
+    const auto fn = reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>);
+    int cap = p.max_blocks > 0 ? p.max_blocks : resident_blocks(fn, 64 * NCH * RG, lds, resident_cache);
+    if (cap < 1) cap = 1024;
+    if (EPI == EPI_ARGMAX && cap > kArgmaxMaxBlocks) cap = kArgmaxMaxBlocks;
+    const int units = (p.rows + R * RG - 1) / (R * RG);
+    const int trips = (units + cap - 1) / cap;
+    const int blocks = trips > 0 ? (units + trips - 1) / trips : 1;
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
-                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.y, p.y_f16, p.partial,
-                       p.counter, p.out_idx, p.out_val);
+                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro, p.y,
+                       p.y_f16, p.partial, p.counter, p.out_idx, p.out_val);
     return hipGetLastError();
 }
 
@@ -593,7 +658,9 @@ static hipError_t launch_generic_t(const GemvLaunch& p, hipStream_t s) {
     const int units = (p.rows + per_unit - 1) / per_unit;
     const int nw = kThreads / kWave;
     int blocks = (units + nw - 1) / nw;
-    if (blocks > p.max_blocks) blocks = p.max_blocks;
+    const int cap = p.max_blocks > 0 ? p.max_blocks : 1024;
+    if (blocks > cap) blocks = cap;
+    if (EPI == EPI_ARGMAX && blocks > kArgmaxMaxBlocks) blocks = kArgmaxMaxBlocks;
     if (blocks < 1) blocks = 1;
     const float* sc = static_cast<const float*>(p.meta);
     const int G = (p.cols + p.group - 1) / p.group;

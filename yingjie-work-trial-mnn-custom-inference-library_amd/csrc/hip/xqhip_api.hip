@@ -41,14 +41,14 @@ int env_int(const char* name, int dflt) {
     return std::atoi(v);
 }
 
-// Blocks per GEMV launch: enough waves to cover HBM latency while each wave
-// handles several row batches, so the per-block activation staging is amortised.
+// Blocks per tiled GEMV launch: 0 lets the launcher use the device's resident
+// block count; XQHIP_GEMV_MAX_BLOCKS overrides it (launch-shape sweeps).
 int gemv_block_cap() {
-    static const int cap = env_int("XQHIP_GEMV_MAX_BLOCKS", 1024);
-    return cap > 0 ? cap : 1024;
+    static const int cap = env_int("XQHIP_GEMV_MAX_BLOCKS", 0);
+    return cap > 0 ? cap : 0;
 }
 
-constexpr int kArgmaxMaxBlocks = 2048;
+using xqhip::kArgmaxMaxBlocks;
 
 uint16_t f32_to_f16_bits(float f, bool* exact) {
     const _Float16 h = static_cast<_Float16>(f);
@@ -265,6 +265,18 @@ static int validate_prologue(const xqhip_prologue* pro, int cols, const char* wh
     return fail(XQHIP_EINVAL, "%s: bad prologue (mode %d)", who, pro->mode);
 }
 
+// The TILED64 kernels read x and the prologue vectors with 16-byte loads.
+static int validate_alignment(const xqhip_w4* w, const void* x, const xqhip_prologue* pro, const char* who) {
+    if (w->layout != XQHIP_LAYOUT_TILED64) return XQHIP_OK;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!a16(x)) return fail(XQHIP_EINVAL, "%s: x must be 16-byte aligned", who);
+    if (pro && pro->mode != XQHIP_PRO_NONE && !a16(pro->weight))
+        return fail(XQHIP_EINVAL, "%s: prologue weight must be 16-byte aligned", who);
+    if (pro && pro->mode == XQHIP_PRO_GATED_HEAD && !a16(pro->gate))
+        return fail(XQHIP_EINVAL, "%s: prologue gate must be 16-byte aligned", who);
+    return XQHIP_OK;
+}
+
 static xqhip::GemvLaunch base_launch(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro) {
     xqhip::GemvLaunch p{};
     p.nib = static_cast<const uint8_t*>(w->nib);
@@ -285,6 +297,7 @@ int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const xqhip_p
     if (int rc = validate_w4(w, "xqhip_gemv_w4a16")) return rc;
     if (int rc = validate_prologue(pro, w->cols, "xqhip_gemv_w4a16")) return rc;
     if (!x || !y) return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: null vector");
+    if (int rc = validate_alignment(w, x, pro, "xqhip_gemv_w4a16")) return rc;
     if (epilogue < XQHIP_EPI_STORE || epilogue > XQHIP_EPI_SILU_PAIR)
         return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16: unknown epilogue %d", epilogue);
     if (epilogue == XQHIP_EPI_SILU_PAIR && (w->rows % 2 != 0))
@@ -310,13 +323,14 @@ int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const 
     if (int rc = validate_prologue(pro, w->cols, "xqhip_gemv_w4a16_argmax")) return rc;
     if (!x || !workspace || !out_index || !out_value)
         return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax: null argument");
+    if (int rc = validate_alignment(w, x, pro, "xqhip_gemv_w4a16_argmax")) return rc;
     xqhip::GemvLaunch p = base_launch(w, x, x_type, pro);
     p.epi = 3;
     p.counter = static_cast<uint32_t*>(workspace);
     p.partial = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(workspace) + 256);
     p.out_idx = out_index;
     p.out_val = out_value;
-    p.max_blocks = std::min(kArgmaxMaxBlocks, gemv_block_cap());
+    p.max_blocks = gemv_block_cap() > 0 ? std::min(kArgmaxMaxBlocks, gemv_block_cap()) : 0;
     return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax launch");
 }
 

@@ -75,6 +75,22 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return t;
 }
 
+// block_sum for a block of NW waves known at compile time (no blockDim read,
+// which is a vector-memory load of the dispatch packet on this target).
+template <int NW>
+__device__ __forceinline__ float block_sum_t(float v, float* red) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += red[i];
+    return t;
+}
+
 __device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float sigmoid_dev(float x) {

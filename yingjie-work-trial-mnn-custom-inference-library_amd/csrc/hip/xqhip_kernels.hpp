@@ -33,8 +33,11 @@ struct GemvLaunch {
     uint32_t* counter;
     int32_t* out_idx;
     float* out_val;
-    int max_blocks;
+    int max_blocks;  // <= 0: as many blocks as are resident on the device at once
 };
+
+// Argmax partial keys the workspace holds (one per block).
+constexpr int kArgmaxMaxBlocks = 2048;
 
 hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s);
 
