@@ -135,10 +135,10 @@ XQHIP_API int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, con
 XQHIP_API size_t xqhip_argmax_workspace_bytes(int rows);
 /* Greedy lm_head: argmax_r (W x)[r] without materialising logits, ties to the
  * lowest row, replacing gemvW4A16ArgmaxNeon (xq_gemv_w4a16_neon.cpp:293-348)
- * and sampleGreedy (custom_model.cpp:1281-1338).  Block-level argmax, then the
- * last block to finish reduces the partials.  workspace: device memory of
- * xqhip_argmax_workspace_bytes(rows), zero-filled once before first use (the
- * kernel leaves it ready for the next call).  out_index / out_value: device. */
+ * and sampleGreedy (custom_model.cpp:1281-1338).  Every GEMV block stores its
+ * best (value, row) key in the workspace, then a one-block kernel reduces them.
+ * workspace: device memory of xqhip_argmax_workspace_bytes(rows), no
+ * initialisation needed.  out_index / out_value: device. */
 XQHIP_API int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
                                       void* workspace, int32_t* out_index, float* out_value, void* stream);
 
@@ -170,7 +170,10 @@ XQHIP_API int xqhip_attn_prep(const float* q_src, const float* k_src, const floa
 /* GQA decode over the fp16 caches for context *pos + 1 (scores, softmax and
  * V reduction of custom_model.cpp:840-928) followed by the sigmoid output gate
  * (custom_model.cpp:929-951): out = softmax(q k^T / sqrt(d)) v * sigmoid(gate).
- * workspace: xqhip_gqa_workspace_bytes(), zero-filled once before first use. */
+ * Two kernels: per-(kv head, 64-token chunk) partial softmax-attention into the
+ * workspace, then a per-query-head merge.  max_ctx <= 16384.
+ * workspace: xqhip_gqa_workspace_bytes() (sized for 16384 tokens), no
+ * initialisation needed. */
 XQHIP_API size_t xqhip_gqa_workspace_bytes(int nq, int nkv, int head_dim);
 XQHIP_API int xqhip_gqa_decode(const float* q, const void* k_cache, const void* v_cache, const float* gate, int nq,
                                int nkv, int head_dim, int max_ctx, const int32_t* pos, float* out, void* workspace,

@@ -17,10 +17,6 @@
 
 namespace xqhip {
 
-constexpr int kAttnSplits = 16;
-constexpr int kAttnMaxGroup = 8;
-constexpr int kAttnMaxSlice = 1024;  // tokens per split: context <= 16384
-
 // ---------------------------------------------------------------------------
 // embedding: bf16 row -> fp32 hidden (exact), token read from device memory.
 // ---------------------------------------------------------------------------
@@ -103,206 +99,228 @@ hipError_t launch_qk_prep(const QkPrepLaunch& p, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// GQA decode attention, split over the context.  Block (kh, split) takes the
-// `group` query heads of kv head kh over a slice of the context: scores
-// q.k/sqrt(d), a local max/sum softmax and the partial sum p*v.  The last split
-// of each kv head to finish merges the partials (rescaling by exp(m_s - m)),
-// applies the sigmoid output gate and writes the head outputs.
+// GQA decode attention in two kernels.
+//
+// gqa_chunk_kernel: block (kh, j) takes the `group` query heads of kv head kh
+// over the 64-token chunks j, j + gridDim.y, ... of the context: scores
+// q.k/sqrt(d), the chunk's max m and sum l of exp(s - m), and the unnormalised
+// sum of exp(s - m) v, written to the workspace per (head, chunk).
+// gqa_combine_kernel: one block per query head merges the chunks of the
+// context (weights exp(m_c - M)), normalises, applies the sigmoid output gate.
+// The kernel boundary orders the two, so no block waits on another and no
+// grid-wide fence is needed.
 // ---------------------------------------------------------------------------
+constexpr int kAttnChunk = 64;
+constexpr int kAttnMaxGroup = 8;
+constexpr int kAttnMaxCtx = 16384;
+constexpr int kAttnMaxChunks = kAttnMaxCtx / kAttnChunk;
+constexpr int kAttnGridChunks = 64;  // chunk slots per kv head in the grid
+constexpr int kAttnThreads = 256;
 
-// Partial softmax-attention of `group` query heads over tokens [t0, t0+n) of one
-// kv head.  Scores: 8 lanes per token, each lane owning HD/8 consecutive dims
-// (16-byte loads); the 8 partial dots of every query head are summed across the
-// 8 lanes.  V: each lane owns HD/64 dims of all heads for a quarter of the
-// tokens; the quarters are summed through LDS.  HD == 0: any head_dim
-// (scalar loads, tiny shapes).
 template <int HD>
-__device__ void gqa_slice(const GqaLaunch& p, int kh, int t0, int n, int group, int hd, float* qs, float* sc, float* ml,
-                          float* vpart) {
+__device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, int t0, int n, int group, int hd,
+                                          const float* qs, float* sc, float* vred) {
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
-    const int per_stride = blockDim.x / 8;  // tokens per pass
+    const int qh0 = kh * group;
+    // scores: 4 lanes per token, each lane HD/4 consecutive dims (16-byte loads)
     if constexpr (HD > 0) {
-        constexpr int DL = HD / 8;  // dims per lane
-        const int sub = threadIdx.x & 7;
-        for (int tt = threadIdx.x / 8; tt < ((n + per_stride - 1) / per_stride) * per_stride; tt += per_stride) {
-            const bool valid = tt < n;
-            float kv[DL];
-            if (valid) {
-                const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + tt) * p.nkv + kh) * HD + sub * DL;
+        constexpr int DL = HD / 4;
+        const int sub = threadIdx.x & 3, tt = threadIdx.x >> 2;
+        const bool valid = tt < n;
+        const _Float16* krow =
+            p.k_cache + (static_cast<size_t>(t0 + (valid ? tt : 0)) * p.nkv + kh) * HD + sub * DL;
+        float kv[DL];
 #pragma unroll
-                for (int u = 0; u < DL / 8; ++u) {
-                    const uint4 w = *reinterpret_cast<const uint4*>(krow + 8 * u);
-                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        for (int u = 0; u < DL / 8; ++u) {
+            const uint4 w = *reinterpret_cast<const uint4*>(krow + 8 * u);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kv[8 * u + 2 * e] = half_lo(ww[e]);
-                        kv[8 * u + 2 * e + 1] = half_hi(ww[e]);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int d = 0; d < DL; ++d) kv[d] = 0.0f;
-            }
-            for (int g = 0; g < group; ++g) {
-                const float* qv = qs + g * HD + sub * DL;
-                float dot = 0.0f;
-#pragma unroll
-                for (int d = 0; d < DL; ++d) dot += qv[d] * kv[d];
-                dot += __shfl_xor(dot, 1, kWave);
-                dot += __shfl_xor(dot, 2, kWave);
-                dot += __shfl_xor(dot, 4, kWave);
-                if (valid && sub == 0) sc[g * p.slice + tt] = dot * rscale;
+            for (int e = 0; e < 4; ++e) {
+                kv[8 * u + 2 * e] = half_lo(ww[e]);
+                kv[8 * u + 2 * e + 1] = half_hi(ww[e]);
             }
         }
+        for (int g = 0; g < group; ++g) {
+            const float* qv = qs + g * HD + sub * DL;
+            float dot = 0.0f;
+#pragma unroll
+            for (int d = 0; d < DL; ++d) dot += qv[d] * kv[d];
+            dot += __shfl_xor(dot, 1, kWave);
+            dot += __shfl_xor(dot, 2, kWave);
+            if (valid && sub == 0) sc[g * kAttnChunk + tt] = dot * rscale;
+        }
     } else {
-        for (int pr = threadIdx.x; pr < n * group; pr += blockDim.x) {
+        for (int pr = threadIdx.x; pr < n * group; pr += kAttnThreads) {
             const int t = pr / group, g = pr % group;
             const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * hd;
             float dot = 0.0f;
             for (int d = 0; d < hd; ++d) dot += qs[g * hd + d] * static_cast<float>(krow[d]);
-            sc[g * p.slice + t] = dot * rscale;
+            sc[g * kAttnChunk + t] = dot * rscale;
         }
     }
     __syncthreads();
-    for (int g = wid; g < group; g += blockDim.x / kWave) {
-        float m = -INFINITY;
-        for (int t = lane; t < n; t += kWave) m = fmaxf(m, sc[g * p.slice + t]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int t = lane; t < n; t += kWave) {
-            const float e = expf(sc[g * p.slice + t] - m);
-            sc[g * p.slice + t] = e;
-            l += e;
-        }
-        l = wave_sum(l);
+    // chunk softmax statistics: one wave per head, one lane per token
+    for (int g = wid; g < group; g += kAttnThreads / kWave) {
+        const float sv = lane < n ? sc[g * kAttnChunk + lane] : -INFINITY;
+        const float m = wave_max(sv);
+        const float e = lane < n ? expf(sv - m) : 0.0f;
+        const float l = wave_sum(e);
+        sc[g * kAttnChunk + lane] = e;
         if (lane == 0) {
-            ml[2 * g] = m;
-            ml[2 * g + 1] = l;
+            p.part_m[(qh0 + g) * kAttnMaxChunks + ch] = m;
+            p.part_l[(qh0 + g) * kAttnMaxChunks + ch] = l;
         }
     }
     __syncthreads();
-    const int quarters = blockDim.x / kWave;  // token groups
-    for (int d0 = lane; d0 < hd; d0 += kWave) {  // this lane's dims: d0, d0 + 64, ...
-        float o[kAttnMaxGroup];
-#pragma unroll
-        for (int g = 0; g < kAttnMaxGroup; ++g) o[g] = 0.0f;
-        for (int t = wid; t < n; t += quarters) {
-            const float vv = static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d0]);
-#pragma unroll
-            for (int g = 0; g < kAttnMaxGroup; ++g)
-                if (g < group) o[g] += sc[g * p.slice + t] * vv;
-        }
+    // sum_t e_t v_t: 16-byte loads of v, HD/8 lanes per token
+    if constexpr (HD > 0) {
+        constexpr int LPT = HD / 8;
+        constexpr int TPP = kAttnThreads / LPT;
+        const int dsl = threadIdx.x % LPT, ts = threadIdx.x / LPT;
+        float o[kAttnMaxGroup][8];
 #pragma unroll
         for (int g = 0; g < kAttnMaxGroup; ++g)
-            if (g < group) vpart[(wid * group + g) * hd + d0] = o[g];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+        for (int t = ts; t < n; t += TPP) {
+            const uint4 w =
+                *reinterpret_cast<const uint4*>(p.v_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * HD + dsl * 8);
+            const float vv[8] = {half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y),
+                                 half_lo(w.z), half_hi(w.z), half_lo(w.w), half_hi(w.w)};
+#pragma unroll
+            for (int g = 0; g < kAttnMaxGroup; ++g) {
+                if (g < group) {
+                    const float pr = sc[g * kAttnChunk + t];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[g][e] += pr * vv[e];
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kAttnMaxGroup; ++g) {
+            if (g < group) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+#pragma unroll
+                    for (int m = LPT; m < kWave; m <<= 1) o[g][e] += __shfl_xor(o[g][e], m, kWave);
+                }
+            }
+        }
+        if (lane < LPT) {
+#pragma unroll
+            for (int g = 0; g < kAttnMaxGroup; ++g)
+                if (g < group)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) vred[(wid * group + g) * HD + dsl * 8 + e] = o[g][e];
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < group * HD; i += kAttnThreads) {
+            const int g = i / HD, d = i % HD;
+            float acc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kAttnThreads / kWave; ++w) acc += vred[(w * group + g) * HD + d];
+            p.part_o[(static_cast<size_t>(qh0 + g) * kAttnMaxChunks + ch) * HD + d] = acc;
+        }
+    } else {
+        for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) {
+            const int g = i / hd, d = i % hd;
+            float acc = 0.0f;
+            for (int t = 0; t < n; ++t)
+                acc += sc[g * kAttnChunk + t] *
+                       static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d]);
+            p.part_o[(static_cast<size_t>(qh0 + g) * kAttnMaxChunks + ch) * hd + d] = acc;
+        }
     }
-    __syncthreads();
+    __syncthreads();  // sc and vred are reused by the block's next chunk
 }
 
-__global__ void __launch_bounds__(256) gqa_decode_kernel(GqaLaunch p) {
+template <int HD>
+__global__ void __launch_bounds__(kAttnThreads) gqa_chunk_kernel(GqaLaunch p) {
     extern __shared__ float smem[];
-    const int hd = p.head_dim;
+    const int hd = HD > 0 ? HD : p.head_dim;
     const int group = p.nq / p.nkv;
     const int kh = blockIdx.x;
-    const int split = blockIdx.y;
     const int ctx = *p.pos + 1;
-    const int per = (ctx + kAttnSplits - 1) / kAttnSplits;
-    const int t0 = split * per;
-    const int n = max(0, min(ctx, t0 + per) - t0);
-    float* qs = smem;                              // [group][hd]
-    float* sc = qs + group * hd;                   // [group][slice]
-    float* ml = sc + group * p.slice;              // [group][2]
-    float* vpart = ml + 2 * group;                 // [4][group][hd]
-    __shared__ int is_last;
+    if (static_cast<int>(blockIdx.y) * kAttnChunk >= ctx) return;  // whole block: nothing to do
+    float* qs = smem;                       // [group][hd]
+    float* sc = qs + group * hd;            // [group][64]
+    float* vred = sc + group * kAttnChunk;  // [4 waves][group][hd]
+    for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) qs[i] = p.q[static_cast<size_t>(kh) * group * hd + i];
+    __syncthreads();
+    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
+    for (int ch = blockIdx.y; ch < nch; ch += gridDim.y) {
+        const int t0 = ch * kAttnChunk;
+        const int n = min(kAttnChunk, ctx - t0);
+        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred);
+    }
+}
 
-    for (int i = threadIdx.x; i < group * hd; i += blockDim.x)
-        qs[i] = p.q[static_cast<size_t>(kh * group + i / hd) * hd + (i % hd)];
+__global__ void __launch_bounds__(256) gqa_combine_kernel(GqaLaunch p) {
+    __shared__ float wgt[kAttnMaxChunks];
+    __shared__ float red[32];
+    const int qh = blockIdx.x;
+    const int hd = p.head_dim;
+    const int ctx = *p.pos + 1;
+    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
+    const float* pm = p.part_m + static_cast<size_t>(qh) * kAttnMaxChunks;
+    const float* pl = p.part_l + static_cast<size_t>(qh) * kAttnMaxChunks;
+    float m = -INFINITY;
+    for (int c = threadIdx.x; c < nch; c += blockDim.x) m = fmaxf(m, pm[c]);
+    m = wave_max(m);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    if (lane == 0) red[wid] = m;
     __syncthreads();
-    if (hd == 128)
-        gqa_slice<128>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
-    else if (hd == 256)
-        gqa_slice<256>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
-    else if (hd == 64)
-        gqa_slice<64>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
-    else
-        gqa_slice<0>(p, kh, t0, n, group, hd, qs, sc, ml, vpart);
-    const int qh0 = kh * group;
-    const int quarters = blockDim.x / kWave;
-    for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
-        const int g = i / hd, d = i % hd;
+    float mm = -INFINITY;
+    for (int i = 0; i < static_cast<int>(blockDim.x) / kWave; ++i) mm = fmaxf(mm, red[i]);
+    __syncthreads();
+    float l = 0.0f;
+    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
+        const float f = expf(pm[c] - mm);
+        wgt[c] = f;
+        l += pl[c] * f;
+    }
+    l = block_sum(l, red);  // also orders the wgt writes before the reads below
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float* po = p.part_o + static_cast<size_t>(qh) * kAttnMaxChunks * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
         float o = 0.0f;
-        for (int w = 0; w < quarters; ++w) o += vpart[(w * group + g) * hd + d];
-        p.part_o[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * hd + d] = o;
-    }
-    for (int g = threadIdx.x; g < group; g += blockDim.x) {
-        p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2] = ml[2 * g];
-        p.part_ml[(static_cast<size_t>(qh0 + g) * kAttnSplits + split) * 2 + 1] = (n > 0) ? ml[2 * g + 1] : 0.0f;
-    }
-    // every wave's partial stores have completed at L2 before wave 0 releases
-    // them (one agent-scope fence per block: it writes back the XCD's L2)
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t ticket = atomicAdd(&p.counters[kh], 1u);
-        is_last = ticket == kAttnSplits - 1;
-        if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    __syncthreads();
-    if (!is_last) return;
-    for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
-        const int g = i / hd, d = i % hd;
-        const size_t base = static_cast<size_t>(qh0 + g) * kAttnSplits;
-        float mm = -INFINITY;
-        for (int s2 = 0; s2 < kAttnSplits; ++s2)
-            mm = fmaxf(mm, __hip_atomic_load(&p.part_ml[(base + s2) * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        float l = 0.0f, o = 0.0f;
-        for (int s2 = 0; s2 < kAttnSplits; ++s2) {
-            const float ms = __hip_atomic_load(&p.part_ml[(base + s2) * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float ls =
-                __hip_atomic_load(&p.part_ml[(base + s2) * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (ls == 0.0f) continue;
-            const float f = expf(ms - mm);
-            l += ls * f;
-            o += __hip_atomic_load(&p.part_o[(base + s2) * hd + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * f;
-        }
-        const size_t oi = static_cast<size_t>(qh0 + g) * hd + d;
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        for (int c = 0; c < nch; ++c) o += po[static_cast<size_t>(c) * hd + d] * wgt[c];
+        const size_t oi = static_cast<size_t>(qh) * hd + d;
         p.out[oi] = (o * inv) * sigmoid_dev(p.gate[oi]);
     }
-    if (threadIdx.x == 0) p.counters[kh] = 0u;
 }
 
 size_t gqa_workspace_bytes(int nq, int nkv, int head_dim) {
-    return 256 + sizeof(uint32_t) * static_cast<size_t>(nkv) +
-           sizeof(float) * static_cast<size_t>(nq) * kAttnSplits * (head_dim + 2);
+    (void)nkv;
+    return sizeof(float) * static_cast<size_t>(nq) * kAttnMaxChunks * (head_dim + 2);
 }
 
-static size_t gqa_lds_bytes(int group, int head_dim, int slice) {
-    return sizeof(float) * (static_cast<size_t>(group) * head_dim + static_cast<size_t>(group) * slice + 2 * group +
-                            4 * static_cast<size_t>(group) * head_dim);
+static size_t gqa_lds_bytes(int group, int head_dim) {
+    return sizeof(float) * (static_cast<size_t>(group) * head_dim + static_cast<size_t>(group) * kAttnChunk +
+                            (kAttnThreads / kWave) * static_cast<size_t>(group) * head_dim);
 }
 
-hipError_t launch_gqa(const GqaLaunch& p0, hipStream_t s) {
-    GqaLaunch p = p0;
+hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
     const int group = p.nq / p.nkv;
-    p.slice = (p.max_ctx + kAttnSplits - 1) / kAttnSplits;
-    const size_t lds = gqa_lds_bytes(group, p.head_dim, p.slice);
-    if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gqa_decode_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (e != hipSuccess) return e;
+    const size_t lds = gqa_lds_bytes(group, p.head_dim);
+    const int slots = min(kAttnGridChunks, (p.max_ctx + kAttnChunk - 1) / kAttnChunk);
+    const dim3 grid(p.nkv, slots);
+    switch (p.head_dim) {
+        case 64: hipLaunchKernelGGL(gqa_chunk_kernel<64>, grid, dim3(kAttnThreads), lds, s, p); break;
+        case 128: hipLaunchKernelGGL(gqa_chunk_kernel<128>, grid, dim3(kAttnThreads), lds, s, p); break;
+        case 256: hipLaunchKernelGGL(gqa_chunk_kernel<256>, grid, dim3(kAttnThreads), lds, s, p); break;
+        default: hipLaunchKernelGGL(gqa_chunk_kernel<0>, grid, dim3(kAttnThreads), lds, s, p); break;
     }
-    hipLaunchKernelGGL(gqa_decode_kernel, dim3(p.nkv, kAttnSplits), dim3(256), lds, s, p);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL(gqa_combine_kernel, dim3(p.nq), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx) {
     if (nkv <= 0 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || head_dim <= 0) return false;
-    const int per_max = (max_ctx + kAttnSplits - 1) / kAttnSplits;
-    if (per_max > kAttnMaxSlice) return false;
-    return gqa_lds_bytes(nq / nkv, head_dim, per_max) <= 160 * 1024;
+    if (max_ctx < 1 || max_ctx > kAttnMaxCtx) return false;
+    return gqa_lds_bytes(nq / nkv, head_dim) <= 64 * 1024;
 }
 
 // ---------------------------------------------------------------------------

@@ -276,36 +276,33 @@ __device__ __forceinline__ void dot8(uint32_t w, uint4 xh, uint4 xl, float& dh, 
     dl = dot2(p3, as_h2(xl.w), dl);
 }
 
-// Final argmax over per-block partial keys; run by the last block to finish.
-__device__ void finish_argmax(uint64_t block_best, uint64_t* partial, uint32_t* counter, int32_t* out_idx,
-                              float* out_val, uint64_t* lds_keys) {
-    __shared__ int is_last;
-    // One release (L2 write-back) per block and one acquire in the last block:
-    // an agent-scope fence costs a whole-L2 write-back/invalidate on this part,
-    // so it is issued by a single wave, never by every wave of the block.
-    if (threadIdx.x == 0) {
-        partial[blockIdx.x] = block_best;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t ticket = atomicAdd(counter, 1u);
-        is_last = (ticket == gridDim.x - 1) ? 1 : 0;
-        if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    __syncthreads();
-    if (!is_last) return;
+// Greedy argmax in two kernels: every GEMV block stores its best (value, row)
+// key, then argmax_finish_kernel reduces the keys.  The kernel boundary orders
+// the two (no grid-wide fence, no completion counter).
+__device__ __forceinline__ void store_block_key(uint64_t block_best, uint64_t* partial) {
+    if (threadIdx.x == 0) partial[blockIdx.x] = block_best;
+}
+
+__global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __restrict__ partial, int n,
+                                                            int32_t* __restrict__ out_idx,
+                                                            float* __restrict__ out_val) {
+    __shared__ uint64_t keys[4];
     uint64_t best = 0;
-    for (int i = threadIdx.x; i < static_cast<int>(gridDim.x); i += blockDim.x)
-        best = u64_max(best, __hip_atomic_load(&partial[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    for (int i = threadIdx.x; i < n; i += 256) best = u64_max(best, partial[i]);
     best = wave_max_u64(best);
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    if (lane == 0) lds_keys[wid] = best;
+    if (lane == 0) keys[wid] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t b = 0;
-        for (int i = 0; i < static_cast<int>(blockDim.x / kWave); ++i) b = u64_max(b, lds_keys[i]);
+        const uint64_t b = u64_max(u64_max(keys[0], keys[1]), u64_max(keys[2], keys[3]));
         *out_idx = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(b));
         *out_val = float_from_order_key(static_cast<uint32_t>(b >> 32));
-        *counter = 0u;  // ready for the next call (no host-side clear needed)
     }
+}
+
+static hipError_t launch_argmax_finish(const GemvLaunch& p, int blocks, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, s, p.partial, blocks, p.out_idx, p.out_val);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -368,8 +365,7 @@ template <int NCH, int RG, int R, int EPI>
 __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
     const void* __restrict__ x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
-    uint64_t* __restrict__ partial, uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
-    float* __restrict__ out_val) {
+    uint64_t* __restrict__ partial) {
     extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
     __shared__ float part[RG * NCH * R];
     __shared__ float red[32];
@@ -511,7 +507,7 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         if (threadIdx.x == 0)
             for (int i = 0; i < NCH * RG; ++i) b = u64_max(b, lds_keys[i]);
         __syncthreads();
-        finish_argmax(b, partial, counter, out_idx, out_val, lds_keys);
+        store_block_key(b, partial);
     }
 }
 
@@ -526,9 +522,7 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
                                                        const float* __restrict__ zeros, int rows, int cols,
                                                        int group, int affine, const void* __restrict__ x, int x_f16,
                                                        Prologue pro, void* __restrict__ y, int y_f16,
-                                                       uint64_t* __restrict__ partial,
-                                                       uint32_t* __restrict__ counter, int32_t* __restrict__ out_idx,
-                                                       float* __restrict__ out_val) {
+                                                       uint64_t* __restrict__ partial) {
     __shared__ float red[32];
     __shared__ uint64_t lds_keys[16];
     __shared__ float inv_lds[kMaxNormHeads];
@@ -588,7 +582,7 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
         if (threadIdx.x == 0)
             for (int i = 0; i < nw; ++i) b = u64_max(b, lds_keys[i]);
         __syncthreads();
-        finish_argmax(b, partial, counter, out_idx, out_val, lds_keys);
+        store_block_key(b, partial);
     }
 }
 
@@ -637,8 +631,9 @@ static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     const int blocks = trips > 0 ? (units + trips - 1) / trips : 1;
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
                        static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro, p.y,
-                       p.y_f16, p.partial, p.counter, p.out_idx, p.out_val);
-    return hipGetLastError();
+                       p.y_f16, p.partial);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    return EPI == EPI_ARGMAX ? launch_argmax_finish(p, blocks, s) : hipSuccess;
 }
 
 template <int NCH>
@@ -666,9 +661,9 @@ static hipError_t launch_generic_t(const GemvLaunch& p, hipStream_t s) {
     const int G = (p.cols + p.group - 1) / p.group;
     const float* zr = sc + static_cast<size_t>(p.rows) * G;
     hipLaunchKernelGGL((gemv_w4_generic<EPI>), dim3(blocks), dim3(kThreads), 0, s, p.nib, sc, zr, p.rows, p.cols,
-                       p.group, p.affine, p.x, p.x_f16, p.pro, p.y, p.y_f16, p.partial, p.counter,
-                       p.out_idx, p.out_val);
-    return hipGetLastError();
+                       p.group, p.affine, p.x, p.x_f16, p.pro, p.y, p.y_f16, p.partial);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    return EPI == EPI_ARGMAX ? launch_argmax_finish(p, blocks, s) : hipSuccess;
 }
 
 hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s) {

@@ -314,7 +314,7 @@ int xqhip_gemv_w4a16(const xqhip_w4* w, const void* x, int x_type, const xqhip_p
 
 size_t xqhip_argmax_workspace_bytes(int rows) {
     (void)rows;
-    return 256 + sizeof(uint64_t) * kArgmaxMaxBlocks;
+    return sizeof(uint64_t) * kArgmaxMaxBlocks;
 }
 
 int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro, void* workspace,
@@ -326,8 +326,7 @@ int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const 
     if (int rc = validate_alignment(w, x, pro, "xqhip_gemv_w4a16_argmax")) return rc;
     xqhip::GemvLaunch p = base_launch(w, x, x_type, pro);
     p.epi = 3;
-    p.counter = static_cast<uint32_t*>(workspace);
-    p.partial = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(workspace) + 256);
+    p.partial = static_cast<uint64_t*>(workspace);
     p.out_idx = out_index;
     p.out_val = out_value;
     p.max_blocks = gemv_block_cap() > 0 ? std::min(kArgmaxMaxBlocks, gemv_block_cap()) : 0;
@@ -404,11 +403,12 @@ int xqhip_gqa_decode(const float* q, const void* k_cache, const void* v_cache, c
     p.max_ctx = max_ctx;
     p.pos = pos;
     p.out = out;
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    p.counters = reinterpret_cast<uint32_t*>(ws);
-    float* f = reinterpret_cast<float*>(ws + 256 + sizeof(uint32_t) * static_cast<size_t>(nkv));
-    p.part_ml = f;
-    p.part_o = f + static_cast<size_t>(nq) * 16 * 2;
+    // workspace: part_m [nq][256], part_l [nq][256], part_o [nq][256][head_dim]
+    float* f = static_cast<float*>(workspace);
+    const size_t per = xqhip::gqa_workspace_bytes(nq, nkv, head_dim) / sizeof(float) / (head_dim + 2);
+    p.part_m = f;
+    p.part_l = f + per;
+    p.part_o = f + 2 * per;
     return check(xqhip::launch_gqa(p, as_stream(stream)), "gqa launch");
 }
 

@@ -29,8 +29,7 @@ struct GemvLaunch {
     void* y;
     int y_f16;
     int epi;  // 0 store, 1 add, 2 silu pair, 3 argmax
-    uint64_t* partial;
-    uint32_t* counter;
+    uint64_t* partial;  // argmax: one key per block
     int32_t* out_idx;
     float* out_val;
     int max_blocks;  // <= 0: as many blocks as are resident on the device at once
@@ -73,12 +72,11 @@ struct GqaLaunch {
     const _Float16* v_cache;
     const float* gate;
     int nq, nkv, head_dim, max_ctx;
-    int slice;  // LDS score row length (set by the launcher)
     const int32_t* pos;
     float* out;
-    uint32_t* counters;
-    float* part_o;
-    float* part_ml;
+    float* part_m;  // workspace: [nq][max chunks] chunk max
+    float* part_l;  //            [nq][max chunks] chunk sum of exp
+    float* part_o;  //            [nq][max chunks][head_dim] unnormalised output
 };
 size_t gqa_workspace_bytes(int nq, int nkv, int head_dim);
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx);
