@@ -1,6 +1,6 @@
 /* xqwen35.h - the public C ABI of the decode library, byte-compatible with the
  * reference's customlib/include/xqwen35.h (status codes :21-28, xq_options
- * :30-40, xq_metrics :42-58, the 16 entry points :60-77), so an existing caller
+ * :30-40, xq_metrics :42-58, the entry points :60-77), so an existing caller
  * (benchmark harness, quality runner, tests) links against this library
  * unchanged.  Behind it, the model runs device-resident on an MI355X through
  * the hand-written gfx950 kernels of libxqhip.so.
