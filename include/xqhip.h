@@ -191,6 +191,17 @@ XQHIP_API int xqhip_linear_conv(const float* mixed, float* conv_state, const flo
 XQHIP_API int xqhip_gated_delta(const float* conv, const float* a, const float* b, const float* a_log,
                                 const float* dt_bias, float* state, int lk_n, int lv_n, int lk_hd, int lv_hd,
                                 float* out, void* stream);
+/* One decode step of the linear-attention state update in a single kernel:
+ * conv1d + SiLU with L2-normalised q/k heads (as xqhip_linear_conv) feeding the
+ * gated delta rule (as xqhip_gated_delta), custom_model.cpp:961-1096.
+ * conv_state holds TWO copies of the [conv_dim][ksize-1] history: copy
+ * (*pos & 1) is read and copy ((*pos + 1) & 1) written, so consecutive
+ * positions alternate (zero both copies to reset).  mixed: conv_dim channels
+ * (q | k | v); a, b: lv_n gate inputs; out: lv_n * lv_hd. */
+XQHIP_API int xqhip_linear_attn_step(const float* mixed, float* conv_state, const float* conv_w, const float* a,
+                                     const float* b, const float* a_log, const float* dt_bias, float* state, int lk_n,
+                                     int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos, float* out,
+                                     void* stream);
 /* y = x * inv * w (rmsnormReference, ref_rmsnorm.cpp:8-17). */
 XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream);
 

@@ -221,6 +221,70 @@ def test_linear_conv_and_gated_delta(shape):
     close(Sd.download(np.float32, S0.size), S_o, "gated delta state", atol=1e-5, rtol=1e-4)
 
 
+def oracle_linear_step(mixed, st, cw, a, b, a_log, dt, S, shape):
+    """conv1d + SiLU + q/k L2 norm + gated delta for one position, in place on st and S."""
+    lk_n, lv_n, lk_hd, lv_hd, ks = shape
+    conv_dim = mixed.size
+    conv_o = np.empty(conv_dim, np.float32)
+    O().orc_conv1d_step(ob.p(mixed), ob.p(st), ob.p(cw), conv_dim, ks, ob.p(conv_o))
+    qv = conv_o[: lk_n * lk_hd].copy()
+    kv = conv_o[lk_n * lk_hd: 2 * lk_n * lk_hd].copy()
+    O().orc_l2norm_heads(ob.p(qv), lk_n, lk_hd)
+    O().orc_l2norm_heads(ob.p(kv), lk_n, lk_hd)
+    out = np.zeros(lv_n * lv_hd, np.float32)
+    factor = max(1, lv_n // max(1, lk_n))
+    for vh in range(lv_n):
+        kh = min(lk_n - 1, vh // factor)
+        beta = O().orc_sigmoid(float(b[vh]))
+        gate = np.float32(-np.exp(np.float32(a_log[vh]))) * np.float32(O().orc_softplus(float(a[vh] + dt[vh])))
+        qh = np.ascontiguousarray(qv[kh * lk_hd:(kh + 1) * lk_hd])
+        kh_v = np.ascontiguousarray(kv[kh * lk_hd:(kh + 1) * lk_hd])
+        vv = np.ascontiguousarray(conv_o[2 * lk_n * lk_hd + vh * lv_hd: 2 * lk_n * lk_hd + (vh + 1) * lv_hd])
+        Sv = np.ascontiguousarray(S[vh * lk_hd * lv_hd:(vh + 1) * lk_hd * lv_hd])
+        ov = np.zeros(lv_hd, np.float32)
+        O().orc_gated_delta(ob.p(qh), ob.p(kh_v), ob.p(vv), beta, float(gate), lk_hd, lv_hd, ob.p(Sv), ob.p(ov))
+        S[vh * lk_hd * lv_hd:(vh + 1) * lk_hd * lv_hd] = Sv
+        out[vh * lv_hd:(vh + 1) * lv_hd] = ov
+    return out
+
+
+@pytest.mark.parametrize("shape", [(16, 32, 128, 128, 4), (1, 2, 2, 2, 2), (3, 6, 64, 32, 3), (2, 2, 256, 40, 4)])
+def test_fused_linear_attn_step_two_positions(shape):
+    """xqhip_linear_attn_step against the oracle's conv + L2 norm + gated delta on
+    two consecutive positions, which exercises both halves of the parity-
+    double-buffered conv history."""
+    lk_n, lv_n, lk_hd, lv_hd, ks = shape
+    rng = np.random.default_rng(21)
+    mixed0, cstate, cw = linear_inputs(lk_n, lv_n, lk_hd, lv_hd, ks, seed=31)
+    mixed1 = rng.normal(0, 1, mixed0.size).astype(np.float32)
+    hist = cstate.size
+    beta_t = rng.uniform(0, 1, lv_n)
+    b = np.log(beta_t / (1 - beta_t)).astype(np.float32)
+    a = rng.normal(0, 1, lv_n).astype(np.float32)
+    a_log = rng.normal(-1, 0.5, lv_n).astype(np.float32)
+    dt = rng.normal(0, 0.5, lv_n).astype(np.float32)
+    S0 = rng.normal(0, 0.1, lv_n * lk_hd * lv_hd).astype(np.float32)
+    st_o, S_o = cstate.copy(), S0.copy()
+    want0 = oracle_linear_step(mixed0, st_o, cw, a, b, a_log, dt, S_o, shape)
+    want1 = oracle_linear_step(mixed1, st_o, cw, a, b, a_log, dt, S_o, shape)
+    pos = 5  # odd: the first step reads copy 1
+    two = np.concatenate([np.full(hist, 777.0, np.float32), cstate])
+    sd, Sd, wd = dev(two), dev(S0), dev(cw)
+    ad, bd, ald, dtd = dev(a), dev(b), dev(a_log), dev(dt)
+    outs = []
+    for step, mixed in enumerate([mixed0, mixed1]):
+        md, pd = dev(mixed), dev(np.array([pos + step], np.int32))
+        od = xb.DeviceBuffer(lv_n * lv_hd * 4)
+        xb.ck(xb.hip().xqhip_linear_attn_step(md.ptr, sd.ptr, wd.ptr, ad.ptr, bd.ptr, ald.ptr, dtd.ptr, Sd.ptr, lk_n,
+                                              lk_hd, lv_n, lv_hd, ks, pd.ptr, od.ptr, None))
+        outs.append(od.download(np.float32, lv_n * lv_hd))
+    close(outs[0], want0, "fused linear step, first position", atol=1e-4, rtol=1e-4)
+    close(outs[1], want1, "fused linear step, second position", atol=1e-4, rtol=1e-4)
+    close(Sd.download(np.float32, S0.size), S_o, "fused linear step state", atol=1e-5, rtol=1e-4)
+    got_hist = sd.download(np.float32, 2 * hist)
+    assert np.array_equal(got_hist[hist:], st_o)  # the second step wrote copy 1 again; shifts are exact
+
+
 def test_rmsnorm_kernel():
     rng = np.random.default_rng(3)
     x = rng.normal(0, 5, 4096).astype(np.float32)

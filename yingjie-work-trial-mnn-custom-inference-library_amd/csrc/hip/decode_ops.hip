@@ -462,6 +462,130 @@ hipError_t launch_delta(const DeltaLaunch& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Fused linear-attention step: block (vh, column slice) recomputes the conv1d +
+// SiLU + L2 norm of its key head's q and k channels (cheap: 2 * lk_hd channels
+// of ksize taps), the conv of its own kDeltaCols value channels, then runs the
+// gated delta update of gated_delta_kernel on those columns.  Conv history is
+// double-buffered by position parity (read copy pos & 1, write the other): the
+// q/k history is written by one block per key head (vh % factor == 0, first
+// slice), the value history by the block that owns the channel.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
+    __shared__ float qk[2 * 256];
+    __shared__ float vsh[kDeltaCols];
+    __shared__ float colsum[4][kDeltaCols];
+    __shared__ float red[2][4];
+    const int vh = blockIdx.x;
+    const int j0 = blockIdx.y * kDeltaCols;
+    const int factor = max(1, p.lv_n / max(1, p.lk_n));
+    const int kh = min(p.lk_n - 1, vh / factor);
+    const int dk = p.lk_hd, dv = p.lv_hd;
+    const int hist = max(0, p.ksize - 1);
+    const int conv_dim = 2 * p.lk_n * dk + p.lv_n * dv;
+    const int par = *p.pos & 1;
+    const float* st_in = p.conv_state + static_cast<size_t>(par) * conv_dim * hist;
+    float* st_out = p.conv_state + static_cast<size_t>(par ^ 1) * conv_dim * hist;
+    const bool qk_writer = (vh % factor == 0) && blockIdx.y == 0;
+    const int jl = threadIdx.x % kDeltaCols;
+    const int ig = threadIdx.x / kDeltaCols;
+    const int j = j0 + jl;
+    const bool active = j < dv;
+    float* S = p.state + static_cast<size_t>(vh) * dk * dv;
+    float sreg[kDeltaMaxKPerThread];
+#pragma unroll
+    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {  // state loads first: they depend on nothing
+        const int i = ig + r * kDeltaIGroups;
+        sreg[r] = (active && i < dk) ? S[static_cast<size_t>(i) * dv + j] : 0.0f;
+    }
+    auto conv = [&](int c, bool write) {
+        const float* st = st_in + static_cast<size_t>(c) * hist;
+        const float* w = p.conv_w + static_cast<size_t>(c) * p.ksize;
+        float acc = 0.0f;
+        for (int t = 0; t < hist; ++t) acc += st[t] * w[t];
+        const float xv = p.mixed[c];
+        acc += xv * w[hist];
+        if (write && hist > 0) {
+            float* so = st_out + static_cast<size_t>(c) * hist;
+            for (int t = 0; t + 1 < hist; ++t) so[t] = st[t + 1];
+            so[hist - 1] = xv;
+        }
+        return silu_dev(acc);
+    };
+    // q and k channels of key head kh: thread t < dk -> q[t], dk <= t < 2 dk -> k[t - dk]
+    float ssq = 0.0f, ssk = 0.0f;
+    for (int t = threadIdx.x; t < 2 * dk; t += blockDim.x) {
+        const bool is_k = t >= dk;
+        const int d = is_k ? t - dk : t;
+        const int c = (is_k ? p.lk_n * dk : 0) + kh * dk + d;
+        const float y = conv(c, qk_writer);
+        qk[(is_k ? 256 : 0) + d] = y;
+        if (is_k) ssk += y * y; else ssq += y * y;
+    }
+    if (threadIdx.x < kDeltaCols && j0 + threadIdx.x < dv)
+        vsh[threadIdx.x] = conv(2 * p.lk_n * dk + vh * dv + j0 + threadIdx.x, true);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    ssq = wave_sum(ssq);
+    ssk = wave_sum(ssk);
+    if (lane == 0) {
+        red[0][wid] = ssq;
+        red[1][wid] = ssk;
+    }
+    const float beta = sigmoid_dev(p.b[vh]);
+    const float gate = -expf(p.a_log[vh]) * softplus_dev(p.a[vh] + p.dt_bias[vh]);
+    const float decay = expf(gate);
+    __syncthreads();
+    // l2NormalizeHeads: x * 1/sqrt(sum x^2 + 1e-6)
+    const float invq = 1.0f / sqrtf(red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1.0e-6f);
+    const float invk = 1.0f / sqrtf(red[1][0] + red[1][1] + red[1][2] + red[1][3] + 1.0e-6f);
+    const float vj = active ? vsh[jl] : 0.0f;
+    float pred = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
+        const int i = ig + r * kDeltaIGroups;
+        if (active && i < dk) {
+            sreg[r] *= decay;
+            pred += sreg[r] * (qk[256 + i] * invk);
+        }
+    }
+    pred += __shfl_xor(pred, 16, kWave);
+    pred += __shfl_xor(pred, 32, kWave);
+    if (lane < kDeltaCols) colsum[wid][lane] = pred;
+    __syncthreads();
+    pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
+    __syncthreads();
+    const float delta = active ? beta * (vj - pred) : 0.0f;
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
+        const int i = ig + r * kDeltaIGroups;
+        if (active && i < dk) {
+            sreg[r] += (qk[256 + i] * invk) * delta;
+            S[static_cast<size_t>(i) * dv + j] = sreg[r];
+            o += sreg[r] * (qk[i] * invq);
+        }
+    }
+    o += __shfl_xor(o, 16, kWave);
+    o += __shfl_xor(o, 32, kWave);
+    if (lane < kDeltaCols) colsum[wid][lane] = o;
+    __syncthreads();
+    if (threadIdx.x < kDeltaCols && active) {
+        const float tot = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
+        p.out[static_cast<size_t>(vh) * dv + j] = tot * (1.0f / sqrtf(static_cast<float>(dk)));
+    }
+}
+
+bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
+    return lk_n > 0 && lv_n > 0 && lv_n % lk_n == 0 && lk_hd > 0 && lk_hd <= 256 && lv_hd > 0 && ksize >= 1 &&
+           lk_hd <= kDeltaIGroups * kDeltaMaxKPerThread;
+}
+
+hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s) {
+    hipLaunchKernelGGL(linear_step_kernel, dim3(p.lv_n, (p.lv_hd + kDeltaCols - 1) / kDeltaCols), dim3(256), 0, s,
+                       p);
+    return hipGetLastError();
+}
+
 bool conv_supported(int lk_hd, int lv_hd) { return lk_hd > 0 && lv_hd > 0 && lk_hd <= 1024 && lv_hd <= 1024; }
 
 bool delta_supported(int lk_hd) { return lk_hd > 0 && lk_hd <= kDeltaIGroups * kDeltaMaxKPerThread; }

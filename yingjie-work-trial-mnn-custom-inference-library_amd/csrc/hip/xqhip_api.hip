@@ -430,6 +430,19 @@ int xqhip_gated_delta(const float* conv, const float* a, const float* b, const f
     return check(xqhip::launch_delta(p, as_stream(stream)), "delta launch");
 }
 
+int xqhip_linear_attn_step(const float* mixed, float* conv_state, const float* conv_w, const float* a, const float* b,
+                           const float* a_log, const float* dt_bias, float* state, int lk_n, int lk_hd, int lv_n,
+                           int lv_hd, int ksize, const int32_t* pos, float* out, void* stream) {
+    if (!mixed || !conv_state || !conv_w || !a || !b || !a_log || !dt_bias || !state || !pos || !out)
+        return fail(XQHIP_EINVAL, "xqhip_linear_attn_step: null argument");
+    if (!xqhip::linear_step_supported(lk_n, lk_hd, lv_n, lv_hd, ksize))
+        return fail(XQHIP_EINVAL, "xqhip_linear_attn_step: unsupported shape lk=%dx%d lv=%dx%d k=%d", lk_n, lk_hd, lv_n,
+                    lv_hd, ksize);
+    xqhip::LinearStepLaunch p{mixed, conv_state, conv_w, a, b, a_log, dt_bias, state,
+                              lk_n, lk_hd, lv_n, lv_hd, ksize, pos, out};
+    return check(xqhip::launch_linear_step(p, as_stream(stream)), "linear step launch");
+}
+
 int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream) {
     if (!x || !w || !y || n <= 0) return fail(XQHIP_EINVAL, "xqhip_rmsnorm: bad args");
     return check(xqhip::launch_rmsnorm(x, w, n, eps, y, as_stream(stream)), "rmsnorm launch");

@@ -105,6 +105,26 @@ struct DeltaLaunch {
 bool delta_supported(int lk_hd);
 hipError_t launch_delta(const DeltaLaunch& p, hipStream_t s);
 
+// Fused linear-attention step (conv1d + SiLU + q/k L2 norm + gated delta) for
+// the decode graph.  The conv history is double-buffered by position parity:
+// copy (pos & 1) is read and copy ((pos + 1) & 1) written, so the blocks that
+// recompute a key head's q/k channels never race with the one that stores them.
+struct LinearStepLaunch {
+    const float* mixed;   // conv input: q | k | v channels
+    float* conv_state;    // [2][conv_dim][ksize - 1]
+    const float* conv_w;  // [conv_dim][ksize]
+    const float* a;
+    const float* b;
+    const float* a_log;
+    const float* dt_bias;
+    float* state;  // [lv_n][lk_hd][lv_hd]
+    int lk_n, lk_hd, lv_n, lv_hd, ksize;
+    const int32_t* pos;
+    float* out;  // lv_n * lv_hd
+};
+bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
+hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s);
+
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
 
 }  // namespace xqhip

@@ -153,7 +153,7 @@ bool DeviceModel::load_layer(int index, Layer* L, std::string* error) {
         !upload_vec(conv_w, &L->conv_w, error) || !upload_vec(a_log, &L->a_log, error) ||
         !upload_vec(dt_bias, &L->dt_bias, error))
         return false;
-    return alloc(&L->conv_state, static_cast<size_t>(conv_dim_) * std::max(0, ksize_ - 1), error) &&
+    return alloc(&L->conv_state, 2 * static_cast<size_t>(conv_dim_) * std::max(0, ksize_ - 1), error) &&
            alloc(&L->rec_state, static_cast<size_t>(lv_n_) * lk_hd_ * lv_hd_, error);
 }
 
@@ -245,7 +245,7 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     uint8_t *wa = nullptr, *wg = nullptr;
     if (!alloc(&resid_, hidden_, error) || !alloc(&normed_, hidden_, error) || !alloc(&proj_, max_proj, error) ||
         !alloc(&q_rot_, static_cast<size_t>(nq_) * hd_, error) || !alloc(&gate_, static_cast<size_t>(nq_) * hd_, error) ||
-        !alloc(&attn_, attn_n, error) || !alloc(&conv_out_, std::max(1, conv_dim_), error) ||
+        !alloc(&attn_, attn_n, error) ||
         !alloc(&ffn_, inter_, error) || !alloc(&best_val_, 1, error) || !alloc(&d_ctrl_, 4, error) ||
         !alloc(&wa, ws_argmax, error) || !alloc(&wg, ws_gqa, error))
         return false;
@@ -272,7 +272,7 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
 void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past the position are never read)
     for (Layer& L : layers_) {
         if (L.full) continue;
-        xqhip_fill_u8(L.conv_state, 0, sizeof(float) * conv_dim_ * std::max(0, ksize_ - 1), stream_);
+        xqhip_fill_u8(L.conv_state, 0, 2 * sizeof(float) * conv_dim_ * std::max(0, ksize_ - 1), stream_);
         xqhip_fill_u8(L.rec_state, 0, sizeof(float) * lv_n_ * lk_hd_ * lv_hd_, stream_);
     }
     detail_prefill_ = detail_decode_ = true;
@@ -362,18 +362,14 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
             XQ_CALL(xqhip_gemv_w4a16(&L.in_proj, resid_, XQHIP_F32, &rms_in, proj_, XQHIP_F32, XQHIP_EPI_STORE, stream_),
                     "linear-attention in projection");
             op_end(timed);
-            op_begin(timed, "linear_attention_conv1d_custom(fused:linear_attention_qk_l2norm)");
-            XQ_CALL(xqhip_linear_conv(proj_, L.conv_state, L.conv_w, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, conv_out_,
-                                      stream_),
-                    "conv1d");
-            op_end(timed);
             const float* a = proj_ + conv_dim_;
             const float* b = a + lv_n_;
             const float* z = b + lv_n_;
-            op_begin(timed, "linear_attention_state_update_custom");
-            XQ_CALL(xqhip_gated_delta(conv_out_, a, b, L.a_log, L.dt_bias, L.rec_state, lk_n_, lv_n_, lk_hd_, lv_hd_,
-                                      attn_, stream_),
-                    "gated delta");
+            op_begin(timed, "linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
+                     {"linear_attention_conv1d_custom"}, 2);
+            XQ_CALL(xqhip_linear_attn_step(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias, L.rec_state,
+                                           lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_, stream_),
+                    "linear-attention step");
             op_end(timed);
             xqhip_prologue gated{XQHIP_PRO_GATED_HEAD, lv_hd_, L.lin_norm, z, eps_};
             op_begin(timed, "linear_attn_out_proj_w4a16(fused:linear_attention_gated_rmsnorm,residual_add_attention)");

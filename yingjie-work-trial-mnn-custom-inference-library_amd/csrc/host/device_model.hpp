@@ -111,7 +111,6 @@ private:
     float* q_rot_ = nullptr;
     float* gate_ = nullptr;
     float* attn_ = nullptr;      // attention / delta output
-    float* conv_out_ = nullptr;
     float* ffn_ = nullptr;
     float* logits_ = nullptr;    // debug_json only
     float* best_val_ = nullptr;

@@ -73,6 +73,8 @@ _HIP_SIGS = {
                                   c_void_p]),
     "xqhip_gated_delta": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                   c_int, c_void_p, c_void_p]),
+    "xqhip_linear_attn_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "xqhip_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]),
     "xqhip_stream_create": (c_int, [_P(c_void_p)]),
     "xqhip_stream_destroy": (c_int, [c_void_p]),
