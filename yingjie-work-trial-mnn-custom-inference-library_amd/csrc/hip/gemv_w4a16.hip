@@ -605,30 +605,41 @@ static int resident_blocks(const void* fn, int threads, size_t lds, int* cache) 
     return cache[dev];
 }
 
+// One block per CU: 12 waves (NCH chunks x 12/NCH row groups), so the
+// activation staging is done once per CU rather than once per small block.
+template <int NCH>
+constexpr int kRowGroups = 12 / NCH;
+
+static int device_cus() {
+    static int cache[16] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (cache[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+        cache[dev] = cus;
+    }
+    return cache[dev];
+}
+
 template <int NCH, int R, int EPI>
 static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
-    constexpr int RG = NCH == 1 ? 4 : (NCH == 4 ? 1 : 2);
+    constexpr int RG = kRowGroups<NCH>;
     const int G = p.cols >> 6;
-    if (!stage_supported(p.cols, p.pro)) return hipErrorInvalidValue;
-    // buffer-resource offsets are 32-bit and kOutOfRange must lie past the end
-    if (static_cast<uint64_t>(p.rows) * static_cast<uint64_t>(p.cols / 2) >= kOutOfRange) return hipErrorInvalidValue;
     const size_t lds = static_cast<size_t>(G) * kStageRecord * sizeof(uint4);
+    const auto fn = reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>);
     if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
     }
-    // Every block stages x once, so launch no more blocks than are resident at
-    // once and balance the row trips: trips = ceil(units / cap), blocks =
-    // ceil(units / trips).
+    // No more blocks than are resident at once (each stages x once); trips are
+    // grid-uniform, blocks whose later rows fall past the end skip them.
     static int resident_cache[16] = {};
-    const auto fn = reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>);
     int cap = p.max_blocks > 0 ? p.max_blocks : resident_blocks(fn, 64 * NCH * RG, lds, resident_cache);
-    if (cap < 1) cap = 1024;
+    if (cap < 1) cap = device_cus();
     if (EPI == EPI_ARGMAX && cap > kArgmaxMaxBlocks) cap = kArgmaxMaxBlocks;
     const int units = (p.rows + R * RG - 1) / (R * RG);
-    const int trips = (units + cap - 1) / cap;
-    const int blocks = trips > 0 ? (units + trips - 1) / trips : 1;
+    const int blocks = units < cap ? units : cap;
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
                        static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro, p.y,
                        p.y_f16, p.partial);
@@ -636,13 +647,46 @@ static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     return EPI == EPI_ARGMAX ? launch_argmax_finish(p, blocks, s) : hipSuccess;
 }
 
+// Rows per wave batch: the R in {2, 1} that minimises the rows one wave
+// streams on the critical path, ceil(units_R / blocks) * R (ties: R = 2, more
+// bytes in flight per wave); SILU pairs need R even.  (R = 4 exceeds the
+// 168-VGPR budget of a 12-wave block.)
+template <int NCH>
+static int choose_rows_per_wave(const GemvLaunch& p) {
+    constexpr int RG = kRowGroups<NCH>;
+    const int cap = p.max_blocks > 0 ? p.max_blocks : device_cus();
+    int best_r = 2, best_cost = 1 << 30;
+    for (int r : {2, 1}) {
+        if (p.epi == EPI_SILU && r == 1) continue;
+        const int units = (p.rows + r * RG - 1) / (r * RG);
+        const int cost = ((units + cap - 1) / cap) * r;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best_r = r;
+        }
+    }
+    return best_r;
+}
+
+template <int NCH, int EPI>
+static hipError_t launch_tiled_epi(const GemvLaunch& p, hipStream_t s) {
+    if (choose_rows_per_wave<NCH>(p) == 1) {
+        if constexpr (EPI != EPI_SILU) return launch_tiled_t<NCH, 1, EPI>(p, s);
+        return hipErrorInvalidValue;
+    }
+    return launch_tiled_t<NCH, 2, EPI>(p, s);
+}
+
 template <int NCH>
 static hipError_t launch_tiled_nch(const GemvLaunch& p, hipStream_t s) {
+    if (!stage_supported(p.cols, p.pro)) return hipErrorInvalidValue;
+    // buffer-resource offsets are 32-bit and kOutOfRange must lie past the end
+    if (static_cast<uint64_t>(p.rows) * static_cast<uint64_t>(p.cols / 2) >= kOutOfRange) return hipErrorInvalidValue;
     switch (p.epi) {
-        case EPI_STORE: return launch_tiled_t<NCH, 4, EPI_STORE>(p, s);
-        case EPI_ADD: return launch_tiled_t<NCH, 4, EPI_ADD>(p, s);
-        case EPI_SILU: return launch_tiled_t<NCH, 4, EPI_SILU>(p, s);
-        case EPI_ARGMAX: return launch_tiled_t<NCH, 4, EPI_ARGMAX>(p, s);
+        case EPI_STORE: return launch_tiled_epi<NCH, EPI_STORE>(p, s);
+        case EPI_ADD: return launch_tiled_epi<NCH, EPI_ADD>(p, s);
+        case EPI_SILU: return launch_tiled_epi<NCH, EPI_SILU>(p, s);
+        case EPI_ARGMAX: return launch_tiled_epi<NCH, EPI_ARGMAX>(p, s);
     }
     return hipErrorInvalidValue;
 }
