@@ -6,23 +6,26 @@
 //     acc += s_g * (sum_c q_c x_c  -  z_g * sum_c x_c)          (version 1)
 //     acc += s_g * sum_c q_c x_c  +  z_g * sum_c x_c            (version 2)
 // and so do these kernels: the per-group sums of x are computed once per block
-// and the inner loop is a pure code-times-activation dot product.
+// and the inner loop is a pure code-times-activation integer dot product.
 //
 // Inner loop (TILED64 layout).  One lane owns one 64-column group of a row per
 // 4096-column chunk: it streams the group's 32 bytes of nibbles with two 16-byte
 // loads (a wave's load instruction covers 1 KiB contiguous) and one u32 of
-// (fp16 scale, fp16 zero).  Each u32 of 8 nibbles becomes four fp16 pairs with
-// one v_and_or_b32 each (0x6400 | q = 1024 + q, 0x6400 | q<<4 = 1024 + 16q, exact)
-// and one shift per word.
+// (fp16 scale, fp16 zero).  The device copy of every nibble is q ^ 8, which read
+// as a signed 4-bit integer is q - 8, so a u32 of 8 codes feeds v_dot8_i32_i4
+// directly (no unpacking).
 //
-// Activations are carried at ~22-bit precision as x = hi + lo * 2^-11 with hi, lo
-// fp16 (lo is the fp32 rounding residual of hi, scaled up so it stays normal).
-// Both are staged once per block in LDS as the fp16 pairs matching the nibble
-// order (odd columns pre-divided by 16, exact), with the per-group constants
-// 1024 * sum(staged) that remove the 1024 offsets; each pair of codes then costs
-// two v_dot2_f32_f16 (hi and lo), so a word of 8 weights is 13 VALU ops and the
-// dot products are accurate to fp32 level.  The staged activations of a lane's
-// groups live in registers for the whole block.
+// Activations are staged once per block as integers: each 64-column group is
+// scaled by e = max|x| / 2^21 and rounded, X = rint(x / e) (|X| <= 2^21), and X
+// is written as six signed hex digits, X = sum_d t_d 16^d with t_d in [-8, 7]
+// (t_d = hex digit d of X + 0x888888, minus 8).  Digit d of eight consecutive
+// columns is one u32 of signed nibbles, so per word of weights the lane issues
+// six v_dot8_i32_i4 into six integer accumulators; per group they combine
+// exactly into D = sum_c (q_c - 8) X_c (|D| < 2^30) and, with G = sum_c X_c,
+//     sum_c q_c x_c = e (D + 8 G),   sum_c x_c = e G.
+// The only rounding besides the final fp32 accumulation over groups is that of
+// x to 22 significant bits relative to its group maximum.  Per 8 weights this
+// is 6 VALU ops (the fp16 magic-number path it replaces needed 13).
 //
 // Columns beyond 4096 are split over the waves of a block (one 4096-column chunk
 // per wave), whose partial row sums are combined through LDS in a fixed order.
@@ -79,14 +82,15 @@ __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& 
 }
 
 // ---------------------------------------------------------------------------
-// Activation staging into LDS, done by every GEMV block while its first batch
-// of weights is in flight.  Record of group g (kStageRecord uint4): 8 words of
-// hi pairs, 8 words of lo pairs, then (sum of the effective x of the group,
-// 1024*sum(hi staged), 1024*sum(lo staged), 0).  Word j holds, for columns
-// 8j..8j+7 of the group, the fp16 pairs (x0,x4) (x1/16,x5/16) (x2,x6)
-// (x3/16,x7/16), matching the nibble order produced by dot8.
+// Activation staging into LDS, done by every GEMV block while its first
+// weight batches are in flight.  Record of group g (kStageRecord uint4 = 52
+// words): words [8 d + j] hold digit d of columns 8j..8j+7 (nibble i = column
+// 8j+i, matching the nibble order of a weight word), then e and G (as floats).
 // ---------------------------------------------------------------------------
-constexpr int kStageRecord = 17;
+constexpr int kDigits = 6;
+constexpr int kXMax = 1 << (4 * kDigits - 3);  // 2^21: |X| <= kXMax keeps |D| < 2^30
+constexpr uint32_t kDigitBias = 0x888888u;     // 8 in every hex digit of the 6
+constexpr int kStageRecord = (8 * kDigits + 2 + 3) / 4;
 constexpr int kMaxStageCols = 16384;
 
 // The block stages the whole vector: thread t owns the (group, word) items
@@ -202,50 +206,42 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
             for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i] * silu_dev(zl[i]);
         }
     }
+    uint32_t* xw = reinterpret_cast<uint32_t*>(xs);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
         const int item = threadIdx.x + k * THREADS;
         const int g = item >> 3, w = item & 7;
-        float gsum = 0.0f, st_hi = 0.0f, st_lo = 0.0f;
+        // group maximum over the 8 items of the group (8 consecutive lanes)
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[k][i]));
+#pragma unroll
+        for (int m = 1; m <= 4; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, kWave));
+        const float inv = mx > 0.0f ? static_cast<float>(kXMax) / mx : 0.0f;
+        int X[8];
+        int gs = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            X[i] = min(kXMax, max(-kXMax, static_cast<int>(rintf(v[k][i] * inv))));
+            gs += X[i];
+        }
+#pragma unroll
+        for (int m = 1; m <= 4; m <<= 1) gs += __shfl_xor(gs, m, kWave);
         if (item < n_items) {
-            _Float16 sh[8], sl[8];
+            uint32_t U[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const _Float16 hi = static_cast<_Float16>(v[k][i]);
-                const float lo = (v[k][i] - static_cast<float>(hi)) * 2048.0f;
-                const float sc = (i & 1) ? 0.0625f : 1.0f;
-                sh[i] = static_cast<_Float16>(static_cast<float>(hi) * sc);
-                sl[i] = static_cast<_Float16>(lo * sc);
+            for (int i = 0; i < 8; ++i) U[i] = static_cast<uint32_t>(X[i]) + kDigitBias;
+#pragma unroll
+            for (int d = 0; d < kDigits; ++d) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) word |= ((U[i] >> (4 * d)) & 15u) << (4 * i);
+                xw[g * (4 * kStageRecord) + d * 8 + w] = word ^ 0x88888888u;
             }
-            uint4 word;
-            word.x = as_u32(h2{sh[0], sh[4]});
-            word.y = as_u32(h2{sh[1], sh[5]});
-            word.z = as_u32(h2{sh[2], sh[6]});
-            word.w = as_u32(h2{sh[3], sh[7]});
-            xs[g * kStageRecord + w] = word;
-            word.x = as_u32(h2{sl[0], sl[4]});
-            word.y = as_u32(h2{sl[1], sl[5]});
-            word.z = as_u32(h2{sl[2], sl[6]});
-            word.w = as_u32(h2{sl[3], sl[7]});
-            xs[g * kStageRecord + 8 + w] = word;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float a = static_cast<float>(sh[i]), b = static_cast<float>(sl[i]);
-                st_hi += a;
-                st_lo += b;
-                const float eff = a + b * (1.0f / 2048.0f);
-                gsum += (i & 1) ? 16.0f * eff : eff;
+            if (w == 0) {
+                xw[g * (4 * kStageRecord) + 8 * kDigits] = __float_as_uint(mx * (1.0f / static_cast<float>(kXMax)));
+                xw[g * (4 * kStageRecord) + 8 * kDigits + 1] = __float_as_uint(static_cast<float>(gs));
             }
-        }
-#pragma unroll
-        for (int m = 1; m <= 4; m <<= 1) {  // the 8 words of a group are 8 consecutive lanes
-            gsum += __shfl_xor(gsum, m, kWave);
-            st_hi += __shfl_xor(st_hi, m, kWave);
-            st_lo += __shfl_xor(st_lo, m, kWave);
-        }
-        if (item < n_items && w == 0) {
-            const float4 kk = make_float4(gsum, 1024.0f * st_hi, 1024.0f * st_lo, 0.0f);
-            xs[g * kStageRecord + 16] = *reinterpret_cast<const uint4*>(&kk);
         }
     }
 }
@@ -257,23 +253,6 @@ bool stage_supported(int cols, const Prologue& pro) {
         return pro.head_dim % 8 == 0 && per >= 1 && per <= 64 && (per & (per - 1)) == 0;
     }
     return true;
-}
-
-// m_lo = 0x000F000F, m_hi = 0x00F000F0 and magic = kMagic2 are passed in so
-// they stay in VGPRs across the loop.
-__device__ __forceinline__ void dot8(uint32_t w, uint4 xh, uint4 xl, float& dh, float& dl, uint32_t m_lo,
-                                     uint32_t m_hi, uint32_t magic) {
-    const uint32_t w8 = w >> 8;
-    const h2 p0 = as_h2(and_or(w, m_lo, magic)), p1 = as_h2(and_or(w, m_hi, magic));
-    const h2 p2 = as_h2(and_or(w8, m_lo, magic)), p3 = as_h2(and_or(w8, m_hi, magic));
-    dh = dot2(p0, as_h2(xh.x), dh);
-    dl = dot2(p0, as_h2(xl.x), dl);
-    dh = dot2(p1, as_h2(xh.y), dh);
-    dl = dot2(p1, as_h2(xl.y), dl);
-    dh = dot2(p2, as_h2(xh.z), dh);
-    dl = dot2(p2, as_h2(xl.z), dl);
-    dh = dot2(p3, as_h2(xh.w), dh);
-    dl = dot2(p3, as_h2(xl.w), dl);
 }
 
 // Greedy argmax in two kernels: every GEMV block stores its best (value, row)
@@ -391,19 +370,22 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
     });
     __syncthreads();
-    uint4 xh[8], xl[8];
-    float4 gk = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // this lane's group: kDigits x 8 words of digits, then e and G
+    uint32_t xd[kDigits][8];
+    float ge = 0.0f, gg = 0.0f;
+    {
+        const uint4* rec = xs + (has_group ? g : 0) * kStageRecord;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        xh[j] = has_group ? xs[g * kStageRecord + j] : make_uint4(0, 0, 0, 0);
-        xl[j] = has_group ? xs[g * kStageRecord + 8 + j] : make_uint4(0, 0, 0, 0);
-    }
-    if (has_group) {
-        const uint4 k = xs[g * kStageRecord + 16];
-        gk = *reinterpret_cast<const float4*>(&k);
+        for (int d = 0; d < kDigits; ++d) {
+            const uint4 lo4 = rec[2 * d], hi4 = rec[2 * d + 1];
+            xd[d][0] = lo4.x; xd[d][1] = lo4.y; xd[d][2] = lo4.z; xd[d][3] = lo4.w;
+            xd[d][4] = hi4.x; xd[d][5] = hi4.y; xd[d][6] = hi4.z; xd[d][7] = hi4.w;
+        }
+        const uint4 kk = rec[2 * kDigits];
+        ge = has_group ? __uint_as_float(kk.x) : 0.0f;
+        gg = has_group ? __uint_as_float(kk.y) : 0.0f;
     }
 
-    const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = kMagic2;
     uint64_t best = 0;
 
     auto process = [&](WBatch<R>& cur, int bbase) {
@@ -414,20 +396,27 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         if (r0 < rows) {
 #pragma unroll
             for (int i = 0; i < R; ++i) {
-                float dh = 0.0f, dl = 0.0f;
-                dot8(cur.a[i].x, xh[0], xl[0], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.a[i].y, xh[1], xl[1], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.a[i].z, xh[2], xl[2], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.a[i].w, xh[3], xl[3], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.b[i].x, xh[4], xl[4], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.b[i].y, xh[5], xl[5], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.b[i].z, xh[6], xl[6], dh, dl, m_lo, m_hi, magic);
-                dot8(cur.b[i].w, xh[7], xl[7], dh, dl, m_lo, m_hi, magic);
-                // sum_c q_c x_c of the group, with the 1024 offsets removed per part
-                const float t = fmaf(dl - gk.z, 1.0f / 2048.0f, dh - gk.y);
+                const uint32_t wd[8] = {cur.a[i].x, cur.a[i].y, cur.a[i].z, cur.a[i].w,
+                                        cur.b[i].x, cur.b[i].y, cur.b[i].z, cur.b[i].w};
+                int A[kDigits];
+#pragma unroll
+                for (int d = 0; d < kDigits; ++d) A[d] = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+#pragma unroll
+                    for (int d = 0; d < kDigits; ++d)
+                        A[d] = __builtin_amdgcn_sdot8(static_cast<int>(wd[j]), static_cast<int>(xd[d][j]), A[d], false);
+                // D = sum_d A_d 16^d, exact in int32 (|D| < 2^30, partial sums smaller)
+                int Dg = A[kDigits - 1];
+#pragma unroll
+                for (int d = kDigits - 2; d >= 0; --d) Dg = (Dg << 4) + A[d];
+                // sum_c q_c x_c = e (D + 8 G), sum_c x_c = e G, so
+                //   v1: s (sum qx - z sum x) = s e (D + (8 - z) G)   (exact cancellation for z = 8)
+                //   v2: s sum qx + z sum x   = e (s D + (8 s + z) G)
+                const float df = static_cast<float>(Dg);
                 const float sc = half_lo(cur.m[i]);
                 const float z = half_hi(cur.m[i]);
-                acc[i] = affine ? fmaf(sc, t, z * gk.x) : sc * fmaf(-z, gk.x, t);
+                acc[i] = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
                 acc[i] = wave_sum(acc[i]);
             }
         }
@@ -647,17 +636,17 @@ static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     return EPI == EPI_ARGMAX ? launch_argmax_finish(p, blocks, s) : hipSuccess;
 }
 
-// Rows per wave batch: the R in {2, 1} that minimises the rows one wave
-// streams on the critical path, ceil(units_R / blocks) * R (ties: R = 2, more
-// bytes in flight per wave); SILU pairs need R even.  (R = 4 exceeds the
-// 168-VGPR budget of a 12-wave block.)
+// Rows per wave batch: the R in {1, 2, 4} that minimises the rows one wave
+// streams on the critical path, ceil(units_R / blocks) * R (ties: the smaller
+// R, i.e. more trips and a deeper load pipeline per wave); SILU pairs need R
+// even.
 template <int NCH>
 static int choose_rows_per_wave(const GemvLaunch& p) {
     constexpr int RG = kRowGroups<NCH>;
     const int cap = p.max_blocks > 0 ? p.max_blocks : device_cus();
     int best_r = 2, best_cost = 1 << 30;
-    for (int r : {2, 1}) {
-        if (p.epi == EPI_SILU && r == 1) continue;
+    for (int r : {1, 2, 4}) {
+        if ((p.epi == EPI_SILU && r == 1) || (p.epi == EPI_ARGMAX && r == 4)) continue;  // pairs; VGPR budget
         const int units = (p.rows + r * RG - 1) / (r * RG);
         const int cost = ((units + cap - 1) / cap) * r;
         if (cost < best_cost) {
@@ -670,11 +659,15 @@ static int choose_rows_per_wave(const GemvLaunch& p) {
 
 template <int NCH, int EPI>
 static hipError_t launch_tiled_epi(const GemvLaunch& p, hipStream_t s) {
-    if (choose_rows_per_wave<NCH>(p) == 1) {
-        if constexpr (EPI != EPI_SILU) return launch_tiled_t<NCH, 1, EPI>(p, s);
-        return hipErrorInvalidValue;
+    switch (choose_rows_per_wave<NCH>(p)) {
+        case 1:
+            if constexpr (EPI != EPI_SILU) return launch_tiled_t<NCH, 1, EPI>(p, s);
+            return hipErrorInvalidValue;
+        case 2: return launch_tiled_t<NCH, 2, EPI>(p, s);
+        default:
+            if constexpr (EPI != EPI_ARGMAX) return launch_tiled_t<NCH, 4, EPI>(p, s);
+            return hipErrorInvalidValue;
     }
-    return launch_tiled_t<NCH, 2, EPI>(p, s);
 }
 
 template <int NCH>

@@ -163,7 +163,8 @@ int xqhip_event_elapsed_ms(void* start, void* stop, float* ms) {
 // chunk c of up to 64 groups (gc of them), half h of group c*64+l lands at
 // c*2048 + h*gc*16 + l*16: one wave-wide 16-byte load per half is 1 KiB
 // contiguous.  Nibble order inside each 16 bytes is unchanged (even column in
-// the low nibble).  Metadata becomes one u32 per group: fp16 scale | fp16 zero<<16.
+// the low nibble); every code q is stored as q ^ 8.  Metadata becomes one u32
+// per group: fp16 scale | fp16 zero<<16.
 int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols, int group,
                     int affine, xqhip_w4* out) {
     if (!packed || !scales || !zeros || !out || rows <= 0 || cols <= 0 || group <= 0)
@@ -191,8 +192,12 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
             for (int g = 0; g < G; ++g) {
                 const int c = g / 64, l = g % 64;
                 const int gcnt = std::min(64, G - c * 64);
-                for (int h = 0; h < 2; ++h)
-                    std::memcpy(dst + c * 2048 + h * gcnt * 16 + l * 16, src + g * 32 + h * 16, 16);
+                for (int h = 0; h < 2; ++h) {
+                    // each code q stored as q ^ 8 = (q - 8) in signed 4-bit, the operand of v_dot8_i32_i4
+                    uint8_t* d16 = dst + c * 2048 + h * gcnt * 16 + l * 16;
+                    const uint8_t* s16 = src + g * 32 + h * 16;
+                    for (int i = 0; i < 16; ++i) d16[i] = static_cast<uint8_t>(s16[i] ^ 0x88u);
+                }
             }
         }
         nib_src = nib_host.data();
