@@ -190,6 +190,114 @@ def cpu_baseline_mlp(inp, hidden, inter, step_bytes, seconds):
 MODEL_DIR = os.environ.get("XQ_BENCH_MODEL_DIR", "/tmp/xq_synth_9b_w4a16_g64")
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic of the roofline kernel from rocprofv3 counters (two passes:
+# FETCH_SIZE, then WRITE_SIZE, each in KiB per dispatch), each scaled by what
+# the same counter reads for a plain device-to-device copy of known size.
+# ---------------------------------------------------------------------------
+PMC_COPY_BYTES = 64 << 20
+GATE_UP_KERNEL = "gemv_w4_tiled<1, 12, 2, 2>"  # NCH=1, 12 row groups, 2 rows per wave, SiLU-pair epilogue
+
+
+def time_gate_up_kernel(n=200, ncopy=8):
+    """Average duration of the gate/up GEMV kernel (24576x4096, RMSNorm prologue,
+    SiLU*up epilogue) over n back-to-back launches on the default stream, HIP
+    events around the loop; weights rotated over ncopy copies (> 2x the 256 MB
+    last-level cache) so every launch streams from HBM."""
+    hidden, inter = 4096, 12288
+    hip = xb.hip()
+    inp = mlp_inputs(hidden, inter)
+    copies = [xb.DeviceW4(*inp["gu"], 2 * inter, hidden) for _ in range(ncopy)]
+    nw = xb.DeviceBuffer.from_array(inp["norm_w"])
+    h = xb.DeviceBuffer.from_array(inp["h"])
+    ffn = xb.DeviceBuffer(inter * 4)
+    pro = xb.prologue(xb.PRO_RMS, nw, eps=1e-6)
+    pro_ref = ctypes.byref(pro)
+
+    def launch(i):
+        xb.ck(hip.xqhip_gemv_w4a16(copies[i % ncopy].ref, h.ptr, xb.F32, pro_ref, ffn.ptr, xb.F32,
+                                   xb.EPI_SILU_PAIR, None))
+
+    for i in range(20):
+        launch(i)
+    ev = Events()
+    ev.start()
+    for i in range(n):
+        launch(i)
+    return ev.stop_ms() / n
+
+
+def pmc_probe(args):
+    """Child workload run under rocprofv3 --pmc: 5 copies of PMC_COPY_BYTES,
+    then 6 gate/up GEMVs (24576x4096, RMSNorm prologue, SiLU*up) on rotated
+    weight copies."""
+    hidden, inter = 4096, 12288
+    hip = xb.hip()
+    src, dst = xb.DeviceBuffer(PMC_COPY_BYTES), xb.DeviceBuffer(PMC_COPY_BYTES)
+    src.zero()
+    for _ in range(5):
+        xb.ck(hip.xqhip_copy(dst.ptr, src.ptr, PMC_COPY_BYTES, None))
+    inp = mlp_inputs(hidden, inter)
+    copies = [xb.DeviceW4(*inp["gu"], 2 * inter, hidden) for _ in range(6)]
+    nw = xb.DeviceBuffer.from_array(inp["norm_w"])
+    h = xb.DeviceBuffer.from_array(inp["h"])
+    ffn = xb.DeviceBuffer(inter * 4)
+    pro = xb.prologue(xb.PRO_RMS, nw, eps=1e-6)
+    for w in copies:
+        xb.ck(hip.xqhip_gemv_w4a16(w.ref, h.ptr, xb.F32, ctypes.byref(pro), ffn.ptr, xb.F32, xb.EPI_SILU_PAIR, None))
+    xb.ck(hip.xqhip_device_synchronize())
+    return {"pmc_probe": "done"}
+
+
+def _pmc_pass(counter, workdir):
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    rocprof = shutil.which("rocprofv3")
+    if not rocprof:
+        return None
+    out = os.path.join(workdir, counter)
+    cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "pmc",
+           "--", sys.executable, os.path.join(ROOT, "bench.py"), "--workload", "pmc-probe"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    log(f"[bench] traffic: {' '.join(cmd[4:8])} pass")
+    r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        log(f"[bench] traffic: rocprofv3 {counter} pass produced no counters (rc {r.returncode})")
+        return None
+    vals = {"copy": [], "gemv": []}
+    for f in files:
+        for row in csv.DictReader(open(f)):
+            name = row.get("Kernel_Name", "")
+            v = float(row.get("Counter_Value", "nan"))
+            if "copy_u32x4_kernel" in name:
+                vals["copy"].append(v)
+            elif GATE_UP_KERNEL in name:
+                vals["gemv"].append(v)
+    if not vals["copy"] or not vals["gemv"]:
+        return None
+    return sum(vals["copy"]) / len(vals["copy"]), sum(vals["gemv"]) / len(vals["gemv"]), len(vals["gemv"])
+
+
+def measure_traffic():
+    """HBM bytes per launch of the gate/up GEMV: FETCH_SIZE and WRITE_SIZE,
+    each calibrated on a device-to-device copy of PMC_COPY_BYTES."""
+    import tempfile
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        f = _pmc_pass("FETCH_SIZE", d)
+        w = _pmc_pass("WRITE_SIZE", d)
+    if not f or not w:
+        return None
+    fetch_scale, write_scale = PMC_COPY_BYTES / f[0], PMC_COPY_BYTES / w[0]  # bytes per counted KiB
+    fetch, write = f[1] * fetch_scale, w[1] * write_scale
+    return {"bytes": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
+            "fetch_scale_bytes_per_kib": round(fetch_scale, 2), "write_scale_bytes_per_kib": round(write_scale, 2),
+            "dispatches": f[2], "method": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over a child run of "
+            "bench.py --workload pmc-probe, calibrated on a 64 MiB one-dispatch device copy (xqhip_copy)"}
+
+
 def ensure_model(path):
     marker = os.path.join(path, ".complete")
     if os.path.exists(marker):
@@ -251,7 +359,8 @@ def bench_decode(args):
     bytes_lm = w4_bytes(248320, hidden) + hidden * 4
     info = sess.json("xq_get_backend_info")[1]
     wbytes = int(info.split("weight_bytes_per_token=")[1].split(";")[0]) if "weight_bytes_per_token=" in info else 0
-    ach = bytes_gu / (gu["mean_ms"] * 1e-3) / 1e9 if gu else None
+    t_gu = time_gate_up_kernel()
+    ach = bytes_gu / (t_gu * 1e-3) / 1e9
     step_ms = step["mean_ms"] if step else ms_per_step
     log(f"[bench] decode {args.steps} steps: {ms_per_step:.3f} ms/token wall ({tps:.1f} tok/s), graph step "
         f"{step_ms:.3f} ms, weights {wbytes / 1e9:.3f} GB/token -> {wbytes / (step_ms * 1e-3) / 1e9:.0f} GB/s; "
@@ -268,20 +377,25 @@ def bench_decode(args):
                    "weight_stream_GBps": round(wbytes / (step_ms * 1e-3) / 1e9, 1),
                    "prefill_ms": round(prefill_ms, 2), "prefill_tokens_per_s": round(prompt_len / prefill_ms * 1e3, 1),
                    "model_write_s": round(gen_s, 1), "load_s": round(load_s, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(ach, 1) if ach else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4) if ach else None, "traffic": None,
-                     "kernel": "gemv_w4_tiled gate/up 24576x4096 (+RMSNorm prologue, SiLU*up epilogue), in-model",
-                     "bytes_per_launch": bytes_gu,
-                     "avg_launch_us": round(gu["mean_ms"] * 1e3, 2) if gu else None,
-                     "launches_timed": gu["calls"] if gu else 0,
-                     "down_proj": {"bytes_per_launch": bytes_dn,
-                                   "avg_launch_us": round(dn["mean_ms"] * 1e3, 2) if dn else None},
-                     "lm_head_argmax": {"bytes_per_launch": bytes_lm,
-                                        "avg_launch_us": round(lm["mean_ms"] * 1e3, 2) if lm else None}},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"{GATE_UP_KERNEL}: gate/up 24576x4096 W4A16 g64 + RMSNorm prologue + SiLU*up "
+                               "epilogue, 200 back-to-back launches on rotated weights",
+                     "bytes_per_launch": bytes_gu, "avg_launch_us": round(t_gu * 1e3, 2), "launches_timed": 200,
+                     "in_model_avg_us": {"gate_up": round(gu["mean_ms"] * 1e3, 2) if gu else None,
+                                         "down_proj": round(dn["mean_ms"] * 1e3, 2) if dn else None,
+                                         "lm_head_argmax": round(lm["mean_ms"] * 1e3, 2) if lm else None},
+                     "bytes_per_launch_down_proj": bytes_dn, "bytes_per_launch_lm_head": bytes_lm},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_decode(prompt, sess, args.cpu_seconds)
     sess.close()
+    if not args.no_traffic:
+        t = measure_traffic()
+        if t:
+            result["roofline"]["traffic"] = t["bytes"]
+            result["roofline"]["traffic_detail"] = t
+            log(f"[bench] gate/up traffic {t['bytes']} B per launch (algorithmic {bytes_gu})")
     return result
 
 
@@ -328,8 +442,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "mlp"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "pmc-probe"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -343,7 +458,7 @@ def main():
     name = ctypes.create_string_buffer(256)
     xb.hip().xqhip_device_name(name, 256)
     log(f"[bench] device: {name.value.decode()}")
-    res = {"decode": bench_decode, "mlp": bench_mlp}[args.workload](args)
+    res = {"decode": bench_decode, "mlp": bench_mlp, "pmc-probe": pmc_probe}[args.workload](args)
     print(json.dumps(res), flush=True)
 
 

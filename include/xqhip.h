@@ -87,6 +87,10 @@ XQHIP_API int xqhip_host_alloc(void** ptr, size_t bytes);
 XQHIP_API int xqhip_host_free(void* ptr);
 /* Byte fill done by a kernel (safe inside captured graphs). */
 XQHIP_API int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream);
+/* Device-to-device copy as one plain kernel dispatch (graph-capturable; also
+ * the known-size copy that HBM byte counters are calibrated on).  16-byte
+ * aligned pointers. */
+XQHIP_API int xqhip_copy(void* dst, const void* src, size_t bytes, void* stream);
 XQHIP_API int xqhip_stream_synchronize(void* stream);
 XQHIP_API int xqhip_device_synchronize(void);
 XQHIP_API int xqhip_event_create(void** ev);

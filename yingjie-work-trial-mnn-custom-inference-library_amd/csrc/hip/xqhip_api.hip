@@ -61,6 +61,16 @@ __global__ void fill_u8_kernel(uint8_t* p, uint8_t v, size_t n) {
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 
+// Plain device copy in one dispatch: 16-byte elements over a grid-stride
+// loop, then the tail bytes.
+__global__ void copy_u32x4_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src, size_t n16,
+                                  uint8_t* __restrict__ dst_tail, const uint8_t* __restrict__ src_tail, size_t tail) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    const size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (size_t i = t; i < n16; i += stride) dst[i] = src[i];
+    if (t < tail) dst_tail[t] = src_tail[t];
+}
+
 }  // namespace
 
 extern "C" {
@@ -137,6 +147,19 @@ int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream) {
     hipLaunchKernelGGL(fill_u8_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
                        static_cast<uint8_t*>(dst), value, bytes);
     return check(hipGetLastError(), "fill_u8");
+}
+
+int xqhip_copy(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return XQHIP_OK;
+    if (!dst || !src) return fail(XQHIP_EINVAL, "xqhip_copy: null pointer");
+    if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u)
+        return fail(XQHIP_EINVAL, "xqhip_copy: pointers must be 16-byte aligned");
+    const size_t n16 = bytes / 16, tail = bytes % 16;
+    const size_t blocks = std::max<size_t>(1, std::min<size_t>((n16 + 255) / 256, 4096));
+    hipLaunchKernelGGL(copy_u32x4_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
+                       static_cast<uint4*>(dst), static_cast<const uint4*>(src), n16,
+                       static_cast<uint8_t*>(dst) + n16 * 16, static_cast<const uint8_t*>(src) + n16 * 16, tail);
+    return check(hipGetLastError(), "copy");
 }
 
 int xqhip_stream_synchronize(void* stream) { return check(hipStreamSynchronize(as_stream(stream)), "stream sync"); }

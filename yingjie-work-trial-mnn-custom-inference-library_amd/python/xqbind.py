@@ -49,6 +49,7 @@ _HIP_SIGS = {
     "xqhip_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "xqhip_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "xqhip_fill_u8": (c_int, [c_void_p, c_uint8, c_size_t, c_void_p]),
+    "xqhip_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "xqhip_stream_synchronize": (c_int, [c_void_p]),
     "xqhip_device_synchronize": (c_int, []),
     "xqhip_event_create": (c_int, [ctypes.POINTER(c_void_p)]),
