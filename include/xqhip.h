@@ -209,6 +209,50 @@ XQHIP_API int xqhip_linear_attn_step(const float* mixed, float* conv_state, cons
 /* y = x * inv * w (rmsnormReference, ref_rmsnorm.cpp:8-17). */
 XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream);
 
+/* ---- prefill: a prompt chunk of m tokens at once ------------------------- */
+/* The reference prefills token by token (CustomModel::prefill,
+ * custom_model.cpp:610-640, each token through runLayer :1138-1256); these run
+ * the same per-token arithmetic for a chunk: the projections as GEMMs on the
+ * matrix cores, attention and the linear-attention recurrence as batched
+ * kernels.  Row-major [token][...] activations with explicit row strides. */
+
+/* Workspace bytes xqhip_gemm_w4a16 needs for m tokens of `cols` columns. */
+XQHIP_API size_t xqhip_gemm_workspace_bytes(int m, int cols);
+/* y[t] (op)= W prologue(x[t]) for t < m: every token as xqhip_gemv_w4a16 does it
+ * (same epilogues; EPI_SILU_PAIR writes rows/2 values per token), on a TILED64
+ * matrix.  W is dequantised in fp32 and held in LDS as fp16 hi + lo halves, x is
+ * split the same way, and the products w_hi x_hi + w_hi x_lo + w_lo x_hi run on
+ * fp16 MFMA with fp32 accumulation.  GATED_HEAD reads the gate
+ * of token t at pro->gate + t * ld_gate.  workspace: 16-byte aligned,
+ * xqhip_gemm_workspace_bytes(m, cols). */
+XQHIP_API int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro,
+                               int ld_gate, float* y, int ldy, int epilogue, void* workspace, void* stream);
+/* xqhip_embed_bf16 for n tokens (device ids) into out[n][hidden]. */
+XQHIP_API int xqhip_embed_bf16_batch(const uint16_t* table, int vocab, int hidden, const int32_t* tokens, int n,
+                                     float* out, void* stream);
+/* xqhip_attn_prep for tokens consecutive positions *pos0 .. *pos0 + tokens - 1:
+ * token t reads its projections at q_src/k_src/v_src + t * src_stride and writes
+ * q and gate at t * out_stride; k and v are appended at cache slot *pos0 + t. */
+XQHIP_API int xqhip_attn_prep_batch(const float* q_src, const float* k_src, const float* v_src, int gated, int nq,
+                                    int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
+                                    float eps, const float* rope_cs, const int32_t* pos0, int tokens, int src_stride,
+                                    int out_stride, float* q_out, float* gate_out, void* k_cache, void* v_cache,
+                                    void* stream);
+/* Causal GQA for the chunk: token t (position *pos0 + t) attends to cache slots
+ * 0 .. *pos0 + t, then the sigmoid output gate (custom_model.cpp:840-951 per
+ * token).  q, gate: [tokens][q_stride]; out: [tokens][out_stride]. */
+XQHIP_API int xqhip_prefill_attention(const float* q, const float* gate, const void* k_cache, const void* v_cache,
+                                      int nq, int nkv, int head_dim, int tokens, int q_stride, const int32_t* pos0,
+                                      float* out, int out_stride, void* stream);
+/* xqhip_linear_attn_step for tokens consecutive positions pos0 .. pos0+tokens-1
+ * (pos0 given on the host) in one kernel: mixed, a, b rows of token t at
+ * t * stride; conv_state holds the two parity copies of xqhip_linear_attn_step
+ * and is left as that step expects for position pos0 + tokens. */
+XQHIP_API int xqhip_linear_attn_scan(const float* mixed, const float* a, const float* b, int stride,
+                                     float* conv_state, int pos0, const float* conv_w, const float* a_log,
+                                     const float* dt_bias, float* state, int lk_n, int lk_hd, int lv_n, int lv_hd,
+                                     int ksize, int tokens, float* out, int out_stride, void* stream);
+
 /* ---- streams and graphs ------------------------------------------------ */
 XQHIP_API int xqhip_stream_create(void** stream);
 XQHIP_API int xqhip_stream_destroy(void* stream);

@@ -20,18 +20,21 @@ namespace xqhip {
 // ---------------------------------------------------------------------------
 // embedding: bf16 row -> fp32 hidden (exact), token read from device memory.
 // ---------------------------------------------------------------------------
+// Token t = blockIdx.y reads id tok_ptr[t] and writes row t of out.
 __global__ void embed_bf16_kernel(const uint16_t* __restrict__ table, int vocab, int hidden,
                                   const int32_t* __restrict__ tok_ptr, float* __restrict__ out) {
-    int tok = *tok_ptr;
+    int tok = tok_ptr[blockIdx.y];
     if (tok < 0 || tok >= vocab) tok = abs(tok) % max(1, vocab);
     const uint16_t* row = table + static_cast<size_t>(tok) * hidden;
+    float* o = out + static_cast<size_t>(blockIdx.y) * hidden;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
-        out[i] = __uint_as_float(static_cast<uint32_t>(row[i]) << 16);
+        o[i] = __uint_as_float(static_cast<uint32_t>(row[i]) << 16);
 }
 
 hipError_t launch_embed(const EmbedLaunch& p, hipStream_t s) {
     const int blocks = min(16, (p.hidden + 255) / 256);
-    hipLaunchKernelGGL(embed_bf16_kernel, dim3(blocks), dim3(256), 0, s, p.table, p.vocab, p.hidden, p.tok, p.out);
+    hipLaunchKernelGGL(embed_bf16_kernel, dim3(blocks, max(1, p.tokens)), dim3(256), 0, s, p.table, p.vocab,
+                       p.hidden, p.tok, p.out);
     return hipGetLastError();
 }
 
@@ -41,21 +44,25 @@ hipError_t launch_embed(const EmbedLaunch& p, hipStream_t s) {
 // Block nq + h: kv head h: key RMSNorm + RoPE, key and value stored as fp16 at
 // cache slot `pos` ([t][kv_head][head_dim]).
 // ---------------------------------------------------------------------------
+// Batched form (prefill): token t = blockIdx.y at position *pos + t reads its
+// projections at t * src_stride and writes q/gate at t * out_stride.
 __global__ void qk_norm_rope_append_kernel(QkPrepLaunch p) {
     extern __shared__ float vals[];  // head_dim
     __shared__ float red[32];
     const int b = blockIdx.x;
+    const int t = blockIdx.y;
     const int hd = p.head_dim;
-    const int pos = *p.pos;
+    const int pos = *p.pos + t;
     const bool is_q = b < p.nq;
     const int h = is_q ? b : b - p.nq;
+    const size_t src_off = static_cast<size_t>(t) * p.src_stride;
     const float* src;
     const float* w;
     if (is_q) {
-        src = p.q_src + static_cast<size_t>(h) * (p.gated ? 2 * hd : hd);
+        src = p.q_src + src_off + static_cast<size_t>(h) * (p.gated ? 2 * hd : hd);
         w = p.q_norm;
     } else {
-        src = p.k_src + static_cast<size_t>(h) * hd;
+        src = p.k_src + src_off + static_cast<size_t>(h) * hd;
         w = p.k_norm;
     }
     float ss = 0.0f;
@@ -81,19 +88,20 @@ __global__ void qk_norm_rope_append_kernel(QkPrepLaunch p) {
             v = vals[d] * c.x + vals[d - half] * c.y;
         }
         if (is_q) {
-            p.q_out[static_cast<size_t>(h) * hd + d] = v;
-            p.gate_out[static_cast<size_t>(h) * hd + d] = p.gated ? src[hd + d] : 0.0f;
+            const size_t o = static_cast<size_t>(t) * p.out_stride + static_cast<size_t>(h) * hd + d;
+            p.q_out[o] = v;
+            p.gate_out[o] = p.gated ? src[hd + d] : 0.0f;
         } else {
             const size_t slot = (static_cast<size_t>(pos) * p.nkv + h) * hd + d;
             p.k_cache[slot] = static_cast<_Float16>(v);
-            p.v_cache[slot] = static_cast<_Float16>(p.v_src[static_cast<size_t>(h) * hd + d]);
+            p.v_cache[slot] = static_cast<_Float16>(p.v_src[src_off + static_cast<size_t>(h) * hd + d]);
         }
     }
 }
 
 hipError_t launch_qk_prep(const QkPrepLaunch& p, hipStream_t s) {
     const int threads = p.head_dim >= 256 ? 256 : (p.head_dim > 64 ? 128 : 64);
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(p.nq + p.nkv), dim3(threads),
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(p.nq + p.nkv, max(1, p.tokens)), dim3(threads),
                        static_cast<size_t>(p.head_dim) * sizeof(float), s, p);
     return hipGetLastError();
 }

@@ -1,0 +1,517 @@
+// prefill_ops.hip - the multi-token (prefill) kernels of the decode path on gfx950.
+//
+// The reference prefills token by token (CustomModel::prefill,
+// customlib/runtime/custom_model.cpp:610-640); the arithmetic per token is the
+// same as decode.  Here the dense contractions of a prompt chunk (the
+// q/k/v/o, gate/up and down projections of every layer for up to
+// kPrefillChunk tokens) run as one W4A16 GEMM each on the matrix cores, and
+// the sequential parts run as batched kernels:
+//   prep_x_kernel        per-token RMSNorm / gated head norm, x -> fp16 hi + lo
+//   gemm_w4_mfma_kernel  dequantise a 64x64 weight tile to fp16 hi + lo in LDS,
+//                        then v_mfma_f32_16x16x32_f16 on the hi/lo halves
+//   prefill_attn_kernel  causal GQA over the cache for every prompt token
+//   linear_scan_kernel   conv1d + L2 norm + gated delta over the chunk, with the
+//                        recurrent state and conv history held in registers
+#include "xqhip_common.hpp"
+#include "xqhip_kernels.hpp"
+
+namespace xqhip {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// B operand preparation: token t = blockIdx.x of x (row stride ldx) with the
+// prologue applied (RMS over the row, or per-head gated norm with the gate
+// row at t * ldz) -> xh[t][k] = fp16(v), xl[t][k] = fp16(v - xh): together
+// about 22 significant bits.  Rows m..m_pad-1 are zero-filled.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x, int ldx, int m, int cols,
+                                                     Prologue pro, int ldz, _Float16* __restrict__ xh,
+                                                     _Float16* __restrict__ xl) {
+    __shared__ float red[32];
+    const int t = blockIdx.x;
+    _Float16* oh = xh + static_cast<size_t>(t) * cols;
+    _Float16* ol = xl + static_cast<size_t>(t) * cols;
+    if (t >= m) {
+        for (int c = threadIdx.x; c < cols; c += blockDim.x) oh[c] = ol[c] = static_cast<_Float16>(0.0f);
+        return;
+    }
+    const float* xr = x + static_cast<size_t>(t) * ldx;
+    float inv = 1.0f;
+    if (pro.mode == PRO_RMS) {
+        float ss = 0.0f;
+        for (int c = threadIdx.x; c < cols; c += blockDim.x) ss += xr[c] * xr[c];
+        ss = block_sum(ss, red);
+        inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + pro.eps);
+    }
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    if (pro.mode == PRO_GATED) {
+        // one wave per head: inv_h, then the gated values of the head
+        const float* zr = pro.z + static_cast<size_t>(t) * ldz;
+        const int heads = cols / pro.head_dim;
+        for (int h = wid; h < heads; h += nw) {
+            const float* xv = xr + h * pro.head_dim;
+            float ss = 0.0f;
+            for (int d = lane; d < pro.head_dim; d += kWave) ss += xv[d] * xv[d];
+            ss = wave_sum(ss);
+            const float ih = 1.0f / sqrtf(ss / static_cast<float>(pro.head_dim) + pro.eps);
+            for (int d = lane; d < pro.head_dim; d += kWave) {
+                const int c = h * pro.head_dim + d;
+                const float v = xv[d] * ih * pro.w[d] * silu_dev(zr[c]);
+                const _Float16 hi = static_cast<_Float16>(v);
+                oh[c] = hi;
+                ol[c] = static_cast<_Float16>(v - static_cast<float>(hi));
+            }
+        }
+        return;
+    }
+    for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+        const float v = pro.mode == PRO_RMS ? xr[c] * inv * pro.w[c] : xr[c];
+        const _Float16 hi = static_cast<_Float16>(v);
+        oh[c] = hi;
+        ol[c] = static_cast<_Float16>(v - static_cast<float>(hi));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// W4A16 GEMM, y[t][r] (op)= sum_k w[r][k] x[t][k] for a prompt chunk.
+// Block: 64 weight rows x 64 tokens, 4 waves each owning 32 rows x 32 tokens
+// (2 x 2 tiles of v_mfma_f32_16x16x32_f16).  Per 64-column group: the block
+// dequantises its 64 rows of the TILED64 matrix (codes stored as q ^ 8) to
+// w = (q - z) s (v1) or q s + z (v2) in fp32 and keeps it in LDS as fp16
+// hi + lo halves, stages the hi and lo fp16 halves of its 64 tokens, and every
+// tile issues three MFMAs (w_hi x_hi, w_hi x_lo, w_lo x_hi; both operands then
+// carry about 22 significant bits, as in the fp32 reference).  Token
+// tiles are the fastest grid dimension, so the blocks that share a weight
+// tile run together and the tile is fetched from HBM about once.
+// MFMA operand layout (16x16x32): lane l supplies row/column (l & 15) and the
+// 8 consecutive k at 8 (l >> 4); lane l receives D[4 (l >> 4) + v][l & 15].
+// ---------------------------------------------------------------------------
+constexpr int kGemmRows = 64;
+constexpr int kGemmToks = 64;
+constexpr int kGemmLd = 72;  // LDS row stride in halves (64 + 8 padding)
+
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_w4_mfma_kernel(const uint8_t* __restrict__ nib,
+                                                           const uint32_t* __restrict__ meta, int rows, int cols,
+                                                           int affine, const _Float16* __restrict__ xh,
+                                                           const _Float16* __restrict__ xl, int m,
+                                                           float* __restrict__ y, int ldy) {
+    __shared__ _Float16 As[kGemmRows * kGemmLd];
+    __shared__ _Float16 Al[kGemmRows * kGemmLd];
+    __shared__ _Float16 Bh[kGemmToks * kGemmLd];
+    __shared__ _Float16 Bl[kGemmToks * kGemmLd];
+    const int t0 = blockIdx.x * kGemmToks;
+    const int r0 = blockIdx.y * kGemmRows;
+    const int G = cols >> 6;
+    const size_t row_bytes = static_cast<size_t>(cols) >> 1;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int wr = (wid >> 1) * 32, wt = (wid & 1) * 32;
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int g = 0; g < G; ++g) {
+        // weights: thread < 128 dequantises one 16-byte half (32 codes) of one row
+        if (threadIdx.x < 2 * kGemmRows) {
+            const int rl = threadIdx.x >> 1, h = threadIdx.x & 1;
+            const int r = r0 + rl;
+            _Float16* dst = As + rl * kGemmLd + h * 32;
+            _Float16* dstl = Al + rl * kGemmLd + h * 32;
+            if (r < rows) {
+                const int c = g >> 6, l = g & 63;
+                const int gcnt = min(64, G - c * 64);
+                const uint4 q16 = *reinterpret_cast<const uint4*>(nib + static_cast<size_t>(r) * row_bytes + c * 2048 +
+                                                                  h * gcnt * 16 + l * 16);
+                const uint32_t mt = meta[static_cast<size_t>(r) * G + g];
+                const float s = half_lo(mt), z = half_hi(mt);
+                const uint32_t wv[4] = {q16.x, q16.y, q16.z, q16.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float q = static_cast<float>(((wv[u] >> (4 * i)) & 15u) ^ 8u);
+                        const float wf = affine ? fmaf(q, s, z) : (q - z) * s;
+                        const _Float16 wh = static_cast<_Float16>(wf);
+                        dst[u * 8 + i] = wh;
+                        dstl[u * 8 + i] = static_cast<_Float16>(wf - static_cast<float>(wh));
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) dst[i] = dstl[i] = static_cast<_Float16>(0.0f);
+            }
+        }
+        // activations: 64 tokens x 64 columns of hi and lo, 16 bytes per load
+        {
+            const int tl = threadIdx.x >> 2, part = threadIdx.x & 3;
+            const size_t src = static_cast<size_t>(t0 + tl) * cols + g * 64 + part * 16;
+            const uint4* ph = reinterpret_cast<const uint4*>(xh + src);
+            const uint4* pl = reinterpret_cast<const uint4*>(xl + src);
+            uint4* dh = reinterpret_cast<uint4*>(Bh + tl * kGemmLd + part * 16);
+            uint4* dl = reinterpret_cast<uint4*>(Bl + tl * kGemmLd + part * 16);
+            dh[0] = ph[0];
+            dh[1] = ph[1];
+            dl[0] = pl[0];
+            dl[1] = pl[1];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int k = ks * 32 + (lane >> 4) * 8;
+            half8 a[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = *reinterpret_cast<const half8*>(As + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
+                al[i] = *reinterpret_cast<const half8*>(Al + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                bh[j] = *reinterpret_cast<const half8*>(Bh + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
+                bl[j] = *reinterpret_cast<const half8*>(Bl + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bh[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+    // epilogue: lane holds rows 4 (lane >> 4) + v of tile i, token (lane & 15) of tile j
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t = t0 + wt + j * 16 + (lane & 15);
+            const int rb = r0 + wr + i * 16 + 4 * (lane >> 4);
+            if (t >= m) continue;
+            float* yr = y + static_cast<size_t>(t) * ldy;
+            if constexpr (EPI == 2) {  // interleaved (gate, up) rows -> silu(gate) * up
+#pragma unroll
+                for (int v = 0; v < 4; v += 2)
+                    if (rb + v + 1 < rows) yr[(rb + v) >> 1] = silu_dev(acc[i][j][v]) * acc[i][j][v + 1];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (rb + v >= rows) continue;
+                    if constexpr (EPI == 1)
+                        yr[rb + v] += acc[i][j][v];
+                    else
+                        yr[rb + v] = acc[i][j][v];
+                }
+            }
+        }
+}
+
+size_t gemm_workspace_bytes(int m, int cols) {
+    const size_t m_pad = static_cast<size_t>((m + kGemmToks - 1) / kGemmToks) * kGemmToks;
+    return 2 * m_pad * static_cast<size_t>(cols) * sizeof(_Float16);
+}
+
+bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro) {
+    if (layout != 0 || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0) return false;
+    if (pro.mode == PRO_GATED)
+        return pro.head_dim > 0 && cols % pro.head_dim == 0;
+    return true;
+}
+
+hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
+    const int m_pad = (p.m + kGemmToks - 1) / kGemmToks * kGemmToks;
+    _Float16* xh = static_cast<_Float16*>(p.workspace);
+    _Float16* xl = xh + static_cast<size_t>(m_pad) * p.cols;
+    hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const dim3 grid(m_pad / kGemmToks, (p.rows + kGemmRows - 1) / kGemmRows);
+    const uint32_t* meta = static_cast<const uint32_t*>(p.meta);
+    switch (p.epi) {
+        case 0:
+            hipLaunchKernelGGL(gemm_w4_mfma_kernel<0>, grid, dim3(256), 0, s, p.nib, meta, p.rows, p.cols, p.affine,
+                               xh, xl, p.m, p.y, p.ldy);
+            break;
+        case 1:
+            hipLaunchKernelGGL(gemm_w4_mfma_kernel<1>, grid, dim3(256), 0, s, p.nib, meta, p.rows, p.cols, p.affine,
+                               xh, xl, p.m, p.y, p.ldy);
+            break;
+        case 2:
+            hipLaunchKernelGGL(gemm_w4_mfma_kernel<2>, grid, dim3(256), 0, s, p.nib, meta, p.rows, p.cols, p.affine,
+                               xh, xl, p.m, p.y, p.ldy);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA for a prompt chunk: block (t, kh) takes query token t (position
+// pos0 + t) and the `group` query heads of kv head kh over keys 0..pos0+t in
+// 64-token chunks with a running max / sum (rescaled by exp(m_old - m_new)),
+// then normalises by multiplying with 1/l and applies the sigmoid gate
+// (custom_model.cpp:840-951 per token).
+// ---------------------------------------------------------------------------
+constexpr int kPAttnChunk = 64;
+constexpr int kPAttnMaxGroup = 8;
+
+__global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnLaunch p) {
+    extern __shared__ float smem[];
+    const int t = blockIdx.x, kh = blockIdx.y;
+    const int hd = p.head_dim, group = p.nq / p.nkv;
+    const int ctx = *p.pos0 + t + 1;
+    float* qs = smem;                        // [group][hd]
+    float* sc = qs + group * hd;             // [group][64]
+    float* osum = sc + group * kPAttnChunk;  // [group][hd] running output
+    float* ml = osum + group * hd;           // [group][2] running max, sum
+    float* fac = ml + 2 * group;             // [group] rescale of this chunk
+    const float* qrow = p.q + static_cast<size_t>(t) * p.q_stride + static_cast<size_t>(kh) * group * hd;
+    for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
+        qs[i] = qrow[i];
+        osum[i] = 0.0f;
+    }
+    if (threadIdx.x < group) {
+        ml[2 * threadIdx.x] = -INFINITY;
+        ml[2 * threadIdx.x + 1] = 0.0f;
+    }
+    __syncthreads();
+    const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    for (int c0 = 0; c0 < ctx; c0 += kPAttnChunk) {
+        const int n = min(kPAttnChunk, ctx - c0);
+        // scores: 4 threads per key, each a quarter of the dims
+        {
+            const int sub = threadIdx.x & 3, tt = threadIdx.x >> 2;
+            const int dq = (hd + 3) / 4, d0 = sub * dq, d1 = min(hd, d0 + dq);
+            const bool valid = tt < n;
+            const _Float16* krow = p.k_cache + (static_cast<size_t>(c0 + (valid ? tt : 0)) * p.nkv + kh) * hd;
+            for (int g = 0; g < group; ++g) {
+                float dot = 0.0f;
+                for (int d = d0; d < d1; ++d) dot += qs[g * hd + d] * static_cast<float>(krow[d]);
+                dot += __shfl_xor(dot, 1, kWave);
+                dot += __shfl_xor(dot, 2, kWave);
+                if (valid && sub == 0) sc[g * kPAttnChunk + tt] = dot * rscale;
+            }
+        }
+        __syncthreads();
+        // online softmax update per head (one wave per head)
+        for (int g = wid; g < group; g += blockDim.x / kWave) {
+            const float sv = lane < n ? sc[g * kPAttnChunk + lane] : -INFINITY;
+            const float mc = wave_max(sv);
+            const float m_old = ml[2 * g];
+            const float m_new = fmaxf(m_old, mc);
+            const float e = lane < n ? expf(sv - m_new) : 0.0f;
+            const float lsum = wave_sum(e);
+            sc[g * kPAttnChunk + lane] = e;
+            if (lane == 0) {
+                const float f = expf(m_old - m_new);  // 0 for the first chunk
+                fac[g] = f;
+                ml[2 * g] = m_new;
+                ml[2 * g + 1] = ml[2 * g + 1] * f + lsum;
+            }
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
+            const int g = i / hd, d = i % hd;
+            float o = osum[i] * fac[g];
+            for (int j = 0; j < n; ++j)
+                o += sc[g * kPAttnChunk + j] *
+                     static_cast<float>(p.v_cache[(static_cast<size_t>(c0 + j) * p.nkv + kh) * hd + d]);
+            osum[i] = o;
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < group * hd; i += blockDim.x) {
+        const int g = i / hd;
+        const float l = ml[2 * g + 1];
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const size_t oi = static_cast<size_t>(t) * p.out_stride + static_cast<size_t>(kh) * group * hd + i;
+        const size_t gi = static_cast<size_t>(t) * p.q_stride + static_cast<size_t>(kh) * group * hd + i;
+        p.out[oi] = (osum[i] * inv) * sigmoid_dev(p.gate[gi]);
+    }
+}
+
+bool prefill_attn_supported(int nq, int nkv, int head_dim) {
+    return nkv > 0 && nq % nkv == 0 && nq / nkv <= kPAttnMaxGroup && head_dim > 0 &&
+           sizeof(float) * (2 * (nq / nkv) * head_dim + (nq / nkv) * (kPAttnChunk + 3)) <= 64 * 1024;
+}
+
+hipError_t launch_prefill_attn(const PrefillAttnLaunch& p, hipStream_t s) {
+    const int group = p.nq / p.nkv;
+    const size_t lds = sizeof(float) * (2 * static_cast<size_t>(group) * p.head_dim + group * (kPAttnChunk + 3));
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(p.tokens, p.nkv), dim3(256), lds, s, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Linear attention over a prompt chunk: block (vh, 16-column slice) runs the
+// decode step of linear_step_kernel for tokens 0..tokens-1 in order, with its
+// recurrent-state columns and the conv history of the channels it computes
+// held in registers for the whole chunk.  The history is read from hist_in
+// and the final one written to hist_out (distinct buffers: the caller picks
+// the parity copies); the q/k history is written by one block per key head,
+// the value history by the block that owns the channel.
+// ---------------------------------------------------------------------------
+constexpr int kScanCols = 16;
+constexpr int kScanIGroups = 16;
+constexpr int kScanMaxK = 16;     // key dim <= 256
+constexpr int kScanMaxHist = 7;   // conv kernel <= 8
+constexpr int kScanMaxQkPerThread = 2;
+
+__global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
+    __shared__ float qk[2 * 256];
+    __shared__ float vsh[kScanCols];
+    __shared__ float colsum[4][kScanCols];
+    __shared__ float red[2][4];
+    const int vh = blockIdx.x;
+    const int j0 = blockIdx.y * kScanCols;
+    const int factor = max(1, p.lv_n / max(1, p.lk_n));
+    const int kh = min(p.lk_n - 1, vh / factor);
+    const int dk = p.lk_hd, dv = p.lv_hd;
+    const int hist = max(0, p.ksize - 1);
+    const bool qk_writer = (vh % factor == 0) && blockIdx.y == 0;
+    const int jl = threadIdx.x % kScanCols;
+    const int ig = threadIdx.x / kScanCols;
+    const int j = j0 + jl;
+    const bool active = j < dv;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    float* S = p.state + static_cast<size_t>(vh) * dk * dv;
+    float sreg[kScanMaxK];
+#pragma unroll
+    for (int r = 0; r < kScanMaxK; ++r) {
+        const int i = ig + r * kScanIGroups;
+        sreg[r] = (active && i < dk) ? S[static_cast<size_t>(i) * dv + j] : 0.0f;
+    }
+    // channels this thread convolves: q/k channels tid and tid + 256 (< 2 dk),
+    // and (threads < 16) the value channel of column j0 + tid
+    int ch[kScanMaxQkPerThread + 1];
+    float hreg[kScanMaxQkPerThread + 1][kScanMaxHist];
+    float wreg[kScanMaxQkPerThread + 1][kScanMaxHist];
+    float wx[kScanMaxQkPerThread + 1];
+#pragma unroll
+    for (int u = 0; u <= kScanMaxQkPerThread; ++u) {
+        int c = -1;
+        if (u < kScanMaxQkPerThread) {
+            const int tq = threadIdx.x + u * 256;
+            if (tq < 2 * dk) c = (tq >= dk ? p.lk_n * dk : 0) + kh * dk + (tq >= dk ? tq - dk : tq);
+        } else if (threadIdx.x < kScanCols && j0 + static_cast<int>(threadIdx.x) < dv) {
+            c = 2 * p.lk_n * dk + vh * dv + j0 + threadIdx.x;
+        }
+        ch[u] = c;
+#pragma unroll
+        for (int i = 0; i < kScanMaxHist; ++i) {
+            hreg[u][i] = (c >= 0 && i < hist) ? p.hist_in[static_cast<size_t>(c) * hist + i] : 0.0f;
+            wreg[u][i] = (c >= 0 && i < hist) ? p.conv_w[static_cast<size_t>(c) * p.ksize + i] : 0.0f;
+        }
+        wx[u] = c >= 0 ? p.conv_w[static_cast<size_t>(c) * p.ksize + hist] : 0.0f;
+    }
+    const float rdk = 1.0f / sqrtf(static_cast<float>(dk));
+    for (int t = 0; t < p.tokens; ++t) {
+        const float* mixed = p.mixed + static_cast<size_t>(t) * p.mixed_stride;
+        float ssq = 0.0f, ssk = 0.0f;
+#pragma unroll
+        for (int u = 0; u <= kScanMaxQkPerThread; ++u) {
+            const int c = ch[u];
+            if (c < 0) continue;
+            const float xv = mixed[c];
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kScanMaxHist; ++i)
+                if (i < hist) acc += hreg[u][i] * wreg[u][i];
+            acc += xv * wx[u];
+#pragma unroll
+            for (int i = 0; i < kScanMaxHist; ++i) {
+                if (i + 1 < hist) hreg[u][i] = hreg[u][i + 1];
+                else if (i + 1 == hist) hreg[u][i] = xv;
+            }
+            const float yv = silu_dev(acc);
+            if (u < kScanMaxQkPerThread) {
+                const int tq = threadIdx.x + u * 256;
+                const bool is_k = tq >= dk;
+                qk[(is_k ? 256 : 0) + (is_k ? tq - dk : tq)] = yv;
+                if (is_k)
+                    ssk += yv * yv;
+                else
+                    ssq += yv * yv;
+            } else {
+                vsh[threadIdx.x] = yv;
+            }
+        }
+        ssq = wave_sum(ssq);
+        ssk = wave_sum(ssk);
+        if (lane == 0) {
+            red[0][wid] = ssq;
+            red[1][wid] = ssk;
+        }
+        const float beta = sigmoid_dev(p.b[static_cast<size_t>(t) * p.mixed_stride + vh]);
+        const float gate = -expf(p.a_log[vh]) * softplus_dev(p.a[static_cast<size_t>(t) * p.mixed_stride + vh] +
+                                                              p.dt_bias[vh]);
+        const float decay = expf(gate);
+        __syncthreads();
+        const float invq = 1.0f / sqrtf(red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1.0e-6f);
+        const float invk = 1.0f / sqrtf(red[1][0] + red[1][1] + red[1][2] + red[1][3] + 1.0e-6f);
+        const float vj = active ? vsh[jl] : 0.0f;
+        float pred = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kScanMaxK; ++r) {
+            const int i = ig + r * kScanIGroups;
+            if (active && i < dk) {
+                sreg[r] *= decay;
+                pred += sreg[r] * (qk[256 + i] * invk);
+            }
+        }
+        pred += __shfl_xor(pred, 16, kWave);
+        pred += __shfl_xor(pred, 32, kWave);
+        if (lane < kScanCols) colsum[wid][lane] = pred;
+        __syncthreads();
+        pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
+        __syncthreads();
+        const float delta = active ? beta * (vj - pred) : 0.0f;
+        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kScanMaxK; ++r) {
+            const int i = ig + r * kScanIGroups;
+            if (active && i < dk) {
+                sreg[r] += (qk[256 + i] * invk) * delta;
+                o += sreg[r] * (qk[i] * invq);
+            }
+        }
+        o += __shfl_xor(o, 16, kWave);
+        o += __shfl_xor(o, 32, kWave);
+        if (lane < kScanCols) colsum[wid][lane] = o;
+        __syncthreads();
+        if (threadIdx.x < kScanCols && active) {
+            const float tot = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
+            p.out[static_cast<size_t>(t) * p.out_stride + static_cast<size_t>(vh) * dv + j] = tot * rdk;
+        }
+        __syncthreads();  // qk, vsh, red and colsum are rewritten by the next token
+    }
+#pragma unroll
+    for (int r = 0; r < kScanMaxK; ++r) {
+        const int i = ig + r * kScanIGroups;
+        if (active && i < dk) S[static_cast<size_t>(i) * dv + j] = sreg[r];
+    }
+#pragma unroll
+    for (int u = 0; u <= kScanMaxQkPerThread; ++u) {
+        const int c = ch[u];
+        if (c < 0 || (u < kScanMaxQkPerThread && !qk_writer)) continue;
+#pragma unroll
+        for (int i = 0; i < kScanMaxHist; ++i)
+            if (i < hist) p.hist_out[static_cast<size_t>(c) * hist + i] = hreg[u][i];
+    }
+}
+
+bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
+    return lk_n > 0 && lv_n > 0 && lv_n % lk_n == 0 && lk_hd > 0 && lk_hd <= 256 && lv_hd > 0 && ksize >= 1 &&
+           ksize - 1 <= kScanMaxHist && lk_hd <= kScanIGroups * kScanMaxK;
+}
+
+hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
+    hipLaunchKernelGGL(linear_scan_kernel, dim3(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace xqhip

@@ -471,6 +471,120 @@ int xqhip_linear_attn_step(const float* mixed, float* conv_state, const float* c
     return check(xqhip::launch_linear_step(p, as_stream(stream)), "linear step launch");
 }
 
+// ---- prefill (multi-token) ---------------------------------------------------
+
+size_t xqhip_gemm_workspace_bytes(int m, int cols) { return m > 0 && cols > 0 ? xqhip::gemm_workspace_bytes(m, cols) : 0; }
+
+int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro, int ld_gate,
+                     float* y, int ldy, int epilogue, void* workspace, void* stream) {
+    if (int rc = validate_w4(w, "xqhip_gemm_w4a16")) return rc;
+    if (int rc = validate_prologue(pro, w->cols, "xqhip_gemm_w4a16")) return rc;
+    if (!x || !y || !workspace || m <= 0 || ldx < w->cols)
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: bad vectors (m=%d ldx=%d)", m, ldx);
+    if (epilogue < XQHIP_EPI_STORE || epilogue > XQHIP_EPI_SILU_PAIR)
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: unknown epilogue %d", epilogue);
+    const int out_cols = epilogue == XQHIP_EPI_SILU_PAIR ? w->rows / 2 : w->rows;
+    if ((epilogue == XQHIP_EPI_SILU_PAIR && w->rows % 2 != 0) || ldy < out_cols)
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: bad output layout (rows=%d ldy=%d)", w->rows, ldy);
+    const xqhip::Prologue pr = make_prologue(pro);
+    if (pr.mode == xqhip::PRO_GATED && ld_gate < w->cols)
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: gate row stride %d < cols", ld_gate);
+    if (!xqhip::gemm_supported(w->rows, w->cols, w->group, w->layout, pr))
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: needs a TILED64 matrix (%dx%d g%d)", w->rows, w->cols, w->group);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: workspace must be 16-byte aligned");
+    xqhip::GemmLaunch p{};
+    p.nib = static_cast<const uint8_t*>(w->nib);
+    p.meta = w->meta;
+    p.rows = w->rows;
+    p.cols = w->cols;
+    p.affine = w->affine;
+    p.x = x;
+    p.ldx = ldx;
+    p.m = m;
+    p.pro = pr;
+    p.ldz = ld_gate;
+    p.y = y;
+    p.ldy = ldy;
+    p.epi = epilogue;
+    p.workspace = workspace;
+    return check(xqhip::launch_gemm(p, as_stream(stream)), "gemm launch");
+}
+
+int xqhip_embed_bf16_batch(const uint16_t* table, int vocab, int hidden, const int32_t* tokens, int n, float* out,
+                           void* stream) {
+    if (!table || !tokens || !out || vocab <= 0 || hidden <= 0 || n <= 0 || n > 65535)
+        return fail(XQHIP_EINVAL, "xqhip_embed_bf16_batch: bad args");
+    xqhip::EmbedLaunch p{table, vocab, hidden, tokens, out, n};
+    return check(xqhip::launch_embed(p, as_stream(stream)), "embed batch launch");
+}
+
+int xqhip_attn_prep_batch(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
+                          int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
+                          const float* rope_cs, const int32_t* pos0, int tokens, int src_stride, int out_stride,
+                          float* q_out, float* gate_out, void* k_cache, void* v_cache, void* stream) {
+    if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !pos0 || !q_out || !gate_out || !k_cache || !v_cache ||
+        nq <= 0 || nkv <= 0 || head_dim <= 0 || head_dim > 1024 || (rotary_dim > 0 && !rope_cs) || tokens <= 0 ||
+        tokens > 65535 || out_stride < nq * head_dim)
+        return fail(XQHIP_EINVAL, "xqhip_attn_prep_batch: bad args");
+    const int active = std::max(0, std::min(head_dim, rotary_dim));
+    xqhip::QkPrepLaunch p{};
+    p.q_src = q_src;
+    p.k_src = k_src;
+    p.v_src = v_src;
+    p.gated = gated;
+    p.nq = nq;
+    p.nkv = nkv;
+    p.head_dim = head_dim;
+    p.rotary_dim = active;
+    p.rope_pairs = active / 2;
+    p.q_norm = q_norm;
+    p.k_norm = k_norm;
+    p.eps = eps;
+    p.rope_cs = rope_cs;
+    p.pos = pos0;
+    p.q_out = q_out;
+    p.gate_out = gate_out;
+    p.k_cache = static_cast<_Float16*>(k_cache);
+    p.v_cache = static_cast<_Float16*>(v_cache);
+    p.tokens = tokens;
+    p.src_stride = src_stride;
+    p.out_stride = out_stride;
+    return check(xqhip::launch_qk_prep(p, as_stream(stream)), "attn_prep batch launch");
+}
+
+int xqhip_prefill_attention(const float* q, const float* gate, const void* k_cache, const void* v_cache, int nq,
+                            int nkv, int head_dim, int tokens, int q_stride, const int32_t* pos0, float* out,
+                            int out_stride, void* stream) {
+    if (!q || !gate || !k_cache || !v_cache || !pos0 || !out || tokens <= 0 || tokens > 65535 ||
+        q_stride < nq * head_dim || out_stride < nq * head_dim || !xqhip::prefill_attn_supported(nq, nkv, head_dim))
+        return fail(XQHIP_EINVAL, "xqhip_prefill_attention: bad args (nq=%d nkv=%d hd=%d)", nq, nkv, head_dim);
+    xqhip::PrefillAttnLaunch p{q, gate, static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache),
+                               nq, nkv, head_dim, tokens, q_stride, out_stride, pos0, out};
+    return check(xqhip::launch_prefill_attn(p, as_stream(stream)), "prefill attention launch");
+}
+
+int xqhip_linear_attn_scan(const float* mixed, const float* a, const float* b, int stride, float* conv_state,
+                           int pos0, const float* conv_w, const float* a_log, const float* dt_bias, float* state,
+                           int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, int tokens, float* out,
+                           int out_stride, void* stream) {
+    if (!mixed || !a || !b || !conv_state || !conv_w || !a_log || !dt_bias || !state || !out || tokens <= 0 ||
+        pos0 < 0 || !xqhip::linear_scan_supported(lk_n, lk_hd, lv_n, lv_hd, ksize) || out_stride < lv_n * lv_hd)
+        return fail(XQHIP_EINVAL, "xqhip_linear_attn_scan: bad args");
+    const int conv_dim = 2 * lk_n * lk_hd + lv_n * lv_hd;
+    const size_t hist_floats = static_cast<size_t>(conv_dim) * std::max(0, ksize - 1);
+    float* copy_in = conv_state + static_cast<size_t>(pos0 & 1) * hist_floats;
+    float* copy_next = conv_state + static_cast<size_t>((pos0 + tokens) & 1) * hist_floats;
+    float* other = conv_state + static_cast<size_t>((pos0 & 1) ^ 1) * hist_floats;
+    xqhip::LinearScanLaunch p{mixed, a, b, stride, copy_in, other, conv_w, a_log, dt_bias, state,
+                              lk_n, lk_hd, lv_n, lv_hd, ksize, tokens, out, out_stride};
+    if (int rc = check(xqhip::launch_linear_scan(p, as_stream(stream)), "linear scan launch")) return rc;
+    // the next position reads copy (pos0 + tokens) & 1: when that is the input
+    // copy (even token count), move the new history there
+    if (copy_next != other && hist_floats > 0) return xqhip_copy(copy_next, other, hist_floats * sizeof(float), stream);
+    return XQHIP_OK;
+}
+
 int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream) {
     if (!x || !w || !y || n <= 0) return fail(XQHIP_EINVAL, "xqhip_rmsnorm: bad args");
     return check(xqhip::launch_rmsnorm(x, w, n, eps, y, as_stream(stream)), "rmsnorm launch");

@@ -44,8 +44,9 @@ hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s);
 struct EmbedLaunch {
     const uint16_t* table;
     int vocab, hidden;
-    const int32_t* tok;
-    float* out;
+    const int32_t* tok;  // [tokens]
+    float* out;          // [tokens][hidden]
+    int tokens;
 };
 hipError_t launch_embed(const EmbedLaunch& p, hipStream_t s);
 
@@ -63,6 +64,9 @@ struct QkPrepLaunch {
     float* gate_out;
     _Float16* k_cache;
     _Float16* v_cache;
+    int tokens;      // batch of consecutive positions *pos .. *pos + tokens - 1
+    int src_stride;  // floats between consecutive tokens' projection rows
+    int out_stride;  // floats between consecutive tokens' q / gate rows
 };
 hipError_t launch_qk_prep(const QkPrepLaunch& p, hipStream_t s);
 
@@ -126,5 +130,53 @@ bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
 hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s);
 
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
+
+// prefill_ops.hip: multi-token kernels of a prompt chunk.
+struct GemmLaunch {
+    const uint8_t* nib;  // TILED64 matrix
+    const void* meta;
+    int rows, cols, affine;
+    const float* x;  // [m][ldx]
+    int ldx, m;
+    Prologue pro;  // per token; PRO_GATED reads pro.z + t * ldz
+    int ldz;
+    float* y;  // [m][ldy]
+    int ldy;
+    int epi;          // 0 store, 1 add, 2 silu pair
+    void* workspace;  // gemm_workspace_bytes(m, cols)
+};
+size_t gemm_workspace_bytes(int m, int cols);
+bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro);
+hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s);
+
+struct PrefillAttnLaunch {
+    const float* q;     // [tokens][q_stride], heads [nq][hd]
+    const float* gate;  // same layout as q
+    const _Float16* k_cache;
+    const _Float16* v_cache;
+    int nq, nkv, head_dim, tokens, q_stride, out_stride;
+    const int32_t* pos0;  // device: position of token 0
+    float* out;           // [tokens][out_stride]
+};
+bool prefill_attn_supported(int nq, int nkv, int head_dim);
+hipError_t launch_prefill_attn(const PrefillAttnLaunch& p, hipStream_t s);
+
+struct LinearScanLaunch {
+    const float* mixed;  // [tokens][mixed_stride]: conv input channels q | k | v
+    const float* a;      // [tokens][mixed_stride] rows, lv_n values each
+    const float* b;
+    int mixed_stride;
+    const float* hist_in;  // [conv_dim][ksize - 1] history before token 0
+    float* hist_out;       // [conv_dim][ksize - 1] history after the last token (not hist_in)
+    const float* conv_w;
+    const float* a_log;
+    const float* dt_bias;
+    float* state;  // [lv_n][lk_hd][lv_hd]
+    int lk_n, lk_hd, lv_n, lv_hd, ksize, tokens;
+    float* out;  // [tokens][out_stride]
+    int out_stride;
+};
+bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
+hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s);
 
 }  // namespace xqhip

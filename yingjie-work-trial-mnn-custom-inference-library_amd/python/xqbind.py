@@ -76,6 +76,18 @@ _HIP_SIGS = {
                                   c_int, c_void_p, c_void_p]),
     "xqhip_linear_attn_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "xqhip_gemm_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "xqhip_gemm_w4a16": (c_int, [_P(W4), c_void_p, c_int, c_int, _P(Prologue), c_int, c_void_p, c_int, c_int,
+                                 c_void_p, c_void_p]),
+    "xqhip_embed_bf16_batch": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p]),
+    "xqhip_attn_prep_batch": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                      c_void_p, c_float, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
+                                      c_void_p, c_void_p, c_void_p]),
+    "xqhip_prefill_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                        c_void_p, c_void_p, c_int, c_void_p]),
+    "xqhip_linear_attn_scan": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int,
+                                       c_void_p]),
     "xqhip_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]),
     "xqhip_stream_create": (c_int, [_P(c_void_p)]),
     "xqhip_stream_destroy": (c_int, [c_void_p]),
