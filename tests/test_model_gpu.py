@@ -120,6 +120,37 @@ def test_generate_matches_oracle(which, tiny_dir, small_dir):
     assert m1.prompt_tokens == len(prompt) and m1.generated_tokens == n_new
 
 
+@pytest.mark.parametrize("n_prompt", [37, 600])
+def test_batched_prefill_matches_oracle(small_dir, n_prompt, monkeypatch):
+    """The chunked prefill (MFMA GEMMs, causal prefill attention, linear-attention
+    scan; 600 tokens = two chunks) against the oracle's token-by-token prefill
+    (custom_model.cpp:610-640), and against this library's own token-serial
+    prefill (XQ_PREFILL_BATCH=0): hidden state after prefill within tolerance,
+    then greedy steps exact under the margin rule."""
+    prompt = [int(t) for t in np.random.default_rng(n_prompt).integers(0, 4096, n_prompt)]
+    want, margins, hiddens = oracle_run(small_dir, prompt, 6)
+    runs = {}
+    for mode in ("batched", "serial"):
+        if mode == "serial":
+            monkeypatch.setenv("XQ_PREFILL_BATCH", "0")
+        s = xb.Session(small_dir, xb.options())
+        assert s.status == xb.XQ_OK
+        st, m = s.prefill(prompt)
+        assert st == 0 and m.prompt_tokens == n_prompt
+        close(s.hidden()[1], hiddens[0], f"{mode} prefill hidden ({n_prompt} tokens)")
+        got = []
+        for _ in range(6):
+            st, tok, m = s.decode_one()
+            assert st == 0
+            got.append(tok)
+        compare_tokens(got, want, margins)
+        runs[mode] = s.json("xq_get_kernel_trace_json")[1]
+        s.close()
+    assert "prefill_gemm_w4a16_mfma" in runs["batched"] and "prefill_gemm_w4a16_mfma" not in runs["serial"]
+    rows = json.loads(runs["batched"])["rows"]
+    assert next(r for r in rows if r["name"] == "prefill_token_custom")["calls"] == n_prompt
+
+
 def test_debug_json_and_hidden_buffer_rules(small_dir):
     s = xb.Session(small_dir, xb.options())
     assert s.status == 0

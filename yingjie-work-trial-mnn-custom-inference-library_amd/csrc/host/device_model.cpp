@@ -262,6 +262,9 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
         if (!upload_vec(tab, &rope_cs_, error)) return false;
     }
     (void)any_linear;
+    max_proj_ = max_proj;
+    attn_n_ = attn_n;
+    if (!alloc_prefill_buffers(error)) return false;
     void* pinned = nullptr;
     if (xqhip_host_alloc(&pinned, 4 * sizeof(int32_t)) != 0) return fail_hip(error, "pinned memory");
     h_tok_ = static_cast<int32_t*>(pinned);
@@ -411,6 +414,106 @@ bool DeviceModel::ensure_graphs(std::string* error) {
     return true;
 }
 
+// Batched prefill needs every matrix in the TILED64 layout (group 64) and the
+// shapes of the chunk kernels; tiny models prefill token by token through the
+// decode-step kernels.  XQ_PREFILL_BATCH=0 forces the token-by-token path.
+bool DeviceModel::alloc_prefill_buffers(std::string* error) {
+    const char* env = std::getenv("XQ_PREFILL_BATCH");
+    if (env && env[0] == '0') return true;
+    bool ok = hidden_ % 4 == 0 && inter_ % 4 == 0 && attn_n_ % 4 == 0 && max_proj_ % 4 == 0;
+    for (const Layer& L : layers_) {
+        for (const xqhip_w4* w : {&L.in_proj, &L.out_proj, &L.gate_up, &L.down})
+            ok = ok && w->layout == XQHIP_LAYOUT_TILED64;
+        if (!L.full) ok = ok && lk_hd_ <= 256 && lv_n_ % lk_n_ == 0 && ksize_ >= 1 && ksize_ <= 8 && lv_hd_ % 8 == 0;
+    }
+    ok = ok && (nq_ / nkv_) <= 8;
+    if (!ok) return true;
+    const size_t c = static_cast<size_t>(chunk_);
+    const int max_cols = std::max({hidden_, inter_, attn_n_});
+    uint8_t* ws = nullptr;
+    if (!alloc(&x_all_, c * hidden_, error) || !alloc(&proj_all_, c * max_proj_, error) ||
+        !alloc(&q_all_, c * nq_ * hd_, error) || !alloc(&gate_all_, c * nq_ * hd_, error) ||
+        !alloc(&attn_all_, c * attn_n_, error) || !alloc(&ffn_all_, c * inter_, error) ||
+        !alloc(&ws, xqhip_gemm_workspace_bytes(chunk_, max_cols), error) || !alloc(&tok_dev_, c, error))
+        return false;
+    gemm_ws_ = ws;
+    batched_prefill_ = true;
+    return true;
+}
+
+// One prompt chunk of n tokens at positions pos0 .. pos0+n-1 through every
+// layer; the last token's residual stream ends in resid_.
+// h_tokens / h_pos: pinned host copies that stay untouched until the chunk ran.
+bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, int n, int pos0, bool timed,
+                                std::string* error) {
+    XQ_CALL(xqhip_memcpy_h2d_async(tok_dev_, h_tokens, sizeof(int32_t) * n, stream_), "prompt upload");
+    XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_pos, sizeof(int32_t), stream_), "position upload");
+    const int32_t* pos = d_ctrl_;
+    op_begin(timed, "prefill_embedding_bf16_rows");
+    XQ_CALL(xqhip_embed_bf16_batch(embed_, vocab_, hidden_, tok_dev_, n, x_all_, stream_), "prefill embedding");
+    op_end(timed);
+    const int qd = nq_ * hd_;
+    for (Layer& L : layers_) {
+        xqhip_prologue rms_in{XQHIP_PRO_RMS, 0, L.in_norm, nullptr, eps_};
+        op_begin(timed, L.full ? "prefill_gemm_w4a16_mfma(q_proj,k_proj,v_proj,rmsnorm_input)"
+                               : "prefill_gemm_w4a16_mfma(in_proj_qkv,in_proj_a,in_proj_b,in_proj_z,rmsnorm_input)");
+        XQ_CALL(xqhip_gemm_w4a16(&L.in_proj, x_all_, n, hidden_, &rms_in, 0, proj_all_, max_proj_, XQHIP_EPI_STORE,
+                                 gemm_ws_, stream_),
+                "prefill input projection");
+        op_end(timed);
+        if (L.full) {
+            const float* k_src = proj_all_ + static_cast<size_t>(qd) * (L.q_gated ? 2 : 1);
+            const float* v_src = k_src + static_cast<size_t>(nkv_) * hd_;
+            op_begin(timed, "prefill_kv_build_custom(fused:q_norm,k_norm,rope,kv_append)");
+            XQ_CALL(xqhip_attn_prep_batch(proj_all_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm,
+                                          L.k_norm, eps_, rope_cs_, pos, n, max_proj_, qd, q_all_, gate_all_,
+                                          L.k_cache, L.v_cache, stream_),
+                    "prefill attention prep");
+            op_end(timed);
+            op_begin(timed, "prefill_attention_gqa_causal_custom(fused:output_gate)");
+            XQ_CALL(xqhip_prefill_attention(q_all_, gate_all_, L.k_cache, L.v_cache, nq_, nkv_, hd_, n, qd, pos,
+                                            attn_all_, attn_n_, stream_),
+                    "prefill attention");
+            op_end(timed);
+            op_begin(timed, "prefill_gemm_w4a16_mfma(o_proj,residual_add)");
+            XQ_CALL(xqhip_gemm_w4a16(&L.out_proj, attn_all_, n, attn_n_, nullptr, 0, x_all_, hidden_, XQHIP_EPI_ADD,
+                                     gemm_ws_, stream_),
+                    "prefill o projection");
+            op_end(timed);
+        } else {
+            const float* a = proj_all_ + conv_dim_;
+            const float* b = a + lv_n_;
+            const float* z = b + lv_n_;
+            op_begin(timed, "linear_attention_state_update_custom(prefill_scan:conv1d,qk_l2norm,gated_delta)");
+            XQ_CALL(xqhip_linear_attn_scan(proj_all_, a, b, max_proj_, L.conv_state, pos0, L.conv_w, L.a_log,
+                                           L.dt_bias, L.rec_state, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, n, attn_all_,
+                                           attn_n_, stream_),
+                    "prefill linear-attention scan");
+            op_end(timed);
+            xqhip_prologue gated{XQHIP_PRO_GATED_HEAD, lv_hd_, L.lin_norm, z, eps_};
+            op_begin(timed, "prefill_gemm_w4a16_mfma(out_proj,gated_rmsnorm,residual_add)");
+            XQ_CALL(xqhip_gemm_w4a16(&L.out_proj, attn_all_, n, attn_n_, &gated, max_proj_, x_all_, hidden_,
+                                     XQHIP_EPI_ADD, gemm_ws_, stream_),
+                    "prefill out projection");
+            op_end(timed);
+        }
+        xqhip_prologue rms_post{XQHIP_PRO_RMS, 0, L.post_norm, nullptr, eps_};
+        op_begin(timed, "prefill_gemm_w4a16_mfma(gate_proj,up_proj,rmsnorm_post_attention,silu_gate_mul)");
+        XQ_CALL(xqhip_gemm_w4a16(&L.gate_up, x_all_, n, hidden_, &rms_post, 0, ffn_all_, inter_, XQHIP_EPI_SILU_PAIR,
+                                 gemm_ws_, stream_),
+                "prefill gate/up projection");
+        op_end(timed);
+        op_begin(timed, "prefill_gemm_w4a16_mfma(down_proj,residual_add)");
+        XQ_CALL(xqhip_gemm_w4a16(&L.down, ffn_all_, n, inter_, nullptr, 0, x_all_, hidden_, XQHIP_EPI_ADD, gemm_ws_,
+                                 stream_),
+                "prefill down projection");
+        op_end(timed);
+    }
+    XQ_CALL(xqhip_copy(resid_, x_all_ + static_cast<size_t>(n - 1) * hidden_, sizeof(float) * hidden_, stream_),
+            "last hidden");
+    return true;
+}
+
 bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace* trace, std::string* error) {
     if (!token_ids || n_tokens == 0) {  // custom_model.cpp:611-614
         *error = "custom prefill requires prompt tokens";
@@ -438,6 +541,34 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
     }
     // per-token boundary events live at the top of the pool, op events at the bottom
     auto tok_ev = [&](size_t i) { return event_pool_[event_pool_.size() - 1 - i]; };
+    if (batched_prefill_ && n_tokens > 1) {
+        // chunks of up to chunk_ tokens; every token of a chunk is credited the
+        // chunk's time / its size in the prefill_token_custom rows
+        const size_t n_chunks = (n_tokens + chunk_ - 1) / chunk_;
+        for (size_t i = 0; i < n_tokens; ++i) h_ctrl_[i] = token_ids[i];  // pinned: [tokens][chunk positions]
+        xqhip_event_record(tok_ev(0), stream_);
+        for (size_t c = 0; c < n_chunks; ++c) {
+            const size_t p0 = c * chunk_;
+            const int n = static_cast<int>(std::min<size_t>(chunk_, n_tokens - p0));
+            h_ctrl_[n_tokens + c] = static_cast<int32_t>(p0);
+            if (!prefill_chunk(h_ctrl_ + p0, h_ctrl_ + n_tokens + c, n, static_cast<int>(p0), c == 0 && detail_prefill_,
+                               error))
+                return false;
+            xqhip_event_record(tok_ev(c + 1), stream_);
+        }
+        XQ_CALL(xqhip_stream_synchronize(stream_), "prefill");
+        detail_prefill_ = false;
+        if (trace) {
+            for (size_t c = 0; c < n_chunks; ++c) {
+                const size_t n = std::min<size_t>(chunk_, n_tokens - c * chunk_);
+                const double ms = elapsed_ms(tok_ev(c), tok_ev(c + 1));
+                for (size_t i = 0; i < n; ++i) trace->add("prefill_token_custom", ms / n, kTraceBackend);
+            }
+        }
+        flush_timed(trace);
+        detail_decode_ = true;
+        return true;
+    }
     xqhip_event_record(tok_ev(0), stream_);
     for (size_t i = 0; i < n_tokens; ++i) {
         h_ctrl_[2 * i] = static_cast<int32_t>(i);

@@ -86,6 +86,10 @@ private:
     void op_end(bool timed);
     void flush_timed(KernelTrace* trace);
     bool ensure_graphs(std::string* error);
+    // batched prefill of prompt chunks (GEMMs on the matrix cores)
+    bool prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, int n, int pos0, bool timed,
+                       std::string* error);
+    bool alloc_prefill_buffers(std::string* error);
     bool fail_hip(std::string* error, const char* what);
 
     // dimensions (defaults of custom_model.hpp:98-114)
@@ -124,6 +128,18 @@ private:
     void* g_prefill_ = nullptr;  // graph: embed(input token) + layers
     void* g_decode_ = nullptr;   // graph: lm_head argmax -> embed(sampled) + layers
     bool detail_prefill_ = true, detail_decode_ = true;
+    // prompt-chunk buffers, [token][...] rows (allocated when every matrix is TILED64)
+    bool batched_prefill_ = false;
+    int chunk_ = 512;
+    int max_proj_ = 1, attn_n_ = 1;
+    float* x_all_ = nullptr;     // [chunk][hidden] residual stream
+    float* proj_all_ = nullptr;  // [chunk][max_proj] fused input projections
+    float* q_all_ = nullptr;     // [chunk][nq * hd]
+    float* gate_all_ = nullptr;  // [chunk][nq * hd]
+    float* attn_all_ = nullptr;  // [chunk][attn_n] attention / delta output
+    float* ffn_all_ = nullptr;   // [chunk][inter]
+    void* gemm_ws_ = nullptr;
+    int32_t* tok_dev_ = nullptr;  // [chunk]
     std::vector<TimedOp> ops_;
     std::vector<void*> event_pool_;
     size_t event_next_ = 0;
