@@ -409,14 +409,31 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
         wx[u] = c >= 0 ? p.conv_w[static_cast<size_t>(c) * p.ksize + hist] : 0.0f;
     }
     const float rdk = 1.0f / sqrtf(static_cast<float>(dk));
-    for (int t = 0; t < p.tokens; ++t) {
+    const float neg_exp_alog = -expf(p.a_log[vh]);
+    const float dtb = p.dt_bias[vh];
+    // inputs of token t + 1 are loaded while token t is computed
+    float xnext[kScanMaxQkPerThread + 1];
+    float a_next = 0.0f, b_next = 0.0f;
+    auto load_token = [&](int t) {
         const float* mixed = p.mixed + static_cast<size_t>(t) * p.mixed_stride;
+#pragma unroll
+        for (int u = 0; u <= kScanMaxQkPerThread; ++u) xnext[u] = ch[u] >= 0 ? mixed[ch[u]] : 0.0f;
+        a_next = p.a[static_cast<size_t>(t) * p.mixed_stride + vh];
+        b_next = p.b[static_cast<size_t>(t) * p.mixed_stride + vh];
+    };
+    load_token(0);
+    for (int t = 0; t < p.tokens; ++t) {
+        float xcur[kScanMaxQkPerThread + 1];
+#pragma unroll
+        for (int u = 0; u <= kScanMaxQkPerThread; ++u) xcur[u] = xnext[u];
+        const float a_cur = a_next, b_cur = b_next;
+        if (t + 1 < p.tokens) load_token(t + 1);
         float ssq = 0.0f, ssk = 0.0f;
 #pragma unroll
         for (int u = 0; u <= kScanMaxQkPerThread; ++u) {
             const int c = ch[u];
             if (c < 0) continue;
-            const float xv = mixed[c];
+            const float xv = xcur[u];
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < kScanMaxHist; ++i)
@@ -446,9 +463,8 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
             red[0][wid] = ssq;
             red[1][wid] = ssk;
         }
-        const float beta = sigmoid_dev(p.b[static_cast<size_t>(t) * p.mixed_stride + vh]);
-        const float gate = -expf(p.a_log[vh]) * softplus_dev(p.a[static_cast<size_t>(t) * p.mixed_stride + vh] +
-                                                              p.dt_bias[vh]);
+        const float beta = sigmoid_dev(b_cur);
+        const float gate = neg_exp_alog * softplus_dev(a_cur + dtb);
         const float decay = expf(gate);
         __syncthreads();
         const float invq = 1.0f / sqrtf(red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1.0e-6f);
