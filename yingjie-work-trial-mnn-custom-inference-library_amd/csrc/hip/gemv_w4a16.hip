@@ -126,6 +126,31 @@ __device__ __forceinline__ void unpack8_f16(float* v) {
     v[4] = half_lo(c); v[5] = half_hi(c); v[6] = half_lo(d); v[7] = half_hi(d);
 }
 
+// Nibble transpose: W[d] nibble i = hex digit d of U[i] (i < 8, d < 6).
+// Bytes are gathered with v_perm_b32 (A_k: byte k of U0, U2, U4, U6; B_k:
+// byte k of U1, U3, U5, U7), then each byte's two digits are split with one
+// bit-field insert each, so nibble 2j / 2j+1 of a word come from U_2j / U_2j+1.
+__device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&W)[kDigits]) {
+    static_assert(kDigits == 6, "three bytes of digits");
+    const uint32_t p02 = __builtin_amdgcn_perm(U[2], U[0], 0x05010400u);  // U0.b0 U2.b0 U0.b1 U2.b1
+    const uint32_t q02 = __builtin_amdgcn_perm(U[2], U[0], 0x07030602u);  // U0.b2 U2.b2 U0.b3 U2.b3
+    const uint32_t p46 = __builtin_amdgcn_perm(U[6], U[4], 0x05010400u);
+    const uint32_t q46 = __builtin_amdgcn_perm(U[6], U[4], 0x07030602u);
+    const uint32_t p13 = __builtin_amdgcn_perm(U[3], U[1], 0x05010400u);
+    const uint32_t q13 = __builtin_amdgcn_perm(U[3], U[1], 0x07030602u);
+    const uint32_t p57 = __builtin_amdgcn_perm(U[7], U[5], 0x05010400u);
+    const uint32_t q57 = __builtin_amdgcn_perm(U[7], U[5], 0x07030602u);
+    const uint32_t A[3] = {__builtin_amdgcn_perm(p46, p02, 0x05040100u), __builtin_amdgcn_perm(p46, p02, 0x07060302u),
+                           __builtin_amdgcn_perm(q46, q02, 0x05040100u)};
+    const uint32_t B[3] = {__builtin_amdgcn_perm(p57, p13, 0x05040100u), __builtin_amdgcn_perm(p57, p13, 0x07060302u),
+                           __builtin_amdgcn_perm(q57, q13, 0x05040100u)};
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        W[2 * k] = (A[k] & 0x0F0F0F0Fu) | ((B[k] << 4) & 0xF0F0F0F0u);
+        W[2 * k + 1] = ((A[k] >> 4) & 0x0F0F0F0Fu) | (B[k] & 0xF0F0F0F0u);
+    }
+}
+
 template <int THREADS, int ITEMS, typename Prefetch>
 __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f16, const Prologue& pro, int cols,
                                             uint4* __restrict__ xs, float* red, Prefetch&& prefetch) {
@@ -231,13 +256,10 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
             uint32_t U[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) U[i] = static_cast<uint32_t>(X[i]) + kDigitBias;
+            uint32_t W[kDigits];
+            digit_words(U, W);
 #pragma unroll
-            for (int d = 0; d < kDigits; ++d) {
-                uint32_t word = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) word |= ((U[i] >> (4 * d)) & 15u) << (4 * i);
-                xw[g * (4 * kStageRecord) + d * 8 + w] = word ^ 0x88888888u;
-            }
+            for (int d = 0; d < kDigits; ++d) xw[g * (4 * kStageRecord) + d * 8 + w] = W[d] ^ 0x88888888u;
             if (w == 0) {
                 xw[g * (4 * kStageRecord) + 8 * kDigits] = __float_as_uint(mx * (1.0f / static_cast<float>(kXMax)));
                 xw[g * (4 * kStageRecord) + 8 * kDigits + 1] = __float_as_uint(static_cast<float>(gs));
