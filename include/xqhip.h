@@ -183,6 +183,17 @@ XQHIP_API int xqhip_gqa_decode(const float* q, const void* k_cache, const void* 
                                int nkv, int head_dim, int max_ctx, const int32_t* pos, float* out, void* workspace,
                                void* stream);
 
+/* xqhip_attn_prep followed by xqhip_gqa_decode in two launches: the q/k
+ * RMSNorm + RoPE, the fp16 append of the new key/value at slot *pos and the
+ * gated GQA of custom_model.cpp:740-951 (the decode half of
+ * CustomModel::forwardAttention).  q_src is the q_proj output ([q | gate] per
+ * head when gated, gate 0 otherwise); same caches, limits and workspace as
+ * xqhip_gqa_decode. */
+XQHIP_API int xqhip_attn_decode(const float* q_src, const float* k_src, const float* v_src, int gated, int nq,
+                                int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
+                                float eps, const float* rope_cs, const int32_t* pos, void* k_cache, void* v_cache,
+                                int max_ctx, float* out, void* workspace, void* stream);
+
 /* Linear attention: conv1d + SiLU over the mixed q|k|v channels with the
  * [channels][ksize-1] history updated in place, then L2-normalised q and k
  * heads (custom_model.cpp:961-1047).  out: conv_dim fp32. */

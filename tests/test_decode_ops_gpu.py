@@ -139,6 +139,82 @@ def test_attention_prep_and_gqa_decode_pos511(gated):
         close(out.download(np.float32, nq * hd), want, "gqa decode + gate")
 
 
+def oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, pos, theta, eps, kcache_f16, vcache_f16):
+    """Oracle of one decode attention step over caches that already hold slot pos."""
+    if gated:
+        qq = qsrc.reshape(nq, 2, hd)[:, 0].reshape(-1).copy()
+        gate = qsrc.reshape(nq, 2, hd)[:, 1].reshape(-1).copy()
+    else:
+        qq, gate = qsrc.copy(), np.zeros(nq * hd, np.float32)
+    kk = k.copy()
+    O().orc_head_rms(ob.p(qq), ob.p(qn), nq, hd, eps)
+    O().orc_head_rms(ob.p(kk), ob.p(kn), nkv, hd, eps)
+    O().orc_rope_partial(ob.p(qq), nq, hd, rd, pos, theta)
+    O().orc_rope_partial(ob.p(kk), nkv, hd, rd, pos, theta)
+    ctx = pos + 1
+    kf = kcache_f16[:ctx].astype(np.float32).reshape(-1)
+    vf = vcache_f16[:ctx].astype(np.float32).reshape(-1)
+    att = np.empty(nq * hd, np.float32)
+    O().orc_attention_model(ob.p(qq), ob.p(kf), ob.p(vf), ctx, nkv, nq, hd, ob.p(att))
+    sig = np.array([O().orc_sigmoid(float(g)) for g in gate], np.float32)
+    return kk, att * sig
+
+
+# (nq, nkv, head_dim, rotary, pos, max_ctx, gated): the 9B attention shape, the
+# first position, a position past 64 chunks (grid slots wrap), a head_dim
+# without a specialised kernel, group 8 at the last slot of the first chunk
+FUSED_CASES = [(16, 4, 256, 64, 700, 1024, True), (32, 8, 128, 32, 0, 64, False),
+               (8, 2, 64, 64, 4160, 8192, True), (4, 2, 96, 32, 130, 256, True), (16, 2, 128, 32, 63, 128, False)]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "nq%d_nkv%d_hd%d_rd%d_pos%d" % c[:5])
+def test_fused_attention_decode(case):
+    """xqhip_attn_decode (prep folded into the chunk kernel) against the oracle
+    and against xqhip_attn_prep + xqhip_gqa_decode, for two consecutive positions
+    (the second reads the slot the first appended)."""
+    nq, nkv, hd, rd, pos, max_ctx, gated = case
+    theta, eps = 1e7, 1e-6
+    print(f"fused attention case {case}", flush=True)
+    assert pos + 2 <= max_ctx
+    qsrc, k, v, qn, kn, kc, vc = attn_layer_inputs(nq, nkv, hd, pos, seed=pos + hd, gated=gated)
+    tab = np.empty(max_ctx * rd, np.float32)
+    xb.ck(xb.hip().xqhip_rope_table(theta, rd, max_ctx, xb.ptr(tab)))
+    kcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    vcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    kcache[:pos], vcache[:pos] = kc, vc
+    kd, vd = dev(kcache), dev(vcache)    # fused path
+    kd2, vd2 = dev(kcache), dev(vcache)  # two-launch path
+    qn_d, kn_d, tab_d = dev(qn), dev(kn), dev(tab)
+    ws = dev(np.zeros(xb.hip().xqhip_gqa_workspace_bytes(nq, nkv, hd), np.uint8))
+    out, out2 = xb.DeviceBuffer(nq * hd * 4), xb.DeviceBuffer(nq * hd * 4)
+    qo, go = xb.DeviceBuffer(nq * hd * 4), xb.DeviceBuffer(nq * hd * 4)
+    rng = np.random.default_rng(pos)
+    for step in range(2):
+        p = pos + step
+        if step:
+            qsrc = rng.normal(0, 1, qsrc.size).astype(np.float32)
+            k = rng.normal(0, 1, k.size).astype(np.float32)
+            v = rng.normal(0, 1, v.size).astype(np.float32)
+        qs_d, k_d, v_d = dev(qsrc), dev(k), dev(v)
+        pos_d = dev(np.array([p], np.int32))
+        xb.ck(xb.hip().xqhip_attn_decode(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr, kn_d.ptr,
+                                         eps, tab_d.ptr, pos_d.ptr, kd.ptr, vd.ptr, max_ctx, out.ptr, ws.ptr, None))
+        xb.ck(xb.hip().xqhip_attn_prep(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr, kn_d.ptr,
+                                       eps, tab_d.ptr, pos_d.ptr, qo.ptr, go.ptr, kd2.ptr, vd2.ptr, None))
+        xb.ck(xb.hip().xqhip_gqa_decode(qo.ptr, kd2.ptr, vd2.ptr, go.ptr, nq, nkv, hd, max_ctx, pos_d.ptr, out2.ptr,
+                                        ws.ptr, None))
+        kc_got = kd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        vc_got = vd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        assert np.array_equal(kc_got[:pos], kc) and np.array_equal(vc_got[:pos], vc)  # earlier slots untouched
+        assert not kc_got[p + 1:].any() and not vc_got[p + 1:].any()                  # later slots untouched
+        assert np.array_equal(vc_got[p].reshape(-1), v.astype(np.float16))
+        kk, want = oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, p, theta, eps, kc_got, vc_got)
+        close(kc_got[p].reshape(-1).astype(np.float32), kk, f"appended k pos {p}", atol=2e-3, rtol=1e-3)
+        got = out.download(np.float32, nq * hd)
+        close(got, want, f"fused attention pos {p}")
+        close(got, out2.download(np.float32, nq * hd), f"fused vs two-launch pos {p}", atol=1e-5, rtol=1e-4)
+
+
 @pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 100])
 def test_gqa_short_contexts(ctx):
     nq, nkv, hd = 4, 2, 8

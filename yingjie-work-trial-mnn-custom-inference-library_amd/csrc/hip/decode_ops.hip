@@ -125,9 +125,12 @@ constexpr int kAttnMaxChunks = kAttnMaxCtx / kAttnChunk;
 constexpr int kAttnGridChunks = 64;  // chunk slots per kv head in the grid
 constexpr int kAttnThreads = 256;
 
+// pos_new >= 0: key/value of position pos_new come from kn / vn (LDS, the
+// values the same launch appends to the cache) instead of the cache.
 template <int HD>
 __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, int t0, int n, int group, int hd,
-                                          const float* qs, float* sc, float* vred) {
+                                          const float* qs, float* sc, float* vred, int pos_new = -1,
+                                          const float* kn = nullptr, const float* vn = nullptr) {
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
     const int qh0 = kh * group;
@@ -149,6 +152,10 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
                 kv[8 * u + 2 * e + 1] = half_hi(ww[e]);
             }
         }
+        if (valid && t0 + tt == pos_new) {
+#pragma unroll
+            for (int d = 0; d < DL; ++d) kv[d] = kn[sub * DL + d];
+        }
         for (int g = 0; g < group; ++g) {
             const float* qv = qs + g * HD + sub * DL;
             float dot = 0.0f;
@@ -162,8 +169,9 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
         for (int pr = threadIdx.x; pr < n * group; pr += kAttnThreads) {
             const int t = pr / group, g = pr % group;
             const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * hd;
+            const bool is_new = t0 + t == pos_new;
             float dot = 0.0f;
-            for (int d = 0; d < hd; ++d) dot += qs[g * hd + d] * static_cast<float>(krow[d]);
+            for (int d = 0; d < hd; ++d) dot += qs[g * hd + d] * (is_new ? kn[d] : static_cast<float>(krow[d]));
             sc[g * kAttnChunk + t] = dot * rscale;
         }
     }
@@ -194,8 +202,12 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
         for (int t = ts; t < n; t += TPP) {
             const uint4 w =
                 *reinterpret_cast<const uint4*>(p.v_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * HD + dsl * 8);
-            const float vv[8] = {half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y),
-                                 half_lo(w.z), half_hi(w.z), half_lo(w.w), half_hi(w.w)};
+            float vv[8] = {half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y),
+                           half_lo(w.z), half_hi(w.z), half_lo(w.w), half_hi(w.w)};
+            if (t0 + t == pos_new) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vv[e] = vn[dsl * 8 + e];
+            }
 #pragma unroll
             for (int g = 0; g < kAttnMaxGroup; ++g) {
                 if (g < group) {
@@ -236,7 +248,8 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
             float acc = 0.0f;
             for (int t = 0; t < n; ++t)
                 acc += sc[g * kAttnChunk + t] *
-                       static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d]);
+                       (t0 + t == pos_new ? vn[d]
+                                          : static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d]));
             p.part_o[(static_cast<size_t>(qh0 + g) * kAttnMaxChunks + ch) * hd + d] = acc;
         }
     }
@@ -261,6 +274,81 @@ __global__ void __launch_bounds__(kAttnThreads) gqa_chunk_kernel(GqaLaunch p) {
         const int t0 = ch * kAttnChunk;
         const int n = min(kAttnChunk, ctx - t0);
         gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred);
+    }
+}
+
+// Decode attention with the q/k preparation folded in: every block normalises
+// and rotates the q heads of its kv head (cheap), and the block whose chunks
+// include position pos also prepares that position's key and value, appends
+// them to the fp16 caches and uses them (rounded to fp16, like every cached
+// position) from LDS; the slot this launch writes is never taken from memory.
+template <int HD>
+__global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLaunch a) {
+    extern __shared__ float smem[];
+    const GqaLaunch& p = a.g;
+    const int hd = HD > 0 ? HD : p.head_dim;
+    const int group = p.nq / p.nkv;
+    const int kh = blockIdx.x;
+    const int pos = *p.pos;
+    const int ctx = pos + 1;
+    if (static_cast<int>(blockIdx.y) * kAttnChunk >= ctx) return;  // whole block: nothing to do
+    float* qs = smem;                       // [group][hd]
+    float* sc = qs + group * hd;            // [group][64]
+    float* vred = sc + group * kAttnChunk;  // [4 waves][group][hd]
+    float* kn = vred + (kAttnThreads / kWave) * group * hd;  // [hd]
+    float* vn = kn + hd;                                     // [hd]
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int half = a.rotary_dim / 2;
+    const float2* cs = reinterpret_cast<const float2*>(a.rope_cs) + static_cast<size_t>(pos) * a.rope_pairs;
+    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
+    const bool owns_new = (pos / kAttnChunk) % static_cast<int>(gridDim.y) == static_cast<int>(blockIdx.y);
+    // per-head RMSNorm (custom_model.cpp:301-313): one wave per head; heads
+    // 0..group-1 are q, head `group` (owner only) is the new key
+    const int nheads = group + (owns_new ? 1 : 0);
+    for (int h = wid; h < nheads; h += kAttnThreads / kWave) {
+        const bool is_k = h == group;
+        const float* src = is_k ? a.k_src + static_cast<size_t>(kh) * hd
+                                : a.q_src + static_cast<size_t>(kh * group + h) * (a.gated ? 2 * hd : hd);
+        const float* w = is_k ? a.k_norm : a.q_norm;
+        float* dst = is_k ? kn : qs + h * hd;
+        float ss = 0.0f;
+        for (int d = lane; d < hd; d += kWave) {
+            const float v = src[d];
+            dst[d] = v;
+            ss += v * v;
+        }
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(hd) + a.eps);
+        for (int d = lane; d < hd; d += kWave) dst[d] = dst[d] * (inv * w[d]);
+    }
+    if (owns_new)
+        for (int d = threadIdx.x; d < hd; d += kAttnThreads) vn[d] = a.v_src[static_cast<size_t>(kh) * hd + d];
+    __syncthreads();
+    // partial RoPE (custom_model.cpp:351-370) on the first rotary_dim dims, pairs (i, half + i)
+    for (int i = threadIdx.x; i < nheads * half; i += kAttnThreads) {
+        const int h = i / half, d = i % half;
+        float* v = h == group ? kn : qs + h * hd;
+        const float2 c = cs[d];
+        const float x0 = v[d], x1 = v[half + d];
+        v[d] = x0 * c.x - x1 * c.y;
+        v[half + d] = x1 * c.x + x0 * c.y;
+    }
+    __syncthreads();
+    if (owns_new) {  // append at slot pos, and use the fp16-rounded values like every other slot
+        for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
+            const size_t slot = (static_cast<size_t>(pos) * p.nkv + kh) * hd + d;
+            const _Float16 kq = static_cast<_Float16>(kn[d]), vq = static_cast<_Float16>(vn[d]);
+            a.k_cache[slot] = kq;
+            a.v_cache[slot] = vq;
+            kn[d] = static_cast<float>(kq);
+            vn[d] = static_cast<float>(vq);
+        }
+        __syncthreads();
+    }
+    for (int ch = blockIdx.y; ch < nch; ch += gridDim.y) {
+        const int t0 = ch * kAttnChunk;
+        const int n = min(kAttnChunk, ctx - t0);
+        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred, pos, kn, vn);
     }
 }
 
@@ -295,7 +383,9 @@ __global__ void __launch_bounds__(256) gqa_combine_kernel(GqaLaunch p) {
         float o = 0.0f;
         for (int c = 0; c < nch; ++c) o += po[static_cast<size_t>(c) * hd + d] * wgt[c];
         const size_t oi = static_cast<size_t>(qh) * hd + d;
-        p.out[oi] = (o * inv) * sigmoid_dev(p.gate[oi]);
+        // no gate projection: the reference's zero gate, sigmoid(0) (custom_model.cpp:750-753)
+        const float gv = p.gate ? p.gate[static_cast<size_t>(qh) * p.gate_stride + d] : 0.0f;
+        p.out[oi] = (o * inv) * sigmoid_dev(gv);
     }
 }
 
@@ -307,6 +397,23 @@ size_t gqa_workspace_bytes(int nq, int nkv, int head_dim) {
 static size_t gqa_lds_bytes(int group, int head_dim) {
     return sizeof(float) * (static_cast<size_t>(group) * head_dim + static_cast<size_t>(group) * kAttnChunk +
                             (kAttnThreads / kWave) * static_cast<size_t>(group) * head_dim);
+}
+
+hipError_t launch_attn_decode(const AttnDecodeLaunch& a, hipStream_t s) {
+    const GqaLaunch& p = a.g;
+    const int group = p.nq / p.nkv;
+    const size_t lds = gqa_lds_bytes(group, p.head_dim) + 2 * sizeof(float) * p.head_dim;
+    const int slots = min(kAttnGridChunks, (p.max_ctx + kAttnChunk - 1) / kAttnChunk);
+    const dim3 grid(p.nkv, slots);
+    switch (p.head_dim) {
+        case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kAttnThreads), lds, s, a); break;
+        case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kAttnThreads), lds, s, a); break;
+        case 256: hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, s, a); break;
+        default: hipLaunchKernelGGL(attn_decode_kernel<0>, grid, dim3(kAttnThreads), lds, s, a); break;
+    }
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL(gqa_combine_kernel, dim3(p.nq), dim3(256), 0, s, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
@@ -328,7 +435,7 @@ hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx) {
     if (nkv <= 0 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || head_dim <= 0) return false;
     if (max_ctx < 1 || max_ctx > kAttnMaxCtx) return false;
-    return gqa_lds_bytes(nq / nkv, head_dim) <= 64 * 1024;
+    return gqa_lds_bytes(nq / nkv, head_dim) + 2 * sizeof(float) * head_dim <= 64 * 1024;
 }
 
 // ---------------------------------------------------------------------------

@@ -81,7 +81,25 @@ struct GqaLaunch {
     float* part_m;  // workspace: [nq][max chunks] chunk max
     float* part_l;  //            [nq][max chunks] chunk sum of exp
     float* part_o;  //            [nq][max chunks][head_dim] unnormalised output
+    int gate_stride;  // floats between the gates of consecutive query heads (gate == nullptr: none)
 };
+
+// Decode attention with the q/k preparation and KV append folded in
+// (attn_decode_kernel + gqa_combine_kernel).
+struct AttnDecodeLaunch {
+    GqaLaunch g;  // g.q unused; g.gate = q projection + head_dim (gated) or nullptr
+    const float* q_src;  // q projection output (gated: per head [q | gate])
+    const float* k_src;
+    const float* v_src;
+    int gated, rotary_dim, rope_pairs;
+    const float* q_norm;
+    const float* k_norm;
+    float eps;
+    const float* rope_cs;
+    _Float16* k_cache;
+    _Float16* v_cache;
+};
+hipError_t launch_attn_decode(const AttnDecodeLaunch& a, hipStream_t s);
 size_t gqa_workspace_bytes(int nq, int nkv, int head_dim);
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx);
 hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s);

@@ -244,7 +244,6 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     size_t ws_gqa = any_full ? xqhip_gqa_workspace_bytes(nq_, nkv_, hd_) : 1;
     uint8_t *wa = nullptr, *wg = nullptr;
     if (!alloc(&resid_, hidden_, error) || !alloc(&normed_, hidden_, error) || !alloc(&proj_, max_proj, error) ||
-        !alloc(&q_rot_, static_cast<size_t>(nq_) * hd_, error) || !alloc(&gate_, static_cast<size_t>(nq_) * hd_, error) ||
         !alloc(&attn_, attn_n, error) ||
         !alloc(&ffn_, inter_, error) || !alloc(&best_val_, 1, error) || !alloc(&d_ctrl_, 4, error) ||
         !alloc(&wa, ws_argmax, error) || !alloc(&wg, ws_gqa, error))
@@ -345,16 +344,13 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
             op_end(timed);
             const float* k_src = proj_ + static_cast<size_t>(nq_) * hd_ * (L.q_gated ? 2 : 1);
             const float* v_src = k_src + static_cast<size_t>(nkv_) * hd_;
-            op_begin(timed, "rope_qk_custom(fused:q_norm,k_norm,kv_append)", {"prefill_kv_build_custom"});
-            XQ_CALL(xqhip_attn_prep(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm, L.k_norm,
-                                    eps_, rope_cs_, pos, q_rot_, gate_, L.k_cache, L.v_cache, stream_),
-                    "attention prep");
-            op_end(timed);
-            op_begin(timed, "attention_gqa_decode_custom(fused:output_gate)",
-                     {"attention_score_custom", "attention_softmax_custom", "attention_v_reduce_custom"}, 3);
-            XQ_CALL(xqhip_gqa_decode(q_rot_, L.k_cache, L.v_cache, gate_, nq_, nkv_, hd_, max_ctx_, pos, attn_,
-                                     gqa_ws_, stream_),
-                    "gqa decode");
+            op_begin(timed, "attention_gqa_decode_custom(fused:q_norm,k_norm,rope_qk,kv_append,output_gate)",
+                     {"prefill_kv_build_custom", "attention_score_custom", "attention_softmax_custom",
+                      "attention_v_reduce_custom"},
+                     4);
+            XQ_CALL(xqhip_attn_decode(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm, L.k_norm,
+                                      eps_, rope_cs_, pos, L.k_cache, L.v_cache, max_ctx_, attn_, gqa_ws_, stream_),
+                    "attention decode");
             op_end(timed);
             op_begin(timed, "linear_o_proj_w4a16(fused:residual_add_attention)");
             XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, nullptr, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),

@@ -112,8 +112,6 @@ private:
     float* resid_ = nullptr;     // fp32 residual stream (pre final-norm)
     float* normed_ = nullptr;    // final-normed hidden (exposed hidden state)
     float* proj_ = nullptr;      // fused input projection output
-    float* q_rot_ = nullptr;
-    float* gate_ = nullptr;
     float* attn_ = nullptr;      // attention / delta output
     float* ffn_ = nullptr;
     float* logits_ = nullptr;    // debug_json only
