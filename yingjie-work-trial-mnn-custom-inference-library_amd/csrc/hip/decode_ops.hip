@@ -161,8 +161,7 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
             float dot = 0.0f;
 #pragma unroll
             for (int d = 0; d < DL; ++d) dot += qv[d] * kv[d];
-            dot += __shfl_xor(dot, 1, kWave);
-            dot += __shfl_xor(dot, 2, kWave);
+            dot = lanes_sum<4>(dot);
             if (valid && sub == 0) sc[g * kAttnChunk + tt] = dot * rscale;
         }
     } else {

@@ -213,7 +213,11 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
             float hs = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) hs += v[k][i] * v[k][i];
-            for (int m = 1; m < per_head; m <<= 1) hs += __shfl_xor(hs, m, kWave);
+            if (per_head >= 2) hs += dpp_f32<kDppXor1>(hs);
+            if (per_head >= 4) hs += dpp_f32<kDppXor2>(hs);
+            if (per_head >= 8) hs += dpp_f32<kDppHalfMirror>(hs);
+            if (per_head >= 16) hs += dpp_f32<kDppMirror>(hs);
+            for (int m = 16; m < per_head; m <<= 1) hs += __shfl_xor(hs, m, kWave);
             const float inv = 1.0f / sqrtf(hs / static_cast<float>(pro.head_dim) + pro.eps);
             float wl[8], zl[8];
             if constexpr (kPre) {
@@ -240,8 +244,7 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
         float mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[k][i]));
-#pragma unroll
-        for (int m = 1; m <= 4; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, kWave));
+        mx = lanes_max<8>(mx);
         const float inv = mx > 0.0f ? static_cast<float>(kXMax) / mx : 0.0f;
         int X[8];
         int gs = 0;
@@ -250,8 +253,7 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
             X[i] = min(kXMax, max(-kXMax, static_cast<int>(rintf(v[k][i] * inv))));
             gs += X[i];
         }
-#pragma unroll
-        for (int m = 1; m <= 4; m <<= 1) gs += __shfl_xor(gs, m, kWave);
+        gs = lanes_sum_i<8>(gs);
         if (item < n_items) {
             uint32_t U[8];
 #pragma unroll

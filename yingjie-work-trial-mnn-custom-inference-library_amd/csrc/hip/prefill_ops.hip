@@ -291,8 +291,7 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnLaunch p) 
             for (int g = 0; g < group; ++g) {
                 float dot = 0.0f;
                 for (int d = d0; d < d1; ++d) dot += qs[g * hd + d] * static_cast<float>(krow[d]);
-                dot += __shfl_xor(dot, 1, kWave);
-                dot += __shfl_xor(dot, 2, kWave);
+                dot = lanes_sum<4>(dot);
                 if (valid && sub == 0) sc[g * kPAttnChunk + tt] = dot * rscale;
             }
         }

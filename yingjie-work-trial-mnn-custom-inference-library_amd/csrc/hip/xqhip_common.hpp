@@ -47,17 +47,68 @@ __device__ __forceinline__ float half_hi(uint32_t u) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16)));
 }
 
-// Butterfly sum over the 64 lanes of a wave; every lane ends with the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Cross-lane reductions by DPP lane moves inside the VALU (no LDS round trip,
+// unlike ds_bpermute): quad_perm [1,0,3,2] and [2,3,0,1] exchange lanes i^1
+// and i^2, row_half_mirror maps lane i to 7-i within each 8, row_mirror maps
+// lane i to 15-i within each 16.  After the quad steps every lane of a quad
+// holds the quad's value, so each mirror step pairs it with the neighbouring
+// quad / half-row: the result is the reduction over the aligned group of N
+// lanes, identical in every lane of the group.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, dpp_i32<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+// Reduction over each aligned group of N in {2, 4, 8, 16} consecutive lanes.
+template <int N>
+__device__ __forceinline__ float lanes_sum(float v) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16, "lane group");
+    v += dpp_f32<kDppXor1>(v);
+    if constexpr (N >= 4) v += dpp_f32<kDppXor2>(v);
+    if constexpr (N >= 8) v += dpp_f32<kDppHalfMirror>(v);
+    if constexpr (N >= 16) v += dpp_f32<kDppMirror>(v);
+    return v;
+}
+template <int N>
+__device__ __forceinline__ int lanes_sum_i(int v) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16, "lane group");
+    v += dpp_i32<kDppXor1>(v);
+    if constexpr (N >= 4) v += dpp_i32<kDppXor2>(v);
+    if constexpr (N >= 8) v += dpp_i32<kDppHalfMirror>(v);
+    if constexpr (N >= 16) v += dpp_i32<kDppMirror>(v);
+    return v;
+}
+template <int N>
+__device__ __forceinline__ float lanes_max(float v) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16, "lane group");
+    v = fmaxf(v, dpp_f32<kDppXor1>(v));
+    if constexpr (N >= 4) v = fmaxf(v, dpp_f32<kDppXor2>(v));
+    if constexpr (N >= 8) v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_f32<kDppMirror>(v));
     return v;
 }
 
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes of a wave (rows of 16 by DPP, then the four row sums
+// read as scalars); every lane gets the total.  Must be called by the whole
+// wave (all lanes active).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = lanes_sum<16>(v);
+    return (readlane_f32(v, 0) + readlane_f32(v, 16)) + (readlane_f32(v, 32) + readlane_f32(v, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    v = lanes_max<16>(v);
+    return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)), fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
 // Sum over all threads of a block (blockDim.x a multiple of 64, <= 1024).
