@@ -191,6 +191,7 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
     // sum_t e_t v_t: 16-byte loads of v, HD/8 lanes per token
     if constexpr (HD > 0) {
         constexpr int LPT = HD / 8;
+        static_assert(LPT >= 8 && LPT <= 32, "pair sums below cover lane distances 8..32");
         constexpr int TPP = kAttnThreads / LPT;
         const int dsl = threadIdx.x % LPT, ts = threadIdx.x / LPT;
         float o[kAttnMaxGroup][8];
@@ -221,8 +222,9 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
             if (g < group) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-#pragma unroll
-                    for (int m = LPT; m < kWave; m <<= 1) o[g][e] += __shfl_xor(o[g][e], m, kWave);
+                    if constexpr (LPT <= 8) o[g][e] = xor_pair_sum<8>(o[g][e]);
+                    if constexpr (LPT <= 16) o[g][e] = xor_pair_sum<16>(o[g][e]);
+                    o[g][e] = xor_pair_sum<32>(o[g][e]);
                 }
             }
         }
@@ -544,8 +546,7 @@ __global__ void __launch_bounds__(256) gated_delta_kernel(DeltaLaunch p) {
     }
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     // threads of one column inside a wave are 16 lanes apart
-    pred += __shfl_xor(pred, 16, kWave);
-    pred += __shfl_xor(pred, 32, kWave);
+    pred = xor_pair_sum<32>(xor_pair_sum<16>(pred));
     if (lane < kDeltaCols) colsum[wid][lane] = pred;
     __syncthreads();
     pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
@@ -561,8 +562,7 @@ __global__ void __launch_bounds__(256) gated_delta_kernel(DeltaLaunch p) {
             o += sreg[r] * qk[i];
         }
     }
-    o += __shfl_xor(o, 16, kWave);
-    o += __shfl_xor(o, 32, kWave);
+    o = xor_pair_sum<32>(xor_pair_sum<16>(o));
     if (lane < kDeltaCols) colsum[wid][lane] = o;
     __syncthreads();
     if (threadIdx.x < kDeltaCols && active) {
@@ -662,8 +662,7 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
             pred += sreg[r] * (qk[256 + i] * invk);
         }
     }
-    pred += __shfl_xor(pred, 16, kWave);
-    pred += __shfl_xor(pred, 32, kWave);
+    pred = xor_pair_sum<32>(xor_pair_sum<16>(pred));
     if (lane < kDeltaCols) colsum[wid][lane] = pred;
     __syncthreads();
     pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
@@ -679,8 +678,7 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
             o += sreg[r] * (qk[i] * invq);
         }
     }
-    o += __shfl_xor(o, 16, kWave);
-    o += __shfl_xor(o, 32, kWave);
+    o = xor_pair_sum<32>(xor_pair_sum<16>(o));
     if (lane < kDeltaCols) colsum[wid][lane] = o;
     __syncthreads();
     if (threadIdx.x < kDeltaCols && active) {

@@ -93,39 +93,6 @@ constexpr uint32_t kDigitBias = 0x888888u;     // 8 in every hex digit of the 6
 constexpr int kStageRecord = (8 * kDigits + 2 + 3) / 4;
 constexpr int kMaxStageCols = 16384;
 
-// The block stages the whole vector: thread t owns the (group, word) items
-// t, t + THREADS, ... (8 consecutive columns each).  It first issues the
-// 16-byte loads of x and of the prologue vectors (x, the RMS weight and the
-// gate are 16-byte aligned, checked by the C ABI), then calls `prefetch`,
-// which issues the block's first weight loads, so the (cache-resident)
-// activations return first and the staging arithmetic below overlaps the
-// weight stream (vector loads return in issue order).  The norm factors come
-// from the same registers: the RMS over the vector by one block reduction, the
-// per-head factors of PRO_GATED by a lane butterfly over the head's
-// consecutive items.  ITEMS * THREADS * 8 must cover `cols`; the caller
-// synchronises the block before reading xs.  Prologue vectors are preloaded
-// only for <= 2 items per thread (the 4096-column launches): wider blocks load
-// them after the prefetch, to keep the register budget of the main loop.
-__device__ __forceinline__ void load8f(const float* p, float* v) {
-    const float4 a = *reinterpret_cast<const float4*>(p);
-    const float4 b = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-
-// f16 x: the 8 halves stay packed in v[0..3] (as raw bits) until unpack8_f16.
-__device__ __forceinline__ void load8h_raw(const _Float16* p, float* v) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
-}
-
-__device__ __forceinline__ void unpack8_f16(float* v) {
-    const uint32_t a = __float_as_uint(v[0]), b = __float_as_uint(v[1]), c = __float_as_uint(v[2]),
-                   d = __float_as_uint(v[3]);
-    v[0] = half_lo(a); v[1] = half_hi(a); v[2] = half_lo(b); v[3] = half_hi(b);
-    v[4] = half_lo(c); v[5] = half_hi(c); v[6] = half_lo(d); v[7] = half_hi(d);
-}
-
 // Nibble transpose: W[d] nibble i = hex digit d of U[i] (i < 8, d < 6).
 // Bytes are gathered with v_perm_b32 (A_k: byte k of U0, U2, U4, U6; B_k:
 // byte k of U1, U3, U5, U7), then each byte's two digits are split with one
@@ -151,34 +118,88 @@ __device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&W
     }
 }
 
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9-family format
+constexpr int kLoadNT = 2;                    // non-temporal (streamed once)
+constexpr uint32_t kOutOfRange = 0x80000000u; // beyond every range (matrices < 2 GiB)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t vec_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ void as_floats8(const u32x4& a, const u32x4& b, float* v) {
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+}
+// 8 activations from two 16-byte loads: fp32 (a, b) or fp16 (a only), chosen
+// by a select rather than a branch
+__device__ __forceinline__ void decode_act8(const u32x4& a, const u32x4& b, int x_f16, float* v) {
+    const uint32_t h[4] = {a.x, a.y, a.z, a.w};
+    float f[8];
+    as_floats8(a, b, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = x_f16 ? ((i & 1) ? half_hi(h[i >> 1]) : half_lo(h[i >> 1])) : f[i];
+}
+
+// The block stages the whole vector: thread t owns the (group, word) items
+// t, t + THREADS, ... (8 consecutive columns each).  Every wave first issues
+// the 16-byte loads of x and of the prologue vectors, the block then passes a
+// barrier that waits for none of them, and only then calls `prefetch`, which
+// issues the block's first weight loads; the activations thus return first and
+// the staging arithmetic below overlaps the weight stream.  The norm factors
+// come from the same registers: the RMS over the vector by one block
+// reduction, the per-head factors of PRO_GATED by a lane reduction over the
+// head's consecutive items.  ITEMS * THREADS * 8 must cover `cols`; the caller
+// synchronises the block before reading xs.  Prologue vectors are preloaded
+// only for <= 2 items per thread (the 4096-column launches): wider blocks load
+// them after the prefetch, to keep the register budget of the main loop.
 template <int THREADS, int ITEMS, typename Prefetch>
-__device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f16, const Prologue& pro, int cols,
+__device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prologue& pro, int cols,
                                             uint4* __restrict__ xs, float* red, Prefetch&& prefetch) {
     constexpr bool kPre = ITEMS <= 2;
     constexpr int kW = kPre ? ITEMS : 1;
     const int G = cols >> 6;
     const int n_items = G * 8;
+    // All activation and prologue loads are unconditional range-checked buffer
+    // loads (an unused vector has range 0 and reads as zeros without a memory
+    // access): straight-line code, so no wait is forced before the barrier.
+    const bool gated = pro.mode == PRO_GATED;
+    const __amdgpu_buffer_rsrc_t xr = vec_rsrc(x, static_cast<uint32_t>(cols) * (x_f16 ? 2u : 4u));
+    const __amdgpu_buffer_rsrc_t wr =
+        vec_rsrc(pro.w, pro.mode == PRO_RMS ? cols * 4u : (gated ? static_cast<uint32_t>(pro.head_dim) * 4u : 0u));
+    const __amdgpu_buffer_rsrc_t zr = vec_rsrc(pro.z, gated ? cols * 4u : 0u);
+    const int hmask = gated ? pro.head_dim - 1 : -1;  // head_dim is a power of two for PRO_GATED
+    u32x4 xa[ITEMS], xb[ITEMS], wa[kW], wb[kW], za[kW], zb[kW];
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t item = static_cast<uint32_t>(min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1));
+        xa[k] = load16(xr, x_f16 ? item * 16u : item * 32u);
+        xb[k] = load16(xr, x_f16 ? kOutOfRange : item * 32u + 16u);
+        if constexpr (kPre) {
+            const uint32_t woff = static_cast<uint32_t>(static_cast<int>(item * 8u) & hmask) * 4u;
+            wa[k] = load16(wr, woff);
+            wb[k] = load16(wr, woff + 16u);
+            za[k] = load16(zr, item * 32u);
+            zb[k] = load16(zr, item * 32u + 16u);
+        }
+    }
+    // Every wave's activation loads are issued before any wave's weight loads:
+    // a CU's vector-memory requests are served in issue order, so without this
+    // barrier (which waits for no load) the activations of late waves queue
+    // behind the weight stream of early ones and the staging, which needs all
+    // of them, finishes only after most of the prefetched weights.
+    // (an asm barrier with a memory clobber: the compiler moves no load across it)
+    asm volatile("s_barrier" ::: "memory");
+    prefetch();
     float v[ITEMS][8], wv[kW][8], zv[kW][8];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
-        const int item = min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1);
-        if (x_f16)
-            load8h_raw(static_cast<const _Float16*>(x) + item * 8, v[k]);
-        else
-            load8f(static_cast<const float*>(x) + item * 8, v[k]);
+        decode_act8(xa[k], xb[k], x_f16, v[k]);
         if constexpr (kPre) {
-            if (pro.mode == PRO_RMS) {
-                load8f(pro.w + item * 8, wv[k]);
-            } else if (pro.mode == PRO_GATED) {
-                load8f(pro.w + (item * 8) % pro.head_dim, wv[k]);
-                load8f(pro.z + item * 8, zv[k]);
-            }
+            as_floats8(wa[k], wb[k], wv[k]);
+            as_floats8(za[k], zb[k], zv[k]);
         }
-    }
-    prefetch();
-    if (x_f16) {
-#pragma unroll
-        for (int k = 0; k < ITEMS; ++k) unpack8_f16(v[k]);
     }
     if (pro.mode == PRO_RMS) {
         float ss = 0.0f;
@@ -198,8 +219,8 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
 #pragma unroll
                 for (int i = 0; i < 8; ++i) wl[i] = wv[k][i];
             } else {
-                const int item = min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1);
-                load8f(pro.w + item * 8, wl);
+                const uint32_t item = static_cast<uint32_t>(min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1));
+                as_floats8(load16(wr, item * 32u), load16(wr, item * 32u + 16u), wl);
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i];
@@ -217,7 +238,8 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
             if (per_head >= 4) hs += dpp_f32<kDppXor2>(hs);
             if (per_head >= 8) hs += dpp_f32<kDppHalfMirror>(hs);
             if (per_head >= 16) hs += dpp_f32<kDppMirror>(hs);
-            for (int m = 16; m < per_head; m <<= 1) hs += __shfl_xor(hs, m, kWave);
+            if (per_head >= 32) hs = xor_pair_sum<16>(hs);
+            if (per_head >= 64) hs = xor_pair_sum<32>(hs);
             const float inv = 1.0f / sqrtf(hs / static_cast<float>(pro.head_dim) + pro.eps);
             float wl[8], zl[8];
             if constexpr (kPre) {
@@ -227,9 +249,10 @@ __device__ __forceinline__ void stage_x_lds(const void* __restrict__ x, int x_f1
                     zl[i] = zv[k][i];
                 }
             } else {
-                const int item = min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1);
-                load8f(pro.w + (item * 8) % pro.head_dim, wl);
-                load8f(pro.z + item * 8, zl);
+                const uint32_t item = static_cast<uint32_t>(min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1));
+                const uint32_t woff = static_cast<uint32_t>(static_cast<int>(item * 8u) & hmask) * 4u;
+                as_floats8(load16(wr, woff), load16(wr, woff + 16u), wl);
+                as_floats8(load16(zr, item * 32u), load16(zr, item * 32u + 16u), zl);
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i] * silu_dev(zl[i]);
@@ -329,9 +352,6 @@ struct WBatch {
     uint32_t m[R];
 };
 
-constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9-family format
-constexpr int kLoadNT = 2;                    // non-temporal (streamed once)
-constexpr uint32_t kOutOfRange = 0x80000000u; // beyond every range (matrices < 2 GiB)
 
 struct WSrc {
     __amdgpu_buffer_rsrc_t nib, meta;
@@ -366,9 +386,11 @@ __device__ __forceinline__ void load_batch(WBatch<R>& wb, const WSrc& src, int r
 
 template <int NCH, int RG, int R, int EPI>
 __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
+    // x is not __restrict__: with it the compiler may move the staging loads of
+    // x across the asm barrier of stage_x_lds (it would assume no aliasing)
     const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
-    const void* __restrict__ x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
-    uint64_t* __restrict__ partial) {
+    const void* x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
+    uint64_t* __restrict__ partial, int grid) {  // grid == gridDim.x (an argument: no late kernarg fetch)
     extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
     __shared__ float part[RG * NCH * R];
     __shared__ float red[32];
@@ -382,17 +404,23 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const bool has_group = g < G;
     const int gcnt = min(64, G - c * 64);
     const uint32_t row_bytes = static_cast<uint32_t>(cols) >> 1;
-    const int stride = gridDim.x * RG;
+    const int stride = grid * RG;
     const WSrc src = make_wsrc(nib, meta, rows, cols);
 
-    // activations first, then the first two weight batches, then the staging
+    // activations first, then the first weight batches, then the staging
     // arithmetic while the weights stream in
     WBatch<R> buf0, buf1;
     int base = blockIdx.x * RG;
+    // With R >= 2 only the first batch is issued before the staging: a second
+    // one would stall its issue on the CU's in-flight memory requests, and the
+    // staging waits behind it.
     stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, [&]() {
         load_batch<R>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-        load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        if constexpr (R == 1)
+            load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
     });
+    if constexpr (R > 1)
+        load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
     __syncthreads();
     // this lane's group: kDigits x 8 words of digits, then e and G
     uint32_t xd[kDigits][8];
@@ -504,7 +532,7 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     // early exit between the two buffers): batches past the end load nothing
     // and are skipped by process().
     const int units = (rows + R * RG - 1) / (R * RG);
-    const int trips = (units + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+    const int trips = (units + grid - 1) / grid;
     for (int t = 0; t < trips; t += 2) {
         process(buf0, base);
         load_batch<R>(buf0, src, (base + 2 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
@@ -655,7 +683,7 @@ static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     const int blocks = units < cap ? units : cap;
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
                        static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro, p.y,
-                       p.y_f16, p.partial);
+                       p.y_f16, p.partial, blocks);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     return EPI == EPI_ARGMAX ? launch_argmax_finish(p, blocks, s) : hipSuccess;
 }

@@ -478,8 +478,7 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
                 pred += sreg[r] * (qk[256 + i] * invk);
             }
         }
-        pred += __shfl_xor(pred, 16, kWave);
-        pred += __shfl_xor(pred, 32, kWave);
+        pred = xor_pair_sum<32>(xor_pair_sum<16>(pred));
         if (lane < kScanCols) colsum[wid][lane] = pred;
         __syncthreads();
         pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
@@ -494,8 +493,7 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
                 o += sreg[r] * (qk[i] * invq);
             }
         }
-        o += __shfl_xor(o, 16, kWave);
-        o += __shfl_xor(o, 32, kWave);
+        o = xor_pair_sum<32>(xor_pair_sum<16>(o));
         if (lane < kScanCols) colsum[wid][lane] = o;
         __syncthreads();
         if (threadIdx.x < kScanCols && active) {

@@ -94,6 +94,24 @@ __device__ __forceinline__ float lanes_max(float v) {
     return v;
 }
 
+// v[l] + v[l ^ M] in every lane l, for M = 8 (DPP row_ror:8 within a row of
+// 16), 16 and 32 (gfx950 v_permlane16_swap / v_permlane32_swap: both
+// outputs of the swap together hold the two halves of every pair).
+template <int M>
+__device__ __forceinline__ float xor_pair_sum(float v) {
+    static_assert(M == 8 || M == 16 || M == 32, "pair distance");
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if constexpr (M == 8) {
+        return v + dpp_f32<0x128>(v);
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) + __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) + __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+    }
+}
+
 __device__ __forceinline__ float readlane_f32(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
