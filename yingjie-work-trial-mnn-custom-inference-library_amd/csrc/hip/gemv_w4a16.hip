@@ -346,6 +346,15 @@ static hipError_t launch_argmax_finish(const GemvLaunch& p, int blocks, hipStrea
 // the same on every path, which lets each wait cover exactly the buffer it
 // consumes (vector loads complete in issue order) instead of draining both.
 // ---------------------------------------------------------------------------
+// Partial row sums of column-split launches (NCH > 1) are kept in LDS,
+// [slot][row group][chunk][R] floats, and combined for kDeferredSlots batches
+// at a time (in practice once, after the loop), one barrier per combine
+// instead of two per batch.
+constexpr int kMaxDeferredPartials = 4096;
+template <int RG, int NCH, int R>
+constexpr int kDeferredSlots = kMaxDeferredPartials / (RG * NCH * R) > 0 ? kMaxDeferredPartials / (RG * NCH * R) : 1;
+__host__ __device__ inline int batches_of(int trips) { return 2 * ((trips + 1) / 2); }
+
 template <int R>
 struct WBatch {
     uint4 a[R], b[R];
@@ -392,7 +401,6 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const void* x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
     uint64_t* __restrict__ partial, int grid) {  // grid == gridDim.x (an argument: no late kernarg fetch)
     extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
-    __shared__ float part[RG * NCH * R];
     __shared__ float red[32];
     __shared__ uint64_t lds_keys[16];
     const int G = cols >> 6;
@@ -439,60 +447,13 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     }
 
     uint64_t best = 0;
+    const int units = (rows + R * RG - 1) / (R * RG);
+    const int trips = (units + grid - 1) / grid;
+    float* partial_all = reinterpret_cast<float*>(xs + G * kStageRecord);
+    constexpr int kSlots = kDeferredSlots<RG, NCH, R>;
 
-    auto process = [&](WBatch<R>& cur, int bbase) {
-        const int r0 = (bbase + rg) * R;
-        float acc[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) acc[i] = 0.0f;
-        if (r0 < rows) {
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const uint32_t wd[8] = {cur.a[i].x, cur.a[i].y, cur.a[i].z, cur.a[i].w,
-                                        cur.b[i].x, cur.b[i].y, cur.b[i].z, cur.b[i].w};
-                int A[kDigits];
-#pragma unroll
-                for (int d = 0; d < kDigits; ++d) A[d] = 0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-#pragma unroll
-                    for (int d = 0; d < kDigits; ++d)
-                        A[d] = __builtin_amdgcn_sdot8(static_cast<int>(wd[j]), static_cast<int>(xd[d][j]), A[d], false);
-                // D = sum_d A_d 16^d, exact in int32 (|D| < 2^30, partial sums smaller)
-                int Dg = A[kDigits - 1];
-#pragma unroll
-                for (int d = kDigits - 2; d >= 0; --d) Dg = (Dg << 4) + A[d];
-                // sum_c q_c x_c = e (D + 8 G), sum_c x_c = e G, so
-                //   v1: s (sum qx - z sum x) = s e (D + (8 - z) G)   (exact cancellation for z = 8)
-                //   v2: s sum qx + z sum x   = e (s D + (8 s + z) G)
-                const float df = static_cast<float>(Dg);
-                const float sc = half_lo(cur.m[i]);
-                const float z = half_hi(cur.m[i]);
-                acc[i] = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
-                acc[i] = wave_sum(acc[i]);
-            }
-        }
-        if constexpr (NCH > 1) {
-            if (lane < R) {
-                float v = acc[0];
-#pragma unroll
-                for (int i = 1; i < R; ++i)
-                    if (lane == i) v = acc[i];
-                part[(rg * NCH + c) * R + lane] = v;
-            }
-            __syncthreads();
-            if (c == 0) {
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    float t = 0.0f;
-#pragma unroll
-                    for (int cc = 0; cc < NCH; ++cc) t += part[(rg * NCH + cc) * R + i];
-                    acc[i] = t;
-                }
-            }
-            __syncthreads();
-        }
-        if (c != 0 || r0 >= rows) return;
+    // epilogue of rows r0 .. r0 + R - 1 (chunk-0 waves; every lane holds the sums)
+    auto finish_rows = [&](const float (&acc)[R], int r0) {
         if constexpr (EPI == EPI_ARGMAX) {
 #pragma unroll
             for (int i = 0; i < R; ++i)
@@ -526,19 +487,88 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         }
     };
 
+    // sums the chunk partials of batches b0 .. b0 + n - 1 and finishes their rows
+    auto combine = [&](int b0, int n) {
+        __syncthreads();
+        if (c == 0) {
+            for (int bi = b0; bi < b0 + n; ++bi) {
+                const int r0 = (static_cast<int>(blockIdx.x) * RG + bi * stride + rg) * R;
+                if (r0 >= rows) continue;
+                float acc[R];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int cc = 0; cc < NCH; ++cc) t += partial_all[(((bi % kSlots) * RG + rg) * NCH + cc) * R + i];
+                    acc[i] = t;
+                }
+                finish_rows(acc, r0);
+            }
+        }
+        __syncthreads();  // the slots are reused by the next batches
+    };
+
+    auto process = [&](WBatch<R>& cur, int bbase, int bidx) {
+        const int r0 = (bbase + rg) * R;
+        float acc[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+        if (r0 < rows) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const uint32_t wd[8] = {cur.a[i].x, cur.a[i].y, cur.a[i].z, cur.a[i].w,
+                                        cur.b[i].x, cur.b[i].y, cur.b[i].z, cur.b[i].w};
+                int A[kDigits];
+#pragma unroll
+                for (int d = 0; d < kDigits; ++d) A[d] = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+#pragma unroll
+                    for (int d = 0; d < kDigits; ++d)
+                        A[d] = __builtin_amdgcn_sdot8(static_cast<int>(wd[j]), static_cast<int>(xd[d][j]), A[d], false);
+                // D = sum_d A_d 16^d, exact in int32 (|D| < 2^30, partial sums smaller)
+                int Dg = A[kDigits - 1];
+#pragma unroll
+                for (int d = kDigits - 2; d >= 0; --d) Dg = (Dg << 4) + A[d];
+                // sum_c q_c x_c = e (D + 8 G), sum_c x_c = e G, so
+                //   v1: s (sum qx - z sum x) = s e (D + (8 - z) G)   (exact cancellation for z = 8)
+                //   v2: s sum qx + z sum x   = e (s D + (8 s + z) G)
+                const float df = static_cast<float>(Dg);
+                const float sc = half_lo(cur.m[i]);
+                const float z = half_hi(cur.m[i]);
+                acc[i] = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
+                acc[i] = wave_sum(acc[i]);
+            }
+        }
+        if constexpr (NCH > 1) {
+            float v = acc[0];
+#pragma unroll
+            for (int i = 1; i < R; ++i)
+                if (lane == i) v = acc[i];
+            if (lane < R) partial_all[(((bidx % kSlots) * RG + rg) * NCH + c) * R + lane] = v;
+            if ((bidx + 1) % kSlots == 0) combine(bidx + 1 - kSlots, kSlots);  // block-uniform
+            return;
+        }
+        if (r0 >= rows) return;
+        finish_rows(acc, r0);
+    };
+
     // two batches per trip so each register buffer has a fixed name; a buffer
     // is refilled with the batch two strides ahead as soon as it is reduced
     // The trip count is the grid-wide maximum (uniform, so the loop has no
     // early exit between the two buffers): batches past the end load nothing
     // and are skipped by process().
-    const int units = (rows + R * RG - 1) / (R * RG);
-    const int trips = (units + grid - 1) / grid;
     for (int t = 0; t < trips; t += 2) {
-        process(buf0, base);
+        process(buf0, base, t);
         load_batch<R>(buf0, src, (base + 2 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-        process(buf1, base + stride);
+        process(buf1, base + stride, t + 1);
         load_batch<R>(buf1, src, (base + 3 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
         base += 2 * stride;
+    }
+    if constexpr (NCH > 1) {
+        const int nb = batches_of(trips);
+        const int done = (nb / kSlots) * kSlots;
+        if (nb > done) combine(done, nb - done);
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
@@ -667,20 +697,31 @@ template <int NCH, int R, int EPI>
 static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     constexpr int RG = kRowGroups<NCH>;
     const int G = p.cols >> 6;
-    const size_t lds = static_cast<size_t>(G) * kStageRecord * sizeof(uint4);
+    const size_t stage_lds = static_cast<size_t>(G) * kStageRecord * sizeof(uint4);
+    // occupancy and the LDS limit are set for the largest partial-sum area
+    const size_t lds_max = stage_lds + (NCH > 1 ? sizeof(float) * kMaxDeferredPartials : 0);
     const auto fn = reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>);
-    if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
-        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (lds_max > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
+        const hipError_t e =
+            hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max));
         if (e != hipSuccess) return e;
     }
     // No more blocks than are resident at once (each stages x once); trips are
     // grid-uniform, blocks whose later rows fall past the end skip them.
     static int resident_cache[16] = {};
-    int cap = p.max_blocks > 0 ? p.max_blocks : resident_blocks(fn, 64 * NCH * RG, lds, resident_cache);
+    int cap = p.max_blocks > 0 ? p.max_blocks : resident_blocks(fn, 64 * NCH * RG, lds_max, resident_cache);
     if (cap < 1) cap = device_cus();
     if (EPI == EPI_ARGMAX && cap > kArgmaxMaxBlocks) cap = kArgmaxMaxBlocks;
     const int units = (p.rows + R * RG - 1) / (R * RG);
     const int blocks = units < cap ? units : cap;
+    const int trips = (units + blocks - 1) / blocks;
+    size_t lds = stage_lds;
+    if (NCH > 1)
+    {
+        constexpr int kSlots = kDeferredSlots<RG, NCH, R>;
+        const int slots = batches_of(trips) < kSlots ? batches_of(trips) : kSlots;
+        lds += sizeof(float) * static_cast<size_t>(slots) * RG * NCH * R;
+    }
     hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
                        static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro, p.y,
                        p.y_f16, p.partial, blocks);
