@@ -324,7 +324,8 @@ def oracle_linear_step(mixed, st, cw, a, b, a_log, dt, S, shape):
     return out
 
 
-@pytest.mark.parametrize("shape", [(16, 32, 128, 128, 4), (1, 2, 2, 2, 2), (3, 6, 64, 32, 3), (2, 2, 256, 40, 4)])
+@pytest.mark.parametrize("shape", [(16, 32, 128, 128, 4), (1, 2, 2, 2, 2), (3, 6, 64, 32, 3), (2, 2, 256, 40, 4),
+                                   (2, 4, 64, 64, 5), (2, 4, 32, 32, 8)])
 def test_fused_linear_attn_step_two_positions(shape):
     """xqhip_linear_attn_step against the oracle's conv + L2 norm + gated delta on
     two consecutive positions, which exercises both halves of the parity-

@@ -503,6 +503,7 @@ hipError_t launch_conv(const ConvLaunch& p, hipStream_t s) {
 constexpr int kDeltaCols = 16;
 constexpr int kDeltaIGroups = 16;   // threads per column
 constexpr int kDeltaMaxKPerThread = 16;  // key dim <= 256
+constexpr int kStepMaxTaps = 8;          // conv kernel size of the fused step
 
 __global__ void __launch_bounds__(256) gated_delta_kernel(DeltaLaunch p) {
     __shared__ float qk[2 * 256];
@@ -585,7 +586,11 @@ hipError_t launch_delta(const DeltaLaunch& p, hipStream_t s) {
 // q/k history is written by one block per key head (vh % factor == 0, first
 // slice), the value history by the block that owns the channel.
 // ---------------------------------------------------------------------------
+// KS > 0: the conv kernel size as a compile-time constant (the tap loops then
+// issue exactly the loads they need); KS == 0: runtime p.ksize <= kStepMaxTaps.
+template <int KS>
 __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
+    constexpr int kTaps = KS > 0 ? KS : kStepMaxTaps;
     __shared__ float qk[2 * 256];
     __shared__ float vsh[kDeltaCols];
     __shared__ float colsum[4][kDeltaCols];
@@ -595,49 +600,118 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
     const int factor = max(1, p.lv_n / max(1, p.lk_n));
     const int kh = min(p.lk_n - 1, vh / factor);
     const int dk = p.lk_hd, dv = p.lv_hd;
-    const int hist = max(0, p.ksize - 1);
+    const int hist = KS > 0 ? KS - 1 : max(0, p.ksize - 1);
     const int conv_dim = 2 * p.lk_n * dk + p.lv_n * dv;
-    const int par = *p.pos & 1;
-    const float* st_in = p.conv_state + static_cast<size_t>(par) * conv_dim * hist;
-    float* st_out = p.conv_state + static_cast<size_t>(par ^ 1) * conv_dim * hist;
     const bool qk_writer = (vh % factor == 0) && blockIdx.y == 0;
     const int jl = threadIdx.x % kDeltaCols;
     const int ig = threadIdx.x / kDeltaCols;
     const int j = j0 + jl;
     const bool active = j < dv;
     float* S = p.state + static_cast<size_t>(vh) * dk * dv;
-    float sreg[kDeltaMaxKPerThread];
+    // Loads in the order their data is needed: the conv inputs (filter taps,
+    // history, the in_proj output: cache-resident) first, the state (HBM)
+    // after them, so the conv arithmetic runs while the state streams in
+    // (a wave's loads return in issue order).  Thread t owns q/k channel t
+    // and t + 256 (dk <= 256), threads < kDeltaCols one value channel.
+    struct Taps {
+        float h[kTaps > 1 ? kTaps - 1 : 1], h_other[kTaps > 1 ? kTaps - 1 : 1], w[kTaps], x;
+    };
+    // Unconditional range-checked loads (c < 0: an unused channel, reads 0).
+    // Both history copies are read, so no load waits for the position; the
+    // copy of this position's parity is selected afterwards.
+    const uint32_t hist_bytes = static_cast<uint32_t>(conv_dim * hist) * 4u;
+    const __amdgpu_buffer_rsrc_t r_hist = buf_rsrc(p.conv_state, 2u * hist_bytes);
+    const __amdgpu_buffer_rsrc_t r_w = buf_rsrc(p.conv_w, static_cast<uint32_t>(conv_dim * p.ksize) * 4u);
+    const __amdgpu_buffer_rsrc_t r_x = buf_rsrc(p.mixed, static_cast<uint32_t>(conv_dim) * 4u);
+    auto load_taps = [&](int c, Taps& tp) {
+        const bool ok = c >= 0;
+        const uint32_t ho = static_cast<uint32_t>(c * hist) * 4u, wo = static_cast<uint32_t>(c * p.ksize) * 4u;
 #pragma unroll
-    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {  // state loads first: they depend on nothing
-        const int i = ig + r * kDeltaIGroups;
-        sreg[r] = (active && i < dk) ? S[static_cast<size_t>(i) * dv + j] : 0.0f;
-    }
-    auto conv = [&](int c, bool write) {
-        const float* st = st_in + static_cast<size_t>(c) * hist;
-        const float* w = p.conv_w + static_cast<size_t>(c) * p.ksize;
-        float acc = 0.0f;
-        for (int t = 0; t < hist; ++t) acc += st[t] * w[t];
-        const float xv = p.mixed[c];
-        acc += xv * w[hist];
-        if (write && hist > 0) {
-            float* so = st_out + static_cast<size_t>(c) * hist;
-            for (int t = 0; t + 1 < hist; ++t) so[t] = st[t + 1];
-            so[hist - 1] = xv;
+        for (int t = 0; t < kTaps - 1; ++t) {
+            tp.h[t] = buf_load_f32(r_hist, ok && t < hist ? ho + 4u * t : kBufOOB);
+            tp.h_other[t] = buf_load_f32(r_hist, ok && t < hist ? hist_bytes + ho + 4u * t : kBufOOB);
         }
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t) tp.w[t] = buf_load_f32(r_w, ok && t <= hist ? wo + 4u * t : kBufOOB);
+        tp.x = buf_load_f32(r_x, ok ? static_cast<uint32_t>(c) * 4u : kBufOOB);
+    };
+    // per-head gate inputs first (4 uniform loads; read as scalars they would
+    // be fetched only when first used, after the conv)
+    const uint32_t ho4 = static_cast<uint32_t>(vh) * 4u, hbytes = static_cast<uint32_t>(p.lv_n) * 4u;
+    const float gb = buf_load_f32(buf_rsrc(p.b, hbytes), ho4);
+    const float ga = buf_load_f32(buf_rsrc(p.a, hbytes), ho4);
+    const float galog = buf_load_f32(buf_rsrc(p.a_log, hbytes), ho4);
+    const float gdtb = buf_load_f32(buf_rsrc(p.dt_bias, hbytes), ho4);
+    auto select_parity = [&](Taps& tp, int odd) {
+#pragma unroll
+        for (int t = 0; t < kTaps - 1; ++t) tp.h[t] = odd ? tp.h_other[t] : tp.h[t];
+    };
+    // (register arrays indexed by unrolled constants only: a runtime index would
+    // move them to scratch memory)
+    auto conv = [&](const Taps& tp) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kTaps - 1; ++t) acc += tp.h[t] * tp.w[t];  // taps past hist are 0
+#pragma unroll
+        for (int t = 0; t < kTaps; ++t)
+            if (t == hist) acc += tp.x * tp.w[t];
         return silu_dev(acc);
     };
+    // the shifted history goes out at the end of the kernel: a store issued
+    // before the state is consumed would make every later wait a full drain
+    auto write_history = [&](float* st_out, int c, const Taps& tp) {
+        if (hist == 0) return;
+        float* so = st_out + static_cast<size_t>(c) * hist;
+#pragma unroll
+        for (int t = 0; t + 1 < kTaps - 1; ++t)
+            if (t + 1 < hist) so[t] = tp.h[t + 1];
+        so[hist - 1] = tp.x;
+    };
+    constexpr int kThreads = 256;  // the launch's block size
+    const int nqk = (2 * dk + kThreads - 1) / kThreads;  // <= 2
+    Taps tq[2], tv;
+    auto qk_channel = [&](int t, int& d, bool& is_k) {
+        is_k = t >= dk;
+        d = is_k ? t - dk : t;
+        return (is_k ? p.lk_n * dk : 0) + kh * dk + d;
+    };
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int t = threadIdx.x + u * kThreads;
+        int d; bool is_k;
+        const int c = qk_channel(t, d, is_k);
+        load_taps(u < nqk && t < 2 * dk ? c : -1, tq[u]);
+    }
+    const bool has_v = threadIdx.x < kDeltaCols && j0 + static_cast<int>(threadIdx.x) < dv;
+    load_taps(has_v ? 2 * p.lk_n * dk + vh * dv + j0 + static_cast<int>(threadIdx.x) : -1, tv);
+    const __amdgpu_buffer_rsrc_t r_state = buf_rsrc(S, static_cast<uint32_t>(dk * dv) * 4u);
+    float sreg[kDeltaMaxKPerThread];
+#pragma unroll
+    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
+        const int i = ig + r * kDeltaIGroups;
+        sreg[r] = buf_load_f32(r_state, active && i < dk ? static_cast<uint32_t>(i * dv + j) * 4u : kBufOOB);
+    }
+    // the position is read after every load is issued (its parity picks the
+    // history copy read above and the one written at the end)
+    const int par = __builtin_nontemporal_load(p.pos) & 1;
+    float* st_out = p.conv_state + static_cast<size_t>(par ^ 1) * conv_dim * hist;
+    select_parity(tq[0], par);
+    select_parity(tq[1], par);
+    select_parity(tv, par);
     // q and k channels of key head kh: thread t < dk -> q[t], dk <= t < 2 dk -> k[t - dk]
     float ssq = 0.0f, ssk = 0.0f;
-    for (int t = threadIdx.x; t < 2 * dk; t += blockDim.x) {
-        const bool is_k = t >= dk;
-        const int d = is_k ? t - dk : t;
-        const int c = (is_k ? p.lk_n * dk : 0) + kh * dk + d;
-        const float y = conv(c, qk_writer);
-        qk[(is_k ? 256 : 0) + d] = y;
-        if (is_k) ssk += y * y; else ssq += y * y;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int t = threadIdx.x + u * kThreads;
+        if (u < nqk && t < 2 * dk) {
+            int d; bool is_k;
+            qk_channel(t, d, is_k);
+            const float y = conv(tq[u]);
+            qk[(is_k ? 256 : 0) + d] = y;
+            if (is_k) ssk += y * y; else ssq += y * y;
+        }
     }
-    if (threadIdx.x < kDeltaCols && j0 + threadIdx.x < dv)
-        vsh[threadIdx.x] = conv(2 * p.lk_n * dk + vh * dv + j0 + threadIdx.x, true);
+    if (has_v) vsh[threadIdx.x] = conv(tv);
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     ssq = wave_sum(ssq);
     ssk = wave_sum(ssk);
@@ -645,8 +719,8 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
         red[0][wid] = ssq;
         red[1][wid] = ssk;
     }
-    const float beta = sigmoid_dev(p.b[vh]);
-    const float gate = -expf(p.a_log[vh]) * softplus_dev(p.a[vh] + p.dt_bias[vh]);
+    const float beta = sigmoid_dev(gb);
+    const float gate = -expf(galog) * softplus_dev(ga + gdtb);
     const float decay = expf(gate);
     __syncthreads();
     // l2NormalizeHeads: x * 1/sqrt(sum x^2 + 1e-6)
@@ -685,16 +759,30 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
         const float tot = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
         p.out[static_cast<size_t>(vh) * dv + j] = tot * (1.0f / sqrtf(static_cast<float>(dk)));
     }
+    if (qk_writer) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int t = threadIdx.x + u * kThreads;
+            if (u < nqk && t < 2 * dk) {
+                int d; bool is_k;
+                write_history(st_out, qk_channel(t, d, is_k), tq[u]);
+            }
+        }
+    }
+    if (has_v) write_history(st_out, 2 * p.lk_n * dk + vh * dv + j0 + threadIdx.x, tv);
 }
 
 bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
     return lk_n > 0 && lv_n > 0 && lv_n % lk_n == 0 && lk_hd > 0 && lk_hd <= 256 && lv_hd > 0 && ksize >= 1 &&
-           lk_hd <= kDeltaIGroups * kDeltaMaxKPerThread;
+           ksize <= kStepMaxTaps && lk_hd <= kDeltaIGroups * kDeltaMaxKPerThread;
 }
 
 hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s) {
-    hipLaunchKernelGGL(linear_step_kernel, dim3(p.lv_n, (p.lv_hd + kDeltaCols - 1) / kDeltaCols), dim3(256), 0, s,
-                       p);
+    const dim3 grid(p.lv_n, (p.lv_hd + kDeltaCols - 1) / kDeltaCols);
+    if (p.ksize == 4)
+        hipLaunchKernelGGL(linear_step_kernel<4>, grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(linear_step_kernel<0>, grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -47,6 +47,18 @@ __device__ __forceinline__ float half_hi(uint32_t u) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16)));
 }
 
+// Range-checked buffer loads: an offset at or past the resource's byte range
+// returns 0 without a memory access, so a load can be issued unconditionally
+// (straight-line code keeps the compiler's load-count waits exact).
+constexpr uint32_t kBufWord3 = 0x00020000u;  // raw 32-bit buffer, gfx9-family format
+constexpr uint32_t kBufOOB = 0x80000000u;    // an offset past every range used here
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, kBufWord3);
+}
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 // Cross-lane reductions by DPP lane moves inside the VALU (no LDS round trip,
 // unlike ds_bpermute): quad_perm [1,0,3,2] and [2,3,0,1] exchange lanes i^1
 // and i^2, row_half_mirror maps lane i to 7-i within each 8, row_mirror maps
