@@ -359,6 +359,7 @@ constexpr int kScanIGroups = 16;
 constexpr int kScanMaxK = 16;     // key dim <= 256
 constexpr int kScanMaxHist = 7;   // conv kernel <= 8
 constexpr int kScanMaxQkPerThread = 2;
+constexpr int kScanAhead = 4;       // tokens per load group
 
 __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
     __shared__ float qk[2 * 256];
@@ -410,23 +411,37 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
     const float rdk = 1.0f / sqrtf(static_cast<float>(dk));
     const float neg_exp_alog = -expf(p.a_log[vh]);
     const float dtb = p.dt_bias[vh];
-    // inputs of token t + 1 are loaded while token t is computed
-    float xnext[kScanMaxQkPerThread + 1];
-    float a_next = 0.0f, b_next = 0.0f;
-    auto load_token = [&](int t) {
-        const float* mixed = p.mixed + static_cast<size_t>(t) * p.mixed_stride;
+    // Token inputs are loaded kScanAhead tokens at a time, one group ahead of
+    // the group being computed (a token's compute is shorter than a load's
+    // latency), with range-checked buffer loads: rows past the last token
+    // read as 0 without a memory access, so every load is unconditional.
+    const uint32_t stride4 = static_cast<uint32_t>(p.mixed_stride) * 4u;
+    const __amdgpu_buffer_rsrc_t r_mixed = buf_rsrc(p.mixed, static_cast<uint32_t>(p.tokens) * stride4);
+    const uint32_t ab_bytes = static_cast<uint32_t>(p.tokens - 1) * stride4 + static_cast<uint32_t>(p.lv_n) * 4u;
+    const __amdgpu_buffer_rsrc_t r_a = buf_rsrc(p.a, ab_bytes), r_b = buf_rsrc(p.b, ab_bytes);
+    float xg[2][kScanAhead][kScanMaxQkPerThread + 1], ag[2][kScanAhead], bg[2][kScanAhead];
+    auto load_group = [&](int t0, int buf) {
 #pragma unroll
-        for (int u = 0; u <= kScanMaxQkPerThread; ++u) xnext[u] = ch[u] >= 0 ? mixed[ch[u]] : 0.0f;
-        a_next = p.a[static_cast<size_t>(t) * p.mixed_stride + vh];
-        b_next = p.b[static_cast<size_t>(t) * p.mixed_stride + vh];
+        for (int k = 0; k < kScanAhead; ++k) {
+            const uint32_t row = static_cast<uint32_t>(t0 + k) * stride4;
+#pragma unroll
+            for (int u = 0; u <= kScanMaxQkPerThread; ++u)
+                xg[buf][k][u] = buf_load_f32(r_mixed, ch[u] >= 0 ? row + static_cast<uint32_t>(ch[u]) * 4u : kBufOOB);
+            ag[buf][k] = buf_load_f32(r_a, row + static_cast<uint32_t>(vh) * 4u);
+            bg[buf][k] = buf_load_f32(r_b, row + static_cast<uint32_t>(vh) * 4u);
+        }
     };
-    load_token(0);
-    for (int t = 0; t < p.tokens; ++t) {
+    load_group(0, 0);
+    for (int t0 = 0; t0 < p.tokens; t0 += kScanAhead) {
+        load_group(t0 + kScanAhead, 1);
+#pragma unroll
+        for (int k = 0; k < kScanAhead; ++k) {
+        const int t = t0 + k;
+        if (t >= p.tokens) break;  // block-uniform
         float xcur[kScanMaxQkPerThread + 1];
 #pragma unroll
-        for (int u = 0; u <= kScanMaxQkPerThread; ++u) xcur[u] = xnext[u];
-        const float a_cur = a_next, b_cur = b_next;
-        if (t + 1 < p.tokens) load_token(t + 1);
+        for (int u = 0; u <= kScanMaxQkPerThread; ++u) xcur[u] = xg[0][k][u];
+        const float a_cur = ag[0][k], b_cur = bg[0][k];
         float ssq = 0.0f, ssk = 0.0f;
 #pragma unroll
         for (int u = 0; u <= kScanMaxQkPerThread; ++u) {
@@ -501,6 +516,14 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
             p.out[static_cast<size_t>(t) * p.out_stride + static_cast<size_t>(vh) * dv + j] = tot * rdk;
         }
         __syncthreads();  // qk, vsh, red and colsum are rewritten by the next token
+        }
+#pragma unroll
+        for (int k = 0; k < kScanAhead; ++k) {
+#pragma unroll
+            for (int u = 0; u <= kScanMaxQkPerThread; ++u) xg[0][k][u] = xg[1][k][u];
+            ag[0][k] = ag[1][k];
+            bg[0][k] = bg[1][k];
+        }
     }
 #pragma unroll
     for (int r = 0; r < kScanMaxK; ++r) {
@@ -517,13 +540,164 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
     }
 }
 
+// Wave-independent form for key dim DK and conv size KS (the 9B shape: 128, 4).
+// Wave w of block (vh, y) owns value columns y*16 + 4w .. +3 of head vh; lane
+// l owns column l/16 and key rows i = l%16 + 16r, so both sums over the key
+// dimension (the prediction and the output) are reductions over 16 lanes of
+// one DPP row.  Every wave convolves the whole q/k head itself (cheap) and
+// exchanges the convolved channels through its own LDS slice, so a token
+// needs no block barrier at all.
+template <int DK, int KS>
+__global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch p) {
+    constexpr int CH = 2 * DK / kWave;  // q/k channels per lane
+    constexpr int RS = DK / 16;         // state rows per lane
+    constexpr int H = KS - 1;
+    static_assert(CH >= 1 && CH % 2 == 0 && RS >= 1, "key dim");
+    __shared__ float qk_lds[4][2 * DK];
+    const int vh = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int factor = max(1, p.lv_n / max(1, p.lk_n));
+    const int kh = min(p.lk_n - 1, vh / factor);
+    const int dv = p.lv_hd;
+    const int ig = lane & 15;
+    const int j = blockIdx.y * kScanCols + wid * 4 + (lane >> 4);
+    const bool active = j < dv;
+    float* qk_w = qk_lds[wid];
+    auto qk_channel = [&](int t) { return (t >= DK ? p.lk_n * DK : 0) + kh * DK + (t % DK); };
+    const int vch = 2 * p.lk_n * DK + vh * dv + j;
+    // filter taps and history (history in registers across the tokens)
+    float hq[CH][H > 0 ? H : 1], wq[CH][KS], hv[H > 0 ? H : 1], wvv[KS];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+        const int c = qk_channel(lane + u * kWave);
+#pragma unroll
+        for (int t = 0; t < H; ++t) hq[u][t] = p.hist_in[static_cast<size_t>(c) * H + t];
+#pragma unroll
+        for (int t = 0; t < KS; ++t) wq[u][t] = p.conv_w[static_cast<size_t>(c) * KS + t];
+    }
+#pragma unroll
+    for (int t = 0; t < H; ++t) hv[t] = active ? p.hist_in[static_cast<size_t>(vch) * H + t] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) wvv[t] = active ? p.conv_w[static_cast<size_t>(vch) * KS + t] : 0.0f;
+    float* S = p.state + static_cast<size_t>(vh) * DK * dv;
+    float sreg[RS];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) sreg[r] = active ? S[static_cast<size_t>(ig + 16 * r) * dv + j] : 0.0f;
+    const float rdk = 1.0f / sqrtf(static_cast<float>(DK));
+    const float neg_exp_alog = -expf(p.a_log[vh]);
+    const float dtb = p.dt_bias[vh];
+    // token inputs, a group of kScanAhead tokens ahead (range-checked: rows past
+    // the last token read 0 without a memory access)
+    const uint32_t stride4 = static_cast<uint32_t>(p.mixed_stride) * 4u;
+    const __amdgpu_buffer_rsrc_t r_mixed = buf_rsrc(p.mixed, static_cast<uint32_t>(p.tokens) * stride4);
+    const uint32_t ab_bytes = static_cast<uint32_t>(p.tokens - 1) * stride4 + static_cast<uint32_t>(p.lv_n) * 4u;
+    const __amdgpu_buffer_rsrc_t r_a = buf_rsrc(p.a, ab_bytes), r_b = buf_rsrc(p.b, ab_bytes);
+    float xg[2][kScanAhead][CH + 1], ag[2][kScanAhead], bg[2][kScanAhead];
+    auto load_group = [&](int t0, int buf) {
+#pragma unroll
+        for (int k = 0; k < kScanAhead; ++k) {
+            const uint32_t row = static_cast<uint32_t>(t0 + k) * stride4;
+#pragma unroll
+            for (int u = 0; u < CH; ++u)
+                xg[buf][k][u] = buf_load_f32(r_mixed, row + static_cast<uint32_t>(qk_channel(lane + u * kWave)) * 4u);
+            xg[buf][k][CH] = buf_load_f32(r_mixed, active ? row + static_cast<uint32_t>(vch) * 4u : kBufOOB);
+            ag[buf][k] = buf_load_f32(r_a, row + static_cast<uint32_t>(vh) * 4u);
+            bg[buf][k] = buf_load_f32(r_b, row + static_cast<uint32_t>(vh) * 4u);
+        }
+    };
+    auto conv_step = [&](float (&h)[H > 0 ? H : 1], const float (&w)[KS], float x) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < H; ++t) acc += h[t] * w[t];
+        acc += x * w[H];
+#pragma unroll
+        for (int t = 0; t + 1 < H; ++t) h[t] = h[t + 1];
+        if constexpr (H > 0) h[H - 1] = x;
+        return silu_dev(acc);
+    };
+    load_group(0, 0);
+    for (int t0 = 0; t0 < p.tokens; t0 += kScanAhead) {
+        load_group(t0 + kScanAhead, 1);
+#pragma unroll
+        for (int k = 0; k < kScanAhead; ++k) {
+            const int t = t0 + k;
+            if (t >= p.tokens) break;  // grid-uniform
+            float ssq = 0.0f, ssk = 0.0f;
+#pragma unroll
+            for (int u = 0; u < CH; ++u) {
+                const float y = conv_step(hq[u], wq[u], xg[0][k][u]);
+                qk_w[lane + u * kWave] = y;
+                if (u < CH / 2) ssq += y * y; else ssk += y * y;
+            }
+            const float vj = conv_step(hv, wvv, xg[0][k][CH]);
+            ssq = wave_sum(ssq);
+            ssk = wave_sum(ssk);
+            const float invq = 1.0f / sqrtf(ssq + 1.0e-6f);
+            const float invk = 1.0f / sqrtf(ssk + 1.0e-6f);
+            const float beta = sigmoid_dev(bg[0][k]);
+            const float decay = expf(neg_exp_alog * softplus_dev(ag[0][k] + dtb));
+            // the wave's own LDS writes above complete before these reads (LDS
+            // operations of a wave are performed in order): no barrier
+            float kr[RS], qr[RS];
+#pragma unroll
+            for (int r = 0; r < RS; ++r) {
+                kr[r] = qk_w[DK + ig + 16 * r] * invk;
+                qr[r] = qk_w[ig + 16 * r] * invq;
+            }
+            float pred = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RS; ++r) {
+                sreg[r] *= decay;
+                pred += sreg[r] * kr[r];
+            }
+            pred = lanes_sum<16>(pred);
+            const float delta = beta * (vj - pred);
+            float o = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RS; ++r) {
+                sreg[r] += kr[r] * delta;
+                o += sreg[r] * qr[r];
+            }
+            o = lanes_sum<16>(o);
+            if (ig == 0 && active) p.out[static_cast<size_t>(t) * p.out_stride + static_cast<size_t>(vh) * dv + j] = o * rdk;
+        }
+#pragma unroll
+        for (int k = 0; k < kScanAhead; ++k) {
+#pragma unroll
+            for (int u = 0; u <= CH; ++u) xg[0][k][u] = xg[1][k][u];
+            ag[0][k] = ag[1][k];
+            bg[0][k] = bg[1][k];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RS; ++r)
+        if (active) S[static_cast<size_t>(ig + 16 * r) * dv + j] = sreg[r];
+    const bool qk_writer = (vh % factor == 0) && blockIdx.y == 0 && wid == 0;
+    if (qk_writer) {
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int c = qk_channel(lane + u * kWave);
+#pragma unroll
+            for (int t = 0; t < H; ++t) p.hist_out[static_cast<size_t>(c) * H + t] = hq[u][t];
+        }
+    }
+    if (ig == 0 && active) {
+#pragma unroll
+        for (int t = 0; t < H; ++t) p.hist_out[static_cast<size_t>(vch) * H + t] = hv[t];
+    }
+}
+
 bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
     return lk_n > 0 && lv_n > 0 && lv_n % lk_n == 0 && lk_hd > 0 && lk_hd <= 256 && lv_hd > 0 && ksize >= 1 &&
            ksize - 1 <= kScanMaxHist && lk_hd <= kScanIGroups * kScanMaxK;
 }
 
 hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
-    hipLaunchKernelGGL(linear_scan_kernel, dim3(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols), dim3(256), 0, s, p);
+    const dim3 grid(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols);
+    if (p.lk_hd == 128 && p.ksize == 4)
+        hipLaunchKernelGGL((linear_scan_wave_kernel<128, 4>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(linear_scan_kernel, grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
