@@ -125,12 +125,42 @@ constexpr int kAttnMaxChunks = kAttnMaxCtx / kAttnChunk;
 constexpr int kAttnGridChunks = 64;  // chunk slots per kv head in the grid
 constexpr int kAttnThreads = 256;
 
+// A chunk's K and V as this thread consumes them (HD > 0): K for the scores
+// (4 lanes per token, HD/4 dims each), V for the weighted sum (HD/8 lanes per
+// token, 8 dims each, tokens ts, ts + TPP, ...).  Loaded by load_kv before the
+// query is ready so the cache latency overlaps the q preparation; token
+// indices past the chunk are clamped to its last token (in bounds, unused).
+template <int HD>
+struct KvRegs {
+    static constexpr int kK = HD / 32;             // uint4 of K per thread
+    static constexpr int kV = kAttnChunk * HD / 2048;  // tokens of V per thread
+    uint4 k[kK > 0 ? kK : 1];
+    uint4 v[kV > 0 ? kV : 1];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_kv(const GqaLaunch& p, int kh, int t0, int n, KvRegs<HD>& r) {
+    if constexpr (HD > 0) {
+        constexpr int DL = HD / 4, LPT = HD / 8, TPP = kAttnThreads / LPT;
+        const int sub = threadIdx.x & 3, tt = threadIdx.x >> 2;
+        const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + min(tt, n - 1)) * p.nkv + kh) * HD + sub * DL;
+#pragma unroll
+        for (int u = 0; u < KvRegs<HD>::kK; ++u) r.k[u] = *reinterpret_cast<const uint4*>(krow + 8 * u);
+        const int dsl = threadIdx.x % LPT, ts = threadIdx.x / LPT;
+#pragma unroll
+        for (int u = 0; u < KvRegs<HD>::kV; ++u) {
+            const int t = min(ts + u * TPP, n - 1);
+            r.v[u] = *reinterpret_cast<const uint4*>(p.v_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * HD + dsl * 8);
+        }
+    }
+}
+
 // pos_new >= 0: key/value of position pos_new come from kn / vn (LDS, the
 // values the same launch appends to the cache) instead of the cache.
 template <int HD>
 __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, int t0, int n, int group, int hd,
-                                          const float* qs, float* sc, float* vred, int pos_new = -1,
-                                          const float* kn = nullptr, const float* vn = nullptr) {
+                                          const float* qs, float* sc, float* vred, const KvRegs<HD>& kvr,
+                                          int pos_new = -1, const float* kn = nullptr, const float* vn = nullptr) {
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
     const int qh0 = kh * group;
@@ -139,12 +169,10 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
         constexpr int DL = HD / 4;
         const int sub = threadIdx.x & 3, tt = threadIdx.x >> 2;
         const bool valid = tt < n;
-        const _Float16* krow =
-            p.k_cache + (static_cast<size_t>(t0 + (valid ? tt : 0)) * p.nkv + kh) * HD + sub * DL;
         float kv[DL];
 #pragma unroll
         for (int u = 0; u < DL / 8; ++u) {
-            const uint4 w = *reinterpret_cast<const uint4*>(krow + 8 * u);
+            const uint4 w = kvr.k[u];
             const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -199,9 +227,11 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
         for (int g = 0; g < kAttnMaxGroup; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
-        for (int t = ts; t < n; t += TPP) {
-            const uint4 w =
-                *reinterpret_cast<const uint4*>(p.v_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * HD + dsl * 8);
+#pragma unroll
+        for (int u = 0; u < KvRegs<HD>::kV; ++u) {
+            const int t = ts + u * TPP;
+            if (t >= n) break;
+            const uint4 w = kvr.v[u];
             float vv[8] = {half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y),
                            half_lo(w.z), half_hi(w.z), half_lo(w.w), half_hi(w.w)};
             if (t0 + t == pos_new) {
@@ -268,13 +298,16 @@ __global__ void __launch_bounds__(kAttnThreads) gqa_chunk_kernel(GqaLaunch p) {
     float* qs = smem;                       // [group][hd]
     float* sc = qs + group * hd;            // [group][64]
     float* vred = sc + group * kAttnChunk;  // [4 waves][group][hd]
+    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
+    KvRegs<HD> kvr;
+    load_kv<HD>(p, kh, blockIdx.y * kAttnChunk, min(kAttnChunk, ctx - static_cast<int>(blockIdx.y) * kAttnChunk), kvr);
     for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) qs[i] = p.q[static_cast<size_t>(kh) * group * hd + i];
     __syncthreads();
-    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
     for (int ch = blockIdx.y; ch < nch; ch += gridDim.y) {
         const int t0 = ch * kAttnChunk;
         const int n = min(kAttnChunk, ctx - t0);
-        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred);
+        if (ch != static_cast<int>(blockIdx.y)) load_kv<HD>(p, kh, t0, n, kvr);
+        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred, kvr);
     }
 }
 
@@ -303,6 +336,10 @@ __global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLau
     const float2* cs = reinterpret_cast<const float2*>(a.rope_cs) + static_cast<size_t>(pos) * a.rope_pairs;
     const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
     const bool owns_new = (pos / kAttnChunk) % static_cast<int>(gridDim.y) == static_cast<int>(blockIdx.y);
+    // K/V of the block's first chunk are requested before the q preparation
+    // (the slot of `pos` is read too but replaced by kn / vn below)
+    KvRegs<HD> kvr;
+    load_kv<HD>(p, kh, blockIdx.y * kAttnChunk, min(kAttnChunk, ctx - static_cast<int>(blockIdx.y) * kAttnChunk), kvr);
     // per-head RMSNorm (custom_model.cpp:301-313): one wave per head; heads
     // 0..group-1 are q, head `group` (owner only) is the new key
     const int nheads = group + (owns_new ? 1 : 0);
@@ -349,7 +386,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLau
     for (int ch = blockIdx.y; ch < nch; ch += gridDim.y) {
         const int t0 = ch * kAttnChunk;
         const int n = min(kAttnChunk, ctx - t0);
-        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred, pos, kn, vn);
+        if (ch != static_cast<int>(blockIdx.y)) load_kv<HD>(p, kh, t0, n, kvr);
+        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred, kvr, pos, kn, vn);
     }
 }
 
