@@ -76,119 +76,157 @@ __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x
 
 // ---------------------------------------------------------------------------
 // W4A16 GEMM, y[t][r] (op)= sum_k w[r][k] x[t][k] for a prompt chunk.
-// Block: 64 weight rows x 64 tokens, 4 waves each owning 32 rows x 32 tokens
-// (2 x 2 tiles of v_mfma_f32_16x16x32_f16).  Per 64-column group: the block
-// dequantises its 64 rows of the TILED64 matrix (codes stored as q ^ 8) to
-// w = (q - z) s (v1) or q s + z (v2) in fp32 and keeps it in LDS as fp16
-// hi + lo halves, stages the hi and lo fp16 halves of its 64 tokens, and every
-// tile issues three MFMAs (w_hi x_hi, w_hi x_lo, w_lo x_hi; both operands then
-// carry about 22 significant bits, as in the fp32 reference).  Token
-// tiles are the fastest grid dimension, so the blocks that share a weight
-// tile run together and the tile is fetched from HBM about once.
+// Block: BR weight rows x 128 tokens, 4 waves each owning BR/2 rows x 64
+// tokens (tiles of v_mfma_f32_16x16x32_f16).  Per 64-column group the block
+// dequantises its BR rows of the TILED64 matrix (codes stored as q ^ 8, read
+// as signed nibbles q - 8) to w = (q - z) s (v1) or q s + z (v2) in fp32 and
+// keeps w in LDS as fp16 hi + lo halves, next to the fp16 hi and lo halves of
+// its 128 tokens; every tile issues three MFMAs (w_hi x_hi, w_hi x_lo,
+// w_lo x_hi), so both operands carry about 22 significant bits as in the fp32
+// reference.  Software pipeline: the raw nibbles, metadata and activations of
+// group g + 1 are loaded into registers while the MFMAs of group g run.
+// Token tiles are the fastest grid dimension, so the blocks that share a
+// weight tile run together and the tile is fetched from HBM about once.
 // MFMA operand layout (16x16x32): lane l supplies row/column (l & 15) and the
 // 8 consecutive k at 8 (l >> 4); lane l receives D[4 (l >> 4) + v][l & 15].
 // ---------------------------------------------------------------------------
-constexpr int kGemmRows = 64;
-constexpr int kGemmToks = 64;
+constexpr int kGemmToks = 128;
 constexpr int kGemmLd = 72;  // LDS row stride in halves (64 + 8 padding)
 
-template <int EPI>
+template <int BR>
+constexpr size_t gemm_lds_bytes() {
+    return static_cast<size_t>(BR + kGemmToks) * kGemmLd * 2 * sizeof(_Float16);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
+
+template <int BR, int EPI>
 __global__ void __launch_bounds__(256) gemm_w4_mfma_kernel(const uint8_t* __restrict__ nib,
                                                            const uint32_t* __restrict__ meta, int rows, int cols,
                                                            int affine, const _Float16* __restrict__ xh,
                                                            const _Float16* __restrict__ xl, int m,
                                                            float* __restrict__ y, int ldy) {
-    __shared__ _Float16 As[kGemmRows * kGemmLd];
-    __shared__ _Float16 Al[kGemmRows * kGemmLd];
-    __shared__ _Float16 Bh[kGemmToks * kGemmLd];
-    __shared__ _Float16 Bl[kGemmToks * kGemmLd];
-    const int t0 = blockIdx.x * kGemmToks;
-    const int r0 = blockIdx.y * kGemmRows;
+    constexpr int BT = kGemmToks;
+    constexpr int WR = BR / 2, TI = WR / 16, TJ = 4;  // wave tile: WR rows x 64 tokens
+    extern __shared__ uint4 gemm_lds[];
+    _Float16* Wh = reinterpret_cast<_Float16*>(gemm_lds);
+    _Float16* Wl = Wh + BR * kGemmLd;
+    _Float16* Xh = Wl + BR * kGemmLd;
+    _Float16* Xl = Xh + BT * kGemmLd;
+    const int t0 = blockIdx.x * BT;
+    const int r0 = blockIdx.y * BR;
     const int G = cols >> 6;
     const size_t row_bytes = static_cast<size_t>(cols) >> 1;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    const int wr = (wid >> 1) * 32, wt = (wid & 1) * 32;
-    floatx4 acc[2][2];
+    const int wr = (wid >> 1) * WR, wt = (wid & 1) * 64;
+    // staging roles: weights, thread < 2 BR: row wrow, 16-byte half wh;
+    // activations: token threadIdx / 2, 32 columns (part) of hi and of lo
+    const bool w_thread = threadIdx.x < 2 * BR;
+    const int wrow = threadIdx.x >> 1, whalf = threadIdx.x & 1;
+    const int r = r0 + wrow;
+    const bool row_ok = w_thread && r < rows;
+    const int rr = min(r, rows - 1);
+    const int xtok = threadIdx.x >> 1, xpart = threadIdx.x & 1;
+    // prefetch registers (plain scalars: kept out of arrays so they stay in VGPRs)
+    uint4 wq = make_uint4(0, 0, 0, 0);
+    uint32_t mq = 0;
+    uint4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
+#define GEMM_LOAD_GROUP(gg)                                                                                        \
+    do {                                                                                                           \
+        const int g_ = (gg);                                                                                       \
+        if (w_thread) {                                                                                            \
+            const int c_ = g_ >> 6, l_ = g_ & 63;                                                                   \
+            const int gcnt_ = min(64, G - c_ * 64);                                                                \
+            wq = *reinterpret_cast<const uint4*>(nib + static_cast<size_t>(rr) * row_bytes + c_ * 2048 +            \
+                                                  whalf * gcnt_ * 16 + l_ * 16);                                   \
+            mq = meta[static_cast<size_t>(rr) * G + g_];                                                           \
+        }                                                                                                          \
+        const size_t src_ = static_cast<size_t>(t0 + xtok) * cols + g_ * 64 + xpart * 32;                         \
+        const uint4* ph_ = reinterpret_cast<const uint4*>(xh + src_);                                              \
+        const uint4* pl_ = reinterpret_cast<const uint4*>(xl + src_);                                              \
+        xa0 = ph_[0]; xa1 = ph_[1]; xa2 = ph_[2]; xa3 = ph_[3];                                                    \
+        xb0 = pl_[0]; xb1 = pl_[1]; xb2 = pl_[2]; xb3 = pl_[3];                                                    \
+    } while (0)
+    auto dequant8 = [&](uint32_t wv, float s, float c0, uint4* dh, uint4* dl) {
+        uint32_t ph[4], pl[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int e = 0; e < 4; ++e) {
+            float wf[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int g = 0; g < G; ++g) {
-        // weights: thread < 128 dequantises one 16-byte half (32 codes) of one row
-        if (threadIdx.x < 2 * kGemmRows) {
-            const int rl = threadIdx.x >> 1, h = threadIdx.x & 1;
-            const int r = r0 + rl;
-            _Float16* dst = As + rl * kGemmLd + h * 32;
-            _Float16* dstl = Al + rl * kGemmLd + h * 32;
-            if (r < rows) {
-                const int c = g >> 6, l = g & 63;
-                const int gcnt = min(64, G - c * 64);
-                const uint4 q16 = *reinterpret_cast<const uint4*>(nib + static_cast<size_t>(r) * row_bytes + c * 2048 +
-                                                                  h * gcnt * 16 + l * 16);
-                const uint32_t mt = meta[static_cast<size_t>(r) * G + g];
-                const float s = half_lo(mt), z = half_hi(mt);
-                const uint32_t wv[4] = {q16.x, q16.y, q16.z, q16.w};
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const float q = static_cast<float>(((wv[u] >> (4 * i)) & 15u) ^ 8u);
-                        const float wf = affine ? fmaf(q, s, z) : (q - z) * s;
-                        const _Float16 wh = static_cast<_Float16>(wf);
-                        dst[u * 8 + i] = wh;
-                        dstl[u * 8 + i] = static_cast<_Float16>(wf - static_cast<float>(wh));
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 32; ++i) dst[i] = dstl[i] = static_cast<_Float16>(0.0f);
+            for (int k = 0; k < 2; ++k) {
+                const int sh = 4 * (2 * e + k);
+                const int sn = static_cast<int>(wv << (28 - sh)) >> 28;  // signed nibble q - 8
+                wf[k] = row_ok ? fmaf(static_cast<float>(sn), s, c0) : 0.0f;
             }
+            const _Float16 h0 = static_cast<_Float16>(wf[0]), h1 = static_cast<_Float16>(wf[1]);
+            ph[e] = pack_h2(h0, h1);
+            pl[e] = pack_h2(static_cast<_Float16>(wf[0] - static_cast<float>(h0)),
+                            static_cast<_Float16>(wf[1] - static_cast<float>(h1)));
         }
-        // activations: 64 tokens x 64 columns of hi and lo, 16 bytes per load
-        {
-            const int tl = threadIdx.x >> 2, part = threadIdx.x & 3;
-            const size_t src = static_cast<size_t>(t0 + tl) * cols + g * 64 + part * 16;
-            const uint4* ph = reinterpret_cast<const uint4*>(xh + src);
-            const uint4* pl = reinterpret_cast<const uint4*>(xl + src);
-            uint4* dh = reinterpret_cast<uint4*>(Bh + tl * kGemmLd + part * 16);
-            uint4* dl = reinterpret_cast<uint4*>(Bl + tl * kGemmLd + part * 16);
-            dh[0] = ph[0];
-            dh[1] = ph[1];
-            dl[0] = pl[0];
-            dl[1] = pl[1];
+        *dh = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+        *dl = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    };
+    auto store_group = [&]() {
+        if (w_thread) {
+            const float s = half_lo(mq), z = half_hi(mq);
+            // w = sn * s + c0 with sn = q - 8 the signed nibble
+            const float c0 = affine ? fmaf(8.0f, s, z) : (8.0f - z) * s;
+            uint4* dh = reinterpret_cast<uint4*>(Wh + wrow * kGemmLd + whalf * 32);
+            uint4* dl = reinterpret_cast<uint4*>(Wl + wrow * kGemmLd + whalf * 32);
+            dequant8(wq.x, s, c0, dh + 0, dl + 0);
+            dequant8(wq.y, s, c0, dh + 1, dl + 1);
+            dequant8(wq.z, s, c0, dh + 2, dl + 2);
+            dequant8(wq.w, s, c0, dh + 3, dl + 3);
         }
+        uint4* xdh = reinterpret_cast<uint4*>(Xh + xtok * kGemmLd + xpart * 32);
+        uint4* xdl = reinterpret_cast<uint4*>(Xl + xtok * kGemmLd + xpart * 32);
+        xdh[0] = xa0; xdh[1] = xa1; xdh[2] = xa2; xdh[3] = xa3;
+        xdl[0] = xb0; xdl[1] = xb1; xdl[2] = xb2; xdl[3] = xb3;
+    };
+    floatx4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    GEMM_LOAD_GROUP(0);
+    for (int g = 0; g < G; ++g) {
+        __syncthreads();  // the previous group's MFMA operands have been read
+        store_group();
         __syncthreads();
+        if (g + 1 < G) GEMM_LOAD_GROUP(g + 1);  // in flight during this group's MFMAs
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int k = ks * 32 + (lane >> 4) * 8;
-            half8 a[2], al[2], bh[2], bl[2];
+            half8 ah[TI], al[TI], bh[TJ], bl[TJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                a[i] = *reinterpret_cast<const half8*>(As + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
-                al[i] = *reinterpret_cast<const half8*>(Al + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
+            for (int i = 0; i < TI; ++i) {
+                ah[i] = *reinterpret_cast<const half8*>(Wh + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
+                al[i] = *reinterpret_cast<const half8*>(Wl + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                bh[j] = *reinterpret_cast<const half8*>(Bh + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
-                bl[j] = *reinterpret_cast<const half8*>(Bl + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
+            for (int j = 0; j < TJ; ++j) {
+                bh[j] = *reinterpret_cast<const half8*>(Xh + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
+                bl[j] = *reinterpret_cast<const half8*>(Xl + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < TJ; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
                 }
         }
-        __syncthreads();
     }
     // epilogue: lane holds rows 4 (lane >> 4) + v of tile i, token (lane & 15) of tile j
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             const int t = t0 + wt + j * 16 + (lane & 15);
             const int rb = r0 + wr + i * 16 + 4 * (lane >> 4);
             if (t >= m) continue;
@@ -222,30 +260,46 @@ bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& p
     return true;
 }
 
+template <int BR, int EPI>
+static hipError_t launch_gemm_t(const GemmLaunch& p, const _Float16* xh, const _Float16* xl, int m_pad,
+                                hipStream_t s) {
+    const auto fn = reinterpret_cast<const void*>(&gemm_w4_mfma_kernel<BR, EPI>);
+    constexpr size_t lds = gemm_lds_bytes<BR>();
+    if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
+        if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+            e != hipSuccess)
+            return e;
+    }
+    const dim3 grid(m_pad / kGemmToks, (p.rows + BR - 1) / BR);
+    hipLaunchKernelGGL((gemm_w4_mfma_kernel<BR, EPI>), grid, dim3(256), lds, s, p.nib,
+                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xl, p.m, p.y, p.ldy);
+    return hipGetLastError();
+}
+
+template <int BR>
+static hipError_t launch_gemm_br(const GemmLaunch& p, const _Float16* xh, const _Float16* xl, int m_pad,
+                                 hipStream_t s) {
+    switch (p.epi) {
+        case 0: return launch_gemm_t<BR, 0>(p, xh, xl, m_pad, s);
+        case 1: return launch_gemm_t<BR, 1>(p, xh, xl, m_pad, s);
+        case 2: return launch_gemm_t<BR, 2>(p, xh, xl, m_pad, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     const int m_pad = (p.m + kGemmToks - 1) / kGemmToks * kGemmToks;
     _Float16* xh = static_cast<_Float16*>(p.workspace);
     _Float16* xl = xh + static_cast<size_t>(m_pad) * p.cols;
     hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const dim3 grid(m_pad / kGemmToks, (p.rows + kGemmRows - 1) / kGemmRows);
-    const uint32_t* meta = static_cast<const uint32_t*>(p.meta);
-    switch (p.epi) {
-        case 0:
-            hipLaunchKernelGGL(gemm_w4_mfma_kernel<0>, grid, dim3(256), 0, s, p.nib, meta, p.rows, p.cols, p.affine,
-                               xh, xl, p.m, p.y, p.ldy);
-            break;
-        case 1:
-            hipLaunchKernelGGL(gemm_w4_mfma_kernel<1>, grid, dim3(256), 0, s, p.nib, meta, p.rows, p.cols, p.affine,
-                               xh, xl, p.m, p.y, p.ldy);
-            break;
-        case 2:
-            hipLaunchKernelGGL(gemm_w4_mfma_kernel<2>, grid, dim3(256), 0, s, p.nib, meta, p.rows, p.cols, p.affine,
-                               xh, xl, p.m, p.y, p.ldy);
-            break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    // 128-row tiles unless that leaves CUs idle (the 4096-row projections)
+    int cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const long tiles128 = static_cast<long>((p.rows + 127) / 128) * (m_pad / kGemmToks);
+    if (tiles128 >= cus) return launch_gemm_br<128>(p, xh, xl, m_pad, s);
+    return launch_gemm_br<64>(p, xh, xl, m_pad, s);
 }
 
 // ---------------------------------------------------------------------------
