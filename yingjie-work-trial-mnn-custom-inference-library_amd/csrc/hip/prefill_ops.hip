@@ -387,6 +387,152 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnLaunch p) 
     }
 }
 
+// Tiled form for head_dim 128 and 4 query heads per kv head (the 9B shape):
+// block (16-token tile, kv head) holds the tile's 64 query rows (token, head)
+// in LDS and streams the keys in 64-key chunks through LDS (fp32), so every
+// key is read once per tile instead of once per token.  Thread (rq, kq) =
+// (threadIdx / 16, threadIdx % 16) owns the 4 rows of token rq: the scores of
+// keys 4kq..4kq+3 (row max / sum over a chunk are reductions over the 16 lanes
+// of one DPP row) and output dims 8kq..8kq+7.  Online softmax over chunks
+// (rescale by exp(m_old - m_new)), then the output is multiplied by 1/l and by
+// the sigmoid gate, as in prefill_attn_kernel.
+constexpr int kTQ = 16;         // tokens per tile
+constexpr int kTHd = 128;       // head dim of the tiled kernel
+constexpr int kTGroup = 4;      // query heads per kv head of the tiled kernel
+constexpr int kTRows = kTQ * kTGroup;
+constexpr int kTLdq = kTHd + 4;  // fp32 row stride of Q / K / V in LDS
+constexpr int kTLdp = kPAttnChunk + 4;
+
+constexpr size_t prefill_attn_tile_lds() {
+    return sizeof(float) * (static_cast<size_t>(kTRows) * kTLdq + 2 * static_cast<size_t>(kPAttnChunk) * kTLdq +
+                            static_cast<size_t>(kTRows) * kTLdp);
+}
+
+__global__ void __launch_bounds__(256) prefill_attn_tile_kernel(PrefillAttnLaunch p) {
+    extern __shared__ float4 attn_lds[];
+    float* Qs = reinterpret_cast<float*>(attn_lds);   // [64 rows][kTLdq]
+    float* Ks = Qs + kTRows * kTLdq;                  // [64 keys][kTLdq]
+    float* Vs = Ks + kPAttnChunk * kTLdq;             // [64 keys][kTLdq]
+    float* Ps = Vs + kPAttnChunk * kTLdq;             // [64 rows][kTLdp]
+    const int t0 = blockIdx.x * kTQ, kh = blockIdx.y;
+    const int rq = threadIdx.x >> 4, kq = threadIdx.x & 15;
+    const int pos0 = *p.pos0;
+    const int ntok = min(kTQ, p.tokens - t0);
+    const int qpos = pos0 + t0 + rq;                      // this thread's token
+    const int last = pos0 + t0 + ntok - 1;                // last key any row of the tile sees
+    // Q: row r = token * 4 + head; thread loads 32 floats (8 float4)
+    for (int i = threadIdx.x; i < kTRows * kTHd / 4; i += 256) {
+        const int r = i / (kTHd / 4), d4 = i % (kTHd / 4);
+        const int tok = r / kTGroup, h = r % kTGroup;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (tok < ntok)
+            v = *reinterpret_cast<const float4*>(p.q + static_cast<size_t>(t0 + tok) * p.q_stride +
+                                                 static_cast<size_t>(kh * kTGroup + h) * kTHd + 4 * d4);
+        *reinterpret_cast<float4*>(Qs + r * kTLdq + 4 * d4) = v;
+    }
+    float m[4], l[4], o[4][8];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+    }
+    const float rscale = 1.0f / sqrtf(static_cast<float>(kTHd));
+    for (int c0 = 0; c0 <= last; c0 += kPAttnChunk) {
+        __syncthreads();  // the previous chunk's K, V and P have been read
+        // K and V of keys c0..c0+63 as fp32; keys past `last` are zero (never read as data)
+        for (int i = threadIdx.x; i < kPAttnChunk * kTHd / 8; i += 256) {
+            const int kk = i / (kTHd / 8), d8 = i % (kTHd / 8);
+            uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+            if (c0 + kk <= last) {
+                const size_t off = (static_cast<size_t>(c0 + kk) * p.nkv + kh) * kTHd + 8 * d8;
+                kw = *reinterpret_cast<const uint4*>(p.k_cache + off);
+                vw = *reinterpret_cast<const uint4*>(p.v_cache + off);
+            }
+            float* kd = Ks + kk * kTLdq + 8 * d8;
+            float* vd = Vs + kk * kTLdq + 8 * d8;
+            *reinterpret_cast<float4*>(kd) = make_float4(half_lo(kw.x), half_hi(kw.x), half_lo(kw.y), half_hi(kw.y));
+            *reinterpret_cast<float4*>(kd + 4) = make_float4(half_lo(kw.z), half_hi(kw.z), half_lo(kw.w), half_hi(kw.w));
+            *reinterpret_cast<float4*>(vd) = make_float4(half_lo(vw.x), half_hi(vw.x), half_lo(vw.y), half_hi(vw.y));
+            *reinterpret_cast<float4*>(vd + 4) = make_float4(half_lo(vw.z), half_hi(vw.z), half_lo(vw.w), half_hi(vw.w));
+        }
+        __syncthreads();
+        // scores of rows (rq, h) x keys 4kq + j
+        float sc[4][4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[h][j] = 0.0f;
+        const float* qr = Qs + (rq * kTGroup) * kTLdq;
+        const float* kr = Ks + (4 * kq) * kTLdq;
+#pragma unroll 4
+        for (int d = 0; d < kTHd; d += 4) {
+            float4 qv[4], kv[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) qv[h] = *reinterpret_cast<const float4*>(qr + h * kTLdq + d);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kv[j] = *reinterpret_cast<const float4*>(kr + j * kTLdq + d);
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    sc[h][j] += qv[h].x * kv[j].x + qv[h].y * kv[j].y + qv[h].z * kv[j].z + qv[h].w * kv[j].w;
+        }
+        // causal mask, chunk max / sum per row (16 lanes), online rescale
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            float mc = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = c0 + 4 * kq + j <= qpos;
+                sc[h][j] = ok ? sc[h][j] * rscale : -INFINITY;
+                mc = fmaxf(mc, sc[h][j]);
+            }
+            mc = lanes_max<16>(mc);
+            const float m_new = fmaxf(m[h], mc);
+            float ls = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e = sc[h][j] == -INFINITY ? 0.0f : expf(sc[h][j] - m_new);
+                sc[h][j] = e;
+                ls += e;
+            }
+            ls = lanes_sum<16>(ls);
+            const float f = m[h] == -INFINITY ? 0.0f : expf(m[h] - m_new);
+            m[h] = m_new;
+            l[h] = l[h] * f + ls;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[h][e] *= f;
+            *reinterpret_cast<float4*>(Ps + (rq * kTGroup + h) * kTLdp + 4 * kq) =
+                make_float4(sc[h][0], sc[h][1], sc[h][2], sc[h][3]);
+        }
+        __syncthreads();
+        // o[rows of token rq][dims 8kq..] += P . V over the chunk's keys
+        const int nk = min(kPAttnChunk, last - c0 + 1);
+        for (int k = 0; k < nk; ++k) {
+            const float4 v0 = *reinterpret_cast<const float4*>(Vs + k * kTLdq + 8 * kq);
+            const float4 v1 = *reinterpret_cast<const float4*>(Vs + k * kTLdq + 8 * kq + 4);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const float pk = Ps[(rq * kTGroup + h) * kTLdp + k];
+                o[h][0] += pk * v0.x; o[h][1] += pk * v0.y; o[h][2] += pk * v0.z; o[h][3] += pk * v0.w;
+                o[h][4] += pk * v1.x; o[h][5] += pk * v1.y; o[h][6] += pk * v1.z; o[h][7] += pk * v1.w;
+            }
+        }
+    }
+    if (rq >= ntok) return;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const float inv = l[h] > 0.0f ? 1.0f / l[h] : 0.0f;
+        const size_t head = static_cast<size_t>(kh * kTGroup + h) * kTHd + 8 * kq;
+        const float* gr = p.gate + static_cast<size_t>(t0 + rq) * p.q_stride + head;
+        float* orow = p.out + static_cast<size_t>(t0 + rq) * p.out_stride + head;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) orow[e] = (o[h][e] * inv) * sigmoid_dev(gr[e]);
+    }
+}
+
 bool prefill_attn_supported(int nq, int nkv, int head_dim) {
     return nkv > 0 && nq % nkv == 0 && nq / nkv <= kPAttnMaxGroup && head_dim > 0 &&
            sizeof(float) * (2 * (nq / nkv) * head_dim + (nq / nkv) * (kPAttnChunk + 3)) <= 64 * 1024;
@@ -394,6 +540,19 @@ bool prefill_attn_supported(int nq, int nkv, int head_dim) {
 
 hipError_t launch_prefill_attn(const PrefillAttnLaunch& p, hipStream_t s) {
     const int group = p.nq / p.nkv;
+    if (p.head_dim == kTHd && group == kTGroup) {
+        static bool attr_set = false;
+        constexpr size_t lds = prefill_attn_tile_lds();
+        if (!attr_set) {
+            if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_tile_kernel),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+                e != hipSuccess)
+                return e;
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(prefill_attn_tile_kernel, dim3((p.tokens + kTQ - 1) / kTQ, p.nkv), dim3(256), lds, s, p);
+        return hipGetLastError();
+    }
     const size_t lds = sizeof(float) * (2 * static_cast<size_t>(group) * p.head_dim + group * (kPAttnChunk + 3));
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(p.tokens, p.nkv), dim3(256), lds, s, p);
     return hipGetLastError();
