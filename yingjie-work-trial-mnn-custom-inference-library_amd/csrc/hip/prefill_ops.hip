@@ -754,16 +754,18 @@ __global__ void __launch_bounds__(256) linear_scan_kernel(LinearScanLaunch p) {
 }
 
 // Wave-independent form for key dim DK and conv size KS (the 9B shape: 128, 4).
-// Wave w of block (vh, y) owns value columns y*16 + 4w .. +3 of head vh; lane
-// l owns column l/16 and key rows i = l%16 + 16r, so both sums over the key
-// dimension (the prediction and the output) are reductions over 16 lanes of
-// one DPP row.  Every wave convolves the whole q/k head itself (cheap) and
+// Wave w of block (vh, y) owns CPW value columns of head vh; lane l owns
+// column l / (64/CPW) and key rows i = l % (64/CPW) + (64/CPW) r, so both sums
+// over the key dimension (the prediction and the output) are reductions over
+// the 16 lanes of a DPP row (CPW = 4) or two rows (CPW = 2, one permlane swap).  Every wave convolves the whole q/k head itself (cheap) and
 // exchanges the convolved channels through its own LDS slice, so a token
 // needs no block barrier at all.
-template <int DK, int KS>
+template <int DK, int KS, int CPW>
 __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch p) {
     constexpr int CH = 2 * DK / kWave;  // q/k channels per lane
-    constexpr int RS = DK / 16;         // state rows per lane
+    constexpr int LPC = kWave / CPW;    // lanes per value column
+    constexpr int RS = DK / LPC;        // state rows per lane
+    constexpr int BC = 4 * CPW;         // value columns per block
     constexpr int H = KS - 1;
     static_assert(CH >= 1 && CH % 2 == 0 && RS >= 1, "key dim");
     __shared__ float qk_lds[4][2 * DK];
@@ -772,8 +774,8 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
     const int factor = max(1, p.lv_n / max(1, p.lk_n));
     const int kh = min(p.lk_n - 1, vh / factor);
     const int dv = p.lv_hd;
-    const int ig = lane & 15;
-    const int j = blockIdx.y * kScanCols + wid * 4 + (lane >> 4);
+    const int ig = lane % LPC;
+    const int j = blockIdx.y * BC + wid * CPW + lane / LPC;
     const bool active = j < dv;
     float* qk_w = qk_lds[wid];
     auto qk_channel = [&](int t) { return (t >= DK ? p.lk_n * DK : 0) + kh * DK + (t % DK); };
@@ -795,7 +797,7 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
     float* S = p.state + static_cast<size_t>(vh) * DK * dv;
     float sreg[RS];
 #pragma unroll
-    for (int r = 0; r < RS; ++r) sreg[r] = active ? S[static_cast<size_t>(ig + 16 * r) * dv + j] : 0.0f;
+    for (int r = 0; r < RS; ++r) sreg[r] = active ? S[static_cast<size_t>(ig + LPC * r) * dv + j] : 0.0f;
     const float rdk = 1.0f / sqrtf(static_cast<float>(DK));
     const float neg_exp_alog = -expf(p.a_log[vh]);
     const float dtb = p.dt_bias[vh];
@@ -854,8 +856,8 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
             float kr[RS], qr[RS];
 #pragma unroll
             for (int r = 0; r < RS; ++r) {
-                kr[r] = qk_w[DK + ig + 16 * r] * invk;
-                qr[r] = qk_w[ig + 16 * r] * invq;
+                kr[r] = qk_w[DK + ig + LPC * r] * invk;
+                qr[r] = qk_w[ig + LPC * r] * invq;
             }
             float pred = 0.0f;
 #pragma unroll
@@ -864,6 +866,7 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
                 pred += sreg[r] * kr[r];
             }
             pred = lanes_sum<16>(pred);
+            if constexpr (LPC == 32) pred = xor_pair_sum<16>(pred);
             const float delta = beta * (vj - pred);
             float o = 0.0f;
 #pragma unroll
@@ -872,6 +875,7 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
                 o += sreg[r] * qr[r];
             }
             o = lanes_sum<16>(o);
+            if constexpr (LPC == 32) o = xor_pair_sum<16>(o);
             if (ig == 0 && active) p.out[static_cast<size_t>(t) * p.out_stride + static_cast<size_t>(vh) * dv + j] = o * rdk;
         }
 #pragma unroll
@@ -884,7 +888,7 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
     }
 #pragma unroll
     for (int r = 0; r < RS; ++r)
-        if (active) S[static_cast<size_t>(ig + 16 * r) * dv + j] = sreg[r];
+        if (active) S[static_cast<size_t>(ig + LPC * r) * dv + j] = sreg[r];
     const bool qk_writer = (vh % factor == 0) && blockIdx.y == 0 && wid == 0;
     if (qk_writer) {
 #pragma unroll
@@ -907,8 +911,12 @@ bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) 
 
 hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
     const dim3 grid(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols);
-    if (p.lk_hd == 128 && p.ksize == 4)
-        hipLaunchKernelGGL((linear_scan_wave_kernel<128, 4>), grid, dim3(256), 0, s, p);
+    if (p.lk_hd == 128 && p.ksize == 4) {
+        // four value columns per wave (two per wave, i.e. twice the blocks, measured
+        // slower: every wave convolves the whole q/k head)
+        const dim3 grid4(p.lv_n, (p.lv_hd + 15) / 16);
+        hipLaunchKernelGGL((linear_scan_wave_kernel<128, 4, 4>), grid4, dim3(256), 0, s, p);
+    }
     else
         hipLaunchKernelGGL(linear_scan_kernel, grid, dim3(256), 0, s, p);
     return hipGetLastError();
