@@ -263,6 +263,18 @@ XQHIP_API int xqhip_linear_attn_scan(const float* mixed, const float* a, const f
                                      float* conv_state, int pos0, const float* conv_w, const float* a_log,
                                      const float* dt_bias, float* state, int lk_n, int lk_hd, int lv_n, int lv_hd,
                                      int ksize, int tokens, float* out, int out_stride, void* stream);
+/* xqhip_linear_attn_scan with a workspace of xqhip_linear_scan_workspace_bytes()
+ * (16-byte aligned): the conv1d + SiLU, q/k L2 norms and gates of all tokens
+ * run first as one token-parallel pass, leaving only the state recurrence
+ * sequential (same results up to the fp32 summation order of the norms). No
+ * counterpart in the reference (which prefills token by token,
+ * custom_model.cpp:610-640); same contract as xqhip_linear_attn_scan. */
+XQHIP_API size_t xqhip_linear_scan_workspace_bytes(int tokens, int lk_n, int lk_hd, int lv_n, int lv_hd);
+XQHIP_API int xqhip_linear_attn_scan_ws(const float* mixed, const float* a, const float* b, int stride,
+                                        float* conv_state, int pos0, const float* conv_w, const float* a_log,
+                                        const float* dt_bias, float* state, int lk_n, int lk_hd, int lv_n, int lv_hd,
+                                        int ksize, int tokens, float* out, int out_stride, void* workspace,
+                                        void* stream);
 
 /* ---- streams and graphs ------------------------------------------------ */
 XQHIP_API int xqhip_stream_create(void** stream);

@@ -166,9 +166,14 @@ def test_prefill_attention_vs_causal_oracle(nq, nkv, hd, T, pos0):
         close(got[t], want, f"prefill attention token {t} (ctx {n})")
 
 
+@pytest.mark.parametrize("with_ws", [False, True])
 @pytest.mark.parametrize("shape,T,pos0", [((16, 32, 128, 128, 4), 12, 0), ((16, 32, 128, 128, 4), 7, 5),
-                                          ((3, 6, 64, 32, 3), 9, 2), ((2, 2, 256, 40, 4), 4, 1)])
-def test_linear_scan_matches_consecutive_steps(shape, T, pos0):
+                                          ((16, 32, 128, 128, 4), 37, 3), ((3, 6, 64, 32, 3), 9, 2),
+                                          ((2, 2, 256, 40, 4), 4, 1), ((2, 4, 128, 24, 2), 2, 0)])
+def test_linear_scan_matches_consecutive_steps(shape, T, pos0, with_ws):
+    """The prefill scan (fused per-token kernel, or with a workspace the
+    token-parallel conv pass + recurrence kernel) against consecutive decode
+    steps; 37 tokens cross the 16-token staging groups."""
     lk_n, lv_n, lk_hd, lv_hd, ks = shape
     rng = np.random.default_rng(T * 7 + pos0)
     _, cstate, cw = linear_inputs(lk_n, lv_n, lk_hd, lv_hd, ks, seed=41)
@@ -184,9 +189,13 @@ def test_linear_scan_matches_consecutive_steps(shape, T, pos0):
     # batched
     sd_b, Sd_b, rd = dev(two), dev(S0), dev(rows)
     out_b = xb.DeviceBuffer(T * lv_n * lv_hd * 4)
-    xb.ck(xb.hip().xqhip_linear_attn_scan(rd.ptr, at(rd, conv_dim * 4), at(rd, (conv_dim + lv_n) * 4), stride,
-                                          sd_b.ptr, pos0, dev(cw).ptr, dev(a_log).ptr, dev(dt).ptr, Sd_b.ptr, lk_n,
-                                          lk_hd, lv_n, lv_hd, ks, T, out_b.ptr, lv_n * lv_hd, None))
+    args = (rd.ptr, at(rd, conv_dim * 4), at(rd, (conv_dim + lv_n) * 4), stride, sd_b.ptr, pos0, dev(cw).ptr,
+            dev(a_log).ptr, dev(dt).ptr, Sd_b.ptr, lk_n, lk_hd, lv_n, lv_hd, ks, T, out_b.ptr, lv_n * lv_hd)
+    if with_ws:
+        wsd = xb.DeviceBuffer(xb.hip().xqhip_linear_scan_workspace_bytes(T, lk_n, lk_hd, lv_n, lv_hd))
+        xb.ck(xb.hip().xqhip_linear_attn_scan_ws(*args, wsd.ptr, None))
+    else:
+        xb.ck(xb.hip().xqhip_linear_attn_scan(*args, None))
     # consecutive single steps
     sd_s, Sd_s = dev(two), dev(S0)
     cwd, ald, dtd = dev(cw), dev(a_log), dev(dt)

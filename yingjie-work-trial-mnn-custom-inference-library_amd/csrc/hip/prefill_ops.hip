@@ -904,12 +904,175 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Two-pass form of the prefill linear-attention scan (with a workspace):
+// 1. linear_conv_prefill_kernel, parallel over (token, head): the causal conv1d
+//    + SiLU of every channel for every token of the chunk (inputs of earlier
+//    tokens from the chunk, before the chunk from hist_in), the L2 norm of the
+//    q and k heads, the per-(token, value head) beta = sigmoid(b) and
+//    decay = exp(-exp(A_log) softplus(a + dt_bias)), and the final history.
+// 2. linear_scan_recur_kernel: only the state recurrence stays sequential; a
+//    block stages 16 tokens of normalised q/k, v, beta and decay in LDS at a
+//    time (double-buffered, one barrier per 16 tokens) and each wave updates
+//    its 4 value columns per token exactly as the fused decode step does.
+// Workspace: conv output [tokens][conv_dim] and (beta, decay) [tokens][lv_n][2].
+// ---------------------------------------------------------------------------
+size_t linear_scan_workspace_bytes(int tokens, int lk_n, int lk_hd, int lv_n, int lv_hd) {
+    const size_t conv_dim = 2 * static_cast<size_t>(lk_n) * lk_hd + static_cast<size_t>(lv_n) * lv_hd;
+    return sizeof(float) * static_cast<size_t>(tokens) * (conv_dim + 2 * static_cast<size_t>(lv_n));
+}
+
+__global__ void __launch_bounds__(256) linear_conv_prefill_kernel(LinearScanLaunch p) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, hb = blockIdx.y;
+    const int dk = p.lk_hd, dv = p.lv_hd, H = p.ksize - 1;
+    const int conv_dim = 2 * p.lk_n * dk + p.lv_n * dv;
+    const bool is_qk = hb < 2 * p.lk_n;
+    const int width = is_qk ? dk : dv;
+    const int c = (is_qk ? hb * dk : 2 * p.lk_n * dk + (hb - 2 * p.lk_n) * dv) + static_cast<int>(threadIdx.x);
+    const bool ok = static_cast<int>(threadIdx.x) < width;
+    // input of token tau of the chunk (tau < 0: the history before it)
+    auto xin = [&](int tau) {
+        return tau >= 0 ? p.mixed[static_cast<size_t>(tau) * p.mixed_stride + c]
+                        : p.hist_in[static_cast<size_t>(c) * H + (H + tau)];
+    };
+    float y = 0.0f;
+    if (ok) {
+        const float* w = p.conv_w + static_cast<size_t>(c) * p.ksize;
+        float acc = 0.0f;
+        for (int i = 0; i < H; ++i) acc += xin(t - H + i) * w[i];
+        acc += xin(t) * w[H];
+        y = silu_dev(acc);
+        if (t == p.tokens - 1)
+            for (int i = 0; i < H; ++i) p.hist_out[static_cast<size_t>(c) * H + i] = xin(p.tokens - H + i);
+    }
+    if (is_qk) {  // l2NormalizeHeads: x / sqrt(sum x^2 + 1e-6)
+        float ss = wave_sum(y * y);
+        const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+        if (lane == 0) red[wid] = ss;
+        __syncthreads();
+        ss = 0.0f;
+        for (int i = 0; i < (width + kWave - 1) / kWave; ++i) ss += red[i];
+        y *= 1.0f / sqrtf(ss + 1.0e-6f);
+    } else if (threadIdx.x == 0) {
+        const int vh = hb - 2 * p.lk_n;
+        const size_t row = static_cast<size_t>(t) * p.mixed_stride + vh;
+        float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim + (static_cast<size_t>(t) * p.lv_n + vh) * 2;
+        aux[0] = sigmoid_dev(p.b[row]);
+        aux[1] = expf(-expf(p.a_log[vh]) * softplus_dev(p.a[row] + p.dt_bias[vh]));
+    }
+    if (ok) p.ws[static_cast<size_t>(t) * conv_dim + c] = y;
+}
+
+constexpr int kRecurTokens = 16;  // tokens staged in LDS per barrier
+
+template <int DK>
+__global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch p) {
+    constexpr int RS = DK / 16;  // state rows per lane
+    constexpr int TG = kRecurTokens;
+    __shared__ float qs[2][TG][DK], ks[2][TG][DK], vs[2][TG][16], gs[2][TG][2];
+    const int vh = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int factor = max(1, p.lv_n / max(1, p.lk_n));
+    const int kh = min(p.lk_n - 1, vh / factor);
+    const int dv = p.lv_hd;
+    const int conv_dim = 2 * p.lk_n * DK + p.lv_n * dv;
+    const int ig = lane & 15, col = wid * 4 + (lane >> 4);
+    const int j0 = blockIdx.y * 16;
+    const int j = j0 + col;
+    const bool active = j < dv;
+    float* S = p.state + static_cast<size_t>(vh) * DK * dv;
+    float sreg[RS];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) sreg[r] = active ? S[static_cast<size_t>(ig + 16 * r) * dv + j] : 0.0f;
+    const float rdk = 1.0f / sqrtf(static_cast<float>(DK));
+    const float* conv = p.ws;
+    const float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim;
+    // staging: thread th loads q/k floats th, th + 256, ... of a group, v and (beta, decay)
+    constexpr int QK = TG * 2 * DK / 256;  // per thread
+    float rq[QK], rv = 0.0f, rg = 0.0f;
+    auto load_stage = [&](int g0) {
+#pragma unroll
+        for (int u = 0; u < QK; ++u) {
+            const int e = threadIdx.x + u * 256;
+            const int tk = e / (2 * DK), ch = e % (2 * DK);
+            const int tok = min(g0 + tk, p.tokens - 1);
+            const int cc = (ch >= DK ? p.lk_n * DK : 0) + kh * DK + (ch % DK);
+            rq[u] = conv[static_cast<size_t>(tok) * conv_dim + cc];
+        }
+        {
+            const int tk = threadIdx.x >> 4, cl = threadIdx.x & 15;  // TG x 16 values
+            const int tok = min(g0 + tk, p.tokens - 1);
+            rv = j0 + cl < dv ? conv[static_cast<size_t>(tok) * conv_dim + 2 * p.lk_n * DK + vh * dv + j0 + cl] : 0.0f;
+        }
+        if (threadIdx.x < 2 * TG) {
+            const int tok = min(g0 + static_cast<int>(threadIdx.x >> 1), p.tokens - 1);
+            rg = aux[(static_cast<size_t>(tok) * p.lv_n + vh) * 2 + (threadIdx.x & 1)];
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < QK; ++u) {
+            const int e = threadIdx.x + u * 256;
+            const int tk = e / (2 * DK), ch = e % (2 * DK);
+            if (ch < DK) qs[buf][tk][ch] = rq[u]; else ks[buf][tk][ch - DK] = rq[u];
+        }
+        vs[buf][threadIdx.x >> 4][threadIdx.x & 15] = rv;
+        if (threadIdx.x < 2 * TG) gs[buf][threadIdx.x >> 1][threadIdx.x & 1] = rg;
+    };
+    load_stage(0);
+    for (int g0 = 0, buf = 0; g0 < p.tokens; g0 += TG, buf ^= 1) {
+        store_stage(buf);
+        __syncthreads();  // this buffer is complete; the other one is no longer read
+        if (g0 + TG < p.tokens) load_stage(g0 + TG);
+        const int nt = min(TG, p.tokens - g0);
+        for (int k = 0; k < nt; ++k) {
+            const float beta = gs[buf][k][0], decay = gs[buf][k][1];
+            const float vj = vs[buf][k][col];
+            float kr[RS], qr[RS];
+#pragma unroll
+            for (int r = 0; r < RS; ++r) {
+                kr[r] = ks[buf][k][ig + 16 * r];
+                qr[r] = qs[buf][k][ig + 16 * r];
+            }
+            float pred = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RS; ++r) {
+                sreg[r] *= decay;
+                pred += sreg[r] * kr[r];
+            }
+            pred = lanes_sum<16>(pred);
+            const float delta = beta * (vj - pred);
+            float o = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RS; ++r) {
+                sreg[r] += kr[r] * delta;
+                o += sreg[r] * qr[r];
+            }
+            o = lanes_sum<16>(o);
+            if (ig == 0 && active)
+                p.out[static_cast<size_t>(g0 + k) * p.out_stride + static_cast<size_t>(vh) * dv + j] = o * rdk;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RS; ++r)
+        if (active) S[static_cast<size_t>(ig + 16 * r) * dv + j] = sreg[r];
+}
+
 bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
     return lk_n > 0 && lv_n > 0 && lv_n % lk_n == 0 && lk_hd > 0 && lk_hd <= 256 && lv_hd > 0 && ksize >= 1 &&
            ksize - 1 <= kScanMaxHist && lk_hd <= kScanIGroups * kScanMaxK;
 }
 
 hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
+    if (p.ws && p.lk_hd == 128 && p.lv_hd <= 256) {
+        const int width = max(p.lk_hd, p.lv_hd);
+        hipLaunchKernelGGL(linear_conv_prefill_kernel, dim3(p.tokens, 2 * p.lk_n + p.lv_n),
+                           dim3((width + kWave - 1) / kWave * kWave), 0, s, p);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        hipLaunchKernelGGL(linear_scan_recur_kernel<128>, dim3(p.lv_n, (p.lv_hd + 15) / 16), dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
     const dim3 grid(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols);
     if (p.lk_hd == 128 && p.ksize == 4) {
         // four value columns per wave (two per wave, i.e. twice the blocks, measured

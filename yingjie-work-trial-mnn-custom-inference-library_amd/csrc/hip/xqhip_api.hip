@@ -608,10 +608,15 @@ int xqhip_prefill_attention(const float* q, const float* gate, const void* k_cac
     return check(xqhip::launch_prefill_attn(p, as_stream(stream)), "prefill attention launch");
 }
 
-int xqhip_linear_attn_scan(const float* mixed, const float* a, const float* b, int stride, float* conv_state,
-                           int pos0, const float* conv_w, const float* a_log, const float* dt_bias, float* state,
-                           int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, int tokens, float* out,
-                           int out_stride, void* stream) {
+size_t xqhip_linear_scan_workspace_bytes(int tokens, int lk_n, int lk_hd, int lv_n, int lv_hd) {
+    if (tokens <= 0 || lk_n <= 0 || lk_hd <= 0 || lv_n <= 0 || lv_hd <= 0) return 0;
+    return xqhip::linear_scan_workspace_bytes(tokens, lk_n, lk_hd, lv_n, lv_hd);
+}
+
+static int linear_attn_scan_impl(const float* mixed, const float* a, const float* b, int stride, float* conv_state,
+                                 int pos0, const float* conv_w, const float* a_log, const float* dt_bias, float* state,
+                                 int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, int tokens, float* out,
+                                 int out_stride, void* workspace, void* stream) {
     if (!mixed || !a || !b || !conv_state || !conv_w || !a_log || !dt_bias || !state || !out || tokens <= 0 ||
         pos0 < 0 || !xqhip::linear_scan_supported(lk_n, lk_hd, lv_n, lv_hd, ksize) || out_stride < lv_n * lv_hd)
         return fail(XQHIP_EINVAL, "xqhip_linear_attn_scan: bad args");
@@ -621,12 +626,31 @@ int xqhip_linear_attn_scan(const float* mixed, const float* a, const float* b, i
     float* copy_next = conv_state + static_cast<size_t>((pos0 + tokens) & 1) * hist_floats;
     float* other = conv_state + static_cast<size_t>((pos0 & 1) ^ 1) * hist_floats;
     xqhip::LinearScanLaunch p{mixed, a, b, stride, copy_in, other, conv_w, a_log, dt_bias, state,
-                              lk_n, lk_hd, lv_n, lv_hd, ksize, tokens, out, out_stride};
+                              lk_n, lk_hd, lv_n, lv_hd, ksize, tokens, out, out_stride,
+                              static_cast<float*>(workspace)};
     if (int rc = check(xqhip::launch_linear_scan(p, as_stream(stream)), "linear scan launch")) return rc;
     // the next position reads copy (pos0 + tokens) & 1: when that is the input
     // copy (even token count), move the new history there
     if (copy_next != other && hist_floats > 0) return xqhip_copy(copy_next, other, hist_floats * sizeof(float), stream);
     return XQHIP_OK;
+}
+
+int xqhip_linear_attn_scan(const float* mixed, const float* a, const float* b, int stride, float* conv_state,
+                           int pos0, const float* conv_w, const float* a_log, const float* dt_bias, float* state,
+                           int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, int tokens, float* out,
+                           int out_stride, void* stream) {
+    return linear_attn_scan_impl(mixed, a, b, stride, conv_state, pos0, conv_w, a_log, dt_bias, state, lk_n, lk_hd,
+                                 lv_n, lv_hd, ksize, tokens, out, out_stride, nullptr, stream);
+}
+
+int xqhip_linear_attn_scan_ws(const float* mixed, const float* a, const float* b, int stride, float* conv_state,
+                              int pos0, const float* conv_w, const float* a_log, const float* dt_bias, float* state,
+                              int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, int tokens, float* out,
+                              int out_stride, void* workspace, void* stream) {
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+        return fail(XQHIP_EINVAL, "xqhip_linear_attn_scan_ws: workspace must be non-null and 16-byte aligned");
+    return linear_attn_scan_impl(mixed, a, b, stride, conv_state, pos0, conv_w, a_log, dt_bias, state, lk_n, lk_hd,
+                                 lv_n, lv_hd, ksize, tokens, out, out_stride, workspace, stream);
 }
 
 int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream) {

@@ -193,7 +193,9 @@ struct LinearScanLaunch {
     int lk_n, lk_hd, lv_n, lv_hd, ksize, tokens;
     float* out;  // [tokens][out_stride]
     int out_stride;
+    float* ws;  // optional workspace (linear_scan_workspace_bytes): conv in a token-parallel pass first
 };
+size_t linear_scan_workspace_bytes(int tokens, int lk_n, int lk_hd, int lv_n, int lv_hd);
 bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
 hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s);
 

@@ -433,6 +433,13 @@ bool DeviceModel::alloc_prefill_buffers(std::string* error) {
         !alloc(&ws, xqhip_gemm_workspace_bytes(chunk_, max_cols), error) || !alloc(&tok_dev_, c, error))
         return false;
     gemm_ws_ = ws;
+    bool any_linear = false;
+    for (const Layer& L : layers_) any_linear |= !L.full;
+    if (any_linear) {
+        uint8_t* sw = nullptr;
+        if (!alloc(&sw, xqhip_linear_scan_workspace_bytes(chunk_, lk_n_, lk_hd_, lv_n_, lv_hd_), error)) return false;
+        scan_ws_ = sw;
+    }
     batched_prefill_ = true;
     return true;
 }
@@ -481,9 +488,9 @@ bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, i
             const float* b = a + lv_n_;
             const float* z = b + lv_n_;
             op_begin(timed, "linear_attention_state_update_custom(prefill_scan:conv1d,qk_l2norm,gated_delta)");
-            XQ_CALL(xqhip_linear_attn_scan(proj_all_, a, b, max_proj_, L.conv_state, pos0, L.conv_w, L.a_log,
-                                           L.dt_bias, L.rec_state, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, n, attn_all_,
-                                           attn_n_, stream_),
+            XQ_CALL(xqhip_linear_attn_scan_ws(proj_all_, a, b, max_proj_, L.conv_state, pos0, L.conv_w, L.a_log,
+                                              L.dt_bias, L.rec_state, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, n,
+                                              attn_all_, attn_n_, scan_ws_, stream_),
                     "prefill linear-attention scan");
             op_end(timed);
             xqhip_prologue gated{XQHIP_PRO_GATED_HEAD, lv_hd_, L.lin_norm, z, eps_};

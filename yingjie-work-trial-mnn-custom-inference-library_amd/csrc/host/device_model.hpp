@@ -137,6 +137,7 @@ private:
     float* attn_all_ = nullptr;  // [chunk][attn_n] attention / delta output
     float* ffn_all_ = nullptr;   // [chunk][inter]
     void* gemm_ws_ = nullptr;
+    void* scan_ws_ = nullptr;  // linear-attention scan workspace (token-parallel conv pass)
     int32_t* tok_dev_ = nullptr;  // [chunk]
     std::vector<TimedOp> ops_;
     std::vector<void*> event_pool_;

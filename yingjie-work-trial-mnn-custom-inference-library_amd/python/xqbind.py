@@ -91,6 +91,10 @@ _HIP_SIGS = {
     "xqhip_linear_attn_scan": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int,
                                        c_void_p]),
+    "xqhip_linear_scan_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "xqhip_linear_attn_scan_ws": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p,
+                                          c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                          c_int, c_void_p, c_void_p]),
     "xqhip_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]),
     "xqhip_stream_create": (c_int, [_P(c_void_p)]),
     "xqhip_stream_destroy": (c_int, [c_void_p]),
