@@ -32,6 +32,9 @@ HIP_FLAGS = [
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
     "-I", INCLUDE, "-I", HIP_SRC,
 ]
+# per-source additions: the prefill GEMM scales every MFMA result with VALU ops, so its
+# MFMAs write VGPRs directly instead of accumulation registers that need copying out
+HIP_FILE_FLAGS = {"prefill_ops.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
               "-fvisibility=hidden", "-I", INCLUDE, "-I", HOST_SRC, "-DXQWEN35_BUILD=1"]
 
@@ -56,7 +59,7 @@ def build_hip(jobs):
     for f in srcs:
         o = os.path.join(OBJ, "hip", f[:-4] + ".o")
         objs.append(o)
-        tasks.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(HIP_SRC, f), "-o", o])
+        tasks.append([HIPCC, *HIP_FLAGS, *HIP_FILE_FLAGS.get(f, []), "-c", os.path.join(HIP_SRC, f), "-o", o])
     os.makedirs(os.path.join(OBJ, "hip"), exist_ok=True)
     _compile_many(jobs, tasks)
     out = os.path.join(LIB, "libxqhip.so")

@@ -19,226 +19,340 @@ namespace xqhip {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+// register arrays of native vectors (arrays of HIP's uint4 / uint2 structs are kept in scratch)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
 
 // ---------------------------------------------------------------------------
 // B operand preparation: token t = blockIdx.x of x (row stride ldx) with the
 // prologue applied (RMS over the row, or per-head gated norm with the gate
-// row at t * ldz) -> xh[t][k] = fp16(v), xl[t][k] = fp16(v - xh): together
-// about 22 significant bits.  Rows m..m_pad-1 are zero-filled.
+// row at t * ldz) -> v, stored as xh = fp16(v) and xl = fp16(v - xh) (about
+// 22 significant bits together) with every aligned run of 8 columns in the
+// order [0 4 1 5 2 6 3 7], the order in which the GEMM unpacks a word of 8
+// weight codes; xs[t][g] = fp32 sum of v over column group g (64 columns).
+// Rows m..m_pad-1 are zero-filled.
 // ---------------------------------------------------------------------------
+constexpr int kPrepMaxHeads = 256;
+
 __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x, int ldx, int m, int cols,
                                                      Prologue pro, int ldz, _Float16* __restrict__ xh,
-                                                     _Float16* __restrict__ xl) {
+                                                     _Float16* __restrict__ xl, float* __restrict__ xs) {
     __shared__ float red[32];
+    __shared__ float head_inv[kPrepMaxHeads];
     const int t = blockIdx.x;
-    _Float16* oh = xh + static_cast<size_t>(t) * cols;
-    _Float16* ol = xl + static_cast<size_t>(t) * cols;
+    const int G = cols >> 6, nch = cols >> 3;
+    uint4* oh = reinterpret_cast<uint4*>(xh + static_cast<size_t>(t) * cols);
+    uint4* ol = reinterpret_cast<uint4*>(xl + static_cast<size_t>(t) * cols);
+    float* os = xs + static_cast<size_t>(t) * G;
     if (t >= m) {
-        for (int c = threadIdx.x; c < cols; c += blockDim.x) oh[c] = ol[c] = static_cast<_Float16>(0.0f);
+        for (int c = threadIdx.x; c < nch; c += blockDim.x) oh[c] = ol[c] = make_uint4(0u, 0u, 0u, 0u);
+        for (int g = threadIdx.x; g < G; g += blockDim.x) os[g] = 0.0f;
         return;
     }
     const float* xr = x + static_cast<size_t>(t) * ldx;
+    const float* zr = pro.mode == PRO_GATED ? pro.z + static_cast<size_t>(t) * ldz : nullptr;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = blockDim.x / kWave;
     float inv = 1.0f;
     if (pro.mode == PRO_RMS) {
         float ss = 0.0f;
         for (int c = threadIdx.x; c < cols; c += blockDim.x) ss += xr[c] * xr[c];
         ss = block_sum(ss, red);
         inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + pro.eps);
-    }
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    if (pro.mode == PRO_GATED) {
-        // one wave per head: inv_h, then the gated values of the head
-        const float* zr = pro.z + static_cast<size_t>(t) * ldz;
+    } else if (pro.mode == PRO_GATED) {
         const int heads = cols / pro.head_dim;
-        for (int h = wid; h < heads; h += nw) {
+        for (int h = wid; h < heads; h += nw) {  // one wave per head
             const float* xv = xr + h * pro.head_dim;
             float ss = 0.0f;
             for (int d = lane; d < pro.head_dim; d += kWave) ss += xv[d] * xv[d];
             ss = wave_sum(ss);
-            const float ih = 1.0f / sqrtf(ss / static_cast<float>(pro.head_dim) + pro.eps);
-            for (int d = lane; d < pro.head_dim; d += kWave) {
-                const int c = h * pro.head_dim + d;
-                const float v = xv[d] * ih * pro.w[d] * silu_dev(zr[c]);
-                const _Float16 hi = static_cast<_Float16>(v);
-                oh[c] = hi;
-                ol[c] = static_cast<_Float16>(v - static_cast<float>(hi));
-            }
+            if (lane == 0) head_inv[h] = 1.0f / sqrtf(ss / static_cast<float>(pro.head_dim) + pro.eps);
         }
-        return;
+        __syncthreads();
     }
-    for (int c = threadIdx.x; c < cols; c += blockDim.x) {
-        const float v = pro.mode == PRO_RMS ? xr[c] * inv * pro.w[c] : xr[c];
-        const _Float16 hi = static_cast<_Float16>(v);
-        oh[c] = hi;
-        ol[c] = static_cast<_Float16>(v - static_cast<float>(hi));
+    // one thread per 8 columns; the 8 threads of a group are consecutive lanes (nch % 8 == 0)
+    for (int c8 = threadIdx.x; c8 < nch; c8 += blockDim.x) {
+        const int c = c8 * 8;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = xr[c + e];
+        if (pro.mode == PRO_RMS) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * pro.w[c + e];
+        } else if (pro.mode == PRO_GATED) {
+            const int h = c / pro.head_dim, d = c - h * pro.head_dim;  // head_dim % 8 == 0
+            const float ih = head_inv[h];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = v[e] * ih * pro.w[d + e] * silu_dev(zr[c + e]);
+        }
+        uint32_t ph[4], pl[4];
+        float sum = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {  // positions 2p, 2p + 1 <- columns p, p + 4
+            const float va = v[p], vb = v[p + 4];
+            const _Float16 ha = static_cast<_Float16>(va), hb = static_cast<_Float16>(vb);
+            ph[p] = pack_h2(ha, hb);
+            pl[p] = pack_h2(static_cast<_Float16>(va - static_cast<float>(ha)),
+                            static_cast<_Float16>(vb - static_cast<float>(hb)));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[e];
+        oh[c8] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+        ol[c8] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+        sum = lanes_sum<8>(sum);
+        if ((c8 & 7) == 0) os[c8 >> 3] = sum;
     }
 }
 
 // ---------------------------------------------------------------------------
 // W4A16 GEMM, y[t][r] (op)= sum_k w[r][k] x[t][k] for a prompt chunk.
-// Block: BR weight rows x 128 tokens, 4 waves each owning BR/2 rows x 64
-// tokens (tiles of v_mfma_f32_16x16x32_f16).  Per 64-column group the block
-// dequantises its BR rows of the TILED64 matrix (codes stored as q ^ 8, read
-// as signed nibbles q - 8) to w = (q - z) s (v1) or q s + z (v2) in fp32 and
-// keeps w in LDS as fp16 hi + lo halves, next to the fp16 hi and lo halves of
-// its 128 tokens; every tile issues three MFMAs (w_hi x_hi, w_hi x_lo,
-// w_lo x_hi), so both operands carry about 22 significant bits as in the fp32
-// reference.  Software pipeline: the raw nibbles, metadata and activations of
-// group g + 1 are loaded into registers while the MFMAs of group g run.
-// Token tiles are the fastest grid dimension, so the blocks that share a
-// weight tile run together and the tile is fetched from HBM about once.
-// MFMA operand layout (16x16x32): lane l supplies row/column (l & 15) and the
-// 8 consecutive k at 8 (l >> 4); lane l receives D[4 (l >> 4) + v][l & 15].
+//
+// In column group g (64 columns) a row's weights are w = sn s + c0 with
+// sn = q - 8 the signed code, s the group scale and c0 = (8 - z) s for
+// w = (q - z) s, or 8 s + z for w = q s + z.  Hence
+//     y[t][r] = sum_g s[r][g] A[r][t][g] + sum_g c0[r][g] xs[t][g],
+//     A[r][t][g] = sum_{k in g} sn[r][k] x[t][k],  xs[t][g] = sum_{k in g} x[t][k].
+// sn is exact in fp16, so A takes two v_mfma_f32_16x16x32_f16 passes per 32
+// columns (sn x_hi + sn x_lo, x = x_hi + x_lo to about 22 bits) into a
+// per-group accumulator, which is scaled by s into the fp32 result.  The c0
+// term is a K = G contraction done after the group loop in three fp16 hi/lo
+// passes (c0 scaled by 64 and xs by 1/64, both exact, to stay in fp16 range).
+//
+// Block: WGR x WGT waves, each owning TI x TJ tiles of 16 rows x 16 tokens.
+// A operand: each lane loads its 8 bytes of a tile row's group straight from
+// the TILED64 matrix into registers, in a four-group ring ahead of the MFMAs:
+// lane l takes row l & 15 and words 2 (q & 1), 2 (q & 1) + 1 of half q >> 1,
+// q = l >> 4 (columns 32 (q >> 1) + 16 (q & 1) + 0..15), and unpacks a word
+// of 8 codes to fp16 q - 8 with integer ops ((u >> 4j) & 0x000F000F | 0x64006400
+// is fp16 1024 + q for codes j and j + 4) and one packed fp16 subtraction.
+// B operand: the block's BT tokens x 64 columns of x_hi and x_lo go through a
+// register ring two groups ahead into double-buffered LDS, one barrier per
+// group, with the scales of the block's rows.
+// MFMA operand layout (16x16x32): lane l supplies row/column (l & 15) and 8
+// consecutive k at 8 (l >> 4); lane l receives D[4 (l >> 4) + v][l & 15].
+// Here the k of an MFMA is a permutation of the group's columns, the same for
+// both operands.  Token tiles are the fastest grid dimension, so the blocks
+// that share a weight tile run together and it is fetched from HBM about once.
 // ---------------------------------------------------------------------------
-constexpr int kGemmToks = 128;
-constexpr int kGemmLd = 72;  // LDS row stride in halves (64 + 8 padding)
+constexpr int kGemmPad = 128;  // xh / xl / xs rows are padded to a multiple of this
+constexpr int kGemmLd = 72;    // LDS row stride in halves (64 + 8 padding)
 
-template <int BR>
-constexpr size_t gemm_lds_bytes() {
-    return static_cast<size_t>(BR + kGemmToks) * kGemmLd * 2 * sizeof(_Float16);
+struct GemmArgs {
+    const uint8_t* nib;
+    const uint32_t* meta;
+    int rows, cols, affine;
+    const _Float16* xh;
+    const _Float16* xl;
+    const float* xs;
+    int m;
+    float* y;
+    int ldy;
+};
+
+template <int WGR, int WGT, int TI, int TJ>
+struct GemmTile {
+    static constexpr int kWaves = WGR * WGT, kThreads = kWave * kWaves;
+    static constexpr int kWR = 16 * TI, kWT = 16 * TJ, kBR = WGR * kWR, kBT = WGT * kWT;
+    static constexpr int kXU = kBT * 16 / kThreads;    // 16-byte pieces of x per thread per group
+    static constexpr int kXStage = 2 * kBT * kGemmLd;  // halves per stage: x_hi rows, then x_lo rows
+    static constexpr size_t kLds = 2 * (static_cast<size_t>(kXStage) * sizeof(_Float16) + kBR * sizeof(float));
+    static_assert(kXU * kThreads == kBT * 16, "x staging");
+    static_assert(kBR <= kThreads, "scale staging");
+};
+
+// 8 stored codes (q ^ 8; column n of the word in bits 4n..4n+3) -> fp16 q - 8
+// in the column order [0 4 1 5 2 6 3 7]
+__device__ __forceinline__ half8 codes_to_h8(uint32_t w) {
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    const uint32_t u = w ^ 0x88888888u;
+    const half2_t bias = {static_cast<_Float16>(1032.0f), static_cast<_Float16>(1032.0f)};
+    uint32_t p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const half2_t h = __builtin_bit_cast(half2_t, ((u >> (4 * j)) & 0x000F000Fu) | 0x64006400u) - bias;
+        p[j] = __builtin_bit_cast(uint32_t, h);
+    }
+    return __builtin_bit_cast(half8, make_uint4(p[0], p[1], p[2], p[3]));
 }
 
-__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
-}
-
-template <int BR, int EPI>
-__global__ void __launch_bounds__(256) gemm_w4_mfma_kernel(const uint8_t* __restrict__ nib,
-                                                           const uint32_t* __restrict__ meta, int rows, int cols,
-                                                           int affine, const _Float16* __restrict__ xh,
-                                                           const _Float16* __restrict__ xl, int m,
-                                                           float* __restrict__ y, int ldy) {
-    constexpr int BT = kGemmToks;
-    constexpr int WR = BR / 2, TI = WR / 16, TJ = 4;  // wave tile: WR rows x 64 tokens
+template <int WGR, int WGT, int TI, int TJ, int EPI>
+__global__ void __launch_bounds__(kWave * WGR * WGT) gemm_w4_mfma_kernel(GemmArgs a) {
+    using T = GemmTile<WGR, WGT, TI, TJ>;
+    constexpr int BR = T::kBR, BT = T::kBT, XU = T::kXU, NT = T::kThreads;
+    constexpr int kTokStep = NT / 16;  // tokens between a thread's x pieces
     extern __shared__ uint4 gemm_lds[];
-    _Float16* Wh = reinterpret_cast<_Float16*>(gemm_lds);
-    _Float16* Wl = Wh + BR * kGemmLd;
-    _Float16* Xh = Wl + BR * kGemmLd;
-    _Float16* Xl = Xh + BT * kGemmLd;
-    const int t0 = blockIdx.x * BT;
-    const int r0 = blockIdx.y * BR;
-    const int G = cols >> 6;
-    const size_t row_bytes = static_cast<size_t>(cols) >> 1;
+    _Float16* xlds = reinterpret_cast<_Float16*>(gemm_lds);         // [2 stages][hi, lo][BT][kGemmLd]
+    float* slds = reinterpret_cast<float*>(xlds + 2 * T::kXStage);  // [2 stages][BR] scales
+    const int t0 = blockIdx.x * BT, r0 = blockIdx.y * BR;
+    const int G = a.cols >> 6, gl = G - 1;
+    const size_t row_bytes = static_cast<size_t>(a.cols) >> 1;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    const int wr = (wid >> 1) * WR, wt = (wid & 1) * 64;
-    // staging roles: weights, thread < 2 BR: row wrow, 16-byte half wh;
-    // activations: token threadIdx / 2, 32 columns (part) of hi and of lo
-    const bool w_thread = threadIdx.x < 2 * BR;
-    const int wrow = threadIdx.x >> 1, whalf = threadIdx.x & 1;
-    const int r = r0 + wrow;
-    const bool row_ok = w_thread && r < rows;
-    const int rr = min(r, rows - 1);
-    const int xtok = threadIdx.x >> 1, xpart = threadIdx.x & 1;
-    // prefetch registers (plain scalars: kept out of arrays so they stay in VGPRs)
-    uint4 wq = make_uint4(0, 0, 0, 0);
-    uint32_t mq = 0;
-    uint4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
-#define GEMM_LOAD_GROUP(gg)                                                                                        \
-    do {                                                                                                           \
-        const int g_ = (gg);                                                                                       \
-        if (w_thread) {                                                                                            \
-            const int c_ = g_ >> 6, l_ = g_ & 63;                                                                   \
-            const int gcnt_ = min(64, G - c_ * 64);                                                                \
-            wq = *reinterpret_cast<const uint4*>(nib + static_cast<size_t>(rr) * row_bytes + c_ * 2048 +            \
-                                                  whalf * gcnt_ * 16 + l_ * 16);                                   \
-            mq = meta[static_cast<size_t>(rr) * G + g_];                                                           \
-        }                                                                                                          \
-        const size_t src_ = static_cast<size_t>(t0 + xtok) * cols + g_ * 64 + xpart * 32;                         \
-        const uint4* ph_ = reinterpret_cast<const uint4*>(xh + src_);                                              \
-        const uint4* pl_ = reinterpret_cast<const uint4*>(xl + src_);                                              \
-        xa0 = ph_[0]; xa1 = ph_[1]; xa2 = ph_[2]; xa3 = ph_[3];                                                    \
-        xb0 = pl_[0]; xb1 = pl_[1]; xb2 = pl_[2]; xb3 = pl_[3];                                                    \
-    } while (0)
-    auto dequant8 = [&](uint32_t wv, float s, float c0, uint4* dh, uint4* dl) {
-        uint32_t ph[4], pl[4];
+    const int q = lane >> 4, lr = lane & 15;
+    const int wr = (wid / WGT) * T::kWR, wt = (wid % WGT) * T::kWT;
+    size_t arow[TI];  // byte offset of each tile row of this lane (rows past the end read the last row)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float wf[2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int sh = 4 * (2 * e + k);
-                const int sn = static_cast<int>(wv << (28 - sh)) >> 28;  // signed nibble q - 8
-                wf[k] = row_ok ? fmaf(static_cast<float>(sn), s, c0) : 0.0f;
-            }
-            const _Float16 h0 = static_cast<_Float16>(wf[0]), h1 = static_cast<_Float16>(wf[1]);
-            ph[e] = pack_h2(h0, h1);
-            pl[e] = pack_h2(static_cast<_Float16>(wf[0] - static_cast<float>(h0)),
-                            static_cast<_Float16>(wf[1] - static_cast<float>(h1)));
-        }
-        *dh = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-        *dl = make_uint4(pl[0], pl[1], pl[2], pl[3]);
-    };
-    auto store_group = [&]() {
-        if (w_thread) {
-            const float s = half_lo(mq), z = half_hi(mq);
-            // w = sn * s + c0 with sn = q - 8 the signed nibble
-            const float c0 = affine ? fmaf(8.0f, s, z) : (8.0f - z) * s;
-            uint4* dh = reinterpret_cast<uint4*>(Wh + wrow * kGemmLd + whalf * 32);
-            uint4* dl = reinterpret_cast<uint4*>(Wl + wrow * kGemmLd + whalf * 32);
-            dequant8(wq.x, s, c0, dh + 0, dl + 0);
-            dequant8(wq.y, s, c0, dh + 1, dl + 1);
-            dequant8(wq.z, s, c0, dh + 2, dl + 2);
-            dequant8(wq.w, s, c0, dh + 3, dl + 3);
-        }
-        uint4* xdh = reinterpret_cast<uint4*>(Xh + xtok * kGemmLd + xpart * 32);
-        uint4* xdl = reinterpret_cast<uint4*>(Xl + xtok * kGemmLd + xpart * 32);
-        xdh[0] = xa0; xdh[1] = xa1; xdh[2] = xa2; xdh[3] = xa3;
-        xdl[0] = xb0; xdl[1] = xb1; xdl[2] = xb2; xdl[3] = xb3;
-    };
+    for (int i = 0; i < TI; ++i) arow[i] = static_cast<size_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * row_bytes;
+    const int a_half = q >> 1, a_byte = (q & 1) * 8;
+    // x staging: piece j of this thread is token (tid >> 4) + kTokStep j, half (tid >> 3) & 1, columns 8 (tid & 7)
+    const int xtok = threadIdx.x >> 4, xhl = (threadIdx.x >> 3) & 1, xc8 = threadIdx.x & 7;
+    const _Float16* xsrc = (xhl ? a.xl : a.xh) + static_cast<size_t>(t0 + xtok) * a.cols + xc8 * 8;
+    const int xdst = xhl * BT * kGemmLd + xtok * kGemmLd + xc8 * 8;
+    const bool s_thread = threadIdx.x < BR;
+    const size_t srow = static_cast<size_t>(min(r0 + static_cast<int>(threadIdx.x), a.rows - 1)) * G;
+
+#define GEMM_LOAD_A(W, gg)                                                                                   \
+    {                                                                                                        \
+        const int g_ = (gg), c_ = g_ >> 6, l_ = g_ & 63;                                                     \
+        const size_t off_ = static_cast<size_t>(c_) * 2048 + a_half * min(64, G - (c_ << 6)) * 16 + l_ * 16 + \
+                            a_byte;                                                                          \
+        _Pragma("unroll") for (int i_ = 0; i_ < TI; ++i_) W[i_] =                                            \
+            *reinterpret_cast<const u32x2*>(a.nib + arow[i_] + off_);                                         \
+    }
+#define GEMM_LOAD_X(X, M, gg)                                                                                \
+    {                                                                                                        \
+        const int g_ = (gg);                                                                                 \
+        _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) X[j_] = *reinterpret_cast<const u32x4*>(            \
+            xsrc + static_cast<size_t>(j_ * kTokStep) * a.cols + g_ * 64);                                   \
+        if (s_thread) M = a.meta[srow + g_];                                                                 \
+    }
+#define GEMM_STORE_X(X, M, st)                                                                               \
+    {                                                                                                        \
+        _Float16* d_ = xlds + (st) * T::kXStage + xdst;                                                      \
+        _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) *reinterpret_cast<u32x4*>(d_ + j_ * kTokStep * kGemmLd) = \
+            X[j_];                                                                                           \
+        if (s_thread) slds[(st) * BR + threadIdx.x] = half_lo(M);                                            \
+    }
+#define GEMM_COMPUTE(st, W)                                                                                  \
+    {                                                                                                        \
+        const _Float16* xh_ = xlds + (st) * T::kXStage;                                                      \
+        const _Float16* xl_ = xh_ + BT * kGemmLd;                                                            \
+        half8 bh_[TJ][2], bl_[TJ][2];                                                                        \
+        _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) {                                                  \
+            _Pragma("unroll") for (int k_ = 0; k_ < 2; ++k_) {                                               \
+                const int o_ = (wt + 16 * j_ + lr) * kGemmLd + (2 * q + k_) * 8;                             \
+                bh_[j_][k_] = *reinterpret_cast<const half8*>(xh_ + o_);                                     \
+                bl_[j_][k_] = *reinterpret_cast<const half8*>(xl_ + o_);                                     \
+            }                                                                                                \
+        }                                                                                                    \
+        _Pragma("unroll") for (int i_ = 0; i_ < TI; ++i_) {                                                  \
+            const float4 sv_ = *reinterpret_cast<const float4*>(slds + (st) * BR + wr + 16 * i_ + 4 * q);    \
+            const half8 a0_ = codes_to_h8(W[i_].x), a1_ = codes_to_h8(W[i_].y);                              \
+            _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) {                                              \
+                floatx4 t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0_, bh_[j_][0], zero4, 0, 0, 0);        \
+                t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0_, bl_[j_][0], t_, 0, 0, 0);                   \
+                t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1_, bh_[j_][1], t_, 0, 0, 0);                   \
+                t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1_, bl_[j_][1], t_, 0, 0, 0);                   \
+                acc[i_][j_][0] = fmaf(sv_.x, t_[0], acc[i_][j_][0]);                                         \
+                acc[i_][j_][1] = fmaf(sv_.y, t_[1], acc[i_][j_][1]);                                         \
+                acc[i_][j_][2] = fmaf(sv_.z, t_[2], acc[i_][j_][2]);                                         \
+                acc[i_][j_][3] = fmaf(sv_.w, t_[3], acc[i_][j_][3]);                                         \
+            }                                                                                                \
+        }                                                                                                    \
+    }
+// step U of four: MFMAs of group g + U (LDS stage U & 1, A ring slot W), refill W with
+// group g + U + 4, store the x piece X (group g + U + 1) to the other stage, refill X
+// with group g + U + 3.  Loads past the last group re-read it, so every step issues the
+// same loads and the wait counts stay exact.
+#define GEMM_STEP(U, W, X, M)                                                                                \
+    {                                                                                                        \
+        const int gg_ = g + (U);                                                                             \
+        if (gg_ < G) GEMM_COMPUTE((U) & 1, W);                                                               \
+        GEMM_LOAD_A(W, min(gg_ + 4, gl));                                                                    \
+        GEMM_STORE_X(X, M, ((U) + 1) & 1);                                                                   \
+        GEMM_LOAD_X(X, M, min(gg_ + 3, gl));                                                                 \
+        __syncthreads();                                                                                     \
+    }
+
+    const floatx4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
     floatx4 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < TJ; ++j) acc[i][j] = zero4;
+    u32x2 wa0[TI], wa1[TI], wa2[TI], wa3[TI];
+    u32x4 xa[XU], xb[XU];  // x pieces of the even / odd groups
+    uint32_t ma = 0, mb = 0;
+    GEMM_LOAD_A(wa0, 0);
+    GEMM_LOAD_A(wa1, min(1, gl));
+    GEMM_LOAD_A(wa2, min(2, gl));
+    GEMM_LOAD_A(wa3, min(3, gl));
+    GEMM_LOAD_X(xa, ma, 0);
+    GEMM_LOAD_X(xb, mb, min(1, gl));
+    GEMM_STORE_X(xa, ma, 0);
+    GEMM_LOAD_X(xa, ma, min(2, gl));
+    __syncthreads();
+    for (int g = 0; g < G; g += 4) {
+        GEMM_STEP(0, wa0, xb, mb);
+        GEMM_STEP(1, wa1, xa, ma);
+        GEMM_STEP(2, wa2, xb, mb);
+        GEMM_STEP(3, wa3, xa, ma);
+    }
+#undef GEMM_STEP
+#undef GEMM_COMPUTE
+#undef GEMM_STORE_X
+#undef GEMM_LOAD_X
+#undef GEMM_LOAD_A
 
-    GEMM_LOAD_GROUP(0);
-    for (int g = 0; g < G; ++g) {
-        __syncthreads();  // the previous group's MFMA operands have been read
-        store_group();
-        __syncthreads();
-        if (g + 1 < G) GEMM_LOAD_GROUP(g + 1);  // in flight during this group's MFMAs
+    // c0 term: K = G, lane group q takes groups gb + 8 q + 0..7 of its row / token
+    for (int gb = 0; gb < G; gb += 32) {
+        half8 ch[TI], cl[TI], sh[TJ], sl[TJ];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int k = ks * 32 + (lane >> 4) * 8;
-            half8 ah[TI], al[TI], bh[TJ], bl[TJ];
+        for (int i = 0; i < TI; ++i) {
+            const size_t mrow = static_cast<size_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * G;
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                ah[i] = *reinterpret_cast<const half8*>(Wh + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
-                al[i] = *reinterpret_cast<const half8*>(Wl + (wr + i * 16 + (lane & 15)) * kGemmLd + k);
+            for (int e = 0; e < 8; ++e) {
+                const int g = gb + 8 * q + e;
+                float c0 = 0.0f;
+                if (g < G) {
+                    const uint32_t mw = a.meta[mrow + g];
+                    const float s = half_lo(mw), z = half_hi(mw);
+                    c0 = 64.0f * (a.affine ? fmaf(8.0f, s, z) : (8.0f - z) * s);
+                }
+                ch[i][e] = static_cast<_Float16>(c0);
+                cl[i][e] = static_cast<_Float16>(c0 - static_cast<float>(ch[i][e]));
             }
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const float* xsr = a.xs + static_cast<size_t>(t0 + wt + 16 * j + lr) * G;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int g = gb + 8 * q + e;
+                const float v = g < G ? xsr[g] * 0.015625f : 0.0f;
+                sh[j][e] = static_cast<_Float16>(v);
+                sl[j][e] = static_cast<_Float16>(v - static_cast<float>(sh[j][e]));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                bh[j] = *reinterpret_cast<const half8*>(Xh + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
-                bl[j] = *reinterpret_cast<const half8*>(Xl + (wt + j * 16 + (lane & 15)) * kGemmLd + k);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cl[i], sh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ch[i], sl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ch[i], sh[j], acc[i][j], 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
-                }
-        }
     }
+
     // epilogue: lane holds rows 4 (lane >> 4) + v of tile i, token (lane & 15) of tile j
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const int t = t0 + wt + j * 16 + (lane & 15);
-            const int rb = r0 + wr + i * 16 + 4 * (lane >> 4);
-            if (t >= m) continue;
-            float* yr = y + static_cast<size_t>(t) * ldy;
+            const int t = t0 + wt + j * 16 + lr;
+            const int rb = r0 + wr + i * 16 + 4 * q;
+            if (t >= a.m) continue;
+            float* yr = a.y + static_cast<size_t>(t) * a.ldy;
             if constexpr (EPI == 2) {  // interleaved (gate, up) rows -> silu(gate) * up
 #pragma unroll
                 for (int v = 0; v < 4; v += 2)
-                    if (rb + v + 1 < rows) yr[(rb + v) >> 1] = silu_dev(acc[i][j][v]) * acc[i][j][v + 1];
+                    if (rb + v + 1 < a.rows) yr[(rb + v) >> 1] = silu_dev(acc[i][j][v]) * acc[i][j][v + 1];
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    if (rb + v >= rows) continue;
+                    if (rb + v >= a.rows) continue;
                     if constexpr (EPI == 1)
                         yr[rb + v] += acc[i][j][v];
                     else
@@ -249,57 +363,49 @@ __global__ void __launch_bounds__(256) gemm_w4_mfma_kernel(const uint8_t* __rest
 }
 
 size_t gemm_workspace_bytes(int m, int cols) {
-    const size_t m_pad = static_cast<size_t>((m + kGemmToks - 1) / kGemmToks) * kGemmToks;
-    return 2 * m_pad * static_cast<size_t>(cols) * sizeof(_Float16);
+    const size_t m_pad = static_cast<size_t>((m + kGemmPad - 1) / kGemmPad) * kGemmPad;
+    return m_pad * static_cast<size_t>(cols) * (2 * sizeof(_Float16)) + m_pad * static_cast<size_t>(cols / 64) * sizeof(float);
 }
 
 bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro) {
     if (layout != 0 || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0) return false;
     if (pro.mode == PRO_GATED)
-        return pro.head_dim > 0 && cols % pro.head_dim == 0;
+        return pro.head_dim > 0 && pro.head_dim % 8 == 0 && cols % pro.head_dim == 0 &&
+               cols / pro.head_dim <= kPrepMaxHeads;
     return true;
 }
 
-template <int BR, int EPI>
-static hipError_t launch_gemm_t(const GemmLaunch& p, const _Float16* xh, const _Float16* xl, int m_pad,
-                                hipStream_t s) {
-    const auto fn = reinterpret_cast<const void*>(&gemm_w4_mfma_kernel<BR, EPI>);
-    constexpr size_t lds = gemm_lds_bytes<BR>();
-    if (lds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
-        if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+template <int WGR, int WGT, int TI, int TJ, int EPI>
+static hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
+    using T = GemmTile<WGR, WGT, TI, TJ>;
+    const auto fn = reinterpret_cast<const void*>(&gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI>);
+    if constexpr (T::kLds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
+        if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(T::kLds));
             e != hipSuccess)
             return e;
     }
-    const dim3 grid(m_pad / kGemmToks, (p.rows + BR - 1) / BR);
-    hipLaunchKernelGGL((gemm_w4_mfma_kernel<BR, EPI>), grid, dim3(256), lds, s, p.nib,
-                       static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xl, p.m, p.y, p.ldy);
+    const dim3 grid((a.m + T::kBT - 1) / T::kBT, (a.rows + T::kBR - 1) / T::kBR);
+    hipLaunchKernelGGL((gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI>), grid, dim3(T::kThreads), T::kLds, s, a);
     return hipGetLastError();
 }
 
-template <int BR>
-static hipError_t launch_gemm_br(const GemmLaunch& p, const _Float16* xh, const _Float16* xl, int m_pad,
-                                 hipStream_t s) {
-    switch (p.epi) {
-        case 0: return launch_gemm_t<BR, 0>(p, xh, xl, m_pad, s);
-        case 1: return launch_gemm_t<BR, 1>(p, xh, xl, m_pad, s);
-        case 2: return launch_gemm_t<BR, 2>(p, xh, xl, m_pad, s);
-        default: return hipErrorInvalidValue;
-    }
-}
-
 hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
-    const int m_pad = (p.m + kGemmToks - 1) / kGemmToks * kGemmToks;
+    const int m_pad = (p.m + kGemmPad - 1) / kGemmPad * kGemmPad;
     _Float16* xh = static_cast<_Float16*>(p.workspace);
     _Float16* xl = xh + static_cast<size_t>(m_pad) * p.cols;
-    hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl);
+    float* xs = reinterpret_cast<float*>(xl + static_cast<size_t>(m_pad) * p.cols);
+    hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
+                       xs);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    // 128-row tiles unless that leaves CUs idle (the 4096-row projections)
-    int cus = 256;
-    int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    const long tiles128 = static_cast<long>((p.rows + 127) / 128) * (m_pad / kGemmToks);
-    if (tiles128 >= cus) return launch_gemm_br<128>(p, xh, xl, m_pad, s);
-    return launch_gemm_br<64>(p, xh, xl, m_pad, s);
+    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xl, xs, p.m, p.y,
+                     p.ldy};
+    // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
+    switch (p.epi) {
+        case 0: return launch_gemm_cfg<4, 1, 2, 4, 0>(a, s);
+        case 1: return launch_gemm_cfg<4, 1, 2, 4, 1>(a, s);
+        case 2: return launch_gemm_cfg<4, 1, 2, 4, 2>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 // ---------------------------------------------------------------------------
