@@ -138,117 +138,136 @@ __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x
 // that share a weight tile run together and it is fetched from HBM about once.
 // ---------------------------------------------------------------------------
 constexpr int kGemmPad = 128;  // xh / xl / xs rows are padded to a multiple of this
-constexpr int kGemmLd = 72;    // LDS row stride in halves (64 + 8 padding)
 
 struct GemmArgs {
     const uint8_t* nib;
     const uint32_t* meta;
     int rows, cols, affine;
-    const _Float16* xh;
-    const _Float16* xl;
-    const float* xs;
-    int m;
+    const _Float16* xh;  // [m_pad][cols], followed by xl [m_pad][cols]
+    const float* xs;     // [m_pad][cols / 64]
+    int m, m_pad;
     float* y;
     int ldy;
 };
+
+constexpr int kGemmXLd = 136;  // LDS x row in halves: x_hi[64] | x_lo[64] | 8 padding
 
 template <int WGR, int WGT, int TI, int TJ>
 struct GemmTile {
     static constexpr int kWaves = WGR * WGT, kThreads = kWave * kWaves;
     static constexpr int kWR = 16 * TI, kWT = 16 * TJ, kBR = WGR * kWR, kBT = WGT * kWT;
-    static constexpr int kXU = kBT * 16 / kThreads;    // 16-byte pieces of x per thread per group
-    static constexpr int kXStage = 2 * kBT * kGemmLd;  // halves per stage: x_hi rows, then x_lo rows
+    static constexpr int kXU = kBT * 16 / kThreads;  // 16-byte pieces of x per thread per group
+    static constexpr int kXStage = kBT * kGemmXLd;   // halves per stage
     static constexpr size_t kLds = 2 * (static_cast<size_t>(kXStage) * sizeof(_Float16) + kBR * sizeof(float));
     static_assert(kXU * kThreads == kBT * 16, "x staging");
     static_assert(kBR <= kThreads, "scale staging");
 };
 
 // 8 stored codes (q ^ 8; column n of the word in bits 4n..4n+3) -> fp16 q - 8
-// in the column order [0 4 1 5 2 6 3 7]
+// in the column order [0 4 1 5 2 6 3 7]: ((w >> 4j) & 0x000F000F) ^ 0x64086408
+// is fp16 (1024 + q) for the codes j and j + 4 (one shift and one three-input
+// bit op), less 1032 in one packed fp16 subtraction.
 __device__ __forceinline__ half8 codes_to_h8(uint32_t w) {
     typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-    const uint32_t u = w ^ 0x88888888u;
     const half2_t bias = {static_cast<_Float16>(1032.0f), static_cast<_Float16>(1032.0f)};
     uint32_t p[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const half2_t h = __builtin_bit_cast(half2_t, ((u >> (4 * j)) & 0x000F000Fu) | 0x64006400u) - bias;
+        const half2_t h = __builtin_bit_cast(half2_t, ((w >> (4 * j)) & 0x000F000Fu) ^ 0x64086408u) - bias;
         p[j] = __builtin_bit_cast(uint32_t, h);
     }
     return __builtin_bit_cast(half8, make_uint4(p[0], p[1], p[2], p[3]));
 }
 
+// two waves per SIMD (at most 256 registers per lane), so one block's barrier wait overlaps another's work
 template <int WGR, int WGT, int TI, int TJ, int EPI>
-__global__ void __launch_bounds__(kWave * WGR * WGT) gemm_w4_mfma_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(kWave * WGR * WGT) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_w4_mfma_kernel(GemmArgs a) {
     using T = GemmTile<WGR, WGT, TI, TJ>;
     constexpr int BR = T::kBR, BT = T::kBT, XU = T::kXU, NT = T::kThreads;
     constexpr int kTokStep = NT / 16;  // tokens between a thread's x pieces
     extern __shared__ uint4 gemm_lds[];
-    _Float16* xlds = reinterpret_cast<_Float16*>(gemm_lds);         // [2 stages][hi, lo][BT][kGemmLd]
+    _Float16* xlds = reinterpret_cast<_Float16*>(gemm_lds);         // [2 stages][BT][kGemmXLd]
     float* slds = reinterpret_cast<float*>(xlds + 2 * T::kXStage);  // [2 stages][BR] scales
     const int t0 = blockIdx.x * BT, r0 = blockIdx.y * BR;
     const int G = a.cols >> 6, gl = G - 1;
-    const size_t row_bytes = static_cast<size_t>(a.cols) >> 1;
+    const uint32_t row_bytes = static_cast<uint32_t>(a.cols) >> 1;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int q = lane >> 4, lr = lane & 15;
     const int wr = (wid / WGT) * T::kWR, wt = (wid % WGT) * T::kWT;
-    size_t arow[TI];  // byte offset of each tile row of this lane (rows past the end read the last row)
+    // A operand: byte offsets of this lane's 8 bytes in each tile row (rows past the end read the
+    // last row); the half-1 offset depends on the chunk's group count, full or the last chunk's
+    const __amdgpu_buffer_rsrc_t nib_r = buf_rsrc(a.nib, static_cast<uint32_t>(a.rows) * row_bytes);
+    const int lastc = gl >> 6;
+    const uint32_t gc_full = static_cast<uint32_t>(min(64, G)), gc_last = static_cast<uint32_t>(G - (lastc << 6));
+    uint32_t aoff_full[TI], aoff_last[TI];
 #pragma unroll
-    for (int i = 0; i < TI; ++i) arow[i] = static_cast<size_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * row_bytes;
-    const int a_half = q >> 1, a_byte = (q & 1) * 8;
-    // x staging: piece j of this thread is token (tid >> 4) + kTokStep j, half (tid >> 3) & 1, columns 8 (tid & 7)
-    const int xtok = threadIdx.x >> 4, xhl = (threadIdx.x >> 3) & 1, xc8 = threadIdx.x & 7;
-    const _Float16* xsrc = (xhl ? a.xl : a.xh) + static_cast<size_t>(t0 + xtok) * a.cols + xc8 * 8;
-    const int xdst = xhl * BT * kGemmLd + xtok * kGemmLd + xc8 * 8;
+    for (int i = 0; i < TI; ++i) {
+        const uint32_t base =
+            static_cast<uint32_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * row_bytes + (q & 1) * 8u;
+        aoff_full[i] = base + static_cast<uint32_t>(q >> 1) * gc_full * 16u;
+        aoff_last[i] = base + static_cast<uint32_t>(q >> 1) * gc_last * 16u;
+    }
+    // x staging: piece j of this thread is token (tid >> 4) + kTokStep j, 16 bytes at (tid & 15) of
+    // the token's 256-byte LDS row (x_hi columns 0..63, then x_lo)
+    const __amdgpu_buffer_rsrc_t x_r = buf_rsrc(a.xh, static_cast<uint32_t>(a.m_pad) * a.cols * 4u);
+    const int xtok = threadIdx.x >> 4, c16 = threadIdx.x & 15;
+    uint32_t xoff[XU];
+#pragma unroll
+    for (int j = 0; j < XU; ++j)
+        xoff[j] = (static_cast<uint32_t>((c16 >> 3) * a.m_pad + t0 + xtok + j * kTokStep) * a.cols +
+                   (c16 & 7) * 8u) * 2u;
+    const int xdst = xtok * kGemmXLd + c16 * 8;
+    // scales: thread < BR stages row r0 + tid (the others load out of range: zero, no branch)
+    const __amdgpu_buffer_rsrc_t meta_r = buf_rsrc(a.meta, static_cast<uint32_t>(a.rows) * G * 4u);
     const bool s_thread = threadIdx.x < BR;
-    const size_t srow = static_cast<size_t>(min(r0 + static_cast<int>(threadIdx.x), a.rows - 1)) * G;
+    const uint32_t moff =
+        s_thread ? static_cast<uint32_t>(min(r0 + static_cast<int>(threadIdx.x), a.rows - 1)) * G * 4u : kBufOOB;
 
 #define GEMM_LOAD_A(W, gg)                                                                                   \
     {                                                                                                        \
-        const int g_ = (gg), c_ = g_ >> 6, l_ = g_ & 63;                                                     \
-        const size_t off_ = static_cast<size_t>(c_) * 2048 + a_half * min(64, G - (c_ << 6)) * 16 + l_ * 16 + \
-                            a_byte;                                                                          \
-        _Pragma("unroll") for (int i_ = 0; i_ < TI; ++i_) W[i_] =                                            \
-            *reinterpret_cast<const u32x2*>(a.nib + arow[i_] + off_);                                         \
+        const int g_ = (gg), c_ = g_ >> 6;                                                                   \
+        const uint32_t so_ = static_cast<uint32_t>(c_) * 2048u + static_cast<uint32_t>(g_ & 63) * 16u;       \
+        const bool last_ = c_ == lastc;                                                                      \
+        _Pragma("unroll") for (int i_ = 0; i_ < TI; ++i_) W[i_] = __builtin_amdgcn_raw_buffer_load_b64(      \
+            nib_r, last_ ? aoff_last[i_] : aoff_full[i_], so_, 0);                                            \
     }
 #define GEMM_LOAD_X(X, M, gg)                                                                                \
     {                                                                                                        \
-        const int g_ = (gg);                                                                                 \
-        _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) X[j_] = *reinterpret_cast<const u32x4*>(            \
-            xsrc + static_cast<size_t>(j_ * kTokStep) * a.cols + g_ * 64);                                   \
-        if (s_thread) M = a.meta[srow + g_];                                                                 \
+        const uint32_t g_ = static_cast<uint32_t>(gg);                                                       \
+        _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) X[j_] =                                            \
+            __builtin_amdgcn_raw_buffer_load_b128(x_r, xoff[j_], g_ * 128u, 0);                              \
+        M = __builtin_amdgcn_raw_buffer_load_b32(meta_r, moff, g_ * 4u, 0);                                   \
     }
 #define GEMM_STORE_X(X, M, st)                                                                               \
     {                                                                                                        \
         _Float16* d_ = xlds + (st) * T::kXStage + xdst;                                                      \
-        _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) *reinterpret_cast<u32x4*>(d_ + j_ * kTokStep * kGemmLd) = \
+        _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) *reinterpret_cast<u32x4*>(d_ + j_ * kTokStep * kGemmXLd) = \
             X[j_];                                                                                           \
         if (s_thread) slds[(st) * BR + threadIdx.x] = half_lo(M);                                            \
     }
+// MFMAs of one group, each tile's four chained into a per-group sum that is scaled into acc
 #define GEMM_COMPUTE(st, W)                                                                                  \
     {                                                                                                        \
-        const _Float16* xh_ = xlds + (st) * T::kXStage;                                                      \
-        const _Float16* xl_ = xh_ + BT * kGemmLd;                                                            \
+        const _Float16* xs_ = xlds + (st) * T::kXStage;                                                      \
         half8 bh_[TJ][2], bl_[TJ][2];                                                                        \
         _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) {                                                  \
             _Pragma("unroll") for (int k_ = 0; k_ < 2; ++k_) {                                               \
-                const int o_ = (wt + 16 * j_ + lr) * kGemmLd + (2 * q + k_) * 8;                             \
-                bh_[j_][k_] = *reinterpret_cast<const half8*>(xh_ + o_);                                     \
-                bl_[j_][k_] = *reinterpret_cast<const half8*>(xl_ + o_);                                     \
+                const int o_ = (wt + 16 * j_ + lr) * kGemmXLd + (2 * q + k_) * 8;                            \
+                bh_[j_][k_] = *reinterpret_cast<const half8*>(xs_ + o_);                                     \
+                bl_[j_][k_] = *reinterpret_cast<const half8*>(xs_ + o_ + 64);                                \
             }                                                                                                \
         }                                                                                                    \
         _Pragma("unroll") for (int i_ = 0; i_ < TI; ++i_) {                                                  \
-            const float4 sv_ = *reinterpret_cast<const float4*>(slds + (st) * BR + wr + 16 * i_ + 4 * q);    \
+            const floatx4 sv_ = *reinterpret_cast<const floatx4*>(slds + (st) * BR + wr + 16 * i_ + 4 * q);  \
             const half8 a0_ = codes_to_h8(W[i_].x), a1_ = codes_to_h8(W[i_].y);                              \
             _Pragma("unroll") for (int j_ = 0; j_ < TJ; ++j_) {                                              \
                 floatx4 t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0_, bh_[j_][0], zero4, 0, 0, 0);        \
                 t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0_, bl_[j_][0], t_, 0, 0, 0);                   \
                 t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1_, bh_[j_][1], t_, 0, 0, 0);                   \
                 t_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1_, bl_[j_][1], t_, 0, 0, 0);                   \
-                acc[i_][j_][0] = fmaf(sv_.x, t_[0], acc[i_][j_][0]);                                         \
-                acc[i_][j_][1] = fmaf(sv_.y, t_[1], acc[i_][j_][1]);                                         \
-                acc[i_][j_][2] = fmaf(sv_.z, t_[2], acc[i_][j_][2]);                                         \
-                acc[i_][j_][3] = fmaf(sv_.w, t_[3], acc[i_][j_][3]);                                         \
+                _Pragma("unroll") for (int v_ = 0; v_ < 4; ++v_) acc[i_][j_][v_] =                           \
+                    fmaf(sv_[v_], t_[v_], acc[i_][j_][v_]);                                                  \
             }                                                                                                \
         }                                                                                                    \
     }
@@ -295,37 +314,46 @@ __global__ void __launch_bounds__(kWave * WGR * WGT) gemm_w4_mfma_kernel(GemmArg
 #undef GEMM_STORE_X
 #undef GEMM_LOAD_X
 #undef GEMM_LOAD_A
-
-    // c0 term: K = G, lane group q takes groups gb + 8 q + 0..7 of its row / token
+    // c0 term: K = G, lane group q takes groups gb + 8 q + 0..7 of its row / token.  All loads of a
+    // chunk are issued before any use; groups past G read out of range (zero), so c0 and xs are 0.
+    const __amdgpu_buffer_rsrc_t xs_r = buf_rsrc(a.xs, static_cast<uint32_t>(a.m_pad) * G * 4u);
     for (int gb = 0; gb < G; gb += 32) {
-        half8 ch[TI], cl[TI], sh[TJ], sl[TJ];
+        const int g8 = gb + 8 * q;
+        uint32_t mw[TI][8], xw[TJ][8];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
-            const size_t mrow = static_cast<size_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * G;
+            const uint32_t off =
+                (static_cast<uint32_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * G + static_cast<uint32_t>(g8)) * 4u;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int g = gb + 8 * q + e;
-                float c0 = 0.0f;
-                if (g < G) {
-                    const uint32_t mw = a.meta[mrow + g];
-                    const float s = half_lo(mw), z = half_hi(mw);
-                    c0 = 64.0f * (a.affine ? fmaf(8.0f, s, z) : (8.0f - z) * s);
-                }
-                ch[i][e] = static_cast<_Float16>(c0);
-                cl[i][e] = static_cast<_Float16>(c0 - static_cast<float>(ch[i][e]));
-            }
+            for (int e = 0; e < 8; ++e)
+                mw[i][e] = __builtin_amdgcn_raw_buffer_load_b32(meta_r, g8 + e < G ? off + 4u * e : kBufOOB, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const float* xsr = a.xs + static_cast<size_t>(t0 + wt + 16 * j + lr) * G;
+            const uint32_t off = (static_cast<uint32_t>(t0 + wt + 16 * j + lr) * G + static_cast<uint32_t>(g8)) * 4u;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                xw[j][e] = __builtin_amdgcn_raw_buffer_load_b32(xs_r, g8 + e < G ? off + 4u * e : kBufOOB, 0, 0);
+        }
+        half8 ch[TI], cl[TI], sh[TJ], sl[TJ];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int g = gb + 8 * q + e;
-                const float v = g < G ? xsr[g] * 0.015625f : 0.0f;
+                const uint32_t w = mw[i][e];
+                const float sc = half_lo(w), z = half_hi(w);
+                const float c0 = 64.0f * (a.affine ? fmaf(8.0f, sc, z) : (8.0f - z) * sc);
+                ch[i][e] = static_cast<_Float16>(c0);
+                cl[i][e] = static_cast<_Float16>(c0 - static_cast<float>(ch[i][e]));
+            }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = __builtin_bit_cast(float, xw[j][e]) * 0.015625f;
                 sh[j][e] = static_cast<_Float16>(v);
                 sl[j][e] = static_cast<_Float16>(v - static_cast<float>(sh[j][e]));
             }
-        }
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -397,7 +425,7 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
                        xs);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xl, xs, p.m, p.y,
+    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xs, p.m, m_pad, p.y,
                      p.ldy};
     // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
     switch (p.epi) {
