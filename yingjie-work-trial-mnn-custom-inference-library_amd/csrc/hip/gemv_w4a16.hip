@@ -148,8 +148,9 @@ __device__ __forceinline__ void decode_act8(const u32x4& a, const u32x4& b, int 
 // barrier that waits for none of them, and only then calls `prefetch`, which
 // issues the block's first weight loads; the activations thus return first and
 // the staging arithmetic below overlaps the weight stream.  The norm factors
-// come from the same registers: the RMS over the vector by one block
-// reduction, the per-head factors of PRO_GATED by a lane reduction over the
+// come from the same registers: for PRO_RMS each wave's sum of squares (the
+// factor itself is applied to the group scales after the barrier, see
+// rms_factor), for PRO_GATED the per-head factors by a lane reduction over the
 // head's consecutive items.  ITEMS * THREADS * 8 must cover `cols`; the caller
 // synchronises the block before reading xs.  Prologue vectors are preloaded
 // only for <= 2 items per thread (the 4096-column launches): wider blocks load
@@ -202,6 +203,10 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
         }
     }
     if (pro.mode == PRO_RMS) {
+        // The RMS factor is one scalar for the whole vector and the digits are
+        // relative to each group's maximum, so the groups are staged from x * w
+        // and the factor multiplies the group scales after the caller's barrier
+        // (rms_factor): here each wave only leaves its sum of squares in red.
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
@@ -210,8 +215,8 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
 #pragma unroll
                 for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
         }
-        ss = block_sum_t<THREADS / kWave>(ss, red);
-        const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + pro.eps);
+        ss = wave_sum(ss);
+        if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
             float wl[8];
@@ -223,7 +228,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
                 as_floats8(load16(wr, item * 32u), load16(wr, item * 32u + 16u), wl);
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i];
+            for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * wl[i];
         }
     } else if (pro.mode == PRO_GATED) {
         // head_dim % 8 == 0 and head_dim / 8 a power of two <= 64: the items of a
@@ -291,6 +296,16 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
             }
         }
     }
+}
+
+// PRO_RMS factor 1/sqrt(mean(x^2) + eps) from the per-wave sums of squares
+// stage_x_lds left in red (read after the block barrier that follows it)
+template <int NW>
+__device__ __forceinline__ float rms_factor(const float* red, int cols, float eps) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) ss += red[i];
+    return 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
 }
 
 bool stage_supported(int cols, const Prologue& pro) {
@@ -445,6 +460,7 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         ge = has_group ? __uint_as_float(kk.x) : 0.0f;
         gg = has_group ? __uint_as_float(kk.y) : 0.0f;
     }
+    if (pro.mode == PRO_RMS) ge *= rms_factor<NCH * RG>(red, cols, pro.eps);
 
     uint64_t best = 0;
     const int units = (rows + R * RG - 1) / (R * RG);
