@@ -90,6 +90,8 @@ __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& 
 constexpr int kDigits = 6;
 constexpr int kXMax = 1 << (4 * kDigits - 3);  // 2^21: |X| <= kXMax keeps |D| < 2^30
 constexpr uint32_t kDigitBias = 0x888888u;     // 8 in every hex digit of the 6
+constexpr float kRoundMagic = 12582912.0f;     // 1.5 * 2^23: x + it rounds x to an integer in the low bits
+constexpr uint32_t kRoundMagicBits = 0x4B400000u;
 constexpr int kStageRecord = (8 * kDigits + 2 + 3) / 4;
 constexpr int kMaxStageCols = 16384;
 
@@ -273,19 +275,18 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
 #pragma unroll
         for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[k][i]));
         mx = lanes_max<8>(mx);
-        const float inv = mx > 0.0f ? static_cast<float>(kXMax) / mx : 0.0f;
-        int X[8];
-        int gs = 0;
+        // X = rint(x * 2^21 / mx) is the low mantissa of fma(x, inv, 1.5 * 2^23) (|x inv| <= 2^21 + 1/4,
+        // inv from v_rcp_f32 within an ulp), so U = X + kDigitBias is that float's bits minus a constant
+        const float inv = mx > 0.0f ? static_cast<float>(kXMax) * __builtin_amdgcn_rcpf(mx) : 0.0f;
+        uint32_t U[8];
+        uint32_t us = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            X[i] = min(kXMax, max(-kXMax, static_cast<int>(rintf(v[k][i] * inv))));
-            gs += X[i];
+            U[i] = __float_as_uint(fmaf(v[k][i], inv, kRoundMagic)) - (kRoundMagicBits - kDigitBias);
+            us += U[i];
         }
-        gs = lanes_sum_i<8>(gs);
+        const int gs = lanes_sum_i<8>(static_cast<int>(us)) - 64 * static_cast<int>(kDigitBias);
         if (item < n_items) {
-            uint32_t U[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) U[i] = static_cast<uint32_t>(X[i]) + kDigitBias;
             uint32_t W[kDigits];
             digit_words(U, W);
 #pragma unroll
