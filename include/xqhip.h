@@ -231,9 +231,10 @@ XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, fl
 XQHIP_API size_t xqhip_gemm_workspace_bytes(int m, int cols);
 /* y[t] (op)= W prologue(x[t]) for t < m: every token as xqhip_gemv_w4a16 does it
  * (same epilogues; EPI_SILU_PAIR writes rows/2 values per token), on a TILED64
- * matrix.  W is dequantised in fp32 and held in LDS as fp16 hi + lo halves, x is
- * split the same way, and the products w_hi x_hi + w_hi x_lo + w_lo x_hi run on
- * fp16 MFMA with fp32 accumulation.  GATED_HEAD reads the gate
+ * matrix.  Per 64-column group the codes q - 8 (exact in fp16) multiply x held
+ * as fp16 hi + lo halves on fp16 MFMA with fp32 accumulation, the group sum is
+ * scaled by the group scale, and the zero-point term is added as the product of
+ * the per-group offsets with the per-token group sums of x.  GATED_HEAD reads the gate
  * of token t at pro->gate + t * ld_gate.  workspace: 16-byte aligned,
  * xqhip_gemm_workspace_bytes(m, cols). */
 XQHIP_API int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro,

@@ -7,11 +7,16 @@
 // kPrefillChunk tokens) run as one W4A16 GEMM each on the matrix cores, and
 // the sequential parts run as batched kernels:
 //   prep_x_kernel        per-token RMSNorm / gated head norm, x -> fp16 hi + lo
-//   gemm_w4_mfma_kernel  dequantise a 64x64 weight tile to fp16 hi + lo in LDS,
-//                        then v_mfma_f32_16x16x32_f16 on the hi/lo halves
-//   prefill_attn_kernel  causal GQA over the cache for every prompt token
-//   linear_scan_kernel   conv1d + L2 norm + gated delta over the chunk, with the
-//                        recurrent state and conv history held in registers
+//                        and per-group sums of x
+//   gemm_w4_mfma_kernel  per 64-column group: codes q - 8 (exact in fp16) times
+//                        x hi / lo on v_mfma_f32_16x16x32_f16, group sums scaled
+//                        by the group scale; the zero-point term as a K = G
+//                        MFMA contraction after the group loop
+//   prefill_attn_tile_kernel / prefill_attn_kernel   causal GQA over the cache
+//   linear_conv_prefill_kernel + linear_scan_recur_kernel   conv1d + norms +
+//                        gates for all tokens, then the gated-delta recurrence
+//                        with the state in registers (one-pass kernels
+//                        linear_scan_wave_kernel / linear_scan_kernel otherwise)
 #include "xqhip_common.hpp"
 #include "xqhip_kernels.hpp"
 
