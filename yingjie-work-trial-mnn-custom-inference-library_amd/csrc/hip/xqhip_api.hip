@@ -537,6 +537,10 @@ int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xq
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: needs a TILED64 matrix (%dx%d g%d)", w->rows, w->cols, w->group);
     if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: workspace must be 16-byte aligned");
+    // the kernels address the staged x (hi and lo halves) with 32-bit buffer offsets
+    if (xqhip::gemm_workspace_bytes(m, w->cols) >= (size_t{1} << 31))
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: %d tokens of %d columns exceed one call (2 GiB of staged x)", m,
+                    w->cols);
     xqhip::GemmLaunch p{};
     p.nib = static_cast<const uint8_t*>(w->nib);
     p.meta = w->meta;
