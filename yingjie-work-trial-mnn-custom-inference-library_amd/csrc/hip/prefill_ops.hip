@@ -1108,6 +1108,7 @@ constexpr int kRecurTokens = 16;  // tokens staged in LDS per barrier
 template <int DK>
 __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch p) {
     constexpr int RS = DK / 16;  // state rows per lane
+    static_assert(RS % 2 == 0, "two accumulation chains");
     constexpr int TG = kRecurTokens;
     __shared__ float qs[2][TG][DK], ks[2][TG][DK], vs[2][TG][16], gs[2][TG][2];
     const int vh = blockIdx.x;
@@ -1165,8 +1166,14 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
         __syncthreads();  // this buffer is complete; the other one is no longer read
         if (g0 + TG < p.tokens) load_stage(g0 + TG);
         const int nt = min(TG, p.tokens - g0);
-        for (int k = 0; k < nt; ++k) {
-            const float beta = gs[buf][k][0], decay = gs[buf][k][1];
+        // A fixed, unrolled TG-token loop (so the LDS reads of later tokens are issued
+        // early); tokens past the end run with beta 0 and decay 1, leaving the state as
+        // is.  Each token's output is kept by lane ig == k and stored after the loop.
+        float my_o = 0.0f;
+#pragma unroll
+        for (int k = 0; k < TG; ++k) {
+            const bool live = k < nt;
+            const float beta = live ? gs[buf][k][0] : 0.0f, decay = live ? gs[buf][k][1] : 1.0f;
             const float vj = vs[buf][k][col];
             float kr[RS], qr[RS];
 #pragma unroll
@@ -1174,24 +1181,29 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
                 kr[r] = ks[buf][k][ig + 16 * r];
                 qr[r] = qs[buf][k][ig + 16 * r];
             }
-            float pred = 0.0f;
+            float pa = 0.0f, pb = 0.0f;  // two chains
 #pragma unroll
-            for (int r = 0; r < RS; ++r) {
+            for (int r = 0; r < RS; r += 2) {
                 sreg[r] *= decay;
-                pred += sreg[r] * kr[r];
+                sreg[r + 1] *= decay;
+                pa = fmaf(sreg[r], kr[r], pa);
+                pb = fmaf(sreg[r + 1], kr[r + 1], pb);
             }
-            pred = lanes_sum<16>(pred);
+            const float pred = lanes_sum<16>(pa + pb);
             const float delta = beta * (vj - pred);
-            float o = 0.0f;
+            float oa = 0.0f, ob = 0.0f;
 #pragma unroll
-            for (int r = 0; r < RS; ++r) {
-                sreg[r] += kr[r] * delta;
-                o += sreg[r] * qr[r];
+            for (int r = 0; r < RS; r += 2) {
+                sreg[r] = fmaf(kr[r], delta, sreg[r]);
+                sreg[r + 1] = fmaf(kr[r + 1], delta, sreg[r + 1]);
+                oa = fmaf(sreg[r], qr[r], oa);
+                ob = fmaf(sreg[r + 1], qr[r + 1], ob);
             }
-            o = lanes_sum<16>(o);
-            if (ig == 0 && active)
-                p.out[static_cast<size_t>(g0 + k) * p.out_stride + static_cast<size_t>(vh) * dv + j] = o * rdk;
+            const float o = lanes_sum<16>(oa + ob);
+            if (ig == k) my_o = o;
         }
+        if (active && ig < nt)
+            p.out[static_cast<size_t>(g0 + ig) * p.out_stride + static_cast<size_t>(vh) * dv + j] = my_o * rdk;
     }
 #pragma unroll
     for (int r = 0; r < RS; ++r)
