@@ -181,3 +181,10 @@ def test_selftest_entry_point():
     j = json.loads(buf.value.decode())
     assert st == 0 and j["pass"] is True and j["custom_backend_actual"] == "hip"
     assert all(r["pass"] for r in j["results"])
+    # the reference self-test's nine element-wise checks (vulkan_backend.cpp:1723-2022)
+    names = ["rmsnorm_vector", "rope_qk_vector", "silu_gate_mul_vector", "residual_add_vector", "gqa_decode_vector",
+             "linear_attention_conv1d_vector", "linear_attention_state_update_vector", "append_vector", "argmax_vector"]
+    assert [r["name"] for r in j["vector_results"]] == names
+    bad = [r for r in j["vector_results"] if not r["pass"]]
+    assert not bad, bad
+    assert j["wall_clock_ms"] > 0

@@ -3,6 +3,11 @@
   lib/libxqhip.so    hand-written gfx950 HIP kernels + the thin C ABI of include/xqhip.h
   lib/libxqwen35.so  C++ host runtime (Session / model / XQ4 reader) exporting the
                      reference C ABI of include/xqwen35.h; links libxqhip.so
+  bin/xq_host_quality_runner, bin/xq_benchmark
+                     the caller-side harness programs (csrc/tools), linked against
+                     lib/libxqwen35.so through the xqwen35.h ABI only (RUNPATH
+                     $ORIGIN/../lib, so LD_LIBRARY_PATH can put another build of
+                     that ABI behind them)
 
 Usage: python build.py [--jobs N] [--only hip|host]
 Compiles every time it is called (hipcc cross-compiles for gfx950 without a GPU).
@@ -19,7 +24,9 @@ ROOT = os.path.dirname(HERE)
 INCLUDE = os.path.join(ROOT, "include")
 HIP_SRC = os.path.join(HERE, "csrc", "hip")
 HOST_SRC = os.path.join(HERE, "csrc", "host")
+TOOL_SRC = os.path.join(HERE, "csrc", "tools")
 LIB = os.path.join(HERE, "lib")
+BIN = os.path.join(HERE, "bin")
 OBJ = os.path.join(HERE, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
@@ -91,6 +98,23 @@ def build_host(jobs):
     return out
 
 
+# tool -> the libraries it links besides libxqwen35.so
+TOOLS = {"xq_host_quality_runner": [], "xq_benchmark": ["-lxqhip"]}
+
+
+def build_tools(jobs):
+    os.makedirs(BIN, exist_ok=True)
+    tasks, outs = [], []
+    for name, extra in TOOLS.items():
+        out = os.path.join(BIN, name)
+        outs.append(out)
+        tasks.append(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", INCLUDE, "-I", TOOL_SRC,
+                      os.path.join(TOOL_SRC, name + ".cpp"), "-o", out, "-L", LIB, "-lxqwen35", *extra,
+                      "-Wl,--enable-new-dtags,-rpath,$ORIGIN/../lib"])
+    _compile_many(jobs, tasks)
+    return outs
+
+
 def build(jobs=None, only=None):
     jobs = jobs or min(8, os.cpu_count() or 1)
     os.makedirs(LIB, exist_ok=True)
@@ -101,6 +125,8 @@ def build(jobs=None, only=None):
         h = build_host(jobs)
         if h:
             built.append(h)
+    if only in (None, "tools"):
+        built.extend(build_tools(jobs))
     shutil.rmtree(OBJ, ignore_errors=True)
     return built
 
@@ -108,7 +134,7 @@ def build(jobs=None, only=None):
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
-    ap.add_argument("--only", choices=["hip", "host"], default=None)
+    ap.add_argument("--only", choices=["hip", "host", "tools"], default=None)
     a = ap.parse_args()
     for p in build(a.jobs, a.only):
         print(p)
