@@ -63,7 +63,8 @@ typedef struct xqhip_w4 {
     int32_t affine;
     int32_t layout;
     int32_t inexact_meta; /* scales/zeros not exactly representable in fp16 (TILED64) */
-    void* nib;            /* device nibbles                                       */
+    int32_t bits;         /* code width: 4 (xqhip_w4_upload), 3 or 2 (xqhip_wlb_upload) */
+    void* nib;            /* device codes                                         */
     void* meta;           /* device per-group metadata                            */
     uint64_t nib_bytes;
     uint64_t meta_bytes;
@@ -105,6 +106,20 @@ XQHIP_API int xqhip_event_elapsed_ms(void* start, void* stop, float* ms);
  * cols % 64 == 0, else GENERIC. */
 XQHIP_API int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols,
                               int group, int affine, xqhip_w4* out);
+/* 3- and 2-bit matrices (W3A16 / W2A16): the reference's low-bit format
+ * (QuantizedMatrix with bits 3 or 2, kernels/kernels.hpp:11-21; packed by
+ * quantizeLowBit, read by readBits / dequantizeValue, ref_gemv.cpp:10-30,
+ * 38-87): one LSB-first bitstream, code of (r, c) at bit (r * cols + c) * bits,
+ * no row padding; scales/zeros as for 4 bits.  Replaces the matrix side of
+ * gemvW3A16Neon / gemvW2A16Neon (arm64_neon/xq_gemv_w{3,2}a16_neon.cpp:6-8);
+ * the result works with xqhip_gemv_w4a16 and xqhip_gemv_w4a16_argmax (not
+ * with xqhip_gemm_w4a16).  group 64 with cols % 64 == 0 gives the TILED64
+ * layout (codes split into bit planes, fp16 metadata), anything else the
+ * GENERIC one (the bitstream as given, fp32 metadata).  The reference's
+ * per-row bias is always zero (quantizeLowBit, and no file format sets it)
+ * and is not carried. */
+XQHIP_API int xqhip_wlb_upload(const uint8_t* bitstream, const float* scales, const float* zeros, int rows, int cols,
+                               int group, int bits, int affine, xqhip_w4* out);
 XQHIP_API int xqhip_w4_free(xqhip_w4* w);
 /* Bytes the GEMV must read per call for this matrix (nibbles + metadata). */
 XQHIP_API uint64_t xqhip_w4_weight_bytes(const xqhip_w4* w);
@@ -128,7 +143,8 @@ typedef struct xqhip_prologue {
 } xqhip_prologue;
 
 /* y = W x, replacing gemvW4A16Neon
- * (customlib/kernels/generated/arm64_neon/xq_gemv_w4a16_neon.cpp:259-291).
+ * (customlib/kernels/generated/arm64_neon/xq_gemv_w4a16_neon.cpp:259-291), and
+ * gemvW3A16Neon / gemvW2A16Neon for matrices from xqhip_wlb_upload.
  * x: `cols` values of x_type, optionally normalised by `pro` (NULL = none).
  * y: `rows` values of y_type (EPI_SILU_PAIR: rows/2 values).  Inputs must not
  * alias outputs. */

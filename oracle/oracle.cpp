@@ -1000,6 +1000,29 @@ void orc_gemv_textbook(const uint8_t* packed, const float* scales, const float* 
     }
 }
 
+// W3A16 / W2A16 (and the 4-bit bitstream): gemvW3A16Neon / gemvW2A16Neon
+// (arm64_neon/xq_gemv_w{3,2}a16_neon.cpp:6-8) are gemvLowBitReference
+// (ref_gemv.cpp:98-106): per row, bias (zero) then per column in order
+// acc += dequantizeValue(r, c) * x[c], with the LSB-first bitstream reader.
+void orc_gemv_lowbit(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols, int group,
+                     int bits, int affine, const float* x, float* y) {
+    QMat m;
+    m.rows = rows;
+    m.cols = cols;
+    m.group = group;
+    m.bits = bits;
+    m.affine = affine != 0;
+    const size_t g_n = static_cast<size_t>(m.groups()) * rows;
+    m.packed.assign(packed, packed + (static_cast<size_t>(rows) * cols * bits + 7) / 8);
+    m.scales.assign(scales, scales + g_n);
+    m.zeros.assign(zeros, zeros + g_n);
+    for (int r = 0; r < rows; ++r) {
+        float acc = 0.0f;
+        for (int c = 0; c < cols; ++c) acc += dequant_one(m, r, c) * x[c];
+        y[r] = acc;
+    }
+}
+
 void orc_dequantize(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols, int group,
                     int affine, float* out) {
     const QMat m = make_qmat(packed, scales, zeros, rows, cols, group, affine);

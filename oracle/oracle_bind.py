@@ -27,6 +27,7 @@ _ORACLE_SIGS = {
     "orc_gemv_w4a16_argmax": (_i, _GEMV),
     "orc_gemv_textbook": (None, _GEMV),
     "orc_dequantize": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "orc_gemv_lowbit": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "orc_rmsnorm": (None, [_vp, _vp, _i, _f, _vp]),
     "orc_head_rms": (None, [_vp, _vp, _i, _i, _f]),
     "orc_l2norm_heads": (None, [_vp, _i, _i]),
@@ -66,6 +67,7 @@ _REF_SIGS = {
     "ref_gemv_w4a16_argmax": (_i, _GEMV),
     "ref_gemv_textbook": (None, _GEMV),
     "ref_quantize_lowbit": (None, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "ref_gemv_lowbit": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "ref_rmsnorm": (None, [_vp, _vp, _i, _f, _vp]),
     "ref_rope": (None, [_vp, _vp, _i, _i, _i, _f]),
     "ref_attention": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
@@ -150,6 +152,15 @@ def quantize_lowbit(w, rows, cols, bits=4, group=64, lib=None, fn="orc_quantize_
     zeros = np.empty(rows * g, np.float32)
     getattr(lib, fn)(p(w), rows, cols, bits, group, p(packed), p(scales), p(zeros))
     return Quantized(packed, scales, zeros, rows, cols, group, 0)
+
+
+def gemv_lowbit(q, bits, x, lib=None, fn="orc_gemv_lowbit"):
+    """y = W x for a bitstream matrix of `bits`-bit codes (gemvLowBitReference)."""
+    lib = lib or oracle()
+    x = f32(x)
+    y = np.empty(q.rows, np.float32)
+    getattr(lib, fn)(p(q.packed), p(q.scales), p(q.zeros), q.rows, q.cols, q.group, bits, q.affine, p(x), p(y))
+    return y
 
 
 def det_fill(n, scale):

@@ -50,6 +50,29 @@ void ref_gemv_textbook(const uint8_t* packed, const float* scales, const float* 
     xq::kernels::gemvLowBitReference(m, x, y);
 }
 
+// The reference's W3A16 / W2A16 kernels (and gemvLowBitReference for other widths)
+// on a bitstream matrix.
+void ref_gemv_lowbit(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols, int group,
+                     int bits, int affine, const float* x, float* y) {
+    xq::kernels::QuantizedMatrix m;
+    m.rows = rows;
+    m.cols = cols;
+    m.bits = bits;
+    m.group_size = group;
+    m.affine_asymmetric = affine != 0;
+    const size_t groups = static_cast<size_t>((cols + group - 1) / group) * rows;
+    m.packed.assign(packed, packed + (static_cast<size_t>(rows) * cols * bits + 7) / 8);
+    m.scales.assign(scales, scales + groups);
+    m.zeros.assign(zeros, zeros + groups);
+    m.bias.assign(static_cast<size_t>(rows), 0.0f);
+    if (bits == 3)
+        xq::kernels::gemvW3A16Neon(m, x, y);
+    else if (bits == 2)
+        xq::kernels::gemvW2A16Neon(m, x, y);
+    else
+        xq::kernels::gemvLowBitReference(m, x, y);
+}
+
 void ref_quantize_lowbit(const float* w, int rows, int cols, int bits, int group, uint8_t* packed_out,
                          float* scales_out, float* zeros_out) {
     const auto q = xq::kernels::quantizeLowBit(w, rows, cols, bits, group);

@@ -29,6 +29,14 @@
 //
 // Columns beyond 4096 are split over the waves of a block (one 4096-column chunk
 // per wave), whose partial row sums are combined through LDS in a fixed order.
+//
+// 3- and 2-bit codes (the reference's W3A16 / W2A16 bitstreams,
+// customlib/kernels/reference/ref_gemv.cpp:10-30, 77-106) run through the same
+// kernel: the upload splits each group's codes into bit planes laid out so that
+// one or two shift-and-mask steps rebuild exactly the eight signed-nibble words
+// (q | 8, i.e. q - 8 in signed 4-bit) the W4 layout stores, so staging,
+// metadata, epilogues and argmax are shared; only the bytes streamed per group
+// shrink (32 -> 24 -> 16).
 #include "xqhip_common.hpp"
 #include "xqhip_kernels.hpp"
 
@@ -382,8 +390,15 @@ struct WSrc {
     __amdgpu_buffer_rsrc_t nib, meta;
 };
 
+// Bytes of one TILED64 row: cols * BITS / 8 (cols % 64 == 0).
+template <int BITS>
+__host__ __device__ constexpr uint32_t tiled_row_bytes(int cols) {
+    return static_cast<uint32_t>(cols >> 3) * BITS;
+}
+
+template <int BITS>
 __device__ __forceinline__ WSrc make_wsrc(const uint8_t* nib, const uint32_t* meta, int rows, int cols) {
-    const uint32_t nib_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 1);
+    const uint32_t nib_bytes = static_cast<uint32_t>(rows) * tiled_row_bytes<BITS>(cols);
     const uint32_t meta_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 6) * 4u;
     WSrc s;
     s.nib = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(nib), 0, nib_bytes, kRsrcWord3);
@@ -393,23 +408,67 @@ __device__ __forceinline__ WSrc make_wsrc(const uint8_t* nib, const uint32_t* me
 
 __device__ __forceinline__ uint4 as_uint4(u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
 
-template <int R>
+// Row layout per 4096-column chunk c (64 groups, gcnt of them present), at
+// c * 512 * BITS bytes into the row:
+//   BITS 4: [gcnt x 16 B: bytes 0-15 of each group][gcnt x 16 B: bytes 16-31]
+//   BITS 3: [gcnt x 16 B: low-two-bit plane][gcnt x 8 B: high-bit plane]
+//   BITS 2: [gcnt x 16 B: two-bit plane]
+// so each load instruction of a wave reads one contiguous run.
+template <int R, int BITS>
 __device__ __forceinline__ void load_batch(WBatch<R>& wb, const WSrc& src, int r0, int rows, uint32_t row_bytes,
                                            int G, int c, int lane, int gcnt, bool has_group) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         const int row = r0 + i;
         const bool ok = has_group && row < rows;
-        const uint32_t off = static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(c * 2048 + lane * 16);
+        const uint32_t base = static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(c * 512 * BITS);
+        const uint32_t off = base + static_cast<uint32_t>(lane * 16);
         const uint32_t moff = (static_cast<uint32_t>(row) * static_cast<uint32_t>(G) + c * 64 + lane) * 4u;
         wb.a[i] = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off : kOutOfRange, 0, kLoadNT));
-        wb.b[i] = as_uint4(
-            __builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off + gcnt * 16 : kOutOfRange, 0, kLoadNT));
+        if constexpr (BITS == 4) {
+            wb.b[i] = as_uint4(
+                __builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off + gcnt * 16 : kOutOfRange, 0, kLoadNT));
+        } else if constexpr (BITS == 3) {
+            const uint32_t hoff = base + static_cast<uint32_t>(gcnt * 16 + lane * 8);
+            const u32x2 h = __builtin_amdgcn_raw_buffer_load_b64(src.nib, ok ? hoff : kOutOfRange, 0, kLoadNT);
+            wb.b[i] = make_uint4(h.x, h.y, 0u, 0u);
+        }
         wb.m[i] = __builtin_amdgcn_raw_buffer_load_b32(src.meta, ok ? moff : kOutOfRange, 0, kLoadNT);
     }
 }
 
-template <int NCH, int RG, int R, int EPI>
+// The eight signed-nibble words (column 8j + i in nibble i of word j, code q as
+// q | 8) of one group from its loaded bytes.
+//   BITS 2: plane word m holds columns 16m..16m+15: nibble i bits 0-1 = q(16m + i),
+//           bits 2-3 = q(16m + 8 + i)
+//   BITS 3: the low two bits as BITS 2; high-bit word k holds, at bit 4i + r,
+//           bit 2 of q(8 (4k + r) + i)
+template <int BITS>
+__device__ __forceinline__ void group_words(const uint4& a, const uint4& b, uint32_t (&wd)[8]) {
+    if constexpr (BITS == 4) {
+        wd[0] = a.x; wd[1] = a.y; wd[2] = a.z; wd[3] = a.w;
+        wd[4] = b.x; wd[5] = b.y; wd[6] = b.z; wd[7] = b.w;
+    } else {
+        const uint32_t v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            wd[2 * m] = (v[m] & 0x33333333u) | 0x88888888u;
+            wd[2 * m + 1] = ((v[m] >> 2) & 0x33333333u) | 0x88888888u;
+        }
+        if constexpr (BITS == 3) {
+            const uint32_t h[2] = {b.x, b.y};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t hk = h[j >> 2];
+                const int r = j & 3;
+                const uint32_t hb = r <= 2 ? (hk << (2 - r)) : (hk >> 1);
+                wd[j] |= hb & 0x44444444u;
+            }
+        }
+    }
+}
+
+template <int NCH, int RG, int R, int EPI, int BITS>
 __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     // x is not __restrict__: with it the compiler may move the staging loads of
     // x across the asm barrier of stage_x_lds (it would assume no aliasing)
@@ -427,9 +486,9 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     const int g = c * 64 + lane;
     const bool has_group = g < G;
     const int gcnt = min(64, G - c * 64);
-    const uint32_t row_bytes = static_cast<uint32_t>(cols) >> 1;
+    const uint32_t row_bytes = tiled_row_bytes<BITS>(cols);
     const int stride = grid * RG;
-    const WSrc src = make_wsrc(nib, meta, rows, cols);
+    const WSrc src = make_wsrc<BITS>(nib, meta, rows, cols);
 
     // activations first, then the first weight batches, then the staging
     // arithmetic while the weights stream in
@@ -439,12 +498,12 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     // one would stall its issue on the CU's in-flight memory requests, and the
     // staging waits behind it.
     stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, [&]() {
-        load_batch<R>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
         if constexpr (R == 1)
-            load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+            load_batch<R, BITS>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
     });
     if constexpr (R > 1)
-        load_batch<R>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
     __syncthreads();
     // this lane's group: kDigits x 8 words of digits, then e and G
     uint32_t xd[kDigits][8];
@@ -533,8 +592,8 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         if (r0 < rows) {
 #pragma unroll
             for (int i = 0; i < R; ++i) {
-                const uint32_t wd[8] = {cur.a[i].x, cur.a[i].y, cur.a[i].z, cur.a[i].w,
-                                        cur.b[i].x, cur.b[i].y, cur.b[i].z, cur.b[i].w};
+                uint32_t wd[8];
+                group_words<BITS>(cur.a[i], cur.b[i], wd);
                 int A[kDigits];
 #pragma unroll
                 for (int d = 0; d < kDigits; ++d) A[d] = 0;
@@ -577,9 +636,9 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     // and are skipped by process().
     for (int t = 0; t < trips; t += 2) {
         process(buf0, base, t);
-        load_batch<R>(buf0, src, (base + 2 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS>(buf0, src, (base + 2 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
         process(buf1, base + stride, t + 1);
-        load_batch<R>(buf1, src, (base + 3 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS>(buf1, src, (base + 3 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
         base += 2 * stride;
     }
     if constexpr (NCH > 1) {
@@ -608,7 +667,8 @@ template <int EPI>
 __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict__ nib,
                                                        const float* __restrict__ scales,
                                                        const float* __restrict__ zeros, int rows, int cols,
-                                                       int group, int affine, const void* __restrict__ x, int x_f16,
+                                                       int group, int affine, int bits, uint64_t nib_bytes,
+                                                       const void* __restrict__ x, int x_f16,
                                                        Prologue pro, void* __restrict__ y, int y_f16,
                                                        uint64_t* __restrict__ partial) {
     __shared__ float red[32];
@@ -634,8 +694,18 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
                 const int n = min(group, cols - c0);
                 float cd = 0.0f, gs = 0.0f;
                 for (int c = c0; c < c0 + n; ++c) {
-                    const uint8_t b = nib[static_cast<size_t>(row) * row_bytes + (c >> 1)];
-                    const float q = static_cast<float>((c & 1) ? (b >> 4) : (b & 0x0f));
+                    uint32_t code;
+                    if (bits == 4) {
+                        const uint8_t b = nib[static_cast<size_t>(row) * row_bytes + (c >> 1)];
+                        code = (c & 1) ? (b >> 4) : (b & 0x0f);
+                    } else {
+                        // LSB-first bitstream without row padding (ref_gemv.cpp:10-18, 77-81)
+                        const uint64_t bit = (static_cast<uint64_t>(row) * cols + c) * bits;
+                        const uint64_t byte = bit >> 3;
+                        const uint32_t lo = nib[byte], hi = byte + 1 < nib_bytes ? nib[byte + 1] : 0u;
+                        code = ((lo | (hi << 8)) >> (bit & 7)) & ((1u << bits) - 1u);
+                    }
+                    const float q = static_cast<float>(code);
                     const float xv = prologue_apply(load_act(x, x_f16, c), c, pro, inv_lds);
                     cd += q * xv;
                     gs += xv;
@@ -710,14 +780,14 @@ static int device_cus() {
     return cache[dev];
 }
 
-template <int NCH, int R, int EPI>
+template <int NCH, int R, int EPI, int BITS>
 static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
     constexpr int RG = kRowGroups<NCH>;
     const int G = p.cols >> 6;
     const size_t stage_lds = static_cast<size_t>(G) * kStageRecord * sizeof(uint4);
     // occupancy and the LDS limit are set for the largest partial-sum area
     const size_t lds_max = stage_lds + (NCH > 1 ? sizeof(float) * kMaxDeferredPartials : 0);
-    const auto fn = reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI>);
+    const auto fn = reinterpret_cast<const void*>(&gemv_w4_tiled<NCH, RG, R, EPI, BITS>);
     if (lds_max > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
         const hipError_t e =
             hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max));
@@ -739,7 +809,7 @@ static hipError_t launch_tiled_t(const GemvLaunch& p, hipStream_t s) {
         const int slots = batches_of(trips) < kSlots ? batches_of(trips) : kSlots;
         lds += sizeof(float) * static_cast<size_t>(slots) * RG * NCH * R;
     }
-    hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
+    hipLaunchKernelGGL((gemv_w4_tiled<NCH, RG, R, EPI, BITS>), dim3(blocks), dim3(64 * NCH * RG), lds, s, p.nib,
                        static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.x, p.x_f16, p.pro, p.y,
                        p.y_f16, p.partial, blocks);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
@@ -764,34 +834,52 @@ static int choose_rows_per_wave(const GemvLaunch& p) {
             best_r = r;
         }
     }
+    // 3- and 2-bit rows are shorter: when two rows per wave still give every
+    // block work and cost at most 5 % more, they stream faster (measured on the
+    // 4096x12288, 24576x4096 and 248320x4096 shapes)
+    if (p.bits != 4 && best_r == 1) {
+        const int units2 = (p.rows + 2 * RG - 1) / (2 * RG);
+        if (units2 >= cap && ((units2 + cap - 1) / cap) * 2 * 20 <= best_cost * 21) best_r = 2;
+    }
     return best_r;
 }
 
-template <int NCH, int EPI>
+template <int NCH, int EPI, int BITS>
 static hipError_t launch_tiled_epi(const GemvLaunch& p, hipStream_t s) {
     switch (choose_rows_per_wave<NCH>(p)) {
         case 1:
-            if constexpr (EPI != EPI_SILU) return launch_tiled_t<NCH, 1, EPI>(p, s);
+            if constexpr (EPI != EPI_SILU) return launch_tiled_t<NCH, 1, EPI, BITS>(p, s);
             return hipErrorInvalidValue;
-        case 2: return launch_tiled_t<NCH, 2, EPI>(p, s);
+        case 2: return launch_tiled_t<NCH, 2, EPI, BITS>(p, s);
         default:
-            if constexpr (EPI != EPI_ARGMAX) return launch_tiled_t<NCH, 4, EPI>(p, s);
+            if constexpr (EPI != EPI_ARGMAX) return launch_tiled_t<NCH, 4, EPI, BITS>(p, s);
             return hipErrorInvalidValue;
     }
 }
 
-template <int NCH>
+template <int NCH, int BITS>
 static hipError_t launch_tiled_nch(const GemvLaunch& p, hipStream_t s) {
     if (!stage_supported(p.cols, p.pro)) return hipErrorInvalidValue;
     // buffer-resource offsets are 32-bit and kOutOfRange must lie past the end
-    if (static_cast<uint64_t>(p.rows) * static_cast<uint64_t>(p.cols / 2) >= kOutOfRange) return hipErrorInvalidValue;
+    if (static_cast<uint64_t>(p.rows) * tiled_row_bytes<BITS>(p.cols) >= kOutOfRange) return hipErrorInvalidValue;
     switch (p.epi) {
-        case EPI_STORE: return launch_tiled_epi<NCH, EPI_STORE>(p, s);
-        case EPI_ADD: return launch_tiled_epi<NCH, EPI_ADD>(p, s);
-        case EPI_SILU: return launch_tiled_epi<NCH, EPI_SILU>(p, s);
-        case EPI_ARGMAX: return launch_tiled_epi<NCH, EPI_ARGMAX>(p, s);
+        case EPI_STORE: return launch_tiled_epi<NCH, EPI_STORE, BITS>(p, s);
+        case EPI_ADD: return launch_tiled_epi<NCH, EPI_ADD, BITS>(p, s);
+        case EPI_SILU: return launch_tiled_epi<NCH, EPI_SILU, BITS>(p, s);
+        case EPI_ARGMAX: return launch_tiled_epi<NCH, EPI_ARGMAX, BITS>(p, s);
     }
     return hipErrorInvalidValue;
+}
+
+template <int BITS>
+static hipError_t launch_tiled_bits(const GemvLaunch& p, hipStream_t s) {
+    switch (((p.cols >> 6) + 63) / 64) {
+        case 1: return launch_tiled_nch<1, BITS>(p, s);
+        case 2: return launch_tiled_nch<2, BITS>(p, s);
+        case 3: return launch_tiled_nch<3, BITS>(p, s);
+        case 4: return launch_tiled_nch<4, BITS>(p, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int EPI>
@@ -808,20 +896,17 @@ static hipError_t launch_generic_t(const GemvLaunch& p, hipStream_t s) {
     const int G = (p.cols + p.group - 1) / p.group;
     const float* zr = sc + static_cast<size_t>(p.rows) * G;
     hipLaunchKernelGGL((gemv_w4_generic<EPI>), dim3(blocks), dim3(kThreads), 0, s, p.nib, sc, zr, p.rows, p.cols,
-                       p.group, p.affine, p.x, p.x_f16, p.pro, p.y, p.y_f16, p.partial);
+                       p.group, p.affine, p.bits, p.nib_bytes, p.x, p.x_f16, p.pro, p.y, p.y_f16, p.partial);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     return EPI == EPI_ARGMAX ? launch_argmax_finish(p, blocks, s) : hipSuccess;
 }
 
 hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s) {
     if (p.layout == 0) {
-        const int G = p.cols >> 6;
-        const int nch = (G + 63) / 64;
-        switch (nch) {
-            case 1: return launch_tiled_nch<1>(p, s);
-            case 2: return launch_tiled_nch<2>(p, s);
-            case 3: return launch_tiled_nch<3>(p, s);
-            case 4: return launch_tiled_nch<4>(p, s);
+        switch (p.bits) {
+            case 4: return launch_tiled_bits<4>(p, s);
+            case 3: return launch_tiled_bits<3>(p, s);
+            case 2: return launch_tiled_bits<2>(p, s);
             default: return hipErrorInvalidValue;
         }
     }

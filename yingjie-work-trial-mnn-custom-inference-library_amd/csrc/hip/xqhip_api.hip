@@ -197,6 +197,7 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
     out->cols = cols;
     out->group = group;
     out->affine = affine ? 1 : 0;
+    out->bits = 4;
     const size_t row_bytes = (static_cast<size_t>(cols) + 1) / 2;
     const int G = (cols + group - 1) / group;
     const bool tiled = group == 64 && cols % 64 == 0 && G <= 256;
@@ -262,6 +263,88 @@ int xqhip_w4_free(xqhip_w4* w) {
     return rc ? rc : rc2;
 }
 
+// fp16 (scale, zero) pairs of the TILED64 layout; returns the count of inexact values.
+static int pack_meta_f16(const float* scales, const float* zeros, size_t n, std::vector<uint32_t>* out) {
+    out->resize(n);
+    int inexact = 0;
+    for (size_t i = 0; i < n; ++i) {
+        bool e1, e2;
+        const uint16_t s = f32_to_f16_bits(scales[i], &e1);
+        const uint16_t z = f32_to_f16_bits(zeros[i], &e2);
+        inexact += (!e1) + (!e2);
+        (*out)[i] = static_cast<uint32_t>(s) | (static_cast<uint32_t>(z) << 16);
+    }
+    return inexact;
+}
+
+static int upload_pair(xqhip_w4* out, const void* nib, const void* meta) {
+    if (int rc = xqhip_malloc(&out->nib, out->nib_bytes)) return rc;
+    if (int rc = xqhip_malloc(&out->meta, out->meta_bytes)) {
+        xqhip_free(out->nib);
+        out->nib = nullptr;
+        return rc;
+    }
+    if (int rc = check(hipMemcpy(out->nib, nib, out->nib_bytes, hipMemcpyHostToDevice), "upload codes")) return rc;
+    return check(hipMemcpy(out->meta, meta, out->meta_bytes, hipMemcpyHostToDevice), "upload metadata");
+}
+
+int xqhip_wlb_upload(const uint8_t* bitstream, const float* scales, const float* zeros, int rows, int cols, int group,
+                     int bits, int affine, xqhip_w4* out) {
+    if (!bitstream || !scales || !zeros || !out || rows <= 0 || cols <= 0 || group <= 0 || (bits != 2 && bits != 3))
+        return fail(XQHIP_EINVAL, "xqhip_wlb_upload: bad arguments (rows=%d cols=%d group=%d bits=%d)", rows, cols,
+                    group, bits);
+    std::memset(out, 0, sizeof(*out));
+    out->rows = rows;
+    out->cols = cols;
+    out->group = group;
+    out->affine = affine ? 1 : 0;
+    out->bits = bits;
+    const int G = (cols + group - 1) / group;
+    const size_t n_meta = static_cast<size_t>(rows) * G;
+    const size_t total_bytes = (static_cast<size_t>(rows) * cols * bits + 7) / 8;
+    if (!(group == 64 && cols % 64 == 0 && G <= 256)) {
+        // GENERIC: the bitstream as it is, fp32 scales then zeros
+        out->layout = XQHIP_LAYOUT_GENERIC;
+        out->nib_bytes = total_bytes;
+        std::vector<float> meta(2 * n_meta);
+        std::memcpy(meta.data(), scales, n_meta * 4);
+        std::memcpy(meta.data() + n_meta, zeros, n_meta * 4);
+        out->meta_bytes = meta.size() * 4;
+        return upload_pair(out, bitstream, meta.data());
+    }
+    // TILED64: per 4096-column chunk, the groups' 16-byte two-bit planes, then (3 bits)
+    // their 8-byte high-bit planes; the word layout is the one group_words() expands
+    out->layout = XQHIP_LAYOUT_TILED64;
+    const size_t row_bytes = static_cast<size_t>(cols / 8) * bits;
+    out->nib_bytes = row_bytes * rows;
+    std::vector<uint8_t> dev(out->nib_bytes, 0);
+    auto code = [&](int r, int c) {
+        const size_t bit = (static_cast<size_t>(r) * cols + c) * bits;
+        const uint32_t lo = bitstream[bit >> 3], hi = (bit >> 3) + 1 < total_bytes ? bitstream[(bit >> 3) + 1] : 0u;
+        return ((lo | (hi << 8)) >> (bit & 7)) & ((1u << bits) - 1u);
+    };
+    for (int r = 0; r < rows; ++r) {
+        uint8_t* row = dev.data() + static_cast<size_t>(r) * row_bytes;
+        for (int g = 0; g < G; ++g) {
+            const int ch = g / 64, l = g % 64, gcnt = std::min(64, G - ch * 64);
+            uint8_t* chunk = row + static_cast<size_t>(ch) * 512 * bits;
+            uint32_t plane[4] = {0, 0, 0, 0}, high[2] = {0, 0};
+            for (int j = 0; j < 8; ++j)      // word j: columns 8j .. 8j+7 of the group
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t q = code(r, g * 64 + 8 * j + i);
+                    plane[j >> 1] |= (q & 3u) << (4 * i + 2 * (j & 1));
+                    high[j >> 2] |= ((q >> 2) & 1u) << (4 * i + (j & 3));
+                }
+            std::memcpy(chunk + l * 16, plane, 16);
+            if (bits == 3) std::memcpy(chunk + gcnt * 16 + l * 8, high, 8);
+        }
+    }
+    std::vector<uint32_t> meta;
+    out->inexact_meta = pack_meta_f16(scales, zeros, n_meta, &meta);
+    out->meta_bytes = meta.size() * 4;
+    return upload_pair(out, dev.data(), meta.data());
+}
+
 uint64_t xqhip_w4_weight_bytes(const xqhip_w4* w) { return w ? w->nib_bytes + w->meta_bytes : 0; }
 
 static int validate_w4(const xqhip_w4* w, const char* who) {
@@ -269,6 +352,8 @@ static int validate_w4(const xqhip_w4* w, const char* who) {
         return fail(XQHIP_EINVAL, "%s: matrix is not uploaded", who);
     if (w->layout == XQHIP_LAYOUT_TILED64 && (w->group != 64 || w->cols % 64 != 0 || w->cols / 64 > 256))
         return fail(XQHIP_EINVAL, "%s: inconsistent TILED64 matrix %dx%d g%d", who, w->rows, w->cols, w->group);
+    if (w->bits != 4 && w->bits != 3 && w->bits != 2)
+        return fail(XQHIP_EINVAL, "%s: unsupported code width %d", who, w->bits);
     return XQHIP_OK;
 }
 
@@ -314,6 +399,8 @@ static xqhip::GemvLaunch base_launch(const xqhip_w4* w, const void* x, int x_typ
     p.group = w->group;
     p.affine = w->affine;
     p.layout = w->layout;
+    p.bits = w->bits;
+    p.nib_bytes = w->nib_bytes;
     p.x = x;
     p.x_f16 = x_type == XQHIP_F16;
     p.pro = make_prologue(pro);
@@ -522,6 +609,7 @@ size_t xqhip_gemm_workspace_bytes(int m, int cols) { return m > 0 && cols > 0 ? 
 int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro, int ld_gate,
                      float* y, int ldy, int epilogue, void* workspace, void* stream) {
     if (int rc = validate_w4(w, "xqhip_gemm_w4a16")) return rc;
+    if (w->bits != 4) return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: 4-bit matrices only (got %d bits)", w->bits);
     if (int rc = validate_prologue(pro, w->cols, "xqhip_gemm_w4a16")) return rc;
     if (!x || !y || !workspace || m <= 0 || ldx < w->cols)
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: bad vectors (m=%d ldx=%d)", m, ldx);

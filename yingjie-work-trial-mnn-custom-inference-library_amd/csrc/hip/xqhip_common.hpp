@@ -9,6 +9,7 @@ namespace xqhip {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 

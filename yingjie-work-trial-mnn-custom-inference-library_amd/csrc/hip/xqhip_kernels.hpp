@@ -23,6 +23,8 @@ struct GemvLaunch {
     const uint8_t* nib;
     const void* meta;
     int rows, cols, group, affine, layout;
+    int bits;            // 4, 3 or 2
+    uint64_t nib_bytes;  // code bytes (the GENERIC bitstream's bound)
     const void* x;
     int x_f16;
     Prologue pro;

@@ -27,7 +27,7 @@ class W4(ctypes.Structure):
     """Mirror of xqhip_w4 (include/xqhip.h)."""
     _fields_ = [("rows", ctypes.c_int32), ("cols", ctypes.c_int32), ("group", ctypes.c_int32),
                 ("affine", ctypes.c_int32), ("layout", ctypes.c_int32), ("inexact_meta", ctypes.c_int32),
-                ("nib", c_void_p), ("meta", c_void_p), ("nib_bytes", c_uint64), ("meta_bytes", c_uint64)]
+                ("bits", ctypes.c_int32), ("nib", c_void_p), ("meta", c_void_p), ("nib_bytes", c_uint64), ("meta_bytes", c_uint64)]
 
 
 class Prologue(ctypes.Structure):
@@ -57,6 +57,8 @@ _HIP_SIGS = {
     "xqhip_event_record": (c_int, [c_void_p, c_void_p]),
     "xqhip_event_elapsed_ms": (c_int, [c_void_p, c_void_p, ctypes.POINTER(c_float)]),
     "xqhip_w4_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, ctypes.POINTER(W4)]),
+    "xqhip_wlb_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                 ctypes.POINTER(W4)]),
     "xqhip_w4_free": (c_int, [ctypes.POINTER(W4)]),
     "xqhip_w4_weight_bytes": (c_uint64, [ctypes.POINTER(W4)]),
     "xqhip_gemv_w4a16": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_int, c_int, c_void_p]),
@@ -193,15 +195,20 @@ class DeviceBuffer:
 
 
 class DeviceW4:
-    """A W4A16 matrix uploaded into the device layout (xqhip_w4_upload)."""
+    """A W4A16 matrix uploaded into the device layout (xqhip_w4_upload), or with
+    bits 3 / 2 a W3A16 / W2A16 bitstream matrix (xqhip_wlb_upload)."""
 
-    def __init__(self, packed, scales, zeros, rows, cols, group=64, affine=0):
+    def __init__(self, packed, scales, zeros, rows, cols, group=64, affine=0, bits=4):
         packed = np.ascontiguousarray(packed, dtype=np.uint8)
         scales = np.ascontiguousarray(scales, dtype=np.float32)
         zeros = np.ascontiguousarray(zeros, dtype=np.float32)
         self.w = W4()
-        ck(hip().xqhip_w4_upload(ptr(packed), ptr(scales), ptr(zeros), rows, cols, group, affine,
-                                 ctypes.byref(self.w)))
+        if bits == 4:
+            ck(hip().xqhip_w4_upload(ptr(packed), ptr(scales), ptr(zeros), rows, cols, group, affine,
+                                     ctypes.byref(self.w)))
+        else:
+            ck(hip().xqhip_wlb_upload(ptr(packed), ptr(scales), ptr(zeros), rows, cols, group, bits, affine,
+                                      ctypes.byref(self.w)))
 
     @property
     def ref(self):
