@@ -733,6 +733,15 @@ static bool load_model(Model& M, const std::string& dir) {
     M.lk_dim = M.lk_hd * M.lk_n;
     M.lv_dim = M.lv_hd * M.lv_n;
     M.conv_dim = 2 * M.lk_dim + M.lv_dim;
+    // The reference sizes its query, gate and attention-output buffers by the
+    // hidden size (custom_model.cpp:481-486), so a wider attention or linear
+    // value dimension overruns them there; refuse such a model instead.
+    if (M.nq * M.hd > M.hidden || M.lv_dim > M.hidden) {
+        M.err = "attention width " + std::to_string(M.nq * M.hd) + " / linear value width " +
+                std::to_string(M.lv_dim) + " exceeds hidden_size " + std::to_string(M.hidden) +
+                " (the reference's buffers are sized by hidden_size)";
+        return false;
+    }
     M.eps = json_float(js, "rms_norm_eps", M.eps);
     M.theta = json_float(js, "rope_theta", M.theta);
     const int n_layers = json_int(js, "num_hidden_layers", 32);

@@ -16,7 +16,7 @@ import pytest
 
 import oracle_bind as ob
 import xqbind as xb
-from tiny_model import SMALL, write_tiny_model
+from tiny_model import QWEN35_9B_HEADS, SMALL, write_tiny_model
 
 pytestmark = pytest.mark.gpu
 ATOL, RTOL = 1e-2, 1e-3
@@ -149,6 +149,43 @@ def test_batched_prefill_matches_oracle(small_dir, n_prompt, monkeypatch):
     assert "prefill_gemm_w4a16_mfma" in runs["batched"] and "prefill_gemm_w4a16_mfma" not in runs["serial"]
     rows = json.loads(runs["batched"])["rows"]
     assert next(r for r in rows if r["name"] == "prefill_token_custom")["calls"] == n_prompt
+
+
+@pytest.fixture(scope="module")
+def heads9b_dir(tmp_path_factory):
+    d = str(tmp_path_factory.mktemp("heads9b"))
+    xb.write_synth_model(d, **QWEN35_9B_HEADS)
+    return d
+
+
+@pytest.mark.parametrize("n_prompt", [12, 80])
+def test_qwen35_9b_head_layout_matches_oracle(heads9b_dir, n_prompt):
+    """The Qwen3.5-9B head layout (16 q / 4 kv heads of 256, rotary 64, gated
+    q_proj; 16 key / 32 value heads of 128 in the linear layers): batched
+    prefill (80 tokens: two 64-token attention chunks), decode attention at
+    head_dim 256 and the 2:1 value/key head sharing, end to end against the
+    oracle under the same rules as test_generate_matches_oracle."""
+    prompt = [int(t) for t in np.random.default_rng(100 + n_prompt).integers(0, 4096, n_prompt)]
+    n_new = 8
+    print(f"9B head layout, {n_prompt}-token prompt", flush=True)
+    want, margins, hiddens = oracle_run(heads9b_dir, prompt, n_new)
+    s = xb.Session(heads9b_dir, xb.options())
+    assert s.status == xb.XQ_OK
+    st, m = s.prefill(prompt)
+    assert st == 0 and m.prompt_tokens == n_prompt
+    close(s.hidden()[1], hiddens[0], f"hidden after a {n_prompt}-token prefill")
+    got = []
+    for i in range(n_new):
+        st, tok, m = s.decode_one()
+        assert st == 0
+        got.append(tok)
+        if got == want[: i + 1]:
+            close(s.hidden()[1], hiddens[i + 1], f"hidden after decode step {i}")
+    steps = compare_tokens(got, want, margins)
+    assert steps >= min(4, n_new) or min(margins[:4]) <= MARGIN
+    st, info = s.json("xq_get_backend_info")
+    assert "full_custom_decode=true" in info and "fallback_ops=none" in info
+    s.close()
 
 
 def test_debug_json_and_hidden_buffer_rules(small_dir):

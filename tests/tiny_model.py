@@ -87,3 +87,15 @@ def write_tiny_model(d):
 SMALL = dict(hidden_size=512, intermediate_size=960, vocab_size=4096, num_layers=4, num_attention_heads=2,
              num_key_value_heads=1, head_dim=128, linear_key_head_dim=128, linear_value_head_dim=128,
              linear_num_key_heads=1, linear_num_value_heads=2, seed=7)
+
+
+# The head layout of Qwen3.5-9B (custom_model.hpp:101-104: 16 query heads, 4
+# kv heads, head_dim 256, gated q_proj; partial rotary 0.25 -> 64 dims;
+# linear attention 16 key heads and 32 value heads of 128,
+# docs/model_facts.md:17-21) with its hidden size 4096 (the reference sizes
+# its attention buffers by the hidden size, custom_model.cpp:481-486) and a
+# small MLP and vocabulary, so the oracle runs it in seconds.
+QWEN35_9B_HEADS = dict(hidden_size=4096, intermediate_size=1024, vocab_size=4096, num_layers=4,
+                       num_attention_heads=16, num_key_value_heads=4, head_dim=256, partial_rotary_factor=0.25,
+                       gated_q_proj=1, linear_key_head_dim=128, linear_value_head_dim=128, linear_num_key_heads=16,
+                       linear_num_value_heads=32, seed=31)
