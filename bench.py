@@ -10,6 +10,11 @@ Prints ONE JSON line.  Workloads (--workload):
   mlp    decode MLP block, hidden 4096 -> 12288 -> 4096, W4A16 g64: fused
          RMSNorm + gate/up GEMV + SiLU*up, then down GEMV + residual add.
          value = algorithmic HBM GB/s of the block (the GEMV bandwidth metric).
+  gemv-sweep
+         every decode-step projection shape of the 9B-shaped model (with the
+         prologue and epilogue it runs with in the model) for 4-, 3- and 2-bit
+         codes (--bits), n back-to-back launches each on rotated weight copies;
+         value = algorithmic HBM GB/s of the gate/up launch at the first width.
 A step is one pass of the workload over inputs already resident in HBM.  Weight
 copies are rotated so the working set (> 2x the 256 MB Infinity Cache) is
 streamed from HBM on every step.
@@ -185,6 +190,104 @@ def cpu_baseline_mlp(inp, hidden, inter, step_bytes, seconds):
 
 
 # ---------------------------------------------------------------------------
+# per-projection GEMV timing: the decode step's matrices at their real shapes,
+# each with the prologue and epilogue it runs with in the model
+# ---------------------------------------------------------------------------
+# (name, rows, cols, prologue, epilogue); rows of gate/up are the interleaved
+# (gate_i, up_i) pairs, in_proj the fused projections of each layer kind
+PROJECTIONS = [
+    ("gate_up", 24576, 4096, "rms", "silu"),
+    ("down", 4096, 12288, "none", "add"),
+    ("in_proj_linear", 12352, 4096, "rms", "store"),   # qkv 8192 | a 32 | b 32 | z 4096
+    ("in_proj_full", 10240, 4096, "rms", "store"),     # q 8192 (gated) | k 1024 | v 1024
+    ("out_proj_linear", 4096, 4096, "gated", "add"),   # gated head RMSNorm prologue
+    ("o_proj_full", 4096, 4096, "none", "add"),
+    ("lm_head", 248320, 4096, "rms", "argmax"),
+]
+# launches of each projection per decode step of the 9B-shaped model (24 linear + 8 full layers)
+PROJ_PER_STEP = {"gate_up": 32, "down": 32, "in_proj_linear": 24, "in_proj_full": 8, "out_proj_linear": 24,
+                 "o_proj_full": 8, "lm_head": 1}
+
+
+def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6):
+    """Average duration of n back-to-back launches of one projection (HIP events
+    on the default stream around the loop), weights rotated over enough copies
+    (> 2x the 256 MB last-level cache) that every launch streams from HBM.
+    Algorithmic bytes = codes + fp16 (scale, zero) per group + x + y."""
+    hip = xb.hip()
+    rng = np.random.default_rng(rows + cols + bits)
+    g = cols // 64
+    packed = rng.integers(0, 256, (rows * cols * bits + 7) // 8, dtype=np.uint8)
+    scales = np.abs(rng.normal(0.0, 0.02, rows * g)).astype(np.float16).astype(np.float32)
+    zeros = np.full(rows * g, float(1 << (bits - 1)), np.float32)
+    one = w4_bytes(rows, cols) if bits == 4 else rows * cols * bits // 8 + rows * g * 4
+    ncopy = max(2, min(64, int(np.ceil(budget / one))))
+    copies = [xb.DeviceW4(packed, scales, zeros, rows, cols, 64, 0, bits=bits) for _ in range(ncopy)]
+    x = xb.DeviceBuffer.from_array(rng.normal(0, 1, cols).astype(np.float32))
+    nw = xb.DeviceBuffer.from_array(rng.normal(1.0, 0.1, cols).astype(np.float32))
+    hw = xb.DeviceBuffer.from_array(rng.normal(1.0, 0.1, 128).astype(np.float32))
+    z = xb.DeviceBuffer.from_array(rng.normal(0, 1, cols).astype(np.float32))
+    out_n = rows // 2 if epi == "silu" else rows
+    y = xb.DeviceBuffer(out_n * 4)
+    y.zero()
+    ws = xb.DeviceBuffer(hip.xqhip_argmax_workspace_bytes(rows))
+    idx, val = xb.DeviceBuffer(4), xb.DeviceBuffer(4)
+    pro = {"none": None, "rms": xb.prologue(xb.PRO_RMS, nw, eps=1e-6),
+           "gated": xb.prologue(xb.PRO_GATED_HEAD, hw, z, head_dim=128, eps=1e-6)}[pro_kind]
+    pro_ref = ctypes.byref(pro) if pro is not None else None
+    epi_code = {"store": xb.EPI_STORE, "add": xb.EPI_ADD, "silu": xb.EPI_SILU_PAIR}.get(epi)
+
+    def launch(i):
+        w = copies[i % ncopy].ref
+        if epi == "argmax":
+            xb.ck(hip.xqhip_gemv_w4a16_argmax(w, x.ptr, xb.F32, pro_ref, ws.ptr, idx.ptr, val.ptr, None))
+        else:
+            xb.ck(hip.xqhip_gemv_w4a16(w, x.ptr, xb.F32, pro_ref, y.ptr, xb.F32, epi_code, None))
+
+    if name == "lm_head":
+        n = min(n, 50)
+    for i in range(max(10, 2 * ncopy)):
+        launch(i)
+    ev = Events()
+    ev.start()
+    for i in range(n):
+        launch(i)
+    us = ev.stop_ms() * 1e3 / n
+    algo = copies[0].weight_bytes() + cols * 4 + (rows // 2 if epi == "silu" else rows) * 4 * (2 if epi == "add" else 1)
+    if epi == "argmax":
+        algo = copies[0].weight_bytes() + cols * 4
+    for c in copies:
+        c.free()
+    return {"name": name, "bits": bits, "rows": rows, "cols": cols, "prologue": pro_kind, "epilogue": epi,
+            "launches": n, "weight_copies": ncopy, "avg_us": round(us, 2), "bytes": int(algo),
+            "GBps": round(algo / us / 1e3, 1), "frac": round(algo / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+
+
+def projection_table(bits=4, n=200):
+    rows = []
+    for name, r, c, pro, epi in PROJECTIONS:
+        rows.append(time_projection(name, r, c, pro, epi, bits=bits, n=n))
+        t = rows[-1]
+        log(f"[bench] W{bits} {name:16s} {r}x{c} {t['avg_us']:8.2f} us {t['bytes'] / 1e6:8.2f} MB "
+            f"{t['GBps']:7.1f} GB/s frac {t['frac']:.3f}")
+    return rows
+
+
+def bench_gemv_sweep(args):
+    table = []
+    for bits in args.bits:
+        table.extend(projection_table(bits, n=args.steps))
+    first = table[0]
+    return {"metric": METRIC, "value": first["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": 0, "ms_per_step": round(first["avg_us"] / 1e3, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "u4xf16->f32", "data": "synthetic",
+            "config": {"workload": "decode-step projection GEMVs of the 9B-shaped model, batch 1, g64, "
+                                   f"{args.steps} back-to-back launches per shape on rotated weights",
+                       "bits": args.bits},
+            "projections": table}
+
+
+# ---------------------------------------------------------------------------
 # workload: end-to-end batch-1 decode of the 9B-shaped model
 # ---------------------------------------------------------------------------
 MODEL_DIR = os.environ.get("XQ_BENCH_MODEL_DIR", "/tmp/xq_synth_9b_w4a16_g64")
@@ -197,34 +300,6 @@ MODEL_DIR = os.environ.get("XQ_BENCH_MODEL_DIR", "/tmp/xq_synth_9b_w4a16_g64")
 # ---------------------------------------------------------------------------
 PMC_COPY_BYTES = 64 << 20
 GATE_UP_KERNEL = "gemv_w4_tiled<1, 12, 2, 2, 4>"  # NCH=1, 12 row groups, 2 rows per wave, SiLU pair, 4-bit codes
-
-
-def time_gate_up_kernel(n=200, ncopy=8):
-    """Average duration of the gate/up GEMV kernel (24576x4096, RMSNorm prologue,
-    SiLU*up epilogue) over n back-to-back launches on the default stream, HIP
-    events around the loop; weights rotated over ncopy copies (> 2x the 256 MB
-    last-level cache) so every launch streams from HBM."""
-    hidden, inter = 4096, 12288
-    hip = xb.hip()
-    inp = mlp_inputs(hidden, inter)
-    copies = [xb.DeviceW4(*inp["gu"], 2 * inter, hidden) for _ in range(ncopy)]
-    nw = xb.DeviceBuffer.from_array(inp["norm_w"])
-    h = xb.DeviceBuffer.from_array(inp["h"])
-    ffn = xb.DeviceBuffer(inter * 4)
-    pro = xb.prologue(xb.PRO_RMS, nw, eps=1e-6)
-    pro_ref = ctypes.byref(pro)
-
-    def launch(i):
-        xb.ck(hip.xqhip_gemv_w4a16(copies[i % ncopy].ref, h.ptr, xb.F32, pro_ref, ffn.ptr, xb.F32,
-                                   xb.EPI_SILU_PAIR, None))
-
-    for i in range(20):
-        launch(i)
-    ev = Events()
-    ev.start()
-    for i in range(n):
-        launch(i)
-    return ev.stop_ms() / n
 
 
 def pmc_probe(args):
@@ -332,11 +407,15 @@ def bench_decode(args):
     for _ in range(args.warmup):
         st, tok, m = sess.decode_one()
         assert st == 0
-    # timed: fresh prefill (untimed), then exactly K decode steps
+    # timed: fresh prefill and the first decode step after it (untimed: that
+    # step launches its kernels one by one with per-op events for the kernel
+    # trace), then exactly K decode steps, each a pair of captured graphs
     assert sess.lib.xq_reset(sess.h) == 0
     st, m = sess.prefill(prompt)
     assert st == 0, m.error
     prefill_ms = m.prefill_ms
+    st, tok, m = sess.decode_one()
+    assert st == 0, m.error
     xb.ck(xb.hip().xqhip_device_synchronize())
     toks = []
     t0 = time.perf_counter()
@@ -359,8 +438,11 @@ def bench_decode(args):
     bytes_lm = w4_bytes(248320, hidden) + hidden * 4
     info = sess.json("xq_get_backend_info")[1]
     wbytes = int(info.split("weight_bytes_per_token=")[1].split(";")[0]) if "weight_bytes_per_token=" in info else 0
-    t_gu = time_gate_up_kernel()
+    proj = projection_table(4, n=200)
+    t_gu = next(p["avg_us"] for p in proj if p["name"] == "gate_up") * 1e-3
     ach = bytes_gu / (t_gu * 1e-3) / 1e9
+    gemv_us = sum(p["avg_us"] * PROJ_PER_STEP[p["name"]] for p in proj)
+    gemv_bytes = sum(p["bytes"] * PROJ_PER_STEP[p["name"]] for p in proj)
     step_ms = step["mean_ms"] if step else ms_per_step
     log(f"[bench] decode {args.steps} steps: {ms_per_step:.3f} ms/token wall ({tps:.1f} tok/s), graph step "
         f"{step_ms:.3f} ms, weights {wbytes / 1e9:.3f} GB/token -> {wbytes / (step_ms * 1e-3) / 1e9:.0f} GB/s; "
@@ -371,7 +453,8 @@ def bench_decode(args):
         "vs_baseline": None, "dtype": "u4xf16->f32", "data": "synthetic",
         "config": {"workload": "batch-1 greedy decode, random-init 9B-shaped hybrid model (32 layers 3:1 linear:full, "
                                "hidden 4096, MLP 12288, vocab 248320, 32q/8kv heads d128, W4A16 g64), "
-                               f"{prompt_len}-token prefill then {args.steps} decode steps",
+                               f"{prompt_len}-token prefill and one untimed decode step, then {args.steps} timed "
+                               "decode steps",
                    "prompt_tokens": prompt_len, "weight_bytes_per_token": wbytes,
                    "graph_step_ms": round(step_ms, 4), "decode_total_ms_from_xq_metrics": round(decode_ms, 3),
                    "weight_stream_GBps": round(wbytes / (step_ms * 1e-3) / 1e9, 1),
@@ -380,15 +463,23 @@ def bench_decode(args):
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": f"{GATE_UP_KERNEL}: gate/up 24576x4096 W4A16 g64 + RMSNorm prologue + SiLU*up "
-                               "epilogue, 200 back-to-back launches on rotated weights",
+                               "epilogue",
+                     "method": "HIP events on the launch stream around 200 back-to-back launches on rotated weight "
+                               "copies (> 2x the last-level cache); algorithmic bytes = codes + fp16 (scale, zero) per "
+                               "group + x + y",
                      "bytes_per_launch": bytes_gu, "avg_launch_us": round(t_gu * 1e3, 2), "launches_timed": 200,
+                     "per_projection": [{k: p[k] for k in ("name", "rows", "cols", "prologue", "epilogue", "avg_us",
+                                                           "bytes", "GBps", "frac")} for p in proj],
+                     "projections_per_step": {"launches": sum(PROJ_PER_STEP.values()), "bytes": gemv_bytes,
+                                              "sum_avg_us": round(gemv_us, 1),
+                                              "frac": round(gemv_bytes / (gemv_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)},
                      "in_model_avg_us": {"gate_up": round(gu["mean_ms"] * 1e3, 2) if gu else None,
                                          "down_proj": round(dn["mean_ms"] * 1e3, 2) if dn else None,
                                          "lm_head_argmax": round(lm["mean_ms"] * 1e3, 2) if lm else None},
                      "bytes_per_launch_down_proj": bytes_dn, "bytes_per_launch_lm_head": bytes_lm},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_decode(prompt, sess, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline_decode(prompt, sess)
     sess.close()
     if not args.no_traffic:
         t = measure_traffic()
@@ -399,42 +490,68 @@ def bench_decode(args):
     return result
 
 
-def cpu_baseline_decode(prompt, gpu_sess, seconds):
+def cpu_baseline_decode(prompt, gpu_sess, runs=3):
     """The compiled reference customlib (oracle/_ref) on the same model files and
-    host cores, timed by its own xq_metrics; falls back to the oracle port.
-    Bounded sample: a short prompt and a few greedy steps.  The GPU session runs
-    the same sample so the greedy ids can be compared at full size."""
+    host cores, timed by its own xq_metrics (decode tokens / decode ms,
+    session.cpp:595-602); falls back to the oracle port.  Bounded sample: an
+    8-token prompt and 4 greedy steps, one warmup run and `runs` measured runs
+    (each xq_reset + xq_generate, as the reference harness,
+    benchmark_jni.cpp:1324-1357).  The GPU session runs the same sample so the
+    greedy ids, and the GPU's top-2 logit margin at each step, can be compared
+    at full size."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle_bind as ob
     n_prompt, n_new = 8, 4
     sample = prompt[:n_prompt]
     threads = min(8, os.cpu_count() or 1)
-    st, gpu_toks, _ = gpu_sess.generate(sample, n_new)
+    # GPU ids and margins, step by step (xq_get_debug_json top-k before each step)
+    assert gpu_sess.prefill(sample)[0] == 0
+    gpu_toks, margins = [], []
+    for _ in range(n_new):
+        st, txt = gpu_sess.json("xq_get_debug_json", 1 << 16)
+        top = json.loads(txt)["lm_head_topk"] if st == 0 else []
+        margins.append(round(top[0]["logit"] - top[1]["logit"], 5) if len(top) > 1 else None)
+        st, tok, _ = gpu_sess.decode_one()
+        gpu_toks.append(tok)
     if ob.ref_available():
         ref = xb.bind_xq_abi(ctypes.CDLL(ob.REF_SO))
         t0 = time.perf_counter()
         rs = xb.Session(MODEL_DIR, xb.options(backend=b"cpu", threads=threads), lib=ref)
         load_s = time.perf_counter() - t0
-        st, toks, m = rs.generate(sample, n_new)
+        tps, pre = [], []
+        for r in range(1 + runs):
+            assert ref.xq_reset(rs.h) == 0
+            st, toks, m = rs.generate(sample, n_new)
+            assert st == 0, m.error
+            if r > 0:
+                tps.append(m.decode_tokens_per_second)
+                pre.append(m.prefill_tokens_per_second)
         rs.close()
-        kind, tps, pre = "reference", m.decode_tokens_per_second, m.prefill_tokens_per_second
+        kind = "reference"
     else:
         t0 = time.perf_counter()
         om = ob.OracleModel(MODEL_DIR)
         load_s = time.perf_counter() - t0
-        t1 = time.perf_counter()
-        om.prefill(sample)
-        t2 = time.perf_counter()
-        toks = np.array([om.decode_one(n_prompt + i) for i in range(n_new)])
-        t3 = time.perf_counter()
-        kind, tps, pre = "port", n_new / (t3 - t2), n_prompt / (t2 - t1)
+        tps, pre = [], []
+        for r in range(1 + runs):
+            t1 = time.perf_counter()
+            om.prefill(sample)
+            t2 = time.perf_counter()
+            toks = np.array([om.decode_one(n_prompt + i) for i in range(n_new)])
+            t3 = time.perf_counter()
+            if r > 0:
+                tps.append(n_new / (t3 - t2))
+                pre.append(n_prompt / (t2 - t1))
+        kind = "port"
     match = [int(a) == int(b) for a, b in zip(gpu_toks, toks)]
-    return {"value": round(tps, 4), "unit": "tokens/s", "cores": threads, "kind": kind,
-            "sample": f"{n_prompt}-token prompt + {n_new} greedy decode steps on the same 9B-shaped model files "
-                      f"(reference worker pool {threads} threads of {os.cpu_count()} host cores; load {load_s:.1f} s; "
-                      f"prefill {pre:.3f} tok/s)",
+    return {"value": round(float(np.mean(tps)), 4), "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"{n_prompt}-token prompt + {n_new} greedy decode steps on the same 9B-shaped model files, "
+                      f"1 warmup + {runs} measured runs (reset + generate each), mean decode tok/s "
+                      f"{', '.join(f'{t:.3f}' for t in tps)}; reference worker pool {threads} threads of "
+                      f"{os.cpu_count()} host cores; load {load_s:.1f} s; prefill {np.mean(pre):.3f} tok/s",
+            "runs_decode_tps": [round(t, 4) for t in tps],
             "greedy_ids_gpu": [int(t) for t in gpu_toks], "greedy_ids_cpu": [int(t) for t in toks],
-            "greedy_ids_match": all(match)}
+            "greedy_ids_match": all(match), "gpu_top2_margins": margins}
 
 
 def main():
@@ -442,7 +559,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "pmc-probe"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "gemv-sweep", "pmc-probe"])
+    ap.add_argument("--bits", type=int, nargs="+", default=[4, 3, 2], help="gemv-sweep code widths")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -458,7 +576,8 @@ def main():
     name = ctypes.create_string_buffer(256)
     xb.hip().xqhip_device_name(name, 256)
     log(f"[bench] device: {name.value.decode()}")
-    res = {"decode": bench_decode, "mlp": bench_mlp, "pmc-probe": pmc_probe}[args.workload](args)
+    res = {"decode": bench_decode, "mlp": bench_mlp, "gemv-sweep": bench_gemv_sweep,
+           "pmc-probe": pmc_probe}[args.workload](args)
     print(json.dumps(res), flush=True)
 
 

@@ -97,6 +97,8 @@ XQHIP_API int xqhip_device_synchronize(void);
 XQHIP_API int xqhip_event_create(void** ev);
 XQHIP_API int xqhip_event_destroy(void* ev);
 XQHIP_API int xqhip_event_record(void* ev, void* stream);
+/* Blocks the host until the work recorded before `ev` has finished. */
+XQHIP_API int xqhip_event_synchronize(void* ev);
 XQHIP_API int xqhip_event_elapsed_ms(void* start, void* stop, float* ms);
 
 /* ---- W4A16 weights ----------------------------------------------------- */

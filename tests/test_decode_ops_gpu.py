@@ -133,7 +133,7 @@ def test_attention_prep_and_gqa_decode_pos511(gated):
     ws = xb.DeviceBuffer(xb.hip().xqhip_gqa_workspace_bytes(nq, nkv, hd))
     ws.zero()
     out = xb.DeviceBuffer(nq * hd * 4)
-    for _ in range(2):  # the combine counters re-arm themselves
+    for _ in range(2):  # a second call on the same workspace gives the same result
         xb.ck(xb.hip().xqhip_gqa_decode(qo.ptr, kd.ptr, vd.ptr, go.ptr, nq, nkv, hd, max_ctx, pos_d.ptr, out.ptr,
                                         ws.ptr, None))
         close(out.download(np.float32, nq * hd), want, "gqa decode + gate")

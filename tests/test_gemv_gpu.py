@@ -153,7 +153,7 @@ def test_argmax_matches_oracle(rows, cols, seed):
     want_idx, want_val = ob.gemv_argmax(q, x)
     logits = ob.gemv(q, x)
     assert want_idx == int(np.argmax(logits))
-    for got_idx, got_val in run_argmax(q, x, calls=3):  # repeated calls: the kernel re-arms its counter
+    for got_idx, got_val in run_argmax(q, x, calls=3):  # repeated calls reuse the same workspace
         assert abs(got_val - want_val) <= ATOL + RTOL * abs(want_val)
         if top2_margin(logits) > 1e-2:
             assert got_idx == want_idx

@@ -24,7 +24,13 @@ namespace xqhip {
 __global__ void embed_bf16_kernel(const uint16_t* __restrict__ table, int vocab, int hidden,
                                   const int32_t* __restrict__ tok_ptr, float* __restrict__ out) {
     int tok = tok_ptr[blockIdx.y];
-    if (tok < 0 || tok >= vocab) tok = abs(tok) % max(1, vocab);
+    if (tok < 0 || tok >= vocab) {
+        // |id| % vocab as loadEmbeddingRow (custom_model.cpp:573-575), with the
+        // magnitude taken in uint32 so even INT_MIN maps to a row in range (the
+        // host rejects that id before a prompt reaches the device)
+        const uint32_t mag = tok < 0 ? 0u - static_cast<uint32_t>(tok) : static_cast<uint32_t>(tok);
+        tok = static_cast<int>(mag % static_cast<uint32_t>(max(1, vocab)));
+    }
     const uint16_t* row = table + static_cast<size_t>(tok) * hidden;
     float* o = out + static_cast<size_t>(blockIdx.y) * hidden;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)

@@ -175,6 +175,10 @@ int xqhip_event_destroy(void* ev) { return check(hipEventDestroy(static_cast<hip
 int xqhip_event_record(void* ev, void* stream) {
     return check(hipEventRecord(static_cast<hipEvent_t>(ev), as_stream(stream)), "hipEventRecord");
 }
+int xqhip_event_synchronize(void* ev) {
+    return check(hipEventSynchronize(static_cast<hipEvent_t>(ev)), "hipEventSynchronize");
+}
+
 int xqhip_event_elapsed_ms(void* start, void* stop, float* ms) {
     if (int rc = check(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize")) return rc;
     return check(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),

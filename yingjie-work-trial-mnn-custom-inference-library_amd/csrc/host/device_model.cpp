@@ -31,7 +31,12 @@ double elapsed_ms(void* a, void* b) {
 DeviceModel::~DeviceModel() {
     if (stream_) xqhip_stream_synchronize(stream_);
     if (g_prefill_) xqhip_graph_destroy(g_prefill_);
-    if (g_decode_) xqhip_graph_destroy(g_decode_);
+    if (g_sample_) xqhip_graph_destroy(g_sample_);
+    if (g_forward_) xqhip_graph_destroy(g_forward_);
+    if (ev_token_) xqhip_event_destroy(ev_token_);
+    for (auto& pair : step_ev_)
+        for (void* e : pair)
+            if (e) xqhip_event_destroy(e);
     for (xqhip_w4* m : matrices_) xqhip_w4_free(m);
     for (void* p : allocations_) xqhip_free(p);
     for (void* e : event_pool_) xqhip_event_destroy(e);
@@ -267,11 +272,17 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     void* pinned = nullptr;
     if (xqhip_host_alloc(&pinned, 4 * sizeof(int32_t)) != 0) return fail_hip(error, "pinned memory");
     h_tok_ = static_cast<int32_t*>(pinned);
+    if (xqhip_event_create(&ev_token_) != 0) return fail_hip(error, "event");
+    for (auto& pair : step_ev_)
+        for (void*& e : pair)
+            if (xqhip_event_create(&e) != 0) return fail_hip(error, "event");
     reset_state();
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "load sync");
 }
 
 void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past the position are never read)
+    std::string ignored;
+    sync(nullptr, &ignored);  // the trace of the steps being discarded is dropped with them
     for (Layer& L : layers_) {
         if (L.full) continue;
         xqhip_fill_u8(L.conv_state, 0, 2 * sizeof(float) * conv_dim_ * std::max(0, ksize_ - 1), stream_);
@@ -396,18 +407,18 @@ static bool graphs_enabled() {
 
 bool DeviceModel::ensure_graphs(std::string* error) {
     if (!graphs_enabled()) return true;  // eager launches of the same kernels
-    if (g_prefill_ && g_decode_) return true;
-    XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
-    bool ok = enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error);
-    void* g = nullptr;
-    if (xqhip_graph_end(stream_, &g) != 0 || !ok) return ok ? fail_hip(error, "graph instantiate") : false;
-    g_prefill_ = g;
-    XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
-    ok = enqueue_lm_head(false, error) && enqueue_embed(d_ctrl_ + 2, false, error) && enqueue_layers(false, error);
-    g = nullptr;
-    if (xqhip_graph_end(stream_, &g) != 0 || !ok) return ok ? fail_hip(error, "graph instantiate") : false;
-    g_decode_ = g;
-    return true;
+    if (g_prefill_ && g_sample_ && g_forward_) return true;
+    auto capture = [&](void** out, auto&& enqueue) {
+        XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
+        const bool ok = enqueue();
+        void* g = nullptr;
+        if (xqhip_graph_end(stream_, &g) != 0 || !ok) return ok ? fail_hip(error, "graph instantiate") : false;
+        *out = g;
+        return true;
+    };
+    return capture(&g_prefill_, [&] { return enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error); }) &&
+           capture(&g_sample_, [&] { return enqueue_lm_head(false, error); }) &&
+           capture(&g_forward_, [&] { return enqueue_embed(d_ctrl_ + 2, false, error) && enqueue_layers(false, error); });
 }
 
 // Batched prefill needs every matrix in the TILED64 layout (group 64) and the
@@ -526,6 +537,16 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
         *error = "prompt longer than the KV capacity (" + std::to_string(max_ctx_) + " tokens)";
         return false;
     }
+    for (size_t i = 0; i < n_tokens; ++i) {
+        // std::abs(INT_MIN) has no positive value: the reference's row offset
+        // turns negative and its read fails (custom_model.cpp:573-597)
+        if (token_ids[i] == INT32_MIN) {
+            *error = "short embeddings_bf16.bin row read (token id " + std::to_string(token_ids[i]) + " at prompt index " +
+                     std::to_string(i) + " has no row)";
+            return false;
+        }
+    }
+    if (!sync(trace, error)) return false;
     reset_state();
     if (!ensure_graphs(error)) return false;
     if (h_ctrl_cap_ < 2 * n_tokens) {
@@ -611,23 +632,54 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         return false;
     }
     if (!ensure_graphs(error)) return false;
+    // The previous step's forward pass may still be running: h_tok_[0..1] are
+    // free again because their upload preceded that step's sampling, which the
+    // previous call waited for.
     h_tok_[0] = static_cast<int32_t>(position);
     h_tok_[1] = 0;
     XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
-    if (detail_decode_ || !g_decode_) {
+    if (detail_decode_ || !g_sample_ || !g_forward_) {
+        // per-op events: the whole step is waited for before its times are read
         const bool timed = detail_decode_;
-        if (!enqueue_lm_head(timed, error) || !enqueue_embed(d_ctrl_ + 2, timed, error) || !enqueue_layers(timed, error))
-            return false;
-    } else {
-        op_begin(true, "decode_step_graph_custom");
-        XQ_CALL(xqhip_graph_launch(g_decode_, stream_), "decode graph");
-        op_end(true);
+        if (!sync(trace, error)) return false;
+        if (!enqueue_lm_head(timed, error)) return false;
+        XQ_CALL(xqhip_memcpy_d2h_async(h_tok_ + 2, d_ctrl_ + 2, sizeof(int32_t), stream_), "token readback");
+        if (!enqueue_embed(d_ctrl_ + 2, timed, error) || !enqueue_layers(timed, error)) return false;
+        XQ_CALL(xqhip_stream_synchronize(stream_), "decode");
+        *token_id = h_tok_[2];
+        detail_decode_ = false;
+        flush_timed(trace);
+        return true;
     }
+    // sample, hand the token to the host, then enqueue the forward pass and
+    // return once the token is known
+    void** ev = step_ev_[step_slot_];
+    XQ_CALL(xqhip_event_record(ev[0], stream_), "step event");
+    XQ_CALL(xqhip_graph_launch(g_sample_, stream_), "sampling graph");
     XQ_CALL(xqhip_memcpy_d2h_async(h_tok_ + 2, d_ctrl_ + 2, sizeof(int32_t), stream_), "token readback");
-    XQ_CALL(xqhip_stream_synchronize(stream_), "decode");
+    XQ_CALL(xqhip_event_record(ev_token_, stream_), "token event");
+    XQ_CALL(xqhip_graph_launch(g_forward_, stream_), "forward graph");
+    XQ_CALL(xqhip_event_record(ev[1], stream_), "step event");
+    XQ_CALL(xqhip_event_synchronize(ev_token_), "decode");
     *token_id = h_tok_[2];
-    detail_decode_ = false;
-    flush_timed(trace);
+    // the previous step's forward pass preceded this step's sampling: complete
+    if (step_pending_ && trace) {
+        void** prev = step_ev_[step_slot_ ^ 1];
+        trace->add("decode_step_graph_custom", elapsed_ms(prev[0], prev[1]), kTraceBackend);
+    }
+    step_pending_ = true;
+    step_slot_ ^= 1;
+    return true;
+}
+
+bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
+    if (!stream_) return true;
+    if (xqhip_stream_synchronize(stream_) != 0) return fail_hip(error, "decode step");
+    if (step_pending_ && trace) {
+        void** prev = step_ev_[step_slot_ ^ 1];
+        trace->add("decode_step_graph_custom", elapsed_ms(prev[0], prev[1]), kTraceBackend);
+    }
+    step_pending_ = false;
     return true;
 }
 
@@ -635,7 +687,7 @@ std::string DeviceModel::coverage_summary() const {  // fields of custom_model.c
     std::ostringstream o;
     o << "custom_decode_loop;hotpath_replaced=true;full_custom_decode=true;"
       << "backend_request=" << backend_request_ << ";device=hip:" << device_name_ << ";"
-      << "linear_backend=hip_gfx950_w4a16_dequant_gemv_dot2;"
+      << "linear_backend=hip_gfx950_w4a16_int4_digit_gemv_sdot8;"
       << "linear=q_proj,k_proj,v_proj,o_proj,gate_proj,up_proj,down_proj,linear_attn_qkv_a_b_z_out,lm_head;"
       << "rmsnorm=hip_fused_gemv_prologue;rope=hip_table_libm;attention=hip_gqa_decode_split_fp16_kv;"
       << "attention_output_gate=hip_fused;linear_attention_state=hip_gated_delta_fp32_state;"

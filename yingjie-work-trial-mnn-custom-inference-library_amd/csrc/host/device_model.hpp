@@ -5,7 +5,12 @@
 // resetState / coverageSummary / debugJson / copyHidden behaviour.  All weights,
 // the fp16 KV cache, the fp32 recurrent state and every activation live in HBM;
 // the host only feeds (position, token) and reads back the sampled token.
-// Each token runs as one captured HIP graph (about six kernels per layer).
+// A decode step is two captured HIP graphs: the lm_head argmax that samples the
+// token, then the forward pass of that token through every layer (about six
+// kernels per layer).  decode_one returns as soon as the token is known and
+// leaves the forward pass running on the stream, so the host's work between
+// steps overlaps the device's; every call that reads device state first waits
+// for it (sync).
 #pragma once
 
 #include <cstdint>
@@ -28,6 +33,9 @@ public:
     bool load(const std::string& model_dir, const std::string& backend_request, int max_context, std::string* error);
     bool prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace* trace, std::string* error);
     bool decode_one(int32_t* token_id, size_t position, KernelTrace* trace, std::string* error);
+    // Waits for every enqueued step and credits the last graph step's time to
+    // `trace` (dropped when null).  false on a device error.
+    bool sync(KernelTrace* trace, std::string* error);
     void reset_state();
 
     int hidden_size() const { return hidden_; }
@@ -124,7 +132,12 @@ private:
     int32_t* h_tok_ = nullptr;   // pinned sampled-token readback
     void* stream_ = nullptr;
     void* g_prefill_ = nullptr;  // graph: embed(input token) + layers
-    void* g_decode_ = nullptr;   // graph: lm_head argmax -> embed(sampled) + layers
+    void* g_sample_ = nullptr;   // graph: lm_head argmax -> sampled token (d_ctrl_[2])
+    void* g_forward_ = nullptr;  // graph: embed(sampled token) + layers
+    void* ev_token_ = nullptr;   // recorded once the sampled token reached h_tok_[2]
+    void* step_ev_[2][2] = {};   // (start, end) of the last two graph steps
+    int step_slot_ = 0;          // slot of the next graph step
+    bool step_pending_ = false;  // slot step_slot_ ^ 1 holds a step not yet credited to the trace
     bool detail_prefill_ = true, detail_decode_ = true;
     // prompt-chunk buffers, [token][...] rows (allocated when every matrix is TILED64)
     bool batched_prefill_ = false;

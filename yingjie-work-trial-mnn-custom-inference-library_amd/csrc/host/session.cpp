@@ -178,6 +178,14 @@ public:
                 return st;
             }
         }
+        if (model_ && max_new > 0) {
+            // the last token's forward pass is still on the device: wait for it
+            // and count it as decode time, so the rates cover all the work
+            const auto t1 = Clock::now();
+            std::string err;
+            if (!model_->sync(&trace_, &err)) return fail(XQ_ERR_RUNTIME, err, out);
+            m_.decode_total_ms += ms_between(t1, Clock::now());
+        }
         m_.total_generate_ms = ms_between(t0, Clock::now());
         rates();
         copy_cstr(m_.selected_kernels, sizeof(m_.selected_kernels), kernel_summary());
@@ -214,7 +222,13 @@ public:
         return copy_json(o.str(), out, cap);
     }
 
-    xq_status trace_json(char* out, size_t cap) const { return copy_json(trace_.to_json(), out, cap); }
+    xq_status trace_json(char* out, size_t cap) {
+        if (model_) {
+            std::string err;
+            if (!model_->sync(&trace_, &err)) return fail(XQ_ERR_RUNTIME, err, nullptr);
+        }
+        return copy_json(trace_.to_json(), out, cap);
+    }
 
     xq_status debug_json(char* out, size_t cap) {
         if (!out || cap == 0) return XQ_ERR_INVALID_ARGUMENT;

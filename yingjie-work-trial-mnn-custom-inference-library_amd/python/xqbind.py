@@ -55,6 +55,7 @@ _HIP_SIGS = {
     "xqhip_event_create": (c_int, [ctypes.POINTER(c_void_p)]),
     "xqhip_event_destroy": (c_int, [c_void_p]),
     "xqhip_event_record": (c_int, [c_void_p, c_void_p]),
+    "xqhip_event_synchronize": (c_int, [c_void_p]),
     "xqhip_event_elapsed_ms": (c_int, [c_void_p, c_void_p, ctypes.POINTER(c_float)]),
     "xqhip_w4_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, ctypes.POINTER(W4)]),
     "xqhip_wlb_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
