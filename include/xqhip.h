@@ -164,6 +164,18 @@ XQHIP_API size_t xqhip_argmax_workspace_bytes(int rows);
 XQHIP_API int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
                                       void* workspace, int32_t* out_index, float* out_value, void* stream);
 
+/* xqhip_gemv_w4a16_argmax without a workspace argument and without any
+ * allocation: no counterpart in the reference.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  The per-block keys go to a 16 KiB array
+ * of the library's own device memory (one per GPU, held until the process
+ * ends; any matrix size fits, the launch caps its blocks), which keeps the last
+ * call's contents and needs no clearing.  Calls that overlap on one GPU (other
+ * streams, other threads) race on that array: serialise them.  Same results as
+ * xqhip_gemv_w4a16_argmax. */
+XQHIP_API int xqhip_gemv_w4a16_argmax_static(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
+                                             int32_t* out_index, float* out_value, void* stream);
+
 /* ---- decode-step ops (all device pointers; `pos` is a device int32) ----- */
 /* out[hidden] = bf16 table row of *token as fp32; ids outside [0, vocab) wrap
  * to |id| % vocab (loadEmbeddingRow, custom_model.cpp:569-608). */

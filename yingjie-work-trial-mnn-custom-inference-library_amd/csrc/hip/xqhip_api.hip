@@ -10,9 +10,16 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
+// Device memory of the library itself for xqhip_gemv_w4a16_argmax_static: the
+// per-block argmax keys (uint64 each, at most kArgmaxMaxBlocks blocks), 16 KiB
+// on every device the library runs on, held until the process ends.  Host code
+// never uses this name as an address: it reads each device's copy's address
+// once with hipGetSymbolAddress (static_scratch below) and passes that.
+static __device__ __align__(256) uint64_t scratch[xqhip::kArgmaxMaxBlocks];
 
 namespace {
 
@@ -71,6 +78,27 @@ __global__ void copy_u32x4_kernel(uint4* __restrict__ dst, const uint4* __restri
     if (t < tail) dst_tail[t] = src_tail[t];
 }
 
+// Address of `scratch` on the current device, resolved once per device with
+// that device current.  nullptr (and the error set) on failure.
+constexpr int kMaxDevices = 64;
+void* static_scratch() {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= kMaxDevices) {
+        fail(XQHIP_EDEVICE, "device %d beyond the %d devices the static scratch covers", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        if (check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return nullptr;
+        addr[dev] = ptr;
+    }
+    return addr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -83,7 +111,10 @@ int xqhip_device_count(void) {
     return n;
 }
 
-int xqhip_set_device(int device) { return check(hipSetDevice(device), "hipSetDevice"); }
+int xqhip_set_device(int device) {
+    if (int rc = check(hipSetDevice(device), "hipSetDevice")) return rc;
+    return static_scratch() ? XQHIP_OK : XQHIP_EDEVICE;  // set-up of the no-allocation entry point
+}
 
 int xqhip_device_name(char* out, size_t capacity) {
     int dev = 0;
@@ -450,6 +481,19 @@ int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const 
     p.out_val = out_value;
     p.max_blocks = gemv_block_cap() > 0 ? std::min(kArgmaxMaxBlocks, gemv_block_cap()) : 0;
     return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax launch");
+}
+
+int xqhip_gemv_w4a16_argmax_static(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
+                                   int32_t* out_index, float* out_value, void* stream) {
+    const size_t need = xqhip_argmax_workspace_bytes(w ? w->rows : 0);
+    if (need > sizeof(scratch))
+        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax_static: needs %zu bytes of scratch, the library holds %zu",
+                    need, sizeof(scratch));
+    void* ptr = static_scratch();
+    if (!ptr) return XQHIP_EDEVICE;
+    // the keys need no clearing: every block of the launch writes its own
+    // before the finishing kernel reads exactly those
+    return xqhip_gemv_w4a16_argmax(w, x, x_type, pro, ptr, out_index, out_value, stream);
 }
 
 int xqhip_embed_bf16(const uint16_t* table, int vocab, int hidden, const int32_t* token, float* out, void* stream) {

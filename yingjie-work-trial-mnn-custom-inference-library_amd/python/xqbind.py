@@ -66,6 +66,8 @@ _HIP_SIGS = {
     "xqhip_argmax_workspace_bytes": (c_size_t, [c_int]),
     "xqhip_gemv_w4a16_argmax": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p, c_void_p,
                                         c_void_p]),
+    "xqhip_gemv_w4a16_argmax_static": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p,
+                                               c_void_p]),
     "xqhip_embed_bf16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "xqhip_rope_table": (c_int, [c_float, c_int, c_int, c_void_p]),
     "xqhip_attn_prep": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
