@@ -160,11 +160,17 @@ def oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, pos, theta, e
     return kk, att * sig
 
 
-# (nq, nkv, head_dim, rotary, pos, max_ctx, gated): the 9B attention shape, the
-# first position, a position past 64 chunks (grid slots wrap), a head_dim
-# without a specialised kernel, group 8 at the last slot of the first chunk
-FUSED_CASES = [(16, 4, 256, 64, 700, 1024, True), (32, 8, 128, 32, 0, 64, False),
-               (8, 2, 64, 64, 4160, 8192, True), (4, 2, 96, 32, 130, 256, True), (16, 2, 128, 32, 63, 128, False)]
+# (nq, nkv, head_dim, rotary, pos, max_ctx, gated).  The chunk kernel spreads
+# the context over 256 / nkv slots per kv head (at most 64) in chunks of
+# 16, 32 or 64 tokens, a slot taking several chunks past 64 per slot.  Cases:
+# the Qwen3.5-9B head layout (16-token chunks of head_dim 256); the config-3
+# point (32q/8kv d128 at position 511: 16-token chunks, one per slot); the
+# first position; 32-token chunks; 64-token chunks, several per slot; a
+# head_dim without a specialised kernel; group 8 at the end of the first
+# chunk; and a context past 16384 tokens (one kv head, 64 slots of 5 chunks).
+FUSED_CASES = [(16, 4, 256, 64, 700, 1024, True), (32, 8, 128, 32, 511, 1024, True), (32, 8, 128, 32, 0, 64, False),
+               (32, 8, 128, 32, 700, 1024, True), (8, 2, 64, 64, 4160, 8192, True), (32, 8, 128, 32, 9000, 9216, True),
+               (4, 2, 96, 32, 130, 256, True), (16, 2, 128, 32, 63, 128, False), (4, 1, 128, 32, 20000, 20480, False)]
 
 
 @pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "nq%d_nkv%d_hd%d_rd%d_pos%d" % c[:5])

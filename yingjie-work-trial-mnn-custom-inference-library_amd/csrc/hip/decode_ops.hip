@@ -115,69 +115,116 @@ hipError_t launch_qk_prep(const QkPrepLaunch& p, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // GQA decode attention in two kernels.
 //
-// gqa_chunk_kernel: block (kh, j) takes the `group` query heads of kv head kh
-// over the 64-token chunks j, j + gridDim.y, ... of the context: scores
-// q.k/sqrt(d), the chunk's max m and sum l of exp(s - m), and the unnormalised
-// sum of exp(s - m) v, written to the workspace per (head, chunk).
-// gqa_combine_kernel: one block per query head merges the chunks of the
-// context (weights exp(m_c - M)), normalises, applies the sigmoid output gate.
-// The kernel boundary orders the two, so no block waits on another and no
-// grid-wide fence is needed.
+// Chunk kernel: grid (kv head kh, slot s), S = gridDim.y slots per kv head
+// (about one block per CU in all).  The context of ctx tokens is cut into
+// chunks of C tokens, C = attn_chunk_len(ctx, S): a power of two in [16, 64]
+// large enough that the S slots cover the context in one chunk each where
+// they can (ctx <= 64 S), so every slot has work at decode contexts; longer
+// contexts give each slot chunks s, s + S, ...  For each chunk the block
+// takes the `group` query heads of kv head kh: scores q.k/sqrt(d), the chunk's
+// max m and sum l of exp(s - m), and sum exp(s - m) v; its chunks are merged
+// in registers (rescaling by exp(m_old - m_new)), and the block writes one
+// partial (m, l, o) per query head.
+// Merge kernel: one block per query head combines the slots' partials
+// (weights exp(m_s - M)), multiplies by 1/l (custom_model.cpp:901-904) and
+// applies the sigmoid output gate.  The kernel boundary orders the two, so no
+// block waits on another and no grid-wide fence is needed.
 // ---------------------------------------------------------------------------
-constexpr int kAttnChunk = 64;
+constexpr int kAttnChunk = 64;     // most tokens in one chunk
 constexpr int kAttnMaxGroup = 8;
-constexpr int kAttnMaxCtx = 16384;
-constexpr int kAttnMaxChunks = kAttnMaxCtx / kAttnChunk;
-constexpr int kAttnGridChunks = 64;  // chunk slots per kv head in the grid
+constexpr int kAttnMaxSlots = 64;  // slots per kv head = partials per query head
+constexpr int kAttnMaxCtx = 1 << 20;
 constexpr int kAttnThreads = 256;
 
-// A chunk's K and V as this thread consumes them (HD > 0): K for the scores
-// (4 lanes per token, HD/4 dims each), V for the weighted sum (HD/8 lanes per
-// token, 8 dims each, tokens ts, ts + TPP, ...).  Loaded by load_kv before the
-// query is ready so the cache latency overlaps the q preparation; token
-// indices past the chunk are clamped to its last token (in bounds, unused).
-template <int HD>
+// The head sizes with a compiled chunk kernel; others run the generic one (0).
+__host__ __device__ inline int attn_hd_class(int head_dim) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) ? head_dim : 0;
+}
+// Shortest chunk of a head size: the score phase splits a key over
+// kAttnThreads / C lanes of at least 8 dims (one 16-byte load) each.
+__host__ __device__ constexpr int attn_min_chunk(int hd_class) {
+    return hd_class == 0 ? kAttnChunk : (2048 / hd_class > 16 ? 2048 / hd_class : 16);
+}
+__host__ __device__ inline int attn_chunk_len(int ctx, int slots, int hd_class) {
+    const int want = (ctx + slots - 1) / slots;
+    int c = attn_min_chunk(hd_class);
+    while (c < want && c < kAttnChunk) c <<= 1;
+    return c;
+}
+__host__ __device__ inline int attn_slots(int nkv) {
+    const int s = 256 / (nkv > 0 ? nkv : 1);
+    return s < 1 ? 1 : (s > kAttnMaxSlots ? kAttnMaxSlots : s);
+}
+
+// K and V of one chunk as this thread consumes them: K for the scores (LPK =
+// 256 / C lanes per token, DL = HD / LPK consecutive dims each), V for the
+// weighted sum (HD / 8 lanes per token, 8 dims each, tokens ts, ts + TPP, ...).
+// Token indices past the chunk are clamped to its last token (in bounds, unused).
+template <int HD, int C>
 struct KvRegs {
-    static constexpr int kK = HD / 32;             // uint4 of K per thread
-    static constexpr int kV = kAttnChunk * HD / 2048;  // tokens of V per thread
-    uint4 k[kK > 0 ? kK : 1];
-    uint4 v[kV > 0 ? kV : 1];
+    static constexpr int kLPK = kAttnThreads / C;
+    static constexpr int kDL = HD / kLPK;
+    static constexpr int kK = kDL / 8;                  // uint4 of K per thread
+    static constexpr int kLPT = HD / 8;                 // lanes per token of V
+    static constexpr int kTPP = kAttnThreads / kLPT;    // tokens per V pass
+    static constexpr int kV = (C + kTPP - 1) / kTPP;    // V passes
+    static_assert(kDL >= 8 && kDL % 8 == 0, "a score lane reads whole 16-byte pieces of K");
+    uint4 k[kK];
+    uint4 v[kV];
 };
 
-template <int HD>
-__device__ __forceinline__ void load_kv(const GqaLaunch& p, int kh, int t0, int n, KvRegs<HD>& r) {
-    if constexpr (HD > 0) {
-        constexpr int DL = HD / 4, LPT = HD / 8, TPP = kAttnThreads / LPT;
-        const int sub = threadIdx.x & 3, tt = threadIdx.x >> 2;
-        const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + min(tt, n - 1)) * p.nkv + kh) * HD + sub * DL;
+template <int HD, int C>
+__device__ __forceinline__ void load_kv(const GqaLaunch& p, int kh, int t0, int n, KvRegs<HD, C>& r) {
+    using R = KvRegs<HD, C>;
+    const int sub = threadIdx.x % R::kLPK, tt = threadIdx.x / R::kLPK;
+    const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + min(tt, n - 1)) * p.nkv + kh) * HD + sub * R::kDL;
 #pragma unroll
-        for (int u = 0; u < KvRegs<HD>::kK; ++u) r.k[u] = *reinterpret_cast<const uint4*>(krow + 8 * u);
-        const int dsl = threadIdx.x % LPT, ts = threadIdx.x / LPT;
+    for (int u = 0; u < R::kK; ++u) r.k[u] = *reinterpret_cast<const uint4*>(krow + 8 * u);
+    const int dsl = threadIdx.x % R::kLPT, ts = threadIdx.x / R::kLPT;
 #pragma unroll
-        for (int u = 0; u < KvRegs<HD>::kV; ++u) {
-            const int t = min(ts + u * TPP, n - 1);
-            r.v[u] = *reinterpret_cast<const uint4*>(p.v_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * HD + dsl * 8);
-        }
+    for (int u = 0; u < R::kV; ++u) {
+        const int t = min(ts + u * R::kTPP, n - 1);
+        r.v[u] = *reinterpret_cast<const uint4*>(p.v_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * HD + dsl * 8);
     }
 }
 
-// pos_new >= 0: key/value of position pos_new come from kn / vn (LDS, the
-// values the same launch appends to the cache) instead of the cache.
+// Per-thread running state of a block's chunks: items i = threadIdx.x + k *
+// kAttnThreads of the group x HD outputs (head g = i / HD).
 template <int HD>
-__device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, int t0, int n, int group, int hd,
-                                          const float* qs, float* sc, float* vred, const KvRegs<HD>& kvr,
-                                          int pos_new = -1, const float* kn = nullptr, const float* vn = nullptr) {
+struct AttnRun {
+    static constexpr int kItems = (kAttnMaxGroup * (HD > 0 ? HD : 256) + kAttnThreads - 1) / kAttnThreads;
+    float m[kItems], l[kItems], o[kItems];
+};
+
+// Merges a chunk (stats cm / cl per head in LDS, output `acc` of item k) into
+// the running state.  The first chunk gives exactly (cm, cl, acc).
+template <int HD>
+__device__ __forceinline__ void run_merge(AttnRun<HD>& run, int k, float cm, float cl, float acc) {
+    const float mn = fmaxf(run.m[k], cm);
+    const float a = expf(run.m[k] - mn), b = expf(cm - mn);
+    run.o[k] = run.o[k] * a + acc * b;
+    run.l[k] = run.l[k] * a + cl * b;
+    run.m[k] = mn;
+}
+
+// One chunk of C tokens (t0 .. t0 + n - 1, n <= C) for the query heads of kv
+// head kh.  pos_new >= 0: the key/value of position pos_new come from kn / vn
+// (LDS: the values the same launch appends to the cache) instead of the cache.
+// LDS: qs [group][hd], sc [group][64] scores / weights, cst [2][8] chunk stats,
+// vred [4 waves][group][hd].
+template <int HD, int C>
+__device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int t0, int n, int group, const float* qs,
+                                          float* sc, float* cst, float* vred, const KvRegs<HD, C>& kvr,
+                                          AttnRun<HD>& run, int pos_new, const float* kn, const float* vn) {
+    using R = KvRegs<HD, C>;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
-    const int qh0 = kh * group;
-    // scores: 4 lanes per token, each lane HD/4 consecutive dims (16-byte loads)
-    if constexpr (HD > 0) {
-        constexpr int DL = HD / 4;
-        const int sub = threadIdx.x & 3, tt = threadIdx.x >> 2;
+    const float rscale = 1.0f / sqrtf(static_cast<float>(HD));
+    {  // scores
+        const int sub = threadIdx.x % R::kLPK, tt = threadIdx.x / R::kLPK;
         const bool valid = tt < n;
-        float kv[DL];
+        float kv[R::kDL];
 #pragma unroll
-        for (int u = 0; u < DL / 8; ++u) {
+        for (int u = 0; u < R::kK; ++u) {
             const uint4 w = kvr.k[u];
             const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -188,24 +235,15 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
         }
         if (valid && t0 + tt == pos_new) {
 #pragma unroll
-            for (int d = 0; d < DL; ++d) kv[d] = kn[sub * DL + d];
+            for (int d = 0; d < R::kDL; ++d) kv[d] = kn[sub * R::kDL + d];
         }
         for (int g = 0; g < group; ++g) {
-            const float* qv = qs + g * HD + sub * DL;
+            const float* qv = qs + g * HD + sub * R::kDL;
             float dot = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DL; ++d) dot += qv[d] * kv[d];
-            dot = lanes_sum<4>(dot);
+            for (int d = 0; d < R::kDL; ++d) dot += qv[d] * kv[d];
+            dot = lanes_sum<R::kLPK>(dot);
             if (valid && sub == 0) sc[g * kAttnChunk + tt] = dot * rscale;
-        }
-    } else {
-        for (int pr = threadIdx.x; pr < n * group; pr += kAttnThreads) {
-            const int t = pr / group, g = pr % group;
-            const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * hd;
-            const bool is_new = t0 + t == pos_new;
-            float dot = 0.0f;
-            for (int d = 0; d < hd; ++d) dot += qs[g * hd + d] * (is_new ? kn[d] : static_cast<float>(krow[d]));
-            sc[g * kAttnChunk + t] = dot * rscale;
         }
     }
     __syncthreads();
@@ -217,25 +255,22 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
         const float l = wave_sum(e);
         sc[g * kAttnChunk + lane] = e;
         if (lane == 0) {
-            p.part_m[(qh0 + g) * kAttnMaxChunks + ch] = m;
-            p.part_l[(qh0 + g) * kAttnMaxChunks + ch] = l;
+            cst[g] = m;
+            cst[kAttnMaxGroup + g] = l;
         }
     }
     __syncthreads();
-    // sum_t e_t v_t: 16-byte loads of v, HD/8 lanes per token
-    if constexpr (HD > 0) {
-        constexpr int LPT = HD / 8;
-        static_assert(LPT >= 8 && LPT <= 32, "pair sums below cover lane distances 8..32");
-        constexpr int TPP = kAttnThreads / LPT;
-        const int dsl = threadIdx.x % LPT, ts = threadIdx.x / LPT;
+    {  // sum_t e_t v_t: 16-byte loads of v, HD/8 lanes per token
+        static_assert(R::kLPT >= 8 && R::kLPT <= 32, "pair sums below cover lane distances 8..32");
+        const int dsl = threadIdx.x % R::kLPT, ts = threadIdx.x / R::kLPT;
         float o[kAttnMaxGroup][8];
 #pragma unroll
         for (int g = 0; g < kAttnMaxGroup; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
 #pragma unroll
-        for (int u = 0; u < KvRegs<HD>::kV; ++u) {
-            const int t = ts + u * TPP;
+        for (int u = 0; u < R::kV; ++u) {
+            const int t = ts + u * R::kTPP;
             if (t >= n) break;
             const uint4 w = kvr.v[u];
             float vv[8] = {half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y),
@@ -258,62 +293,170 @@ __device__ __forceinline__ void gqa_chunk(const GqaLaunch& p, int kh, int ch, in
             if (g < group) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    if constexpr (LPT <= 8) o[g][e] = xor_pair_sum<8>(o[g][e]);
-                    if constexpr (LPT <= 16) o[g][e] = xor_pair_sum<16>(o[g][e]);
+                    if constexpr (R::kLPT <= 8) o[g][e] = xor_pair_sum<8>(o[g][e]);
+                    if constexpr (R::kLPT <= 16) o[g][e] = xor_pair_sum<16>(o[g][e]);
                     o[g][e] = xor_pair_sum<32>(o[g][e]);
                 }
             }
         }
-        if (lane < LPT) {
+        if (lane < R::kLPT) {
 #pragma unroll
             for (int g = 0; g < kAttnMaxGroup; ++g)
                 if (g < group)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) vred[(wid * group + g) * HD + dsl * 8 + e] = o[g][e];
         }
-        __syncthreads();
-        for (int i = threadIdx.x; i < group * HD; i += kAttnThreads) {
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < AttnRun<HD>::kItems; ++k) {
+        const int i = threadIdx.x + k * kAttnThreads;
+        if (i < group * HD) {
             const int g = i / HD, d = i % HD;
             float acc = 0.0f;
 #pragma unroll
             for (int w = 0; w < kAttnThreads / kWave; ++w) acc += vred[(w * group + g) * HD + d];
-            p.part_o[(static_cast<size_t>(qh0 + g) * kAttnMaxChunks + ch) * HD + d] = acc;
+            run_merge<HD>(run, k, cst[g], cst[kAttnMaxGroup + g], acc);
         }
-    } else {
-        for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) {
+    }
+    __syncthreads();  // sc, cst and vred are reused by the block's next chunk
+}
+
+// Generic head size (HD == 0, C == 64): the same steps with plain loops.
+__device__ void gqa_chunk_generic(const GqaLaunch& p, int kh, int t0, int n, int group, int hd, const float* qs,
+                                  float* sc, float* cst, AttnRun<0>& run, int pos_new, const float* kn,
+                                  const float* vn) {
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const float rscale = 1.0f / sqrtf(static_cast<float>(hd));
+    for (int pr = threadIdx.x; pr < n * group; pr += kAttnThreads) {
+        const int t = pr / group, g = pr % group;
+        const _Float16* krow = p.k_cache + (static_cast<size_t>(t0 + t) * p.nkv + kh) * hd;
+        const bool is_new = t0 + t == pos_new;
+        float dot = 0.0f;
+        for (int d = 0; d < hd; ++d) dot += qs[g * hd + d] * (is_new ? kn[d] : static_cast<float>(krow[d]));
+        sc[g * kAttnChunk + t] = dot * rscale;
+    }
+    __syncthreads();
+    for (int g = wid; g < group; g += kAttnThreads / kWave) {
+        const float sv = lane < n ? sc[g * kAttnChunk + lane] : -INFINITY;
+        const float m = wave_max(sv);
+        const float e = lane < n ? expf(sv - m) : 0.0f;
+        const float l = wave_sum(e);
+        sc[g * kAttnChunk + lane] = e;
+        if (lane == 0) {
+            cst[g] = m;
+            cst[kAttnMaxGroup + g] = l;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < AttnRun<0>::kItems; ++k) {
+        const int i = threadIdx.x + k * kAttnThreads;
+        if (i < group * hd) {
             const int g = i / hd, d = i % hd;
             float acc = 0.0f;
             for (int t = 0; t < n; ++t)
                 acc += sc[g * kAttnChunk + t] *
                        (t0 + t == pos_new ? vn[d]
                                           : static_cast<float>(p.v_cache[(static_cast<size_t>(t0 + t) * p.nkv + kh) * hd + d]));
-            p.part_o[(static_cast<size_t>(qh0 + g) * kAttnMaxChunks + ch) * hd + d] = acc;
+            run_merge<0>(run, k, cst[g], cst[kAttnMaxGroup + g], acc);
         }
     }
-    __syncthreads();  // sc and vred are reused by the block's next chunk
+    __syncthreads();
+}
+
+template <int HD>
+__device__ __forceinline__ void run_init(AttnRun<HD>& run) {
+#pragma unroll
+    for (int k = 0; k < AttnRun<HD>::kItems; ++k) {
+        run.m[k] = -INFINITY;
+        run.l[k] = 0.0f;
+        run.o[k] = 0.0f;
+    }
+}
+
+// The block's partial (m, l, o) per query head of kv head kh, slot s.
+template <int HD>
+__device__ __forceinline__ void store_partial(const GqaLaunch& p, int kh, int s, int group, int hd,
+                                              const AttnRun<HD>& run) {
+#pragma unroll
+    for (int k = 0; k < AttnRun<HD>::kItems; ++k) {
+        const int i = threadIdx.x + k * kAttnThreads;
+        if (i < group * hd) {
+            const int g = i / hd, d = i % hd;
+            const size_t ps = static_cast<size_t>(kh * group + g) * kAttnMaxSlots + s;
+            p.part_o[ps * hd + d] = run.o[k];
+            if (d == 0) {
+                p.part_m[ps] = run.m[k];
+                p.part_l[ps] = run.l[k];
+            }
+        }
+    }
+}
+
+// The chunks of slot s (s, s + S, ...) given the prepared query heads in qs;
+// the first chunk's K/V are already in kvr.
+template <int HD, int C>
+__device__ __forceinline__ void attn_slot(const GqaLaunch& p, int kh, int ctx, int group, const float* qs, float* sc,
+                                          float* cst, float* vred, KvRegs<HD, C>& kvr, int pos_new, const float* kn,
+                                          const float* vn) {
+    const int s = blockIdx.y, S = gridDim.y;
+    const int nch = (ctx + C - 1) / C;
+    AttnRun<HD> run;
+    run_init<HD>(run);
+    for (int ch = s; ch < nch; ch += S) {
+        const int t0 = ch * C;
+        const int n = min(C, ctx - t0);
+        if (ch != s) load_kv<HD, C>(p, kh, t0, n, kvr);
+        gqa_chunk<HD, C>(p, kh, t0, n, group, qs, sc, cst, vred, kvr, run, pos_new, kn, vn);
+    }
+    store_partial<HD>(p, kh, s, group, HD, run);
+}
+
+// The kernel-level GQA (query heads already normalised and rotated in p.q).
+template <int HD, int C>
+__device__ __forceinline__ void gqa_block(const GqaLaunch& p, int kh, int ctx, int group, float* smem) {
+    float* qs = smem;                       // [group][HD]
+    float* sc = qs + group * HD;            // [group][64]
+    float* cst = sc + group * kAttnChunk;   // [2][8]
+    float* vred = cst + 2 * kAttnMaxGroup;  // [4 waves][group][HD]
+    const int s = blockIdx.y;
+    KvRegs<HD, C> kvr;
+    load_kv<HD, C>(p, kh, s * C, min(C, ctx - s * C), kvr);
+    for (int i = threadIdx.x; i < group * HD; i += kAttnThreads) qs[i] = p.q[static_cast<size_t>(kh) * group * HD + i];
+    __syncthreads();
+    attn_slot<HD, C>(p, kh, ctx, group, qs, sc, cst, vred, kvr, -1, nullptr, nullptr);
 }
 
 template <int HD>
 __global__ void __launch_bounds__(kAttnThreads) gqa_chunk_kernel(GqaLaunch p) {
     extern __shared__ float smem[];
-    const int hd = HD > 0 ? HD : p.head_dim;
     const int group = p.nq / p.nkv;
     const int kh = blockIdx.x;
     const int ctx = *p.pos + 1;
-    if (static_cast<int>(blockIdx.y) * kAttnChunk >= ctx) return;  // whole block: nothing to do
-    float* qs = smem;                       // [group][hd]
-    float* sc = qs + group * hd;            // [group][64]
-    float* vred = sc + group * kAttnChunk;  // [4 waves][group][hd]
-    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
-    KvRegs<HD> kvr;
-    load_kv<HD>(p, kh, blockIdx.y * kAttnChunk, min(kAttnChunk, ctx - static_cast<int>(blockIdx.y) * kAttnChunk), kvr);
-    for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) qs[i] = p.q[static_cast<size_t>(kh) * group * hd + i];
-    __syncthreads();
-    for (int ch = blockIdx.y; ch < nch; ch += gridDim.y) {
-        const int t0 = ch * kAttnChunk;
-        const int n = min(kAttnChunk, ctx - t0);
-        if (ch != static_cast<int>(blockIdx.y)) load_kv<HD>(p, kh, t0, n, kvr);
-        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred, kvr);
+    const int C = attn_chunk_len(ctx, gridDim.y, HD);
+    if (static_cast<int>(blockIdx.y) * C >= ctx) return;  // no chunk for this slot: the merge skips it
+    if constexpr (HD == 0) {
+        const int hd = p.head_dim;
+        float* qs = smem;
+        float* sc = qs + group * hd;
+        float* cst = sc + group * kAttnChunk;
+        for (int i = threadIdx.x; i < group * hd; i += kAttnThreads) qs[i] = p.q[static_cast<size_t>(kh) * group * hd + i];
+        __syncthreads();
+        AttnRun<0> run;
+        run_init<0>(run);
+        const int nch = (ctx + C - 1) / C;
+        for (int ch = blockIdx.y; ch < nch; ch += gridDim.y)
+            gqa_chunk_generic(p, kh, ch * C, min(C, ctx - ch * C), group, hd, qs, sc, cst, run, -1, nullptr, nullptr);
+        store_partial<0>(p, kh, blockIdx.y, group, hd, run);
+    } else {
+        if (C == 16 && attn_min_chunk(HD) <= 16) {
+            if constexpr (attn_min_chunk(HD) <= 16) gqa_block<HD, 16>(p, kh, ctx, group, smem);
+        } else if (C == 32) {
+            gqa_block<HD, 32>(p, kh, ctx, group, smem);
+        } else {
+            gqa_block<HD, 64>(p, kh, ctx, group, smem);
+        }
     }
 }
 
@@ -322,32 +465,117 @@ __global__ void __launch_bounds__(kAttnThreads) gqa_chunk_kernel(GqaLaunch p) {
 // include position pos also prepares that position's key and value, appends
 // them to the fp16 caches and uses them (rounded to fp16, like every cached
 // position) from LDS; the slot this launch writes is never taken from memory.
-template <int HD>
-__global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLaunch a) {
-    extern __shared__ float smem[];
+template <int HD, int C>
+__device__ __forceinline__ void attn_decode_block(const AttnDecodeLaunch& a, int kh, int pos, float* smem) {
     const GqaLaunch& p = a.g;
-    const int hd = HD > 0 ? HD : p.head_dim;
     const int group = p.nq / p.nkv;
-    const int kh = blockIdx.x;
-    const int pos = *p.pos;
     const int ctx = pos + 1;
-    if (static_cast<int>(blockIdx.y) * kAttnChunk >= ctx) return;  // whole block: nothing to do
-    float* qs = smem;                       // [group][hd]
-    float* sc = qs + group * hd;            // [group][64]
-    float* vred = sc + group * kAttnChunk;  // [4 waves][group][hd]
-    float* kn = vred + (kAttnThreads / kWave) * group * hd;  // [hd]
-    float* vn = kn + hd;                                     // [hd]
+    const int s = blockIdx.y, S = gridDim.y;
+    float* qs = smem;                                        // [group][HD]
+    float* sc = qs + group * HD;                             // [group][64]
+    float* cst = sc + group * kAttnChunk;                    // [2][8]
+    float* vred = cst + 2 * kAttnMaxGroup;                   // [4 waves][group][HD]
+    float* kn = vred + (kAttnThreads / kWave) * group * HD;  // [HD]
+    float* vn = kn + HD;                                     // [HD]
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int half = a.rotary_dim / 2;
+    const bool owns_new = (pos / C) % S == s;
+    // per-head RMSNorm (custom_model.cpp:301-313): heads 0..group-1 are q,
+    // head `group` (owner only) is the new key; wave w takes heads w, w + 4, ...
+    // The query loads are issued first, then the chunk's K/V, so the q
+    // preparation runs while the cache streams in.
+    constexpr int kPer = HD / kWave;  // values per lane of one head
+    constexpr int kMaxHeadsPerWave = (kAttnMaxGroup + 1 + 3) / 4;
+    const int nheads = group + (owns_new ? 1 : 0);
+    float qr[kMaxHeadsPerWave][kPer];
+#pragma unroll
+    for (int j = 0; j < kMaxHeadsPerWave; ++j) {
+        const int h = wid + 4 * j;
+        if (h < nheads) {
+            const bool is_k = h == group;
+            const float* src = is_k ? a.k_src + static_cast<size_t>(kh) * HD
+                                    : a.q_src + static_cast<size_t>(kh * group + h) * (a.gated ? 2 * HD : HD);
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) qr[j][e] = src[lane + e * kWave];
+        }
+    }
+    float vr[kPer > 0 ? (HD + kAttnThreads - 1) / kAttnThreads : 1];
+    if (owns_new) {
+#pragma unroll
+        for (int e = 0; e < (HD + kAttnThreads - 1) / kAttnThreads; ++e) {
+            const int d = threadIdx.x + e * kAttnThreads;
+            vr[e] = d < HD ? a.v_src[static_cast<size_t>(kh) * HD + d] : 0.0f;
+        }
+    }
+    KvRegs<HD, C> kvr;
+    load_kv<HD, C>(p, kh, s * C, min(C, ctx - s * C), kvr);
+#pragma unroll
+    for (int j = 0; j < kMaxHeadsPerWave; ++j) {
+        const int h = wid + 4 * j;
+        if (h < nheads) {
+            const bool is_k = h == group;
+            const float* w = is_k ? a.k_norm : a.q_norm;
+            float* dst = is_k ? kn : qs + h * HD;
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) ss += qr[j][e] * qr[j][e];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / static_cast<float>(HD) + a.eps);
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                const int d = lane + e * kWave;
+                dst[d] = qr[j][e] * (inv * w[d]);
+            }
+        }
+    }
+    if (owns_new) {
+#pragma unroll
+        for (int e = 0; e < (HD + kAttnThreads - 1) / kAttnThreads; ++e) {
+            const int d = threadIdx.x + e * kAttnThreads;
+            if (d < HD) vn[d] = vr[e];
+        }
+    }
+    __syncthreads();
+    // partial RoPE (custom_model.cpp:351-370) on the first rotary_dim dims, pairs (i, half + i)
     const float2* cs = reinterpret_cast<const float2*>(a.rope_cs) + static_cast<size_t>(pos) * a.rope_pairs;
-    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
-    const bool owns_new = (pos / kAttnChunk) % static_cast<int>(gridDim.y) == static_cast<int>(blockIdx.y);
-    // K/V of the block's first chunk are requested before the q preparation
-    // (the slot of `pos` is read too but replaced by kn / vn below)
-    KvRegs<HD> kvr;
-    load_kv<HD>(p, kh, blockIdx.y * kAttnChunk, min(kAttnChunk, ctx - static_cast<int>(blockIdx.y) * kAttnChunk), kvr);
-    // per-head RMSNorm (custom_model.cpp:301-313): one wave per head; heads
-    // 0..group-1 are q, head `group` (owner only) is the new key
+    for (int i = threadIdx.x; i < nheads * half; i += kAttnThreads) {
+        const int h = i / half, d = i % half;
+        float* v = h == group ? kn : qs + h * HD;
+        const float2 c = cs[d];
+        const float x0 = v[d], x1 = v[half + d];
+        v[d] = x0 * c.x - x1 * c.y;
+        v[half + d] = x1 * c.x + x0 * c.y;
+    }
+    __syncthreads();
+    if (owns_new) {  // append at slot pos, and use the fp16-rounded values like every other slot
+        for (int d = threadIdx.x; d < HD; d += kAttnThreads) {
+            const size_t slot = (static_cast<size_t>(pos) * p.nkv + kh) * HD + d;
+            const _Float16 kq = static_cast<_Float16>(kn[d]), vq = static_cast<_Float16>(vn[d]);
+            a.k_cache[slot] = kq;
+            a.v_cache[slot] = vq;
+            kn[d] = static_cast<float>(kq);
+            vn[d] = static_cast<float>(vq);
+        }
+        __syncthreads();
+    }
+    attn_slot<HD, C>(p, kh, ctx, group, qs, sc, cst, vred, kvr, pos, kn, vn);
+}
+
+// Generic head size: the same steps with plain loops (C = 64).
+__device__ void attn_decode_generic(const AttnDecodeLaunch& a, int kh, int pos, float* smem) {
+    const GqaLaunch& p = a.g;
+    const int hd = p.head_dim;
+    const int group = p.nq / p.nkv;
+    const int ctx = pos + 1;
+    const int C = kAttnChunk;
+    float* qs = smem;
+    float* sc = qs + group * hd;
+    float* cst = sc + group * kAttnChunk;
+    float* kn = cst + 2 * kAttnMaxGroup;
+    float* vn = kn + hd;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int half = a.rotary_dim / 2;
+    const bool owns_new = (pos / C) % static_cast<int>(gridDim.y) == static_cast<int>(blockIdx.y);
     const int nheads = group + (owns_new ? 1 : 0);
     for (int h = wid; h < nheads; h += kAttnThreads / kWave) {
         const bool is_k = h == group;
@@ -368,7 +596,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLau
     if (owns_new)
         for (int d = threadIdx.x; d < hd; d += kAttnThreads) vn[d] = a.v_src[static_cast<size_t>(kh) * hd + d];
     __syncthreads();
-    // partial RoPE (custom_model.cpp:351-370) on the first rotary_dim dims, pairs (i, half + i)
+    const float2* cs = reinterpret_cast<const float2*>(a.rope_cs) + static_cast<size_t>(pos) * a.rope_pairs;
     for (int i = threadIdx.x; i < nheads * half; i += kAttnThreads) {
         const int h = i / half, d = i % half;
         float* v = h == group ? kn : qs + h * hd;
@@ -378,7 +606,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLau
         v[half + d] = x1 * c.x + x0 * c.y;
     }
     __syncthreads();
-    if (owns_new) {  // append at slot pos, and use the fp16-rounded values like every other slot
+    if (owns_new) {
         for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
             const size_t slot = (static_cast<size_t>(pos) * p.nkv + kh) * hd + d;
             const _Float16 kq = static_cast<_Float16>(kn[d]), vq = static_cast<_Float16>(vn[d]);
@@ -389,44 +617,72 @@ __global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLau
         }
         __syncthreads();
     }
-    for (int ch = blockIdx.y; ch < nch; ch += gridDim.y) {
-        const int t0 = ch * kAttnChunk;
-        const int n = min(kAttnChunk, ctx - t0);
-        if (ch != static_cast<int>(blockIdx.y)) load_kv<HD>(p, kh, t0, n, kvr);
-        gqa_chunk<HD>(p, kh, ch, t0, n, group, hd, qs, sc, vred, kvr, pos, kn, vn);
+    AttnRun<0> run;
+    run_init<0>(run);
+    const int nch = (ctx + C - 1) / C;
+    for (int ch = blockIdx.y; ch < nch; ch += gridDim.y)
+        gqa_chunk_generic(p, kh, ch * C, min(C, ctx - ch * C), group, hd, qs, sc, cst, run, pos, kn, vn);
+    store_partial<0>(p, kh, blockIdx.y, group, hd, run);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(kAttnThreads) attn_decode_kernel(AttnDecodeLaunch a) {
+    extern __shared__ float smem[];
+    const int kh = blockIdx.x;
+    const int pos = *a.g.pos;
+    const int ctx = pos + 1;
+    const int C = attn_chunk_len(ctx, gridDim.y, HD);
+    if (static_cast<int>(blockIdx.y) * C >= ctx) return;  // no chunk for this slot: the merge skips it
+    if constexpr (HD == 0) {
+        attn_decode_generic(a, kh, pos, smem);
+    } else {
+        if (C == 16 && attn_min_chunk(HD) <= 16) {
+            if constexpr (attn_min_chunk(HD) <= 16) attn_decode_block<HD, 16>(a, kh, pos, smem);
+        } else if (C == 32) {
+            attn_decode_block<HD, 32>(a, kh, pos, smem);
+        } else {
+            attn_decode_block<HD, 64>(a, kh, pos, smem);
+        }
     }
 }
 
-__global__ void __launch_bounds__(256) gqa_combine_kernel(GqaLaunch p) {
-    __shared__ float wgt[kAttnMaxChunks];
-    __shared__ float red[32];
+// One block per query head: merge the partials of the slots that had chunks,
+// normalise by multiplying with 1/l (custom_model.cpp:901-904), apply the gate.
+// The first wave takes one slot per lane (max, weights exp(m_s - M), l), the
+// block then sums the slots' outputs with those weights.
+__global__ void __launch_bounds__(256) gqa_combine_kernel(GqaLaunch p, int slots) {
+    static_assert(kAttnMaxSlots <= kWave, "one slot per lane of the first wave");
+    __shared__ float wgt[kAttnMaxSlots];
+    __shared__ float inv_l;
     const int qh = blockIdx.x;
     const int hd = p.head_dim;
     const int ctx = *p.pos + 1;
-    const int nch = (ctx + kAttnChunk - 1) / kAttnChunk;
-    const float* pm = p.part_m + static_cast<size_t>(qh) * kAttnMaxChunks;
-    const float* pl = p.part_l + static_cast<size_t>(qh) * kAttnMaxChunks;
-    float m = -INFINITY;
-    for (int c = threadIdx.x; c < nch; c += blockDim.x) m = fmaxf(m, pm[c]);
-    m = wave_max(m);
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    if (lane == 0) red[wid] = m;
-    __syncthreads();
-    float mm = -INFINITY;
-    for (int i = 0; i < static_cast<int>(blockDim.x) / kWave; ++i) mm = fmaxf(mm, red[i]);
-    __syncthreads();
-    float l = 0.0f;
-    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
-        const float f = expf(pm[c] - mm);
-        wgt[c] = f;
-        l += pl[c] * f;
+    const int C = attn_chunk_len(ctx, slots, attn_hd_class(hd));
+    const int nact = min(slots, (ctx + C - 1) / C);
+    if (threadIdx.x < kWave) {
+        const int sl = threadIdx.x;
+        const size_t ps = static_cast<size_t>(qh) * kAttnMaxSlots + sl;
+        const float m = sl < nact ? p.part_m[ps] : -INFINITY;
+        const float l = sl < nact ? p.part_l[ps] : 0.0f;
+        const float M = wave_max(m);
+        const float w = sl < nact ? expf(m - M) : 0.0f;
+        const float tot = wave_sum(l * w);
+        wgt[sl] = w;
+        if (sl == 0) inv_l = tot > 0.0f ? 1.0f / tot : 0.0f;
     }
-    l = block_sum(l, red);  // also orders the wgt writes before the reads below
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const float* po = p.part_o + static_cast<size_t>(qh) * kAttnMaxChunks * hd;
+    __syncthreads();
+    const float inv = inv_l;
+    const float* po = p.part_o + static_cast<size_t>(qh) * kAttnMaxSlots * hd;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
         float o = 0.0f;
-        for (int c = 0; c < nch; ++c) o += po[static_cast<size_t>(c) * hd + d] * wgt[c];
+        for (int s0 = 0; s0 < nact; s0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = s0 + u < nact ? po[static_cast<size_t>(s0 + u) * hd + d] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s0 + u < nact) o += v[u] * wgt[s0 + u];
+        }
         const size_t oi = static_cast<size_t>(qh) * hd + d;
         // no gate projection: the reference's zero gate, sigmoid(0) (custom_model.cpp:750-753)
         const float gv = p.gate ? p.gate[static_cast<size_t>(qh) * p.gate_stride + d] : 0.0f;
@@ -436,50 +692,53 @@ __global__ void __launch_bounds__(256) gqa_combine_kernel(GqaLaunch p) {
 
 size_t gqa_workspace_bytes(int nq, int nkv, int head_dim) {
     (void)nkv;
-    return sizeof(float) * static_cast<size_t>(nq) * kAttnMaxChunks * (head_dim + 2);
+    return sizeof(float) * static_cast<size_t>(nq) * kAttnMaxSlots * (head_dim + 2);
 }
 
 static size_t gqa_lds_bytes(int group, int head_dim) {
     return sizeof(float) * (static_cast<size_t>(group) * head_dim + static_cast<size_t>(group) * kAttnChunk +
-                            (kAttnThreads / kWave) * static_cast<size_t>(group) * head_dim);
+                            2 * kAttnMaxGroup + (kAttnThreads / kWave) * static_cast<size_t>(group) * head_dim);
 }
+
+static int combine_threads(int head_dim) { return min(256, max(64, ((head_dim + 63) / 64) * 64)); }
 
 hipError_t launch_attn_decode(const AttnDecodeLaunch& a, hipStream_t s) {
     const GqaLaunch& p = a.g;
     const int group = p.nq / p.nkv;
     const size_t lds = gqa_lds_bytes(group, p.head_dim) + 2 * sizeof(float) * p.head_dim;
-    const int slots = min(kAttnGridChunks, (p.max_ctx + kAttnChunk - 1) / kAttnChunk);
+    const int slots = attn_slots(p.nkv);
     const dim3 grid(p.nkv, slots);
-    switch (p.head_dim) {
+    switch (attn_hd_class(p.head_dim)) {
         case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kAttnThreads), lds, s, a); break;
         case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kAttnThreads), lds, s, a); break;
         case 256: hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, s, a); break;
         default: hipLaunchKernelGGL(attn_decode_kernel<0>, grid, dim3(kAttnThreads), lds, s, a); break;
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL(gqa_combine_kernel, dim3(p.nq), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(gqa_combine_kernel, dim3(p.nq), dim3(combine_threads(p.head_dim)), 0, s, p, slots);
     return hipGetLastError();
 }
 
 hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
     const int group = p.nq / p.nkv;
     const size_t lds = gqa_lds_bytes(group, p.head_dim);
-    const int slots = min(kAttnGridChunks, (p.max_ctx + kAttnChunk - 1) / kAttnChunk);
+    const int slots = attn_slots(p.nkv);
     const dim3 grid(p.nkv, slots);
-    switch (p.head_dim) {
+    switch (attn_hd_class(p.head_dim)) {
         case 64: hipLaunchKernelGGL(gqa_chunk_kernel<64>, grid, dim3(kAttnThreads), lds, s, p); break;
         case 128: hipLaunchKernelGGL(gqa_chunk_kernel<128>, grid, dim3(kAttnThreads), lds, s, p); break;
         case 256: hipLaunchKernelGGL(gqa_chunk_kernel<256>, grid, dim3(kAttnThreads), lds, s, p); break;
         default: hipLaunchKernelGGL(gqa_chunk_kernel<0>, grid, dim3(kAttnThreads), lds, s, p); break;
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL(gqa_combine_kernel, dim3(p.nq), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(gqa_combine_kernel, dim3(p.nq), dim3(combine_threads(p.head_dim)), 0, s, p, slots);
     return hipGetLastError();
 }
 
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx) {
     if (nkv <= 0 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || head_dim <= 0) return false;
     if (max_ctx < 1 || max_ctx > kAttnMaxCtx) return false;
+    if (attn_hd_class(head_dim) == 0 && head_dim > 256) return false;  // items per thread of AttnRun<0>
     return gqa_lds_bytes(nq / nkv, head_dim) + 2 * sizeof(float) * head_dim <= 64 * 1024;
 }
 

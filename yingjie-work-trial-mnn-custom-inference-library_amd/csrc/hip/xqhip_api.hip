@@ -567,7 +567,7 @@ int xqhip_gqa_decode(const float* q, const void* k_cache, const void* v_cache, c
     p.max_ctx = max_ctx;
     p.pos = pos;
     p.out = out;
-    // workspace: part_m [nq][256], part_l [nq][256], part_o [nq][256][head_dim]
+    // workspace: part_m [nq][slots], part_l [nq][slots], part_o [nq][slots][head_dim]
     float* f = static_cast<float*>(workspace);
     const size_t per = xqhip::gqa_workspace_bytes(nq, nkv, head_dim) / sizeof(float) / (head_dim + 2);
     p.part_m = f;

@@ -28,6 +28,9 @@ double elapsed_ms(void* a, void* b) {
 
 }  // namespace
 
+#define XQ_CALL(expr, what) \
+    if ((expr) != 0) return fail_hip(error, what)
+
 DeviceModel::~DeviceModel() {
     if (stream_) xqhip_stream_synchronize(stream_);
     if (g_prefill_) xqhip_graph_destroy(g_prefill_);
@@ -196,9 +199,16 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     eps_ = manifest_float(js, "rms_norm_eps", eps_);
     theta_ = manifest_float(js, "rope_theta", theta_);
     const int n_layers = manifest_int(js, "num_hidden_layers", 32);
-    // KV capacity: the reference grows its caches without bound; here they are
-    // allocated once, for at least 8192 positions and at most 16384.
-    max_ctx_ = std::min(16384, std::max(8192, max_context));
+    // KV capacity: the reference grows its caches as tokens arrive
+    // (custom_model.cpp:616-622, 673-733); here they start at
+    // max(8192, max_context_tokens) positions and double when a prompt or a
+    // decode position needs more (ensure_capacity), up to kMaxContext.
+    if (max_context > kMaxContext) {
+        *error = "max_context_tokens " + std::to_string(max_context) + " exceeds the supported " +
+                 std::to_string(kMaxContext);
+        return false;
+    }
+    max_ctx_ = std::max(8192, max_context);
     if (hidden_ <= 0 || vocab_ <= 0 || n_layers < 0 || nq_ <= 0 || nkv_ <= 0 || hd_ <= 0 || nq_ % nkv_ != 0) {
         *error = "invalid model dimensions in xqwen35_manifest.json";
         return false;
@@ -260,11 +270,7 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     xqhip_fill_u8(argmax_ws_, 0, ws_argmax, stream_);
     xqhip_fill_u8(gqa_ws_, 0, ws_gqa, stream_);
     xqhip_fill_u8(d_ctrl_, 0, 16, stream_);
-    if (any_full && rot_active > 0) {
-        std::vector<float> tab(static_cast<size_t>(max_ctx_) * (rot_active / 2) * 2);
-        xqhip_rope_table(theta_, rot_active, max_ctx_, tab.data());
-        if (!upload_vec(tab, &rope_cs_, error)) return false;
-    }
+    if (any_full && !build_rope_table(error)) return false;
     (void)any_linear;
     max_proj_ = max_proj;
     attn_n_ = attn_n;
@@ -278,6 +284,56 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
             if (xqhip_event_create(&e) != 0) return fail_hip(error, "event");
     reset_state();
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "load sync");
+}
+
+bool DeviceModel::build_rope_table(std::string* error) {
+    const int rot_active = std::max(0, std::min(hd_, rot_));
+    if (rot_active <= 0) return true;
+    if (rope_cs_) release(rope_cs_);
+    rope_cs_ = nullptr;
+    std::vector<float> tab(static_cast<size_t>(max_ctx_) * (rot_active / 2) * 2);
+    xqhip_rope_table(theta_, rot_active, max_ctx_, tab.data());
+    return upload_vec(tab, &rope_cs_, error);
+}
+
+void DeviceModel::release(void* p) {
+    auto it = std::find(allocations_.begin(), allocations_.end(), p);
+    if (it != allocations_.end()) allocations_.erase(it);
+    xqhip_free(p);
+}
+
+// Grows the KV caches (and the RoPE table) to hold `positions` positions:
+// capacity doubles, the cached prefix is copied, and the step graphs, which
+// hold the old addresses, are captured again on their next use.
+bool DeviceModel::ensure_capacity(size_t positions, std::string* error) {
+    if (positions <= static_cast<size_t>(max_ctx_)) return true;
+    if (positions > static_cast<size_t>(kMaxContext)) {
+        *error = "context of " + std::to_string(positions) + " tokens exceeds the supported " +
+                 std::to_string(kMaxContext);
+        return false;
+    }
+    if (!sync(nullptr, error)) return false;
+    const int old_ctx = max_ctx_;
+    const int new_ctx = static_cast<int>(std::min<size_t>(kMaxContext, std::max<size_t>(positions, 2 * static_cast<size_t>(old_ctx))));
+    const size_t row = static_cast<size_t>(nkv_) * hd_;
+    for (Layer& L : layers_) {
+        if (!L.full) continue;
+        for (void** cache : {&L.k_cache, &L.v_cache}) {
+            uint16_t* grown = nullptr;
+            if (!alloc(&grown, static_cast<size_t>(new_ctx) * row, error)) return false;
+            XQ_CALL(xqhip_memcpy_d2d(grown, *cache, sizeof(uint16_t) * static_cast<size_t>(old_ctx) * row, stream_),
+                    "KV cache copy");
+            release(*cache);
+            *cache = grown;
+        }
+    }
+    max_ctx_ = new_ctx;
+    if (!build_rope_table(error)) return false;
+    for (void** g : {&g_prefill_, &g_sample_, &g_forward_}) {
+        if (*g) xqhip_graph_destroy(*g);
+        *g = nullptr;
+    }
+    return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "KV cache growth");
 }
 
 void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past the position are never read)
@@ -325,8 +381,6 @@ void DeviceModel::flush_timed(KernelTrace* trace) {
     event_next_ = 0;
 }
 
-#define XQ_CALL(expr, what) \
-    if ((expr) != 0) return fail_hip(error, what)
 
 bool DeviceModel::enqueue_embed(const int32_t* token_dev, bool timed, std::string* error) {
     op_begin(timed, "embedding_bf16_row_read");
@@ -533,10 +587,7 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
         *error = "custom prefill requires prompt tokens";
         return false;
     }
-    if (n_tokens > static_cast<size_t>(max_ctx_)) {
-        *error = "prompt longer than the KV capacity (" + std::to_string(max_ctx_) + " tokens)";
-        return false;
-    }
+    if (!ensure_capacity(n_tokens, error)) return false;
     for (size_t i = 0; i < n_tokens; ++i) {
         // std::abs(INT_MIN) has no positive value: the reference's row offset
         // turns negative and its read fails (custom_model.cpp:573-597)
@@ -626,11 +677,7 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         *error = "lm_head matrix is not loaded";
         return false;
     }
-    if (position >= static_cast<size_t>(max_ctx_)) {
-        *error = "context position " + std::to_string(position) + " exceeds the KV capacity (" +
-                 std::to_string(max_ctx_) + " tokens)";
-        return false;
-    }
+    if (!ensure_capacity(position + 1, error)) return false;
     if (!ensure_graphs(error)) return false;
     // The previous step's forward pass may still be running: h_tok_[0..1] are
     // free again because their upload preceded that step's sampling, which the

@@ -85,6 +85,9 @@ private:
     template <typename T>
     bool alloc(T** p, size_t count, std::string* error);
     bool load_layer(int index, Layer* L, std::string* error);
+    bool build_rope_table(std::string* error);
+    bool ensure_capacity(size_t positions, std::string* error);
+    void release(void* p);
 
     // enqueue one token through all layers (reads pos from d_ctrl_[0])
     bool enqueue_layers(bool timed, std::string* error);
@@ -105,7 +108,8 @@ private:
     int lk_hd_ = 128, lv_hd_ = 128, lk_n_ = 16, lv_n_ = 32, ksize_ = 4, lk_dim_ = 2048, lv_dim_ = 4096;
     int conv_dim_ = 8192;
     float eps_ = 1.0e-6f, theta_ = 10000000.0f;
-    int max_ctx_ = 8192;
+    static constexpr int kMaxContext = 1 << 20;  // the attention kernels' limit
+    int max_ctx_ = 8192;                          // KV capacity (positions), grows on demand
     std::string model_dir_, backend_request_, device_name_;
     uint64_t weight_bytes_ = 0;
     int inexact_meta_ = 0;
