@@ -438,9 +438,11 @@ def bench_decode(args):
     bytes_lm = w4_bytes(248320, hidden) + hidden * 4
     info = sess.json("xq_get_backend_info")[1]
     wbytes = int(info.split("weight_bytes_per_token=")[1].split(";")[0]) if "weight_bytes_per_token=" in info else 0
-    proj = projection_table(4, n=200)
-    t_gu = next(p["avg_us"] for p in proj if p["name"] == "gate_up") * 1e-3
-    ach = bytes_gu / (t_gu * 1e-3) / 1e9
+    # --no-projections (profiling runs: only the decode path's own kernels in
+    # the trace) leaves the roofline fields null
+    proj = [] if args.no_projections else projection_table(4, n=200)
+    t_gu = next((p["avg_us"] for p in proj if p["name"] == "gate_up"), None)
+    ach = bytes_gu / (t_gu * 1e-6) / 1e9 if t_gu else None
     gemv_us = sum(p["avg_us"] * PROJ_PER_STEP[p["name"]] for p in proj)
     gemv_bytes = sum(p["bytes"] * PROJ_PER_STEP[p["name"]] for p in proj)
     step_ms = step["mean_ms"] if step else ms_per_step
@@ -460,19 +462,20 @@ def bench_decode(args):
                    "weight_stream_GBps": round(wbytes / (step_ms * 1e-3) / 1e9, 1),
                    "prefill_ms": round(prefill_ms, 2), "prefill_tokens_per_s": round(prompt_len / prefill_ms * 1e3, 1),
                    "model_write_s": round(gen_s, 1), "load_s": round(load_s, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1) if ach else None, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4) if ach else None, "traffic": None,
                      "kernel": f"{GATE_UP_KERNEL}: gate/up 24576x4096 W4A16 g64 + RMSNorm prologue + SiLU*up "
                                "epilogue",
                      "method": "HIP events on the launch stream around 200 back-to-back launches on rotated weight "
                                "copies (> 2x the last-level cache); algorithmic bytes = codes + fp16 (scale, zero) per "
                                "group + x + y",
-                     "bytes_per_launch": bytes_gu, "avg_launch_us": round(t_gu * 1e3, 2), "launches_timed": 200,
+                     "bytes_per_launch": bytes_gu, "avg_launch_us": t_gu, "launches_timed": 200 if proj else 0,
                      "per_projection": [{k: p[k] for k in ("name", "rows", "cols", "prologue", "epilogue", "avg_us",
                                                            "bytes", "GBps", "frac")} for p in proj],
                      "projections_per_step": {"launches": sum(PROJ_PER_STEP.values()), "bytes": gemv_bytes,
                                               "sum_avg_us": round(gemv_us, 1),
-                                              "frac": round(gemv_bytes / (gemv_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)},
+                                              "frac": round(gemv_bytes / (gemv_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)
+                                              if gemv_us else None},
                      "in_model_avg_us": {"gate_up": round(gu["mean_ms"] * 1e3, 2) if gu else None,
                                          "down_proj": round(dn["mean_ms"] * 1e3, 2) if dn else None,
                                          "lm_head_argmax": round(lm["mean_ms"] * 1e3, 2) if lm else None},
@@ -563,6 +566,8 @@ def main():
     ap.add_argument("--bits", type=int, nargs="+", default=[4, 3, 2], help="gemv-sweep code widths")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--no-projections", action="store_true",
+                    help="decode: skip the per-projection GEMV table (roofline fields null; for kernel traces)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:

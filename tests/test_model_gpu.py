@@ -211,6 +211,37 @@ def test_decode_before_prefill_and_context_capacity(small_dir):
     assert st == xb.XQ_ERR_NOT_READY and b"prefill" in m.error
 
 
+def test_kv_cache_growth_keeps_results(small_dir):
+    """KV caches start at max(8192, max_context_tokens) positions and double
+    when a position needs more (the reference grows its caches as tokens
+    arrive, custom_model.cpp:616-622, 673-733).  A session that grows from
+    8192 in the middle of decoding must produce the same ids and hidden states,
+    bit for bit, as one sized for the whole context from the start; and a
+    context beyond the kernels' 2^20 positions is refused at load."""
+    prompt = [int(t) for t in np.random.default_rng(8188).integers(0, 4096, 8188)]
+    runs = []
+    for max_ctx in (8192, 16384):
+        s = xb.Session(small_dir, xb.options(max_context=max_ctx))
+        assert s.status == xb.XQ_OK
+        st, _ = s.prefill(prompt)
+        assert st == 0
+        toks, hs = [], []
+        for _ in range(8):  # positions 8188 .. 8195 cross the 8192 boundary
+            st, tok, m = s.decode_one()
+            assert st == 0, m.error
+            toks.append(tok)
+            hs.append(s.hidden()[1])
+        info = s.json("xq_get_backend_info")[1]
+        runs.append((toks, hs, info))
+        s.close()
+    assert runs[0][0] == runs[1][0]
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert np.array_equal(a, b)
+    assert "kv_capacity=16384" in runs[0][2] and "kv_capacity=16384" in runs[1][2]
+    s = xb.Session(small_dir, xb.options(max_context=(1 << 20) + 1))
+    assert s.status == xb.XQ_ERR_MODEL
+
+
 def test_selftest_entry_point():
     import ctypes
     buf = ctypes.create_string_buffer(1 << 16)
