@@ -299,7 +299,7 @@ MODEL_DIR = os.environ.get("XQ_BENCH_MODEL_DIR", "/tmp/xq_synth_9b_w4a16_g64")
 # the same counter reads for a plain device-to-device copy of known size.
 # ---------------------------------------------------------------------------
 PMC_COPY_BYTES = 64 << 20
-GATE_UP_KERNEL = "gemv_w4_tiled<1, 12, 2, 2, 4>"  # NCH=1, 12 row groups, 2 rows per wave, SiLU pair, 4-bit codes
+GATE_UP_KERNEL = "gemv_w4_tiled<1, 12, 2, 2, 4, 0>"  # NCH=1, 12 row groups, 2 rows per wave, SiLU pair, 4-bit codes, fp16 metadata
 
 
 def pmc_probe(args):

@@ -47,8 +47,12 @@ enum {
     XQHIP_LAYOUT_TILED64 = 0, /* group 64, cols % 64 == 0: 16-byte chunks of each row
                                  permuted so a wave's loads are contiguous; per-group
                                  (fp16 scale, fp16 zero) packed in one u32          */
-    XQHIP_LAYOUT_GENERIC = 1  /* any group size: reference row-major nibbles, fp32
+    XQHIP_LAYOUT_GENERIC = 1, /* any group size: reference row-major nibbles, fp32
                                  scales and zeros (used only for tiny shapes)        */
+    XQHIP_LAYOUT_TILED64_F32META = 2 /* TILED64 codes with the reference's fp32
+                                 (scale, zero) per group (8 bytes): chosen when a
+                                 value is not exact in fp16 (e.g. asymmetric scales
+                                 (max - min) / 15)                                  */
 };
 
 /* A W4A16 matrix resident in HBM.  Semantics of the reference QuantizedMatrix
@@ -62,7 +66,8 @@ typedef struct xqhip_w4 {
     int32_t group;
     int32_t affine;
     int32_t layout;
-    int32_t inexact_meta; /* scales/zeros not exactly representable in fp16 (TILED64) */
+    int32_t inexact_meta; /* scales/zeros fp16 cannot hold exactly: kept in fp32
+                             (layout TILED64_F32META)                            */
     int32_t bits;         /* code width: 4 (xqhip_w4_upload), 3 or 2 (xqhip_wlb_upload) */
     void* nib;            /* device codes                                         */
     void* meta;           /* device per-group metadata                            */

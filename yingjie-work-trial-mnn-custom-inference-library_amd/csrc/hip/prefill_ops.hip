@@ -39,13 +39,18 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
 // 22 significant bits together) with every aligned run of 8 columns in the
 // order [0 4 1 5 2 6 3 7], the order in which the GEMM unpacks a word of 8
 // weight codes; xs[t][g] = fp32 sum of v over column group g (64 columns).
-// Rows m..m_pad-1 are zero-filled.
+// Each row is first scaled by a power of two, ts[t] = 2^k, that brings its
+// largest magnitude into [2^12, 2^13): fp16 then holds any fp32 activation
+// (silu(gate) * up of a large residual stream can exceed 65504) without
+// overflow or subnormal loss, and the GEMM multiplies its results by ts[t]
+// (exact).  Rows m..m_pad-1 are zero-filled (ts 1).
 // ---------------------------------------------------------------------------
 constexpr int kPrepMaxHeads = 256;
 
 __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x, int ldx, int m, int cols,
                                                      Prologue pro, int ldz, _Float16* __restrict__ xh,
-                                                     _Float16* __restrict__ xl, float* __restrict__ xs) {
+                                                     _Float16* __restrict__ xl, float* __restrict__ xs,
+                                                     float* __restrict__ ts) {
     __shared__ float red[32];
     __shared__ float head_inv[kPrepMaxHeads];
     const int t = blockIdx.x;
@@ -56,6 +61,7 @@ __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x
     if (t >= m) {
         for (int c = threadIdx.x; c < nch; c += blockDim.x) oh[c] = ol[c] = make_uint4(0u, 0u, 0u, 0u);
         for (int g = threadIdx.x; g < G; g += blockDim.x) os[g] = 0.0f;
+        if (threadIdx.x == 0) ts[t] = 1.0f;
         return;
     }
     const float* xr = x + static_cast<size_t>(t) * ldx;
@@ -79,9 +85,7 @@ __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x
         __syncthreads();
     }
     // one thread per 8 columns; the 8 threads of a group are consecutive lanes (nch % 8 == 0)
-    for (int c8 = threadIdx.x; c8 < nch; c8 += blockDim.x) {
-        const int c = c8 * 8;
-        float v[8];
+    auto load8 = [&](int c, float (&v)[8]) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = xr[c + e];
         if (pro.mode == PRO_RMS) {
@@ -93,6 +97,30 @@ __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = v[e] * ih * pro.w[d + e] * silu_dev(zr[c + e]);
         }
+    };
+    // the row's power-of-two scale from its largest magnitude
+    float mx = 0.0f;
+    for (int c8 = threadIdx.x; c8 < nch; c8 += blockDim.x) {
+        float v[8];
+        load8(c8 * 8, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+    }
+    mx = wave_max(mx);
+    __syncthreads();  // red may still be read by the norm's block_sum
+    if (lane == 0) red[wid] = mx;
+    __syncthreads();
+    for (int i = 0; i < nw; ++i) mx = fmaxf(mx, red[i]);
+    int ex = 0;
+    frexpf(mx, &ex);                                       // mx = f 2^ex, f in [0.5, 1)
+    const float down = mx > 0.0f ? ldexpf(1.0f, 13 - ex) : 1.0f;  // mx * down in [2^12, 2^13)
+    if (threadIdx.x == 0) ts[t] = mx > 0.0f ? ldexpf(1.0f, ex - 13) : 1.0f;
+    for (int c8 = threadIdx.x; c8 < nch; c8 += blockDim.x) {
+        const int c = c8 * 8;
+        float v[8];
+        load8(c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] *= down;
         uint32_t ph[4], pl[4];
         float sum = 0.0f;
 #pragma unroll
@@ -150,6 +178,7 @@ struct GemmArgs {
     int rows, cols, affine;
     const _Float16* xh;  // [m_pad][cols], followed by xl [m_pad][cols]
     const float* xs;     // [m_pad][cols / 64]
+    const float* ts;     // [m_pad] per-token power-of-two scale of xh / xl / xs
     int m, m_pad;
     float* y;
     int ldy;
@@ -185,9 +214,10 @@ __device__ __forceinline__ half8 codes_to_h8(uint32_t w) {
 }
 
 // two waves per SIMD (at most 256 registers per lane), so one block's barrier wait overlaps another's work
-template <int WGR, int WGT, int TI, int TJ, int EPI>
+template <int WGR, int WGT, int TI, int TJ, int EPI, int META>
 __global__ void __launch_bounds__(kWave * WGR * WGT) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_w4_mfma_kernel(GemmArgs a) {
+    constexpr uint32_t kMetaBytes = META ? 8u : 4u;  // fp16 pair in a u32, or the fp32 pair
     using T = GemmTile<WGR, WGT, TI, TJ>;
     constexpr int BR = T::kBR, BT = T::kBT, XU = T::kXU, NT = T::kThreads;
     constexpr int kTokStep = NT / 16;  // tokens between a thread's x pieces
@@ -224,10 +254,10 @@ gemm_w4_mfma_kernel(GemmArgs a) {
                    (c16 & 7) * 8u) * 2u;
     const int xdst = xtok * kGemmXLd + c16 * 8;
     // scales: thread < BR stages row r0 + tid (the others load out of range: zero, no branch)
-    const __amdgpu_buffer_rsrc_t meta_r = buf_rsrc(a.meta, static_cast<uint32_t>(a.rows) * G * 4u);
+    const __amdgpu_buffer_rsrc_t meta_r = buf_rsrc(a.meta, static_cast<uint32_t>(a.rows) * G * kMetaBytes);
     const bool s_thread = threadIdx.x < BR;
     const uint32_t moff =
-        s_thread ? static_cast<uint32_t>(min(r0 + static_cast<int>(threadIdx.x), a.rows - 1)) * G * 4u : kBufOOB;
+        s_thread ? static_cast<uint32_t>(min(r0 + static_cast<int>(threadIdx.x), a.rows - 1)) * G * kMetaBytes : kBufOOB;
 
 #define GEMM_LOAD_A(W, gg)                                                                                   \
     {                                                                                                        \
@@ -242,14 +272,14 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         const uint32_t g_ = static_cast<uint32_t>(gg);                                                       \
         _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) X[j_] =                                            \
             __builtin_amdgcn_raw_buffer_load_b128(x_r, xoff[j_], g_ * 128u, 0);                              \
-        M = __builtin_amdgcn_raw_buffer_load_b32(meta_r, moff, g_ * 4u, 0);                                   \
+        M = __builtin_amdgcn_raw_buffer_load_b32(meta_r, moff, g_ * kMetaBytes, 0);                           \
     }
 #define GEMM_STORE_X(X, M, st)                                                                               \
     {                                                                                                        \
         _Float16* d_ = xlds + (st) * T::kXStage + xdst;                                                      \
         _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) *reinterpret_cast<u32x4*>(d_ + j_ * kTokStep * kGemmXLd) = \
             X[j_];                                                                                           \
-        if (s_thread) slds[(st) * BR + threadIdx.x] = half_lo(M);                                            \
+        if (s_thread) slds[(st) * BR + threadIdx.x] = META ? __uint_as_float(M) : half_lo(M);                 \
     }
 // MFMAs of one group, each tile's four chained into a per-group sum that is scaled into acc
 #define GEMM_COMPUTE(st, W)                                                                                  \
@@ -324,14 +354,20 @@ gemm_w4_mfma_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t xs_r = buf_rsrc(a.xs, static_cast<uint32_t>(a.m_pad) * G * 4u);
     for (int gb = 0; gb < G; gb += 32) {
         const int g8 = gb + 8 * q;
-        uint32_t mw[TI][8], xw[TJ][8];
+        MetaWord<META> mw[TI][8];
+        uint32_t xw[TJ][8];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
-            const uint32_t off =
-                (static_cast<uint32_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * G + static_cast<uint32_t>(g8)) * 4u;
+            const uint32_t off = (static_cast<uint32_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * G +
+                                  static_cast<uint32_t>(g8)) * kMetaBytes;
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                mw[i][e] = __builtin_amdgcn_raw_buffer_load_b32(meta_r, g8 + e < G ? off + 4u * e : kBufOOB, 0, 0);
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t o = g8 + e < G ? off + kMetaBytes * e : kBufOOB;
+                if constexpr (META)
+                    mw[i][e] = __builtin_amdgcn_raw_buffer_load_b64(meta_r, o, 0, 0);
+                else
+                    mw[i][e] = __builtin_amdgcn_raw_buffer_load_b32(meta_r, o, 0, 0);
+            }
         }
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
@@ -345,8 +381,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const uint32_t w = mw[i][e];
-                const float sc = half_lo(w), z = half_hi(w);
+                const float sc = meta_scale(mw[i][e]), z = meta_zero(mw[i][e]);
                 const float c0 = 64.0f * (a.affine ? fmaf(8.0f, sc, z) : (8.0f - z) * sc);
                 ch[i][e] = static_cast<_Float16>(c0);
                 cl[i][e] = static_cast<_Float16>(c0 - static_cast<float>(ch[i][e]));
@@ -377,6 +412,9 @@ gemm_w4_mfma_kernel(GemmArgs a) {
             const int t = t0 + wt + j * 16 + lr;
             const int rb = r0 + wr + i * 16 + 4 * q;
             if (t >= a.m) continue;
+            const float tsc = a.ts[t];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[i][j][v] *= tsc;
             float* yr = a.y + static_cast<size_t>(t) * a.ldy;
             if constexpr (EPI == 2) {  // interleaved (gate, up) rows -> silu(gate) * up
 #pragma unroll
@@ -397,28 +435,29 @@ gemm_w4_mfma_kernel(GemmArgs a) {
 
 size_t gemm_workspace_bytes(int m, int cols) {
     const size_t m_pad = static_cast<size_t>((m + kGemmPad - 1) / kGemmPad) * kGemmPad;
-    return m_pad * static_cast<size_t>(cols) * (2 * sizeof(_Float16)) + m_pad * static_cast<size_t>(cols / 64) * sizeof(float);
+    return m_pad * static_cast<size_t>(cols) * (2 * sizeof(_Float16)) +
+           m_pad * static_cast<size_t>(cols / 64) * sizeof(float) + m_pad * sizeof(float);
 }
 
 bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro) {
-    if (layout != 0 || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0) return false;
+    if ((layout != 0 && layout != 2) || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0) return false;
     if (pro.mode == PRO_GATED)
         return pro.head_dim > 0 && pro.head_dim % 8 == 0 && cols % pro.head_dim == 0 &&
                cols / pro.head_dim <= kPrepMaxHeads;
     return true;
 }
 
-template <int WGR, int WGT, int TI, int TJ, int EPI>
+template <int WGR, int WGT, int TI, int TJ, int EPI, int META>
 static hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
     using T = GemmTile<WGR, WGT, TI, TJ>;
-    const auto fn = reinterpret_cast<const void*>(&gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI>);
+    const auto fn = reinterpret_cast<const void*>(&gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI, META>);
     if constexpr (T::kLds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
         if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(T::kLds));
             e != hipSuccess)
             return e;
     }
     const dim3 grid((a.m + T::kBT - 1) / T::kBT, (a.rows + T::kBR - 1) / T::kBR);
-    hipLaunchKernelGGL((gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI>), grid, dim3(T::kThreads), T::kLds, s, a);
+    hipLaunchKernelGGL((gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI, META>), grid, dim3(T::kThreads), T::kLds, s, a);
     return hipGetLastError();
 }
 
@@ -427,16 +466,18 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     _Float16* xh = static_cast<_Float16*>(p.workspace);
     _Float16* xl = xh + static_cast<size_t>(m_pad) * p.cols;
     float* xs = reinterpret_cast<float*>(xl + static_cast<size_t>(m_pad) * p.cols);
+    float* ts = xs + static_cast<size_t>(m_pad) * (p.cols / 64);
     hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
-                       xs);
+                       xs, ts);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xs, p.m, m_pad, p.y,
-                     p.ldy};
+    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xs, ts, p.m, m_pad,
+                     p.y, p.ldy};
     // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
+    const bool m32 = p.layout == 2;
     switch (p.epi) {
-        case 0: return launch_gemm_cfg<4, 1, 2, 4, 0>(a, s);
-        case 1: return launch_gemm_cfg<4, 1, 2, 4, 1>(a, s);
-        case 2: return launch_gemm_cfg<4, 1, 2, 4, 2>(a, s);
+        case 0: return m32 ? launch_gemm_cfg<4, 1, 2, 4, 0, 1>(a, s) : launch_gemm_cfg<4, 1, 2, 4, 0, 0>(a, s);
+        case 1: return m32 ? launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, s) : launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, s);
+        case 2: return m32 ? launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, s) : launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -216,6 +216,29 @@ int xqhip_event_elapsed_ms(void* start, void* stop, float* ms) {
                  "hipEventElapsedTime");
 }
 
+// fp16 (scale, zero) pairs of the TILED64 layout; returns the count of inexact values.
+static int pack_meta_f16(const float* scales, const float* zeros, size_t n, std::vector<uint32_t>* out) {
+    out->resize(n);
+    int inexact = 0;
+    for (size_t i = 0; i < n; ++i) {
+        bool e1, e2;
+        const uint16_t s = f32_to_f16_bits(scales[i], &e1);
+        const uint16_t z = f32_to_f16_bits(zeros[i], &e2);
+        inexact += (!e1) + (!e2);
+        (*out)[i] = static_cast<uint32_t>(s) | (static_cast<uint32_t>(z) << 16);
+    }
+    return inexact;
+}
+
+// fp32 (scale, zero) pairs of the TILED64_F32META layout, two words per group.
+static void pack_meta_f32(const float* scales, const float* zeros, size_t n, std::vector<uint32_t>* out) {
+    out->resize(2 * n);
+    for (size_t i = 0; i < n; ++i) {
+        std::memcpy(&(*out)[2 * i], &scales[i], 4);
+        std::memcpy(&(*out)[2 * i + 1], &zeros[i], 4);
+    }
+}
+
 // Reference layout (custom_model.cpp:218-262) -> device layout.
 // TILED64: within each row the 16-byte half-groups are reordered so that, for
 // chunk c of up to 64 groups (gc of them), half h of group c*64+l lands at
@@ -260,16 +283,12 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
             }
         }
         nib_src = nib_host.data();
-        meta_u32.resize(static_cast<size_t>(rows) * G);
-        int inexact = 0;
-        for (size_t i = 0; i < meta_u32.size(); ++i) {
-            bool e1, e2;
-            const uint16_t s = f32_to_f16_bits(scales[i], &e1);
-            const uint16_t z = f32_to_f16_bits(zeros[i], &e2);
-            inexact += (!e1) + (!e2);
-            meta_u32[i] = static_cast<uint32_t>(s) | (static_cast<uint32_t>(z) << 16);
+        const size_t n_meta = static_cast<size_t>(rows) * G;
+        out->inexact_meta = pack_meta_f16(scales, zeros, n_meta, &meta_u32);
+        if (out->inexact_meta > 0) {  // keep the reference's fp32 values
+            pack_meta_f32(scales, zeros, n_meta, &meta_u32);
+            out->layout = XQHIP_LAYOUT_TILED64_F32META;
         }
-        out->inexact_meta = inexact;
         out->meta_bytes = meta_u32.size() * 4;
         meta_src = meta_u32.data();
     } else {
@@ -296,20 +315,6 @@ int xqhip_w4_free(xqhip_w4* w) {
     int rc2 = xqhip_free(w->meta);
     w->nib = w->meta = nullptr;
     return rc ? rc : rc2;
-}
-
-// fp16 (scale, zero) pairs of the TILED64 layout; returns the count of inexact values.
-static int pack_meta_f16(const float* scales, const float* zeros, size_t n, std::vector<uint32_t>* out) {
-    out->resize(n);
-    int inexact = 0;
-    for (size_t i = 0; i < n; ++i) {
-        bool e1, e2;
-        const uint16_t s = f32_to_f16_bits(scales[i], &e1);
-        const uint16_t z = f32_to_f16_bits(zeros[i], &e2);
-        inexact += (!e1) + (!e2);
-        (*out)[i] = static_cast<uint32_t>(s) | (static_cast<uint32_t>(z) << 16);
-    }
-    return inexact;
 }
 
 static int upload_pair(xqhip_w4* out, const void* nib, const void* meta) {
@@ -376,6 +381,10 @@ int xqhip_wlb_upload(const uint8_t* bitstream, const float* scales, const float*
     }
     std::vector<uint32_t> meta;
     out->inexact_meta = pack_meta_f16(scales, zeros, n_meta, &meta);
+    if (out->inexact_meta > 0) {  // keep the reference's fp32 values
+        pack_meta_f32(scales, zeros, n_meta, &meta);
+        out->layout = XQHIP_LAYOUT_TILED64_F32META;
+    }
     out->meta_bytes = meta.size() * 4;
     return upload_pair(out, dev.data(), meta.data());
 }
@@ -385,7 +394,10 @@ uint64_t xqhip_w4_weight_bytes(const xqhip_w4* w) { return w ? w->nib_bytes + w-
 static int validate_w4(const xqhip_w4* w, const char* who) {
     if (!w || !w->nib || !w->meta || w->rows <= 0 || w->cols <= 0)
         return fail(XQHIP_EINVAL, "%s: matrix is not uploaded", who);
-    if (w->layout == XQHIP_LAYOUT_TILED64 && (w->group != 64 || w->cols % 64 != 0 || w->cols / 64 > 256))
+    if (w->layout != XQHIP_LAYOUT_TILED64 && w->layout != XQHIP_LAYOUT_GENERIC &&
+        w->layout != XQHIP_LAYOUT_TILED64_F32META)
+        return fail(XQHIP_EINVAL, "%s: unknown layout %d", who, w->layout);
+    if (w->layout != XQHIP_LAYOUT_GENERIC && (w->group != 64 || w->cols % 64 != 0 || w->cols / 64 > 256))
         return fail(XQHIP_EINVAL, "%s: inconsistent TILED64 matrix %dx%d g%d", who, w->rows, w->cols, w->group);
     if (w->bits != 4 && w->bits != 3 && w->bits != 2)
         return fail(XQHIP_EINVAL, "%s: unsupported code width %d", who, w->bits);
@@ -415,7 +427,7 @@ static int validate_prologue(const xqhip_prologue* pro, int cols, const char* wh
 
 // The TILED64 kernels read x and the prologue vectors with 16-byte loads.
 static int validate_alignment(const xqhip_w4* w, const void* x, const xqhip_prologue* pro, const char* who) {
-    if (w->layout != XQHIP_LAYOUT_TILED64) return XQHIP_OK;
+    if (w->layout == XQHIP_LAYOUT_GENERIC) return XQHIP_OK;
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     if (!a16(x)) return fail(XQHIP_EINVAL, "%s: x must be 16-byte aligned", who);
     if (pro && pro->mode != XQHIP_PRO_NONE && !a16(pro->weight))
@@ -683,6 +695,7 @@ int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xq
     p.rows = w->rows;
     p.cols = w->cols;
     p.affine = w->affine;
+    p.layout = w->layout;
     p.x = x;
     p.ldx = ldx;
     p.m = m;

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace xqhip {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -47,6 +49,16 @@ __device__ __forceinline__ float half_lo(uint32_t u) {
 __device__ __forceinline__ float half_hi(uint32_t u) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16)));
 }
+
+// Group metadata word of a TILED64 matrix: fp16 (scale, zero) in one u32
+// (META 0) or the fp32 (scale, zero) pair in two (META 1, matrices whose values
+// fp16 cannot hold exactly).
+template <int META>
+using MetaWord = typename std::conditional<META != 0, u32x2, uint32_t>::type;
+__device__ __forceinline__ float meta_scale(uint32_t m) { return half_lo(m); }
+__device__ __forceinline__ float meta_zero(uint32_t m) { return half_hi(m); }
+__device__ __forceinline__ float meta_scale(u32x2 m) { return __uint_as_float(m.x); }
+__device__ __forceinline__ float meta_zero(u32x2 m) { return __uint_as_float(m.y); }
 
 // Range-checked buffer loads: an offset at or past the resource's byte range
 // returns 0 without a memory access, so a load can be issued unconditionally

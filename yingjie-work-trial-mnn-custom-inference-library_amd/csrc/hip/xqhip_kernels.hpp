@@ -156,6 +156,7 @@ struct GemmLaunch {
     const uint8_t* nib;  // TILED64 matrix
     const void* meta;
     int rows, cols, affine;
+    int layout;      // 0 TILED64 (fp16 metadata), 2 TILED64_F32META
     const float* x;  // [m][ldx]
     int ldx, m;
     Prologue pro;  // per token; PRO_GATED reads pro.z + t * ldz

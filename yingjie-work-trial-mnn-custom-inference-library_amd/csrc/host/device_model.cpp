@@ -484,7 +484,7 @@ bool DeviceModel::alloc_prefill_buffers(std::string* error) {
     bool ok = hidden_ % 4 == 0 && inter_ % 4 == 0 && attn_n_ % 4 == 0 && max_proj_ % 4 == 0;
     for (const Layer& L : layers_) {
         for (const xqhip_w4* w : {&L.in_proj, &L.out_proj, &L.gate_up, &L.down})
-            ok = ok && w->layout == XQHIP_LAYOUT_TILED64;
+            ok = ok && w->layout != XQHIP_LAYOUT_GENERIC;
         if (!L.full) ok = ok && lk_hd_ <= 256 && lv_n_ % lk_n_ == 0 && ksize_ >= 1 && ksize_ <= 8 && lv_hd_ % 8 == 0;
     }
     ok = ok && (nq_ / nkv_) <= 8;
