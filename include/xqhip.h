@@ -69,6 +69,8 @@ typedef struct xqhip_w4 {
     int32_t inexact_meta; /* scales/zeros fp16 cannot hold exactly: kept in fp32
                              (layout TILED64_F32META)                            */
     int32_t bits;         /* code width: 4 (xqhip_w4_upload), 3 or 2 (xqhip_wlb_upload) */
+    int32_t zero_is_8;    /* affine == 0 and every zero is 8: w = (q - 8) s, so the
+                             zero-point term of the prefill GEMM vanishes          */
     void* nib;            /* device codes                                         */
     void* meta;           /* device per-group metadata                            */
     uint64_t nib_bytes;

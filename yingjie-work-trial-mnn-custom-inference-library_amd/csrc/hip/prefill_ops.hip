@@ -176,6 +176,7 @@ struct GemmArgs {
     const uint8_t* nib;
     const uint32_t* meta;
     int rows, cols, affine;
+    int zero_is_8;       // c0 = (8 - z) s is 0 for every group: the c0 pass is skipped
     const _Float16* xh;  // [m_pad][cols], followed by xl [m_pad][cols]
     const float* xs;     // [m_pad][cols / 64]
     const float* ts;     // [m_pad] per-token power-of-two scale of xh / xl / xs
@@ -352,7 +353,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
     // c0 term: K = G, lane group q takes groups gb + 8 q + 0..7 of its row / token.  All loads of a
     // chunk are issued before any use; groups past G read out of range (zero), so c0 and xs are 0.
     const __amdgpu_buffer_rsrc_t xs_r = buf_rsrc(a.xs, static_cast<uint32_t>(a.m_pad) * G * 4u);
-    for (int gb = 0; gb < G; gb += 32) {
+    for (int gb = 0; gb < (a.zero_is_8 ? 0 : G); gb += 32) {
         const int g8 = gb + 8 * q;
         MetaWord<META> mw[TI][8];
         uint32_t xw[TJ][8];
@@ -470,8 +471,8 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
                        xs, ts);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, xh, xs, ts, p.m, m_pad,
-                     p.y, p.ldy};
+    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.zero_is_8, xh, xs, ts,
+                     p.m, m_pad, p.y, p.ldy};
     // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
     const bool m32 = p.layout == 2;
     switch (p.epi) {

@@ -230,6 +230,15 @@ static int pack_meta_f16(const float* scales, const float* zeros, size_t n, std:
     return inexact;
 }
 
+// 1 when w = (q - 8) s for every group (format v1 with zero 8): the GEMM's
+// zero-point term (8 - z) s x-sum is then identically 0.
+static int32_t zero_is_8(const float* zeros, size_t n, int affine) {
+    if (affine) return 0;
+    for (size_t i = 0; i < n; ++i)
+        if (zeros[i] != 8.0f) return 0;
+    return 1;
+}
+
 // fp32 (scale, zero) pairs of the TILED64_F32META layout, two words per group.
 static void pack_meta_f32(const float* scales, const float* zeros, size_t n, std::vector<uint32_t>* out) {
     out->resize(2 * n);
@@ -258,6 +267,7 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
     out->bits = 4;
     const size_t row_bytes = (static_cast<size_t>(cols) + 1) / 2;
     const int G = (cols + group - 1) / group;
+    out->zero_is_8 = zero_is_8(zeros, static_cast<size_t>(rows) * G, out->affine);
     const bool tiled = group == 64 && cols % 64 == 0 && G <= 256;
     out->layout = tiled ? XQHIP_LAYOUT_TILED64 : XQHIP_LAYOUT_GENERIC;
     out->nib_bytes = row_bytes * rows;
@@ -342,6 +352,7 @@ int xqhip_wlb_upload(const uint8_t* bitstream, const float* scales, const float*
     const int G = (cols + group - 1) / group;
     const size_t n_meta = static_cast<size_t>(rows) * G;
     const size_t total_bytes = (static_cast<size_t>(rows) * cols * bits + 7) / 8;
+    out->zero_is_8 = zero_is_8(zeros, n_meta, out->affine);
     if (!(group == 64 && cols % 64 == 0 && G <= 256)) {
         // GENERIC: the bitstream as it is, fp32 scales then zeros
         out->layout = XQHIP_LAYOUT_GENERIC;
@@ -696,6 +707,7 @@ int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xq
     p.cols = w->cols;
     p.affine = w->affine;
     p.layout = w->layout;
+    p.zero_is_8 = w->zero_is_8;
     p.x = x;
     p.ldx = ldx;
     p.m = m;

@@ -157,6 +157,7 @@ struct GemmLaunch {
     const void* meta;
     int rows, cols, affine;
     int layout;      // 0 TILED64 (fp16 metadata), 2 TILED64_F32META
+    int zero_is_8;   // w = (q - 8) s everywhere: no zero-point term
     const float* x;  // [m][ldx]
     int ldx, m;
     Prologue pro;  // per token; PRO_GATED reads pro.z + t * ldz

@@ -27,7 +27,7 @@ class W4(ctypes.Structure):
     """Mirror of xqhip_w4 (include/xqhip.h)."""
     _fields_ = [("rows", ctypes.c_int32), ("cols", ctypes.c_int32), ("group", ctypes.c_int32),
                 ("affine", ctypes.c_int32), ("layout", ctypes.c_int32), ("inexact_meta", ctypes.c_int32),
-                ("bits", ctypes.c_int32), ("nib", c_void_p), ("meta", c_void_p), ("nib_bytes", c_uint64), ("meta_bytes", c_uint64)]
+                ("bits", ctypes.c_int32), ("zero_is_8", ctypes.c_int32), ("nib", c_void_p), ("meta", c_void_p), ("nib_bytes", c_uint64), ("meta_bytes", c_uint64)]
 
 
 class Prologue(ctypes.Structure):
