@@ -264,8 +264,12 @@ XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, fl
  * matrix cores, attention and the linear-attention recurrence as batched
  * kernels.  Row-major [token][...] activations with explicit row strides. */
 
-/* Workspace bytes xqhip_gemm_w4a16 needs for m tokens of `cols` columns. */
-XQHIP_API size_t xqhip_gemm_workspace_bytes(int m, int cols);
+/* Workspace bytes xqhip_gemm_w4a16 needs for m tokens of `cols` columns and a
+ * matrix of `rows` rows (the staged x, plus the partial products of a launch
+ * whose columns are split over several blocks when it has too few blocks to
+ * fill the device; a workspace sized for the largest rows of a set of
+ * matrices serves them all). */
+XQHIP_API size_t xqhip_gemm_workspace_bytes(int m, int cols, int rows);
 /* y[t] (op)= W prologue(x[t]) for t < m: every token as xqhip_gemv_w4a16 does it
  * (same epilogues; EPI_SILU_PAIR writes rows/2 values per token), on a TILED64
  * matrix.  Per 64-column group the codes q - 8 (exact in fp16) multiply x held
@@ -273,7 +277,7 @@ XQHIP_API size_t xqhip_gemm_workspace_bytes(int m, int cols);
  * scaled by the group scale, and the zero-point term is added as the product of
  * the per-group offsets with the per-token group sums of x.  GATED_HEAD reads the gate
  * of token t at pro->gate + t * ld_gate.  workspace: 16-byte aligned,
- * xqhip_gemm_workspace_bytes(m, cols). */
+ * xqhip_gemm_workspace_bytes(m, cols, rows of w). */
 XQHIP_API int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro,
                                int ld_gate, float* y, int ldy, int epilogue, void* workspace, void* stream);
 /* xqhip_embed_bf16 for n tokens (device ids) into out[n][hidden]. */

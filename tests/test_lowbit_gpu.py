@@ -119,7 +119,7 @@ def test_lowbit_rejected_by_prefill_gemm_and_bad_widths():
     w = upload(q, 3)
     x = xb.DeviceBuffer(4 * 256 * 4)
     y = xb.DeviceBuffer(4 * 64 * 4)
-    ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(4, 256))
+    ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(4, 256, 64))
     rc = xb.hip().xqhip_gemm_w4a16(w.ref, x.ptr, 4, 256, None, 0, y.ptr, 64, xb.EPI_STORE, ws.ptr, None)
     assert rc != 0 and b"4-bit" in xb.hip().xqhip_last_error()
     bad = xb.W4()

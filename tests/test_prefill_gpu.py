@@ -51,7 +51,7 @@ def run_gemm(q, X, epi, pro=None, gamma=None, z=None, head_dim=0, y0=None):
     w = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols, group=q.group, affine=q.affine)
     out_cols = q.rows // 2 if epi == xb.EPI_SILU_PAIR else q.rows
     ydev = dev(y0 if y0 is not None else np.zeros((m, out_cols), np.float32))
-    ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(m, cols))
+    ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(m, cols, q.rows))
     pr, ld_gate = None, 0
     if pro == "rms":
         pr = xb.prologue(xb.PRO_RMS, dev(gamma), eps=1e-6)

@@ -17,6 +17,8 @@
 //                        gates for all tokens, then the gated-delta recurrence
 //                        with the state in registers (one-pass kernels
 //                        linear_scan_wave_kernel / linear_scan_kernel otherwise)
+#include <algorithm>
+
 #include "xqhip_common.hpp"
 #include "xqhip_kernels.hpp"
 
@@ -180,6 +182,8 @@ struct GemmArgs {
     const _Float16* xh;  // [m_pad][cols], followed by xl [m_pad][cols]
     const float* xs;     // [m_pad][cols / 64]
     const float* ts;     // [m_pad] per-token power-of-two scale of xh / xl / xs
+    int gps;             // column groups per K split (blockIdx.z); the whole row when unsplit
+    float* part;         // split K: [gridDim.z][m][rows] partial products (the reduce applies EPI)
     int m, m_pad;
     float* y;
     int ldy;
@@ -227,6 +231,8 @@ gemm_w4_mfma_kernel(GemmArgs a) {
     float* slds = reinterpret_cast<float*>(xlds + 2 * T::kXStage);  // [2 stages][BR] scales
     const int t0 = blockIdx.x * BT, r0 = blockIdx.y * BR;
     const int G = a.cols >> 6, gl = G - 1;
+    // this block's column groups: [g0, g1) of the K split blockIdx.z
+    const int g0 = static_cast<int>(blockIdx.z) * a.gps, g1 = min(G, g0 + a.gps), glast = g1 - 1;
     const uint32_t row_bytes = static_cast<uint32_t>(a.cols) >> 1;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int q = lane >> 4, lr = lane & 15;
@@ -314,10 +320,10 @@ gemm_w4_mfma_kernel(GemmArgs a) {
 #define GEMM_STEP(U, W, X, M)                                                                                \
     {                                                                                                        \
         const int gg_ = g + (U);                                                                             \
-        if (gg_ < G) GEMM_COMPUTE((U) & 1, W);                                                               \
-        GEMM_LOAD_A(W, min(gg_ + 4, gl));                                                                    \
+        if (gg_ < g1) GEMM_COMPUTE((U) & 1, W);                                                              \
+        GEMM_LOAD_A(W, min(gg_ + 4, glast));                                                                 \
         GEMM_STORE_X(X, M, ((U) + 1) & 1);                                                                   \
-        GEMM_LOAD_X(X, M, min(gg_ + 3, gl));                                                                 \
+        GEMM_LOAD_X(X, M, min(gg_ + 3, glast));                                                              \
         __syncthreads();                                                                                     \
     }
 
@@ -330,16 +336,16 @@ gemm_w4_mfma_kernel(GemmArgs a) {
     u32x2 wa0[TI], wa1[TI], wa2[TI], wa3[TI];
     u32x4 xa[XU], xb[XU];  // x pieces of the even / odd groups
     uint32_t ma = 0, mb = 0;
-    GEMM_LOAD_A(wa0, 0);
-    GEMM_LOAD_A(wa1, min(1, gl));
-    GEMM_LOAD_A(wa2, min(2, gl));
-    GEMM_LOAD_A(wa3, min(3, gl));
-    GEMM_LOAD_X(xa, ma, 0);
-    GEMM_LOAD_X(xb, mb, min(1, gl));
+    GEMM_LOAD_A(wa0, g0);
+    GEMM_LOAD_A(wa1, min(g0 + 1, glast));
+    GEMM_LOAD_A(wa2, min(g0 + 2, glast));
+    GEMM_LOAD_A(wa3, min(g0 + 3, glast));
+    GEMM_LOAD_X(xa, ma, g0);
+    GEMM_LOAD_X(xb, mb, min(g0 + 1, glast));
     GEMM_STORE_X(xa, ma, 0);
-    GEMM_LOAD_X(xa, ma, min(2, gl));
+    GEMM_LOAD_X(xa, ma, min(g0 + 2, glast));
     __syncthreads();
-    for (int g = 0; g < G; g += 4) {
+    for (int g = g0; g < g1; g += 4) {
         GEMM_STEP(0, wa0, xb, mb);
         GEMM_STEP(1, wa1, xa, ma);
         GEMM_STEP(2, wa2, xb, mb);
@@ -353,7 +359,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
     // c0 term: K = G, lane group q takes groups gb + 8 q + 0..7 of its row / token.  All loads of a
     // chunk are issued before any use; groups past G read out of range (zero), so c0 and xs are 0.
     const __amdgpu_buffer_rsrc_t xs_r = buf_rsrc(a.xs, static_cast<uint32_t>(a.m_pad) * G * 4u);
-    for (int gb = 0; gb < (a.zero_is_8 ? 0 : G); gb += 32) {
+    for (int gb = g0; gb < (a.zero_is_8 ? g0 : g1); gb += 32) {
         const int g8 = gb + 8 * q;
         MetaWord<META> mw[TI][8];
         uint32_t xw[TJ][8];
@@ -363,7 +369,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
                                   static_cast<uint32_t>(g8)) * kMetaBytes;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const uint32_t o = g8 + e < G ? off + kMetaBytes * e : kBufOOB;
+                const uint32_t o = g8 + e < g1 ? off + kMetaBytes * e : kBufOOB;
                 if constexpr (META)
                     mw[i][e] = __builtin_amdgcn_raw_buffer_load_b64(meta_r, o, 0, 0);
                 else
@@ -375,7 +381,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
             const uint32_t off = (static_cast<uint32_t>(t0 + wt + 16 * j + lr) * G + static_cast<uint32_t>(g8)) * 4u;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                xw[j][e] = __builtin_amdgcn_raw_buffer_load_b32(xs_r, g8 + e < G ? off + 4u * e : kBufOOB, 0, 0);
+                xw[j][e] = __builtin_amdgcn_raw_buffer_load_b32(xs_r, g8 + e < g1 ? off + 4u * e : kBufOOB, 0, 0);
         }
         half8 ch[TI], cl[TI], sh[TJ], sl[TJ];
 #pragma unroll
@@ -416,6 +422,13 @@ gemm_w4_mfma_kernel(GemmArgs a) {
             const float tsc = a.ts[t];
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[i][j][v] *= tsc;
+            if (a.part) {  // K split: this split's partial products, the reduce applies the epilogue
+                float* pr = a.part + (static_cast<size_t>(blockIdx.z) * a.m + t) * a.rows;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (rb + v < a.rows) pr[rb + v] = acc[i][j][v];
+                continue;
+            }
             float* yr = a.y + static_cast<size_t>(t) * a.ldy;
             if constexpr (EPI == 2) {  // interleaved (gate, up) rows -> silu(gate) * up
 #pragma unroll
@@ -434,10 +447,48 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         }
 }
 
-size_t gemm_workspace_bytes(int m, int cols) {
+// The launch's tile (gemm_w4_mfma_kernel<4, 1, 2, 4, ...>): 128 rows x 64 tokens.
+constexpr int kGemmBR = 128, kGemmBT = 64;
+constexpr int kGemmMaxSplits = 4;
+
+// K splits of a launch: with fewer than two blocks per CU (the 4096-row
+// projections of a 512-token chunk: 256 blocks) the column groups are split
+// over blockIdx.z, each split keeping at least 16 groups, and a second kernel
+// adds the splits' partial products in a fixed order (deterministic).  The
+// SiLU-pair epilogue (gate/up, 1536 blocks) is never split.
+static int gemm_splits(int rows, int m, int cols, int epi) {
+    if (epi == 2) return 1;
+    const int blocks = ((m + kGemmBT - 1) / kGemmBT) * ((rows + kGemmBR - 1) / kGemmBR);
+    const int G = cols / 64;
+    int splits = 1;
+    while (splits < kGemmMaxSplits && blocks * splits < 2 * 256 && G / (2 * splits) >= 16) splits *= 2;
+    return splits;
+}
+
+static size_t gemm_prep_bytes(int m, int cols) {
     const size_t m_pad = static_cast<size_t>((m + kGemmPad - 1) / kGemmPad) * kGemmPad;
     return m_pad * static_cast<size_t>(cols) * (2 * sizeof(_Float16)) +
            m_pad * static_cast<size_t>(cols / 64) * sizeof(float) + m_pad * sizeof(float);
+}
+
+size_t gemm_workspace_bytes(int m, int cols, int rows) {
+    const int splits = rows > 0 ? gemm_splits(rows, m, cols, 0) : 1;
+    const size_t part = splits > 1 ? static_cast<size_t>(splits) * m * rows * sizeof(float) : 0;
+    return gemm_prep_bytes(m, cols) + (part + 255) / 256 * 256;
+}
+
+// y[t][r] (op)= sum over splits z (in order) of part[z][t][r]; op: store, add
+__global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits, int m,
+                                                                 int rows, float* __restrict__ y, int ldy, int add) {
+    const size_t n = static_cast<size_t>(m) * rows;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float v = part[i];
+        for (int z = 1; z < splits; ++z) v += part[static_cast<size_t>(z) * n + i];
+        const size_t t = i / rows, r = i - t * rows;
+        float* yp = y + t * ldy + r;
+        *yp = add ? *yp + v : v;
+    }
 }
 
 bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro) {
@@ -449,7 +500,7 @@ bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& p
 }
 
 template <int WGR, int WGT, int TI, int TJ, int EPI, int META>
-static hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
+static hipError_t launch_gemm_cfg(const GemmArgs& a, int splits, hipStream_t s) {
     using T = GemmTile<WGR, WGT, TI, TJ>;
     const auto fn = reinterpret_cast<const void*>(&gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI, META>);
     if constexpr (T::kLds > 64 * 1024) {  // beyond the default dynamic-LDS limit (gfx950 has 160 KiB per CU)
@@ -457,7 +508,8 @@ static hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
             e != hipSuccess)
             return e;
     }
-    const dim3 grid((a.m + T::kBT - 1) / T::kBT, (a.rows + T::kBR - 1) / T::kBR);
+    static_assert(T::kBR == kGemmBR && T::kBT == kGemmBT, "split choice assumes this tile");
+    const dim3 grid((a.m + T::kBT - 1) / T::kBT, (a.rows + T::kBR - 1) / T::kBR, splits);
     hipLaunchKernelGGL((gemm_w4_mfma_kernel<WGR, WGT, TI, TJ, EPI, META>), grid, dim3(T::kThreads), T::kLds, s, a);
     return hipGetLastError();
 }
@@ -471,16 +523,27 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
                        xs, ts);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.zero_is_8, xh, xs, ts,
-                     p.m, m_pad, p.y, p.ldy};
+    const int splits = gemm_splits(p.rows, p.m, p.cols, p.epi);
+    const int G = p.cols / 64;
+    float* part = splits > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(p.workspace) +
+                                                        gemm_prep_bytes(m_pad, p.cols)) : nullptr;
+    GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.zero_is_8, xh, xs, ts,
+               (G + splits - 1) / splits, part, p.m, m_pad, p.y, p.ldy};
     // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
     const bool m32 = p.layout == 2;
+    hipError_t e = hipErrorInvalidValue;
     switch (p.epi) {
-        case 0: return m32 ? launch_gemm_cfg<4, 1, 2, 4, 0, 1>(a, s) : launch_gemm_cfg<4, 1, 2, 4, 0, 0>(a, s);
-        case 1: return m32 ? launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, s) : launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, s);
-        case 2: return m32 ? launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, s) : launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, s);
+        case 0: e = m32 ? launch_gemm_cfg<4, 1, 2, 4, 0, 1>(a, splits, s) : launch_gemm_cfg<4, 1, 2, 4, 0, 0>(a, splits, s); break;
+        case 1: e = m32 ? launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, splits, s) : launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, splits, s); break;
+        case 2: e = m32 ? launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, splits, s) : launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, splits, s); break;
         default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess || splits == 1) return e;
+    const size_t n = static_cast<size_t>(p.m) * p.rows;
+    const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 2048));
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, part, splits, p.m, p.rows, p.y,
+                       p.ldy, p.epi == 1 ? 1 : 0);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

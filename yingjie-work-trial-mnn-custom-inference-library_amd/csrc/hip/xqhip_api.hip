@@ -675,7 +675,9 @@ int xqhip_linear_attn_step(const float* mixed, float* conv_state, const float* c
 
 // ---- prefill (multi-token) ---------------------------------------------------
 
-size_t xqhip_gemm_workspace_bytes(int m, int cols) { return m > 0 && cols > 0 ? xqhip::gemm_workspace_bytes(m, cols) : 0; }
+size_t xqhip_gemm_workspace_bytes(int m, int cols, int rows) {
+    return m > 0 && cols > 0 && rows >= 0 ? xqhip::gemm_workspace_bytes(m, cols, rows) : 0;
+}
 
 int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro, int ld_gate,
                      float* y, int ldy, int epilogue, void* workspace, void* stream) {
@@ -697,7 +699,7 @@ int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xq
     if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: workspace must be 16-byte aligned");
     // the kernels address the staged x (hi and lo halves) with 32-bit buffer offsets
-    if (xqhip::gemm_workspace_bytes(m, w->cols) >= (size_t{1} << 31))
+    if (xqhip::gemm_workspace_bytes(m, w->cols, 0) >= (size_t{1} << 31))
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: %d tokens of %d columns exceed one call (2 GiB of staged x)", m,
                     w->cols);
     xqhip::GemmLaunch p{};

@@ -165,9 +165,9 @@ struct GemmLaunch {
     float* y;  // [m][ldy]
     int ldy;
     int epi;          // 0 store, 1 add, 2 silu pair
-    void* workspace;  // gemm_workspace_bytes(m, cols)
+    void* workspace;  // gemm_workspace_bytes(m, cols, rows)
 };
-size_t gemm_workspace_bytes(int m, int cols);
+size_t gemm_workspace_bytes(int m, int cols, int rows);
 bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro);
 hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s);
 

@@ -490,12 +490,15 @@ bool DeviceModel::alloc_prefill_buffers(std::string* error) {
     ok = ok && (nq_ / nkv_) <= 8;
     if (!ok) return true;
     const size_t c = static_cast<size_t>(chunk_);
-    const int max_cols = std::max({hidden_, inter_, attn_n_});
+    size_t ws_bytes = 0;  // the largest need over the layers' matrices
+    for (const Layer& L : layers_)
+        for (const xqhip_w4* w : {&L.in_proj, &L.out_proj, &L.gate_up, &L.down})
+            ws_bytes = std::max(ws_bytes, xqhip_gemm_workspace_bytes(chunk_, w->cols, w->rows));
     uint8_t* ws = nullptr;
     if (!alloc(&x_all_, c * hidden_, error) || !alloc(&proj_all_, c * max_proj_, error) ||
         !alloc(&q_all_, c * nq_ * hd_, error) || !alloc(&gate_all_, c * nq_ * hd_, error) ||
         !alloc(&attn_all_, c * attn_n_, error) || !alloc(&ffn_all_, c * inter_, error) ||
-        !alloc(&ws, xqhip_gemm_workspace_bytes(chunk_, max_cols), error) || !alloc(&tok_dev_, c, error))
+        !alloc(&ws, ws_bytes, error) || !alloc(&tok_dev_, c, error))
         return false;
     gemm_ws_ = ws;
     bool any_linear = false;

@@ -84,7 +84,7 @@ _HIP_SIGS = {
                                   c_int, c_void_p, c_void_p]),
     "xqhip_linear_attn_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
-    "xqhip_gemm_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "xqhip_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "xqhip_gemm_w4a16": (c_int, [_P(W4), c_void_p, c_int, c_int, _P(Prologue), c_int, c_void_p, c_int, c_int,
                                  c_void_p, c_void_p]),
     "xqhip_embed_bf16_batch": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p]),
