@@ -230,6 +230,17 @@ XQHIP_API int xqhip_attn_decode(const float* q_src, const float* k_src, const fl
                                 int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
                                 float eps, const float* rope_cs, const int32_t* pos, void* k_cache, void* v_cache,
                                 int max_ctx, float* out, void* workspace, void* stream);
+/* The same step in one launch and no workspace: one block per query head
+ * reads its kv head's whole context (in passes of 1024 tokens merged with a
+ * running max) and writes the gated output.  head_dim 128 only; any context
+ * the caches hold.  Same cache layout, append and numerics as
+ * xqhip_attn_decode; faster where the context is short (the slot kernel
+ * spreads long contexts over more CUs).  Replaces the same reference code
+ * (custom_model.cpp:740-951). */
+XQHIP_API int xqhip_attn_decode_head(const float* q_src, const float* k_src, const float* v_src, int gated, int nq,
+                                     int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
+                                     float eps, const float* rope_cs, const int32_t* pos, void* k_cache,
+                                     void* v_cache, float* out, void* stream);
 
 /* Linear attention: conv1d + SiLU over the mixed q|k|v channels with the
  * [channels][ksize-1] history updated in place, then L2-normalised q and k

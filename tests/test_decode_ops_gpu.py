@@ -221,6 +221,69 @@ def test_fused_attention_decode(case):
         close(got, out2.download(np.float32, nq * hd), f"fused vs two-launch pos {p}", atol=1e-5, rtol=1e-4)
 
 
+# head_dim 128 shapes for the one-block-per-query-head kernel: contexts inside
+# one 1024-token pass (first slot, mid, last slot of the pass), exactly at and
+# across pass boundaries (1023 -> 1024, 2047 -> 2048), several passes, group
+# sizes 1, 4 and 8, gated and not.
+HEAD_CASES = [(32, 8, 128, 32, 0, 64, True), (32, 8, 128, 32, 511, 1024, True), (32, 8, 128, 64, 540, 1024, False),
+              (32, 8, 128, 32, 1022, 1040, True), (16, 2, 128, 32, 1023, 2048, True), (8, 8, 128, 128, 2046, 2048, True),
+              (32, 8, 128, 32, 3000, 3072, True), (4, 1, 128, 32, 9000, 9216, False)]
+
+
+@pytest.mark.parametrize("case", HEAD_CASES, ids=lambda c: "nq%d_nkv%d_hd%d_rd%d_pos%d" % c[:5])
+def test_head_attention_decode(case):
+    """xqhip_attn_decode_head (one block per query head, no merge kernel)
+    against the oracle and against xqhip_attn_decode on its own copy of the
+    caches, for two consecutive positions."""
+    nq, nkv, hd, rd, pos, max_ctx, gated = case
+    theta, eps = 1e7, 1e-6
+    print(f"head attention case {case}", flush=True)
+    assert pos + 2 <= max_ctx
+    qsrc, k, v, qn, kn, kc, vc = attn_layer_inputs(nq, nkv, hd, pos, seed=pos + 3, gated=gated)
+    tab = np.empty(max_ctx * rd, np.float32)
+    xb.ck(xb.hip().xqhip_rope_table(theta, rd, max_ctx, xb.ptr(tab)))
+    kcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    vcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    kcache[:pos], vcache[:pos] = kc, vc
+    kd, vd = dev(kcache), dev(vcache)    # per-head kernel
+    kd2, vd2 = dev(kcache), dev(vcache)  # slot kernel + merge
+    qn_d, kn_d, tab_d = dev(qn), dev(kn), dev(tab)
+    ws = dev(np.zeros(xb.hip().xqhip_gqa_workspace_bytes(nq, nkv, hd), np.uint8))
+    out, out2 = xb.DeviceBuffer(nq * hd * 4), xb.DeviceBuffer(nq * hd * 4)
+    rng = np.random.default_rng(pos + 1)
+    for step in range(2):
+        p = pos + step
+        if step:
+            qsrc = rng.normal(0, 1, qsrc.size).astype(np.float32)
+            k = rng.normal(0, 1, k.size).astype(np.float32)
+            v = rng.normal(0, 1, v.size).astype(np.float32)
+        qs_d, k_d, v_d = dev(qsrc), dev(k), dev(v)
+        pos_d = dev(np.array([p], np.int32))
+        xb.ck(xb.hip().xqhip_attn_decode_head(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr,
+                                              kn_d.ptr, eps, tab_d.ptr, pos_d.ptr, kd.ptr, vd.ptr, out.ptr, None))
+        xb.ck(xb.hip().xqhip_attn_decode(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr, kn_d.ptr,
+                                         eps, tab_d.ptr, pos_d.ptr, kd2.ptr, vd2.ptr, max_ctx, out2.ptr, ws.ptr, None))
+        kc_got = kd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        vc_got = vd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        assert np.array_equal(kc_got[:pos], kc) and np.array_equal(vc_got[:pos], vc)  # earlier slots untouched
+        assert not kc_got[p + 1:].any() and not vc_got[p + 1:].any()                  # later slots untouched
+        assert np.array_equal(vc_got[p].reshape(-1), v.astype(np.float16))
+        kc2 = kd2.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        assert np.array_equal(kc_got, kc2)  # the same fp16 append as the slot kernel
+        kk, want = oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, p, theta, eps, kc_got, vc_got)
+        close(kc_got[p].reshape(-1).astype(np.float32), kk, f"appended k pos {p}", atol=2e-3, rtol=1e-3)
+        got = out.download(np.float32, nq * hd)
+        close(got, want, f"head attention pos {p}")
+        close(got, out2.download(np.float32, nq * hd), f"head vs slot kernel pos {p}", atol=1e-5, rtol=1e-4)
+
+
+def test_head_attention_rejects_other_head_sizes():
+    z = dev(np.zeros(64, np.float32))
+    rc = xb.hip().xqhip_attn_decode_head(z.ptr, z.ptr, z.ptr, 1, 8, 2, 64, 32, z.ptr, z.ptr, 1e-6, z.ptr, z.ptr,
+                                         z.ptr, z.ptr, z.ptr, None)
+    assert rc == -1 and b"head_dim 128" in xb.hip().xqhip_last_error()  # XQHIP_EINVAL
+
+
 @pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 100])
 def test_gqa_short_contexts(ctx):
     nq, nkv, hd = 4, 2, 8

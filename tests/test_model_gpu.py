@@ -211,6 +211,41 @@ def test_decode_before_prefill_and_context_capacity(small_dir):
     assert st == xb.XQ_ERR_NOT_READY and b"prefill" in m.error
 
 
+def test_attention_kernel_switch_matches_oracle(small_dir, monkeypatch):
+    """Full-attention layers with head_dim 128 attend with one block per query
+    head up to 1024 context tokens and with the slot kernel + merge beyond;
+    decoding from a 1020-token prompt crosses the switch (contexts 1021 ..
+    1028).  Greedy ids against the oracle under the margin rule, hidden states
+    within tolerance at every step, and against a session that keeps the slot
+    kernel throughout (XQ_HEAD_ATTENTION=0): same ids, hidden states within
+    1e-5 abs + 1e-4 rel (the two kernels sum in different orders)."""
+    prompt = [int(t) for t in np.random.default_rng(1020).integers(0, 4096, 1020)]
+    n_new = 8
+    want, margins, hiddens = oracle_run(small_dir, prompt, n_new)
+    runs = {}
+    for mode in ("switch", "slot"):
+        if mode == "slot":
+            monkeypatch.setenv("XQ_HEAD_ATTENTION", "0")
+        s = xb.Session(small_dir, xb.options())
+        st, _ = s.prefill(prompt)
+        assert st == 0
+        toks, hs = [], []
+        for i in range(n_new):
+            st, tok, m = s.decode_one()
+            assert st == 0, m.error
+            toks.append(tok)
+            hs.append(s.hidden()[1])
+            if toks == want[: i + 1]:
+                close(hs[-1], hiddens[i + 1], f"{mode}: hidden after decode step {i} (context {len(prompt) + i + 1})")
+        compare_tokens(toks, want, margins)
+        runs[mode] = (toks, hs)
+        s.close()
+    assert runs["switch"][0] == runs["slot"][0]
+    for i, (a, b) in enumerate(zip(runs["switch"][1], runs["slot"][1])):
+        err = np.abs(a.astype(np.float64) - b)
+        assert (err <= 1e-5 + 1e-4 * np.abs(b)).all(), (i, err.max())
+
+
 def test_kv_cache_growth_keeps_results(small_dir):
     """KV caches start at max(8192, max_context_tokens) positions and double
     when a position needs more (the reference grows its caches as tokens

@@ -735,6 +735,245 @@ hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Decode attention with one block per query head, no merge kernel: the block
+// reads its kv head's cached context in passes of up to kHeadPass tokens with
+// the whole pass in flight, so at decode contexts a full-attention layer is
+// one launch.  Same per-head preparation as attn_decode_kernel (q and the new
+// key normalised and rotated, the new key / value used fp16-rounded from LDS;
+// the first query head of each kv head appends them to the caches), then
+// scores, one softmax (max subtracted, 1/l multiplied as
+// custom_model.cpp:901-904) and the gated output.  Passes are merged with a
+// running max (exp(m_old - m_new) rescale).
+// HD = 128: 4 lanes per token for the scores (32 dims, four 16-byte K loads),
+// 16 lanes per token for the value sum (8 dims, one 16-byte V load).  The
+// value loads of each 128-token score sub-pass are issued as soon as its keys
+// are consumed (they take over the key registers), and no load is issued past
+// the context.  The new token's score and value come from LDS: cache rows are
+// read only for the positions before it.
+// ---------------------------------------------------------------------------
+constexpr int kHeadThreads = 512;
+constexpr int kHeadPass = 1024;                    // tokens per pass
+constexpr int kHeadKSub = kHeadThreads / 4;        // tokens per K sub-pass (128)
+constexpr int kHeadKSubs = kHeadPass / kHeadKSub;  // 8
+constexpr int kHeadVTok = kHeadThreads / 16;       // tokens per V sub-pass (32)
+constexpr int kHeadVSubs = kHeadPass / kHeadVTok;  // 32
+constexpr int kHeadVPerK = kHeadKSub / kHeadVTok;  // V sub-passes per K sub-pass (4)
+
+template <int HD>
+__global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDecodeLaunch a) {
+    static_assert(HD == 128, "4 score lanes x 32 dims, 16 value lanes x 8 dims");
+    constexpr int kWaves = kHeadThreads / kWave;
+    const GqaLaunch& p = a.g;
+    __shared__ float qs[HD], kn[HD], vn[HD];
+    __shared__ float sc[kHeadPass];
+    __shared__ float red[kWaves];
+    __shared__ float fresh_s;
+    __shared__ float ored[kWaves][HD + 1];
+    const int qh = blockIdx.x;
+    const int group = p.nq / p.nkv;
+    const int kh = qh / group;
+    const int pos = *p.pos;  // cached positions 0 .. pos-1, the new token at pos
+    const bool owner = qh % group == 0;  // appends the new key / value of kv head kh
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const int sub = tid & 3, tt = tid >> 2;   // score lanes: dims 32 u + 8 sub + e of token tt
+    const int dsl = tid & 15, ts = tid >> 4;  // value lanes: dims 8 dsl + e of token ts
+    const float rscale = 1.0f / sqrtf(static_cast<float>(HD));
+    const size_t kv_stride = static_cast<size_t>(p.nkv) * HD;
+    const _Float16* kbase = p.k_cache + static_cast<size_t>(kh) * HD + sub * 8;
+    const _Float16* vbase = p.v_cache + static_cast<size_t>(kh) * HD + dsl * 8;
+    // query (wave 0), new key (wave 1), new value (wave 2): 2 values per lane;
+    // the RoPE pair and the gate are fetched now, off the critical path
+    float hv[2] = {0.0f, 0.0f};
+    if (wid < 3) {
+        const float* src = wid == 0 ? a.q_src + static_cast<size_t>(qh) * (a.gated ? 2 * HD : HD)
+                                    : (wid == 1 ? a.k_src : a.v_src) + static_cast<size_t>(kh) * HD;
+        hv[0] = src[lane];
+        hv[1] = src[lane + kWave];
+    }
+    const int half = a.rotary_dim / 2;
+    float2 cs = make_float2(1.0f, 0.0f);
+    if (tid < 2 * half)
+        cs = reinterpret_cast<const float2*>(a.rope_cs)[static_cast<size_t>(pos) * a.rope_pairs + (tid % half)];
+    // no gate projection: the reference's zero gate, sigmoid(0) (custom_model.cpp:750-753)
+    float gv = 0.0f;
+    if (tid < HD && p.gate) gv = p.gate[static_cast<size_t>(qh) * p.gate_stride + tid];
+    // keys of the first pass's cached tokens, every sub-pass that has one in flight
+    auto load_k = [&](int t0, int nc, bool skip, uint4 (&kr)[kHeadKSubs][4]) {
+#pragma unroll
+        for (int j = 0; j < kHeadKSubs; ++j) {
+            if (!skip || kHeadKSub * j < nc) {
+                const int t = t0 + min(tt + kHeadKSub * j, nc - 1);
+                const _Float16* row = kbase + static_cast<size_t>(t) * kv_stride;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) kr[j][u] = *reinterpret_cast<const uint4*>(row + 32 * u);
+            }
+        }
+    };
+    uint4 kr[kHeadKSubs][4];
+    load_k(0, min(kHeadPass, pos), true, kr);
+    // per-head RMSNorm (custom_model.cpp:301-313) of q and k; v as it is
+    if (wid < 2) {
+        float ss = hv[0] * hv[0] + hv[1] * hv[1];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(HD) + a.eps);
+        const float* w = wid == 0 ? a.q_norm : a.k_norm;
+        float* dst = wid == 0 ? qs : kn;
+        dst[lane] = hv[0] * (inv * w[lane]);
+        dst[lane + kWave] = hv[1] * (inv * w[lane + kWave]);
+    } else if (wid == 2) {
+        vn[lane] = hv[0];
+        vn[lane + kWave] = hv[1];
+    }
+    __syncthreads();
+    // partial RoPE (custom_model.cpp:351-370) of q and the new key, pairs (i, half + i)
+    if (tid < 2 * half) {
+        float* v = tid < half ? qs : kn;
+        const int d = tid % half;
+        const float x0 = v[d], x1 = v[half + d];
+        v[d] = x0 * cs.x - x1 * cs.y;
+        v[half + d] = x1 * cs.x + x0 * cs.y;
+    }
+    __syncthreads();
+    // the new key / value enter the cache in fp16 and are used rounded, like every slot
+    if (tid < HD) {
+        const _Float16 kq = static_cast<_Float16>(kn[tid]), vq = static_cast<_Float16>(vn[tid]);
+        if (owner) {
+            const size_t slot = static_cast<size_t>(pos) * kv_stride + static_cast<size_t>(kh) * HD + tid;
+            a.k_cache[slot] = kq;
+            a.v_cache[slot] = vq;
+        }
+        kn[tid] = static_cast<float>(kq);
+        vn[tid] = static_cast<float>(vq);
+    }
+    __syncthreads();
+    // q in registers, in the score lanes' dim order
+    float qreg[32];
+#pragma unroll
+    for (int d = 0; d < 32; ++d) qreg[d] = qs[(d >> 3) * 32 + sub * 8 + (d & 7)];
+    // the new token's score (the last wave; pos lies in the last pass)
+    if (wid == kWaves - 1) {
+        float s = qs[lane] * kn[lane] + qs[lane + kWave] * kn[lane + kWave];
+        s = wave_sum(s);
+        if (lane == 0) fresh_s = s * rscale;
+    }
+    float run_m = -INFINITY, l = 0.0f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    // one pass over positions [t0, t0 + nc) of the cache with their keys in kp
+    // (and the new token when it falls in this pass)
+    auto pass = [&](int t0, const uint4 (&kp)[kHeadKSubs][4]) {
+        const int nc = min(kHeadPass, pos - t0);
+        const bool last = pos - t0 < kHeadPass;
+        float m = -INFINITY;
+        uint4 vr[kHeadVSubs];
+#pragma unroll
+        for (int j = 0; j < kHeadKSubs; ++j) {
+            if (kHeadKSub * j < nc) {
+                const int tl = tt + kHeadKSub * j;
+                float dot = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t ww[4] = {kp[j][u].x, kp[j][u].y, kp[j][u].z, kp[j][u].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dot += qreg[8 * u + 2 * e] * half_lo(ww[e]);
+                        dot += qreg[8 * u + 2 * e + 1] * half_hi(ww[e]);
+                    }
+                }
+                dot = lanes_sum<4>(dot) * rscale;
+                if (tl < nc) {
+                    if (sub == 0) sc[tl] = dot;
+                    m = fmaxf(m, dot);
+                }
+                // the values of these 128 tokens, into the registers the keys held
+#pragma unroll
+                for (int r = 0; r < kHeadVPerK; ++r) {
+                    const int jj = kHeadVPerK * j + r;
+                    const int t = t0 + min(ts + kHeadVTok * jj, nc - 1);
+                    vr[jj] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(t) * kv_stride);
+                }
+            }
+        }
+        if (last) m = fmaxf(m, fresh_s);
+        m = wave_max(m);
+        if (lane == 0) red[wid] = m;
+        __syncthreads();
+        m = red[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w]);
+        const float mn = fmaxf(run_m, m);
+        const float f_old = expf(run_m - mn);
+        l *= f_old;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] *= f_old;
+        run_m = mn;
+        // sum_t exp(s_t - m) v_t over this thread's tokens ts, ts + 32, ...
+#pragma unroll
+        for (int jj = 0; jj < kHeadVSubs; ++jj) {
+            if (kHeadVTok * jj < nc) {
+                const int tl = ts + kHeadVTok * jj;
+                if (tl < nc) {
+                    const float pr = expf(sc[tl] - mn);
+                    l += pr;
+                    o[0] += pr * half_lo(vr[jj].x);
+                    o[1] += pr * half_hi(vr[jj].x);
+                    o[2] += pr * half_lo(vr[jj].y);
+                    o[3] += pr * half_hi(vr[jj].y);
+                    o[4] += pr * half_lo(vr[jj].z);
+                    o[5] += pr * half_hi(vr[jj].z);
+                    o[6] += pr * half_lo(vr[jj].w);
+                    o[7] += pr * half_hi(vr[jj].w);
+                }
+            }
+        }
+        if (last && ts == 0) {  // the new token, once per dim slice
+            const float pr = expf(fresh_s - mn);
+            l += pr;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] += pr * vn[dsl * 8 + e];
+        }
+        __syncthreads();  // sc and red are rewritten by the next pass
+    };
+    pass(0, kr);
+    // longer contexts: further passes, each loading its keys first (kept apart
+    // from the first pass so that no key register lives across a value phase)
+    for (int t0 = kHeadPass; t0 <= pos; t0 += kHeadPass) {
+        uint4 kr2[kHeadKSubs][4];
+        load_k(t0, max(1, min(kHeadPass, pos - t0)), false, kr2);
+        pass(t0, kr2);
+    }
+    // lanes with the same dsl: 4 per wave (16 apart), then the waves through LDS;
+    // l is the same in every dsl lane of a token group and reduces alongside
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = xor_pair_sum<32>(xor_pair_sum<16>(o[e]));
+    l = xor_pair_sum<32>(xor_pair_sum<16>(l));
+    if (lane < 16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ored[wid][dsl * 8 + e] = o[e];
+        if (lane == 0) ored[wid][HD] = l;
+    }
+    __syncthreads();
+    if (tid < HD) {
+        float acc = 0.0f, lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            acc += ored[w][tid];
+            lt += ored[w][HD];
+        }
+        p.out[static_cast<size_t>(qh) * HD + tid] = (acc * (1.0f / lt)) * sigmoid_dev(gv);
+    }
+}
+
+bool attn_head_supported(int nq, int nkv, int head_dim) {
+    return head_dim == 128 && nkv > 0 && nq % nkv == 0;
+}
+
+hipError_t launch_attn_decode_head(const AttnDecodeLaunch& a, hipStream_t s) {
+    hipLaunchKernelGGL(attn_decode_head_kernel<128>, dim3(a.g.nq), dim3(kHeadThreads), 0, s, a);
+    return hipGetLastError();
+}
+
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx) {
     if (nkv <= 0 || nq % nkv != 0 || nq / nkv > kAttnMaxGroup || head_dim <= 0) return false;
     if (max_ctx < 1 || max_ctx > kAttnMaxCtx) return false;

@@ -599,17 +599,13 @@ int xqhip_gqa_decode(const float* q, const void* k_cache, const void* v_cache, c
     return check(xqhip::launch_gqa(p, as_stream(stream)), "gqa launch");
 }
 
-int xqhip_attn_decode(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
-                      int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
-                      const float* rope_cs, const int32_t* pos, void* k_cache, void* v_cache, int max_ctx, float* out,
-                      void* workspace, void* stream) {
-    if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !pos || !k_cache || !v_cache || !out || !workspace ||
-        (rotary_dim > 0 && !rope_cs))
-        return fail(XQHIP_EINVAL, "xqhip_attn_decode: null argument");
-    if (!xqhip::gqa_supported(nq, nkv, head_dim, max_ctx))
-        return fail(XQHIP_EINVAL, "xqhip_attn_decode: unsupported shape nq=%d nkv=%d hd=%d ctx=%d", nq, nkv,
-                    head_dim, max_ctx);
-    const int active = std::max(0, std::min(head_dim, rotary_dim)) / 2 * 2;
+// The launch arguments shared by the two decode attention entry points
+// (workspace: the slot kernel's partials, nullptr for the per-head kernel).
+static xqhip::AttnDecodeLaunch attn_decode_args(const float* q_src, const float* k_src, const float* v_src, int gated,
+                                                int nq, int nkv, int head_dim, int rotary_dim, const float* q_norm,
+                                                const float* k_norm, float eps, const float* rope_cs,
+                                                const int32_t* pos, void* k_cache, void* v_cache, int max_ctx,
+                                                float* out, void* workspace) {
     xqhip::AttnDecodeLaunch a{};
     xqhip::GqaLaunch& p = a.g;
     p.k_cache = static_cast<const _Float16*>(k_cache);
@@ -622,16 +618,18 @@ int xqhip_attn_decode(const float* q_src, const float* k_src, const float* v_src
     p.max_ctx = max_ctx;
     p.pos = pos;
     p.out = out;
-    float* f = static_cast<float*>(workspace);
-    const size_t per = xqhip::gqa_workspace_bytes(nq, nkv, head_dim) / sizeof(float) / (head_dim + 2);
-    p.part_m = f;
-    p.part_l = f + per;
-    p.part_o = f + 2 * per;
+    if (workspace) {
+        float* f = static_cast<float*>(workspace);
+        const size_t per = xqhip::gqa_workspace_bytes(nq, nkv, head_dim) / sizeof(float) / (head_dim + 2);
+        p.part_m = f;
+        p.part_l = f + per;
+        p.part_o = f + 2 * per;
+    }
     a.q_src = q_src;
     a.k_src = k_src;
     a.v_src = v_src;
     a.gated = gated;
-    a.rotary_dim = active;
+    a.rotary_dim = std::max(0, std::min(head_dim, rotary_dim)) / 2 * 2;
     a.rope_pairs = std::max(0, std::min(head_dim, rotary_dim)) / 2;
     a.q_norm = q_norm;
     a.k_norm = k_norm;
@@ -639,7 +637,39 @@ int xqhip_attn_decode(const float* q_src, const float* k_src, const float* v_src
     a.rope_cs = rope_cs;
     a.k_cache = static_cast<_Float16*>(k_cache);
     a.v_cache = static_cast<_Float16*>(v_cache);
+    return a;
+}
+
+int xqhip_attn_decode(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
+                      int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
+                      const float* rope_cs, const int32_t* pos, void* k_cache, void* v_cache, int max_ctx, float* out,
+                      void* workspace, void* stream) {
+    if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !pos || !k_cache || !v_cache || !out || !workspace ||
+        (rotary_dim > 0 && !rope_cs))
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode: null argument");
+    if (!xqhip::gqa_supported(nq, nkv, head_dim, max_ctx))
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode: unsupported shape nq=%d nkv=%d hd=%d ctx=%d", nq, nkv,
+                    head_dim, max_ctx);
+    const xqhip::AttnDecodeLaunch a = attn_decode_args(q_src, k_src, v_src, gated, nq, nkv, head_dim, rotary_dim,
+                                                       q_norm, k_norm, eps, rope_cs, pos, k_cache, v_cache, max_ctx,
+                                                       out, workspace);
     return check(xqhip::launch_attn_decode(a, as_stream(stream)), "attn_decode launch");
+}
+
+int xqhip_attn_decode_head(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
+                           int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
+                           const float* rope_cs, const int32_t* pos, void* k_cache, void* v_cache, float* out,
+                           void* stream) {
+    if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !pos || !k_cache || !v_cache || !out ||
+        (rotary_dim > 0 && !rope_cs))
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode_head: null argument");
+    if (!xqhip::attn_head_supported(nq, nkv, head_dim))
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode_head: unsupported shape nq=%d nkv=%d hd=%d (head_dim 128 only)",
+                    nq, nkv, head_dim);
+    const xqhip::AttnDecodeLaunch a = attn_decode_args(q_src, k_src, v_src, gated, nq, nkv, head_dim, rotary_dim,
+                                                       q_norm, k_norm, eps, rope_cs, pos, k_cache, v_cache, 0, out,
+                                                       nullptr);
+    return check(xqhip::launch_attn_decode_head(a, as_stream(stream)), "attn_decode_head launch");
 }
 
 int xqhip_linear_conv(const float* mixed, float* conv_state, const float* conv_w, int lk_n, int lk_hd, int lv_n,

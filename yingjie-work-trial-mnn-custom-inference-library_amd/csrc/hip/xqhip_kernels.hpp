@@ -102,6 +102,9 @@ struct AttnDecodeLaunch {
     _Float16* v_cache;
 };
 hipError_t launch_attn_decode(const AttnDecodeLaunch& a, hipStream_t s);
+// one block per query head, no merge kernel (head_dim 128)
+bool attn_head_supported(int nq, int nkv, int head_dim);
+hipError_t launch_attn_decode_head(const AttnDecodeLaunch& a, hipStream_t s);
 size_t gqa_workspace_bytes(int nq, int nkv, int head_dim);
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx);
 hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s);

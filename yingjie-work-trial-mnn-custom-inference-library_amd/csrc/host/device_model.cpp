@@ -249,7 +249,6 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
         any_linear |= !L.full;
         max_proj = std::max(max_proj, L.in_proj.rows);
     }
-    const int rot_active = std::max(0, std::min(hd_, rot_));
     if (any_full && xqhip_gqa_workspace_bytes(nq_, nkv_, hd_) == 0) {
         *error = "attention workspace";
         return false;
@@ -336,6 +335,27 @@ bool DeviceModel::ensure_capacity(size_t positions, std::string* error) {
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "KV cache growth");
 }
 
+static bool head_attention_enabled() {
+    const char* v = std::getenv("XQ_HEAD_ATTENTION");
+    return !(v && v[0] == '0');
+}
+
+// Picks the attention kernel of the full-attention layers for a step whose
+// context is `ctx` tokens.  Both kernels give the same results; the graphs
+// that hold the other one are dropped after the queued steps have finished.
+bool DeviceModel::select_attention(size_t ctx, KernelTrace* trace, std::string* error) {
+    const bool want = head_attention_enabled() && hd_ == 128 && nq_ % nkv_ == 0 &&
+                      ctx <= static_cast<size_t>(kHeadAttnMaxCtx);
+    if (want == attn_head_) return true;
+    if (!sync(trace, error)) return false;
+    attn_head_ = want;
+    for (void** g : {&g_prefill_, &g_forward_}) {
+        if (*g) xqhip_graph_destroy(*g);
+        *g = nullptr;
+    }
+    return true;
+}
+
 void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past the position are never read)
     std::string ignored;
     sync(nullptr, &ignored);  // the trace of the steps being discarded is dropped with them
@@ -413,9 +433,16 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
                      {"prefill_kv_build_custom", "attention_score_custom", "attention_softmax_custom",
                       "attention_v_reduce_custom"},
                      4);
-            XQ_CALL(xqhip_attn_decode(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm, L.k_norm,
-                                      eps_, rope_cs_, pos, L.k_cache, L.v_cache, max_ctx_, attn_, gqa_ws_, stream_),
-                    "attention decode");
+            if (attn_head_) {
+                XQ_CALL(xqhip_attn_decode_head(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm,
+                                               L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache, attn_, stream_),
+                        "attention decode");
+            } else {
+                XQ_CALL(xqhip_attn_decode(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm,
+                                          L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache, max_ctx_, attn_, gqa_ws_,
+                                          stream_),
+                        "attention decode");
+            }
             op_end(timed);
             op_begin(timed, "linear_o_proj_w4a16(fused:residual_add_attention)");
             XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, nullptr, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),
@@ -591,6 +618,7 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
         return false;
     }
     if (!ensure_capacity(n_tokens, error)) return false;
+    if (!select_attention(n_tokens, trace, error)) return false;
     for (size_t i = 0; i < n_tokens; ++i) {
         // std::abs(INT_MIN) has no positive value: the reference's row offset
         // turns negative and its read fails (custom_model.cpp:573-597)
@@ -681,6 +709,7 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         return false;
     }
     if (!ensure_capacity(position + 1, error)) return false;
+    if (!select_attention(position + 1, trace, error)) return false;
     if (!ensure_graphs(error)) return false;
     // The previous step's forward pass may still be running: h_tok_[0..1] are
     // free again because their upload preceded that step's sampling, which the

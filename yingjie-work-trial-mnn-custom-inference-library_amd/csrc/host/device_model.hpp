@@ -87,6 +87,7 @@ private:
     bool load_layer(int index, Layer* L, std::string* error);
     bool build_rope_table(std::string* error);
     bool ensure_capacity(size_t positions, std::string* error);
+    bool select_attention(size_t ctx, KernelTrace* trace, std::string* error);
     void release(void* p);
 
     // enqueue one token through all layers (reads pos from d_ctrl_[0])
@@ -110,6 +111,11 @@ private:
     float eps_ = 1.0e-6f, theta_ = 10000000.0f;
     static constexpr int kMaxContext = 1 << 20;  // the attention kernels' limit
     int max_ctx_ = 8192;                          // KV capacity (positions), grows on demand
+    // Full-attention layers attend with one block per query head (one launch,
+    // no merge) up to this context, with the slot kernel + merge beyond it;
+    // the step graphs hold one of the two and are captured again on a switch.
+    static constexpr int kHeadAttnMaxCtx = 1024;  // measured crossover: 11.4 vs 12.4 us at 1024, 17.5 vs 13.3 at 1536
+    bool attn_head_ = false;
     std::string model_dir_, backend_request_, device_name_;
     uint64_t weight_bytes_ = 0;
     int inexact_meta_ = 0;
