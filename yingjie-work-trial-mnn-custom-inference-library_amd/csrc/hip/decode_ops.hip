@@ -1135,7 +1135,6 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
     constexpr int kTaps = KS > 0 ? KS : kStepMaxTaps;
     __shared__ float qk[2 * 256];
     __shared__ float vsh[kDeltaCols];
-    __shared__ float colsum[4][kDeltaCols];
     __shared__ float red[2][4];
     const int vh = blockIdx.x;
     const int j0 = blockIdx.y * kDeltaCols;
@@ -1145,11 +1144,17 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
     const int hist = KS > 0 ? KS - 1 : max(0, p.ksize - 1);
     const int conv_dim = 2 * p.lk_n * dk + p.lv_n * dv;
     const bool qk_writer = (vh % factor == 0) && blockIdx.y == 0;
-    const int jl = threadIdx.x % kDeltaCols;
-    const int ig = threadIdx.x / kDeltaCols;
+    // the delta rule is wave-local: wave w owns columns 4w .. 4w + 3 of the
+    // slice, 16 lanes per column (lane l: column l / 16, rows l % 16 + 16 r),
+    // so its row sums are DPP reductions inside the wave, with no LDS or
+    // barrier after the conv
+    static_assert(kDeltaCols == 4 * 4 && kDeltaIGroups == 16, "4 waves x 4 columns x 16 lanes");
+    const int jl = 4 * (static_cast<int>(threadIdx.x) / kWave) + (static_cast<int>(threadIdx.x) & (kWave - 1)) / 16;
+    const int ig = threadIdx.x & 15;
     const int j = j0 + jl;
     const bool active = j < dv;
     float* S = p.state + static_cast<size_t>(vh) * dk * dv;
+    const int pos_s = *p.pos;
     // Loads in the order their data is needed: the conv inputs (filter taps,
     // history, the in_proj output: cache-resident) first, the state (HBM)
     // after them, so the conv arithmetic runs while the state streams in
@@ -1170,12 +1175,13 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
         const uint32_t ho = static_cast<uint32_t>(c * hist) * 4u, wo = static_cast<uint32_t>(c * p.ksize) * 4u;
 #pragma unroll
         for (int t = 0; t < kTaps - 1; ++t) {
-            tp.h[t] = buf_load_f32(r_hist, ok && t < hist ? ho + 4u * t : kBufOOB);
-            tp.h_other[t] = buf_load_f32(r_hist, ok && t < hist ? hist_bytes + ho + 4u * t : kBufOOB);
+            tp.h[t] = buf_load_f32(r_hist, opaque_offset(ok && t < hist ? ho + 4u * t : kBufOOB));
+            tp.h_other[t] = buf_load_f32(r_hist, opaque_offset(ok && t < hist ? hist_bytes + ho + 4u * t : kBufOOB));
         }
 #pragma unroll
-        for (int t = 0; t < kTaps; ++t) tp.w[t] = buf_load_f32(r_w, ok && t <= hist ? wo + 4u * t : kBufOOB);
-        tp.x = buf_load_f32(r_x, ok ? static_cast<uint32_t>(c) * 4u : kBufOOB);
+        for (int t = 0; t < kTaps; ++t)
+            tp.w[t] = buf_load_f32(r_w, opaque_offset(ok && t <= hist ? wo + 4u * t : kBufOOB));
+        tp.x = buf_load_f32(r_x, opaque_offset(ok ? static_cast<uint32_t>(c) * 4u : kBufOOB));
     };
     // per-head gate inputs first (4 uniform loads; read as scalars they would
     // be fetched only when first used, after the conv)
@@ -1231,11 +1237,16 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
 #pragma unroll
     for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
         const int i = ig + r * kDeltaIGroups;
-        sreg[r] = buf_load_f32(r_state, active && i < dk ? static_cast<uint32_t>(i * dv + j) * 4u : kBufOOB);
+        // (a 24-bit multiply: the 64-bit multiply-add the compiler picks for
+        // i * dv + j reads an unused high half that can alias a pending load)
+        sreg[r] = buf_load_f32(r_state, active && i < dk ? (__umul24(i, dv) + j) * 4u : kBufOOB);
     }
-    // the position is read after every load is issued (its parity picks the
-    // history copy read above and the one written at the end)
-    const int par = __builtin_nontemporal_load(p.pos) & 1;
+    // every load above is issued before any arithmetic that waits for one
+    __builtin_amdgcn_sched_barrier(0);
+    // the position's parity picks the history copy read above and the one
+    // written at the end (a scalar load, requested at the top with the kernel
+    // arguments: waiting for it drains none of the vector loads)
+    const int par = pos_s & 1;
     float* st_out = p.conv_state + static_cast<size_t>(par ^ 1) * conv_dim * hist;
     select_parity(tq[0], par);
     select_parity(tq[1], par);
@@ -1278,11 +1289,7 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
             pred += sreg[r] * (qk[256 + i] * invk);
         }
     }
-    pred = xor_pair_sum<32>(xor_pair_sum<16>(pred));
-    if (lane < kDeltaCols) colsum[wid][lane] = pred;
-    __syncthreads();
-    pred = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
-    __syncthreads();
+    pred = lanes_sum<16>(pred);
     const float delta = active ? beta * (vj - pred) : 0.0f;
     float o = 0.0f;
 #pragma unroll
@@ -1290,17 +1297,12 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
         const int i = ig + r * kDeltaIGroups;
         if (active && i < dk) {
             sreg[r] += (qk[256 + i] * invk) * delta;
-            S[static_cast<size_t>(i) * dv + j] = sreg[r];
+            S[__umul24(i, dv) + j] = sreg[r];
             o += sreg[r] * (qk[i] * invq);
         }
     }
-    o = xor_pair_sum<32>(xor_pair_sum<16>(o));
-    if (lane < kDeltaCols) colsum[wid][lane] = o;
-    __syncthreads();
-    if (threadIdx.x < kDeltaCols && active) {
-        const float tot = colsum[0][jl] + colsum[1][jl] + colsum[2][jl] + colsum[3][jl];
-        p.out[static_cast<size_t>(vh) * dv + j] = tot * (1.0f / sqrtf(static_cast<float>(dk)));
-    }
+    o = lanes_sum<16>(o);
+    if (ig == 0 && active) p.out[static_cast<size_t>(vh) * dv + j] = o * (1.0f / sqrtf(static_cast<float>(dk)));
     if (qk_writer) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {

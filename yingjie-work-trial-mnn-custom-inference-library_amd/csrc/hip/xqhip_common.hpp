@@ -71,6 +71,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+// A per-lane offset the compiler cannot see through: loads whose offsets are
+// selected between a real one and kBufOOB then stay straight-line code (left
+// visible, identical out-of-range loads get merged under a branch whose join
+// waits for every outstanding load).
+__device__ __forceinline__ uint32_t opaque_offset(uint32_t off) {
+    asm volatile("" : "+v"(off));
+    return off;
+}
 
 // Cross-lane reductions by DPP lane moves inside the VALU (no LDS round trip,
 // unlike ds_bpermute): quad_perm [1,0,3,2] and [2,3,0,1] exchange lanes i^1
