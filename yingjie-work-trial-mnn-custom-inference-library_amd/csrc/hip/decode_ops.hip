@@ -748,160 +748,173 @@ hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s) {
 // HD = 128: 4 lanes per token for the scores (32 dims, four 16-byte K loads),
 // 16 lanes per token for the value sum (8 dims, one 16-byte V load).  The
 // value loads of each 128-token score sub-pass are issued as soon as its keys
-// are consumed (they take over the key registers), and no load is issued past
-// the context.  The new token's score and value come from LDS: cache rows are
-// read only for the positions before it.
+// are consumed (they take over the key registers).  The new token's score and
+// value come from LDS: cache rows are read only for the positions before it.
+// Every load is straight-line code (range-checked buffer loads read 0 past
+// the cached positions): a load under a branch makes the compiler's wait for
+// any earlier load a wait for all of them.  The kernel picks, from the
+// position, a body whose first pass has just enough 128-token sub-passes.
 // ---------------------------------------------------------------------------
 constexpr int kHeadThreads = 512;
 constexpr int kHeadPass = 1024;                    // tokens per pass
 constexpr int kHeadKSub = kHeadThreads / 4;        // tokens per K sub-pass (128)
 constexpr int kHeadKSubs = kHeadPass / kHeadKSub;  // 8
 constexpr int kHeadVTok = kHeadThreads / 16;       // tokens per V sub-pass (32)
-constexpr int kHeadVSubs = kHeadPass / kHeadVTok;  // 32
 constexpr int kHeadVPerK = kHeadKSub / kHeadVTok;  // V sub-passes per K sub-pass (4)
 
 template <int HD>
-__global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDecodeLaunch a) {
+struct HeadSmem {
+    float qs[HD], kn[HD], vn[HD], gate[HD];
+    float sc[kHeadPass];
+    float red[kHeadThreads / kWave];
+    float fresh_s;
+    float ored[kHeadThreads / kWave][HD + 1];
+};
+
+__device__ __forceinline__ uint4 buf_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// One query head with first-pass sub-passes KS (later passes, for contexts
+// past kHeadPass, use all kHeadKSubs).
+template <int HD, int KS>
+__device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSmem<HD>& sm, int pos) {
     static_assert(HD == 128, "4 score lanes x 32 dims, 16 value lanes x 8 dims");
     constexpr int kWaves = kHeadThreads / kWave;
     const GqaLaunch& p = a.g;
-    __shared__ float qs[HD], kn[HD], vn[HD];
-    __shared__ float sc[kHeadPass];
-    __shared__ float red[kWaves];
-    __shared__ float fresh_s;
-    __shared__ float ored[kWaves][HD + 1];
     const int qh = blockIdx.x;
     const int group = p.nq / p.nkv;
     const int kh = qh / group;
-    const int pos = *p.pos;  // cached positions 0 .. pos-1, the new token at pos
     const bool owner = qh % group == 0;  // appends the new key / value of kv head kh
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int sub = tid & 3, tt = tid >> 2;   // score lanes: dims 32 u + 8 sub + e of token tt
     const int dsl = tid & 15, ts = tid >> 4;  // value lanes: dims 8 dsl + e of token ts
     const float rscale = 1.0f / sqrtf(static_cast<float>(HD));
     const size_t kv_stride = static_cast<size_t>(p.nkv) * HD;
-    const _Float16* kbase = p.k_cache + static_cast<size_t>(kh) * HD + sub * 8;
-    const _Float16* vbase = p.v_cache + static_cast<size_t>(kh) * HD + dsl * 8;
-    // query (wave 0), new key (wave 1), new value (wave 2): 2 values per lane;
-    // the RoPE pair and the gate are fetched now, off the critical path
-    float hv[2] = {0.0f, 0.0f};
-    if (wid < 3) {
-        const float* src = wid == 0 ? a.q_src + static_cast<size_t>(qh) * (a.gated ? 2 * HD : HD)
-                                    : (wid == 1 ? a.k_src : a.v_src) + static_cast<size_t>(kh) * HD;
-        hv[0] = src[lane];
-        hv[1] = src[lane + kWave];
-    }
+    const uint32_t row_bytes = static_cast<uint32_t>(kv_stride) * 2u;  // one position of a cache
+    // query (wave 0), new key (wave 1), new value (wave 2, and the idle waves),
+    // their norm weights, the RoPE pair and the gate
+    const float* src = wid == 0 ? a.q_src + static_cast<size_t>(qh) * (a.gated ? 2 * HD : HD)
+                                : (wid == 1 ? a.k_src : a.v_src) + static_cast<size_t>(kh) * HD;
+    const float* nw = wid == 0 ? a.q_norm : a.k_norm;
+    const float hv0 = src[lane], hv1 = src[lane + kWave];
+    const float w0 = nw[lane], w1 = nw[lane + kWave];
     const int half = a.rotary_dim / 2;
-    float2 cs = make_float2(1.0f, 0.0f);
-    if (tid < 2 * half)
-        cs = reinterpret_cast<const float2*>(a.rope_cs)[static_cast<size_t>(pos) * a.rope_pairs + (tid % half)];
+    const __amdgpu_buffer_rsrc_t r_cs =
+        buf_rsrc(a.rope_cs, half > 0 ? static_cast<uint32_t>(pos + 1) * a.rope_pairs * 8u : 0u);
+    const uint32_t cs_off =
+        tid < 2 * half ? (static_cast<uint32_t>(pos) * a.rope_pairs + (tid < half ? tid : tid - half)) * 8u : kBufOOB;
+    const auto csw = __builtin_amdgcn_raw_buffer_load_b64(r_cs, cs_off, 0, 0);
     // no gate projection: the reference's zero gate, sigmoid(0) (custom_model.cpp:750-753)
-    float gv = 0.0f;
-    if (tid < HD && p.gate) gv = p.gate[static_cast<size_t>(qh) * p.gate_stride + tid];
-    // keys of the first pass's cached tokens, every sub-pass that has one in flight
-    auto load_k = [&](int t0, int nc, bool skip, uint4 (&kr)[kHeadKSubs][4]) {
+    const __amdgpu_buffer_rsrc_t r_gate =
+        buf_rsrc(p.gate, p.gate ? static_cast<uint32_t>(p.nq) * p.gate_stride * 4u : 0u);
+    const float gv = buf_load_f32(
+        r_gate, tid < HD ? (static_cast<uint32_t>(qh) * p.gate_stride + tid) * 4u : kBufOOB);
+    // the keys of a pass: cached positions [t0, t0 + nc), rows past nc read 0
+    auto load_k = [&](int t0, int nc, auto& kr) {
+        constexpr int J = sizeof(kr) / sizeof(kr[0]);
+        const __amdgpu_buffer_rsrc_t r = buf_rsrc(p.k_cache + static_cast<size_t>(t0) * kv_stride + kh * HD,
+                                                  static_cast<uint32_t>(nc) * row_bytes);
 #pragma unroll
-        for (int j = 0; j < kHeadKSubs; ++j) {
-            if (!skip || kHeadKSub * j < nc) {
-                const int t = t0 + min(tt + kHeadKSub * j, nc - 1);
-                const _Float16* row = kbase + static_cast<size_t>(t) * kv_stride;
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-                for (int u = 0; u < 4; ++u) kr[j][u] = *reinterpret_cast<const uint4*>(row + 32 * u);
-            }
-        }
+            for (int u = 0; u < 4; ++u)
+                kr[j][u] = buf_load_u4(r, static_cast<uint32_t>(tt + kHeadKSub * j) * row_bytes + sub * 16u + u * 64u);
     };
-    uint4 kr[kHeadKSubs][4];
-    load_k(0, min(kHeadPass, pos), true, kr);
+    uint4 kr[KS][4];
+    load_k(0, min(kHeadPass, pos), kr);
     // per-head RMSNorm (custom_model.cpp:301-313) of q and k; v as it is
     if (wid < 2) {
-        float ss = hv[0] * hv[0] + hv[1] * hv[1];
+        float ss = hv0 * hv0 + hv1 * hv1;
         ss = wave_sum(ss);
         const float inv = 1.0f / sqrtf(ss / static_cast<float>(HD) + a.eps);
-        const float* w = wid == 0 ? a.q_norm : a.k_norm;
-        float* dst = wid == 0 ? qs : kn;
-        dst[lane] = hv[0] * (inv * w[lane]);
-        dst[lane + kWave] = hv[1] * (inv * w[lane + kWave]);
+        float* dst = wid == 0 ? sm.qs : sm.kn;
+        dst[lane] = hv0 * (inv * w0);
+        dst[lane + kWave] = hv1 * (inv * w1);
     } else if (wid == 2) {
-        vn[lane] = hv[0];
-        vn[lane + kWave] = hv[1];
+        sm.vn[lane] = hv0;
+        sm.vn[lane + kWave] = hv1;
     }
+    if (tid < HD) sm.gate[tid] = gv;
     __syncthreads();
     // partial RoPE (custom_model.cpp:351-370) of q and the new key, pairs (i, half + i)
     if (tid < 2 * half) {
-        float* v = tid < half ? qs : kn;
-        const int d = tid % half;
+        float* v = tid < half ? sm.qs : sm.kn;
+        const int d = tid < half ? tid : tid - half;
+        const float cx = __uint_as_float(csw[0]), cy = __uint_as_float(csw[1]);
         const float x0 = v[d], x1 = v[half + d];
-        v[d] = x0 * cs.x - x1 * cs.y;
-        v[half + d] = x1 * cs.x + x0 * cs.y;
+        v[d] = x0 * cx - x1 * cy;
+        v[half + d] = x1 * cx + x0 * cy;
     }
     __syncthreads();
     // the new key / value enter the cache in fp16 and are used rounded, like every slot
     if (tid < HD) {
-        const _Float16 kq = static_cast<_Float16>(kn[tid]), vq = static_cast<_Float16>(vn[tid]);
+        const _Float16 kq = static_cast<_Float16>(sm.kn[tid]), vq = static_cast<_Float16>(sm.vn[tid]);
         if (owner) {
             const size_t slot = static_cast<size_t>(pos) * kv_stride + static_cast<size_t>(kh) * HD + tid;
             a.k_cache[slot] = kq;
             a.v_cache[slot] = vq;
         }
-        kn[tid] = static_cast<float>(kq);
-        vn[tid] = static_cast<float>(vq);
+        sm.kn[tid] = static_cast<float>(kq);
+        sm.vn[tid] = static_cast<float>(vq);
     }
     __syncthreads();
     // q in registers, in the score lanes' dim order
     float qreg[32];
 #pragma unroll
-    for (int d = 0; d < 32; ++d) qreg[d] = qs[(d >> 3) * 32 + sub * 8 + (d & 7)];
+    for (int d = 0; d < 32; ++d) qreg[d] = sm.qs[(d >> 3) * 32 + sub * 8 + (d & 7)];
     // the new token's score (the last wave; pos lies in the last pass)
     if (wid == kWaves - 1) {
-        float s = qs[lane] * kn[lane] + qs[lane + kWave] * kn[lane + kWave];
+        float s = sm.qs[lane] * sm.kn[lane] + sm.qs[lane + kWave] * sm.kn[lane + kWave];
         s = wave_sum(s);
-        if (lane == 0) fresh_s = s * rscale;
+        if (lane == 0) sm.fresh_s = s * rscale;
     }
     float run_m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
-    // one pass over positions [t0, t0 + nc) of the cache with their keys in kp
-    // (and the new token when it falls in this pass)
-    auto pass = [&](int t0, const uint4 (&kp)[kHeadKSubs][4]) {
+    // one pass over cached positions [t0, t0 + nc) with their keys in kp (and
+    // the new token when it falls in this pass)
+    auto pass = [&](int t0, const auto& kp) {
+        constexpr int J = sizeof(kp) / sizeof(kp[0]);
         const int nc = min(kHeadPass, pos - t0);
         const bool last = pos - t0 < kHeadPass;
+        const __amdgpu_buffer_rsrc_t r_v = buf_rsrc(p.v_cache + static_cast<size_t>(t0) * kv_stride + kh * HD,
+                                                    static_cast<uint32_t>(nc) * row_bytes);
         float m = -INFINITY;
-        uint4 vr[kHeadVSubs];
+        uint4 vr[J * kHeadVPerK];
 #pragma unroll
-        for (int j = 0; j < kHeadKSubs; ++j) {
-            if (kHeadKSub * j < nc) {
-                const int tl = tt + kHeadKSub * j;
-                float dot = 0.0f;
+        for (int j = 0; j < J; ++j) {
+            const int tl = tt + kHeadKSub * j;
+            float dot = 0.0f;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const uint32_t ww[4] = {kp[j][u].x, kp[j][u].y, kp[j][u].z, kp[j][u].w};
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t ww[4] = {kp[j][u].x, kp[j][u].y, kp[j][u].z, kp[j][u].w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        dot += qreg[8 * u + 2 * e] * half_lo(ww[e]);
-                        dot += qreg[8 * u + 2 * e + 1] * half_hi(ww[e]);
-                    }
-                }
-                dot = lanes_sum<4>(dot) * rscale;
-                if (tl < nc) {
-                    if (sub == 0) sc[tl] = dot;
-                    m = fmaxf(m, dot);
-                }
-                // the values of these 128 tokens, into the registers the keys held
-#pragma unroll
-                for (int r = 0; r < kHeadVPerK; ++r) {
-                    const int jj = kHeadVPerK * j + r;
-                    const int t = t0 + min(ts + kHeadVTok * jj, nc - 1);
-                    vr[jj] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(t) * kv_stride);
+                for (int e = 0; e < 4; ++e) {
+                    dot += qreg[8 * u + 2 * e] * half_lo(ww[e]);
+                    dot += qreg[8 * u + 2 * e + 1] * half_hi(ww[e]);
                 }
             }
-        }
-        if (last) m = fmaxf(m, fresh_s);
-        m = wave_max(m);
-        if (lane == 0) red[wid] = m;
-        __syncthreads();
-        m = red[0];
+            dot = lanes_sum<4>(dot) * rscale;
+            if (tl < nc) {
+                if (sub == 0) sm.sc[tl] = dot;
+                m = fmaxf(m, dot);
+            }
+            // the values of these 128 tokens, into the registers the keys held
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w]);
+            for (int r = 0; r < kHeadVPerK; ++r) {
+                const int jj = kHeadVPerK * j + r;
+                vr[jj] = buf_load_u4(r_v, static_cast<uint32_t>(ts + kHeadVTok * jj) * row_bytes + dsl * 16u);
+            }
+        }
+        if (last) m = fmaxf(m, sm.fresh_s);
+        m = wave_max(m);
+        if (lane == 0) sm.red[wid] = m;
+        __syncthreads();
+        m = sm.red[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) m = fmaxf(m, sm.red[w]);
         const float mn = fmaxf(run_m, m);
         const float f_old = expf(run_m - mn);
         l *= f_old;
@@ -910,37 +923,36 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDeco
         run_m = mn;
         // sum_t exp(s_t - m) v_t over this thread's tokens ts, ts + 32, ...
 #pragma unroll
-        for (int jj = 0; jj < kHeadVSubs; ++jj) {
-            if (kHeadVTok * jj < nc) {
-                const int tl = ts + kHeadVTok * jj;
-                if (tl < nc) {
-                    const float pr = expf(sc[tl] - mn);
-                    l += pr;
-                    o[0] += pr * half_lo(vr[jj].x);
-                    o[1] += pr * half_hi(vr[jj].x);
-                    o[2] += pr * half_lo(vr[jj].y);
-                    o[3] += pr * half_hi(vr[jj].y);
-                    o[4] += pr * half_lo(vr[jj].z);
-                    o[5] += pr * half_hi(vr[jj].z);
-                    o[6] += pr * half_lo(vr[jj].w);
-                    o[7] += pr * half_hi(vr[jj].w);
-                }
+        for (int jj = 0; jj < J * kHeadVPerK; ++jj) {
+            const int tl = ts + kHeadVTok * jj;
+            if (tl < nc) {
+                const float pr = expf(sm.sc[tl] - mn);
+                l += pr;
+                o[0] += pr * half_lo(vr[jj].x);
+                o[1] += pr * half_hi(vr[jj].x);
+                o[2] += pr * half_lo(vr[jj].y);
+                o[3] += pr * half_hi(vr[jj].y);
+                o[4] += pr * half_lo(vr[jj].z);
+                o[5] += pr * half_hi(vr[jj].z);
+                o[6] += pr * half_lo(vr[jj].w);
+                o[7] += pr * half_hi(vr[jj].w);
             }
         }
         if (last && ts == 0) {  // the new token, once per dim slice
-            const float pr = expf(fresh_s - mn);
+            const float pr = expf(sm.fresh_s - mn);
             l += pr;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] += pr * vn[dsl * 8 + e];
+            for (int e = 0; e < 8; ++e) o[e] += pr * sm.vn[dsl * 8 + e];
         }
         __syncthreads();  // sc and red are rewritten by the next pass
     };
     pass(0, kr);
-    // longer contexts: further passes, each loading its keys first (kept apart
-    // from the first pass so that no key register lives across a value phase)
+    // longer contexts: further passes of kHeadKSubs sub-passes, each loading its
+    // keys first (kept apart from the first pass so that no key register lives
+    // across a value phase)
     for (int t0 = kHeadPass; t0 <= pos; t0 += kHeadPass) {
         uint4 kr2[kHeadKSubs][4];
-        load_k(t0, max(1, min(kHeadPass, pos - t0)), false, kr2);
+        load_k(t0, min(kHeadPass, pos - t0), kr2);
         pass(t0, kr2);
     }
     // lanes with the same dsl: 4 per wave (16 apart), then the waves through LDS;
@@ -950,18 +962,36 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDeco
     l = xor_pair_sum<32>(xor_pair_sum<16>(l));
     if (lane < 16) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ored[wid][dsl * 8 + e] = o[e];
-        if (lane == 0) ored[wid][HD] = l;
+        for (int e = 0; e < 8; ++e) sm.ored[wid][dsl * 8 + e] = o[e];
+        if (lane == 0) sm.ored[wid][HD] = l;
     }
     __syncthreads();
     if (tid < HD) {
         float acc = 0.0f, lt = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            acc += ored[w][tid];
-            lt += ored[w][HD];
+            acc += sm.ored[w][tid];
+            lt += sm.ored[w][HD];
         }
-        p.out[static_cast<size_t>(qh) * HD + tid] = (acc * (1.0f / lt)) * sigmoid_dev(gv);
+        p.out[static_cast<size_t>(qh) * HD + tid] = (acc * (1.0f / lt)) * sigmoid_dev(sm.gate[tid]);
+    }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDecodeLaunch a) {
+    __shared__ HeadSmem<HD> sm;
+    const int pos = *a.g.pos;
+    // 128-token sub-passes holding the first pass's cached positions
+    const int ks = max(1, (min(pos, kHeadPass) + kHeadKSub - 1) / kHeadKSub);
+    switch (ks) {
+        case 1: head_attention<HD, 1>(a, sm, pos); break;
+        case 2: head_attention<HD, 2>(a, sm, pos); break;
+        case 3: head_attention<HD, 3>(a, sm, pos); break;
+        case 4: head_attention<HD, 4>(a, sm, pos); break;
+        case 5: head_attention<HD, 5>(a, sm, pos); break;
+        case 6: head_attention<HD, 6>(a, sm, pos); break;
+        case 7: head_attention<HD, 7>(a, sm, pos); break;
+        default: head_attention<HD, 8>(a, sm, pos); break;
     }
 }
 
