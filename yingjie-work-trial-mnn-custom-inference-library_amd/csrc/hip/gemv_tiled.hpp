@@ -324,9 +324,14 @@ __device__ __forceinline__ void load_batch(WBatch<R, META>& wb, const WSrc& src,
     for (int i = 0; i < R; ++i) {
         const int row = r0 + i;
         const bool ok = has_group && row < rows;
-        const uint32_t base = static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(c * 512 * BITS);
+        // 24-bit multiplies (rows, row bytes and groups per row are below 2^24):
+        // the 64-bit multiply-add the compiler otherwise picks reads an unused
+        // high half that can alias a pending load, and the wait for that load
+        // would hold back this batch
+        const uint32_t base = __umul24(static_cast<uint32_t>(row), row_bytes) + static_cast<uint32_t>(c * 512 * BITS);
         const uint32_t off = base + static_cast<uint32_t>(lane * 16);
-        const uint32_t moff = (static_cast<uint32_t>(row) * static_cast<uint32_t>(G) + c * 64 + lane) * (META ? 8u : 4u);
+        const uint32_t moff = (__umul24(static_cast<uint32_t>(row), static_cast<uint32_t>(G)) + c * 64 + lane) *
+                              (META ? 8u : 4u);
         wb.a[i] = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off : kOutOfRange, 0, kLoadNT));
         if constexpr (BITS == 4) {
             wb.b[i] = as_uint4(
