@@ -783,9 +783,12 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
     static_assert(HD == 128, "4 score lanes x 32 dims, 16 value lanes x 8 dims");
     constexpr int kWaves = kHeadThreads / kWave;
     const GqaLaunch& p = a.g;
-    const int qh = blockIdx.x;
     const int group = p.nq / p.nkv;
-    const int kh = qh / group;
+    // blocks b, b + nkv, b + 2 nkv, ... take the query heads of one kv head:
+    // blocks are dealt to the 8 XCDs round robin, so with nkv a multiple of 8
+    // a kv head's blocks share one XCD's L2 and its K / V come from memory once
+    const int kh = static_cast<int>(blockIdx.x) % p.nkv;
+    const int qh = kh * group + static_cast<int>(blockIdx.x) / p.nkv;
     const bool owner = qh % group == 0;  // appends the new key / value of kv head kh
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int sub = tid & 3, tt = tid >> 2;   // score lanes: dims 32 u + 8 sub + e of token tt
