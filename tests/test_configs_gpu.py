@@ -43,9 +43,9 @@ def assert_close(got, want, what):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     err = np.abs(got - want)
-    bad = np.nonzero(err > ATOL + RTOL * np.abs(want))[0]
+    bad = np.nonzero(~(err <= ATOL + RTOL * np.abs(want)))[0]  # a NaN anywhere counts as bad
     assert bad.size == 0, (f"{what}: {bad.size} of {want.size} outside tolerance; first {bad[0]} got {got[bad[0]]} "
-                           f"want {want[bad[0]]}; max err {err.max():.3g}")
+                           f"want {want[bad[0]]}; max err {np.nanmax(err):.3g}")
 
 
 def interleave(g, u):

@@ -27,8 +27,8 @@ ATOL, RTOL = 1e-2, 1e-3
 def close(got, want, what, atol=ATOL, rtol=RTOL):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     err = np.abs(got - want)
-    bad = err > atol + rtol * np.abs(want)
-    assert not bad.any(), f"{what}: {bad.sum()} / {bad.size} bad, max err {err.max():.3g}"
+    bad = ~(err <= atol + rtol * np.abs(want))  # a NaN anywhere counts as bad
+    assert not bad.any(), f"{what}: {bad.sum()} / {bad.size} bad, max err {np.nanmax(err):.3g}"
 
 
 _keep = []  # device buffers stay alive until the module ends (no free before the kernel ran)

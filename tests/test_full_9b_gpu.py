@@ -90,7 +90,7 @@ def test_full_9b_greedy_decode_matches_reference(model):
         assert st == 0
         want = ref["hidden"][i].astype(np.float64)
         err = np.abs(h - want)
-        bad = err > ATOL + RTOL * np.abs(want)
+        bad = ~(err <= ATOL + RTOL * np.abs(want))  # a NaN anywhere counts as bad
         dev_got, dev_want = deviation(h, w), deviation(want, w)
         dev_rel = float(np.linalg.norm(dev_got - dev_want) / np.linalg.norm(dev_want))
         tk_tok, tk_val = topk(sess)

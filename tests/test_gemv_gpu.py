@@ -24,9 +24,9 @@ def assert_close(got, want, what):
     want = np.asarray(want, np.float64)
     err = np.abs(got - want)
     bound = ATOL + RTOL * np.abs(want)
-    bad = np.nonzero(err > bound)[0]
-    assert bad.size == 0, (f"{what}: {bad.size} of {want.size} outside tolerance; worst idx {bad[np.argmax(err[bad])]} "
-                           f"got {got[bad[0]]} want {want[bad[0]]}; max err {err.max():.3g}")
+    bad = np.nonzero(~(err <= bound))[0]  # a NaN anywhere counts as bad
+    assert bad.size == 0, (f"{what}: {bad.size} of {want.size} outside tolerance; first idx {bad[0]} "
+                           f"got {got[bad[0]]} want {want[bad[0]]}; max err {np.nanmax(err):.3g}")
 
 
 def run_gemv(q, x, x_type=xb.F16, y_type=xb.F32, norm_w=None, eps=1e-6, epi=xb.EPI_STORE, y_init=None):

@@ -51,8 +51,8 @@ def compare_tokens(got, want, margins):
 
 def close(got, want, what):
     err = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
-    bad = err > ATOL + RTOL * np.abs(np.asarray(want, np.float64))
-    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside tolerance (max err {err.max():.3g})"
+    bad = ~(err <= ATOL + RTOL * np.abs(np.asarray(want, np.float64)))  # a NaN anywhere counts as bad
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside tolerance (max err {np.nanmax(err):.3g})"
 
 
 @pytest.fixture(scope="module")

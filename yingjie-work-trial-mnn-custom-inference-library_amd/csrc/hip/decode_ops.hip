@@ -911,13 +911,12 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
                 vr[jj] = buf_load_u4(r_v, static_cast<uint32_t>(ts + kHeadVTok * jj) * row_bytes + dsl * 16u);
             }
         }
-        if (last) m = fmaxf(m, sm.fresh_s);
         m = wave_max(m);
         if (lane == 0) sm.red[wid] = m;
-        __syncthreads();
-        m = sm.red[0];
+        __syncthreads();  // also orders the last wave's fresh_s before it is read
+        m = last ? sm.fresh_s : -INFINITY;
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) m = fmaxf(m, sm.red[w]);
+        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, sm.red[w]);
         const float mn = fmaxf(run_m, m);
         const float f_old = expf(run_m - mn);
         l *= f_old;

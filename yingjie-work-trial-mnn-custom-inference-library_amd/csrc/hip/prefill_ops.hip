@@ -229,10 +229,32 @@ gemm_w4_mfma_kernel(GemmArgs a) {
     extern __shared__ uint4 gemm_lds[];
     _Float16* xlds = reinterpret_cast<_Float16*>(gemm_lds);         // [2 stages][BT][kGemmXLd]
     float* slds = reinterpret_cast<float*>(xlds + 2 * T::kXStage);  // [2 stages][BR] scales
-    const int t0 = blockIdx.x * BT, r0 = blockIdx.y * BR;
+    // Tile of this block.  Blocks are dealt to the 8 XCDs round robin in
+    // launch order; a weight slab (128 rows of one K split, a "unit") is read
+    // by every token tile, so the token tiles of a unit are given launch
+    // indices b = 8 k + (unit mod 8) and share one XCD's L2: the weights come
+    // from memory once instead of once per XCD.  Units past the last multiple
+    // of 8 keep the plain order.
+    int tt, unit;
+    {
+        const int nt = gridDim.x;
+        const int b = blockIdx.x + nt * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int units8 = (gridDim.y * gridDim.z) & ~7;
+        if (b < units8 * nt) {
+            const int k = b >> 3;
+            unit = (k / nt) * 8 + (b & 7);
+            tt = k % nt;
+        } else {
+            const int b2 = b - units8 * nt;
+            unit = units8 + b2 / nt;
+            tt = b2 % nt;
+        }
+    }
+    const int split = unit / static_cast<int>(gridDim.y);
+    const int t0 = tt * BT, r0 = (unit - split * static_cast<int>(gridDim.y)) * BR;
     const int G = a.cols >> 6, gl = G - 1;
-    // this block's column groups: [g0, g1) of the K split blockIdx.z
-    const int g0 = static_cast<int>(blockIdx.z) * a.gps, g1 = min(G, g0 + a.gps), glast = g1 - 1;
+    // this block's column groups: [g0, g1) of K split `split`
+    const int g0 = split * a.gps, g1 = min(G, g0 + a.gps), glast = g1 - 1;
     const uint32_t row_bytes = static_cast<uint32_t>(a.cols) >> 1;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int q = lane >> 4, lr = lane & 15;
@@ -423,7 +445,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[i][j][v] *= tsc;
             if (a.part) {  // K split: this split's partial products, the reduce applies the epilogue
-                float* pr = a.part + (static_cast<size_t>(blockIdx.z) * a.m + t) * a.rows;
+                float* pr = a.part + (static_cast<size_t>(split) * a.m + t) * a.rows;
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
                     if (rb + v < a.rows) pr[rb + v] = acc[i][j][v];
