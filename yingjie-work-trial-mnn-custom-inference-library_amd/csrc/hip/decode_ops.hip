@@ -998,7 +998,7 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDeco
 }
 
 bool attn_head_supported(int nq, int nkv, int head_dim) {
-    return head_dim == 128 && nkv > 0 && nq % nkv == 0;
+    return head_dim == 128 && nkv > 0 && nq >= nkv && nq % nkv == 0;
 }
 
 hipError_t launch_attn_decode_head(const AttnDecodeLaunch& a, hipStream_t s) {
