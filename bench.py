@@ -58,8 +58,11 @@ class Events:
         return ms.value
 
 
-def w4_bytes(rows, cols):
-    return rows * cols // 2 + rows * (cols // 64) * 4
+def w4_bytes(rows, cols, meta=2):
+    """Device bytes of a W4 g64 matrix: the codes plus `meta` bytes of group
+    metadata (2: the fp16 scale the upload keeps when every zero point is 8, as
+    in these synthetic weights; 4: fp16 scale and zero)."""
+    return rows * cols // 2 + rows * (cols // 64) * meta
 
 
 # ---------------------------------------------------------------------------
@@ -213,7 +216,9 @@ def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6
     """Average duration of n back-to-back launches of one projection (HIP events
     on the default stream around the loop), weights rotated over enough copies
     (> 2x the 256 MB last-level cache) that every launch streams from HBM.
-    Algorithmic bytes = codes + fp16 (scale, zero) per group + x + y."""
+    Algorithmic bytes = the uploaded matrix (codes + group metadata: the fp16
+    scale alone here, every zero point being 2^(bits-1) = 8 for 4-bit codes;
+    fp16 (scale, zero) for the 3- and 2-bit widths) + x + y."""
     hip = xb.hip()
     rng = np.random.default_rng(rows + cols + bits)
     g = cols // 64
@@ -299,7 +304,7 @@ MODEL_DIR = os.environ.get("XQ_BENCH_MODEL_DIR", "/tmp/xq_synth_9b_w4a16_g64")
 # the same counter reads for a plain device-to-device copy of known size.
 # ---------------------------------------------------------------------------
 PMC_COPY_BYTES = 64 << 20
-GATE_UP_KERNEL = "gemv_w4_tiled<1, 12, 2, 2, 4, 0>"  # NCH=1, 12 row groups, 2 rows per wave, SiLU pair, 4-bit codes, fp16 metadata
+GATE_UP_KERNEL = "gemv_w4_tiled<1, 12, 2, 2, 4, 2>"  # NCH=1, 12 row groups, 2 rows per wave, SiLU pair, 4-bit codes, fp16 scale (zero 8)
 
 
 def pmc_probe(args):
@@ -467,8 +472,8 @@ def bench_decode(args):
                      "kernel": f"{GATE_UP_KERNEL}: gate/up 24576x4096 W4A16 g64 + RMSNorm prologue + SiLU*up "
                                "epilogue",
                      "method": "HIP events on the launch stream around 200 back-to-back launches on rotated weight "
-                               "copies (> 2x the last-level cache); algorithmic bytes = codes + fp16 (scale, zero) per "
-                               "group + x + y",
+                               "copies (> 2x the last-level cache); algorithmic bytes = codes + fp16 scale per group "
+                               "(every zero point is 8: the layout keeps the scale alone) + x + y",
                      "bytes_per_launch": bytes_gu, "avg_launch_us": t_gu, "launches_timed": 200 if proj else 0,
                      "per_projection": [{k: p[k] for k in ("name", "rows", "cols", "prologue", "epilogue", "avg_us",
                                                            "bytes", "GBps", "frac")} for p in proj],

@@ -49,10 +49,15 @@ enum {
                                  (fp16 scale, fp16 zero) packed in one u32          */
     XQHIP_LAYOUT_GENERIC = 1, /* any group size: reference row-major nibbles, fp32
                                  scales and zeros (used only for tiny shapes)        */
-    XQHIP_LAYOUT_TILED64_F32META = 2 /* TILED64 codes with the reference's fp32
+    XQHIP_LAYOUT_TILED64_F32META = 2, /* TILED64 codes with the reference's fp32
                                  (scale, zero) per group (8 bytes): chosen when a
                                  value is not exact in fp16 (e.g. asymmetric scales
                                  (max - min) / 15)                                  */
+    XQHIP_LAYOUT_TILED64_SCALE16 = 3 /* TILED64 codes with one fp16 scale per group
+                                 (2 bytes): chosen for 4-bit format-v1 matrices whose
+                                 zeros are all 8 (the symmetric quantiser, the
+                                 synthetic weights) and whose scales fp16 holds; the
+                                 zero point is implied                              */
 };
 
 /* A W4A16 matrix resident in HBM.  Semantics of the reference QuantizedMatrix

@@ -188,22 +188,26 @@ def run_one_hot(dw, rows, cols, columns):
     return got
 
 
-@pytest.mark.parametrize("rows,cols,affine", [(96, 4096, 0), (70, 12288, 0), (33, 8256, 0), (64, 4096, 1)])
-def test_nibble_unpack_exact_tiled64(rows, cols, affine):
+@pytest.mark.parametrize("rows,cols,affine,zero", [(96, 4096, 0, 8), (70, 12288, 0, 8), (33, 8256, 0, 8),
+                                                   (64, 4096, 1, 0), (40, 4096, 0, 5)])
+def test_nibble_unpack_exact_tiled64(rows, cols, affine, zero):
+    """Zero 8: the scale-only layout (zero implied); zero 5 and the affine
+    format: fp16 (scale, zero) pairs."""
     rng = np.random.default_rng(rows + cols + affine)
     packed = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
     g = cols // 64
     scales = np.ones(rows * g, np.float32)
-    zeros = np.zeros(rows * g, np.float32) if affine else np.full(rows * g, 8.0, np.float32)
+    zeros = np.full(rows * g, float(zero), np.float32)
     q = ob.Quantized(packed, scales, zeros, rows, cols, 64, affine)
     codes = unpack_codes(q).astype(np.int64)
     # the unpacking the oracle pins (even column low nibble) agrees with a bit reader
     assert np.array_equal(codes, unpack_bits(packed, rows, cols, 4))
     dw = xb.DeviceW4(packed, scales, zeros, rows, cols, 64, affine)
-    assert dw.w.layout == xb.LAYOUT_TILED64 and dw.w.inexact_meta == 0
+    layout = xb.LAYOUT_TILED64_SCALE16 if (zero == 8 and not affine) else xb.LAYOUT_TILED64
+    assert dw.w.layout == layout and dw.w.inexact_meta == 0
     columns = probe_columns(cols)
     got = run_one_hot(dw, rows, cols, columns)
-    want = (codes[:, columns].T - (0 if affine else 8)).astype(np.float32)
+    want = (codes[:, columns].T - (0 if affine else zero)).astype(np.float32)
     assert np.array_equal(got, want), f"{int((got != want).sum())} outputs differ from q - zero"
 
 

@@ -45,15 +45,20 @@ def run_gemv(q, x, x_type=xb.F16, y_type=xb.F32, norm_w=None, eps=1e-6, epi=xb.E
     return yd.download(ydt, out_n).astype(np.float32), w
 
 
+@pytest.mark.parametrize("zero", [8.0, 7.0])
 @pytest.mark.parametrize("rows,cols,seed", [(4096, 4096, 0), (12288, 4096, 1), (4096, 12288, 2), (1000, 1024, 3),
                                             (130, 4160, 4), (8, 64, 5), (1, 8192, 6)])
-def test_gemv_fp16_in_matches_oracle(rows, cols, seed):
-    q = w4_matrix(rows, cols, seed)
+def test_gemv_fp16_in_matches_oracle(rows, cols, seed, zero):
+    """Zero 8 everywhere uploads the fp16 scales alone (TILED64_SCALE16, zero
+    implied); any other zero keeps the fp16 (scale, zero) pairs (TILED64)."""
+    q = w4_matrix(rows, cols, seed, zero=zero)
     x = f16_vector(cols, seed + 100)
     want = ob.gemv(q, x.astype(np.float32))
     got, w = run_gemv(q, x, xb.F16, xb.F32)
-    assert w.w.layout == xb.LAYOUT_TILED64 and w.w.inexact_meta == 0
-    assert_close(got, want, f"gemv {rows}x{cols}")
+    layout = xb.LAYOUT_TILED64_SCALE16 if zero == 8.0 else xb.LAYOUT_TILED64
+    assert w.w.layout == layout and w.w.inexact_meta == 0
+    assert w.weight_bytes() == rows * cols // 2 + rows * (cols // 64) * (2 if zero == 8.0 else 4)
+    assert_close(got, want, f"gemv {rows}x{cols} zero {zero}")
 
 
 def test_gemv_config0_fp16_out():

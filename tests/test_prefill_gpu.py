@@ -64,11 +64,14 @@ def run_gemm(q, X, epi, pro=None, gamma=None, z=None, head_dim=0, y0=None):
     return ydev.download(np.float32, m * out_cols).reshape(m, out_cols)
 
 
-@pytest.mark.parametrize("rows,cols,m,pro,affine", [(4096, 4096, 64, "rms", 0), (200, 4096, 5, "rms", 0),
-                                                    (96, 12288, 70, None, 0), (130, 640, 130, "rms", 1),
-                                                    (64, 4096, 33, "gated", 0)])
-def test_gemm_store_vs_per_token_gemv(rows, cols, m, pro, affine):
-    q = w4_matrix(rows, cols, rows + cols + m, affine=affine)
+@pytest.mark.parametrize("rows,cols,m,pro,affine,zero", [(4096, 4096, 64, "rms", 0, 8.0), (200, 4096, 5, "rms", 0, 8.0),
+                                                         (96, 12288, 70, None, 0, 8.0), (130, 640, 130, "rms", 1, 8.0),
+                                                         (64, 4096, 33, "gated", 0, 8.0),
+                                                         (256, 4096, 40, "rms", 0, 6.0)])
+def test_gemm_store_vs_per_token_gemv(rows, cols, m, pro, affine, zero):
+    """Zero 8 (format v1): the scale-only layout, no zero-point pass; zero 6
+    and the affine format: fp16 (scale, zero) pairs and the zero-point pass."""
+    q = w4_matrix(rows, cols, rows + cols + m, affine=affine, zero=zero)
     rng = np.random.default_rng(m)
     X = rng.normal(0, 1, (m, cols)).astype(np.float32)
     gamma = z = None

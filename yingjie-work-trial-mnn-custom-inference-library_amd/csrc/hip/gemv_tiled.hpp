@@ -302,7 +302,7 @@ __host__ __device__ constexpr uint32_t tiled_row_bytes(int cols) {
 template <int BITS, int META>
 __device__ __forceinline__ WSrc make_wsrc(const uint8_t* nib, const uint32_t* meta, int rows, int cols) {
     const uint32_t nib_bytes = static_cast<uint32_t>(rows) * tiled_row_bytes<BITS>(cols);
-    const uint32_t meta_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 6) * (META ? 8u : 4u);
+    const uint32_t meta_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 6) * kMetaGroupBytes<META>;
     WSrc s;
     s.nib = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(nib), 0, nib_bytes, kRsrcWord3);
     s.meta = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(meta), 0, meta_bytes, kRsrcWord3);
@@ -331,7 +331,7 @@ __device__ __forceinline__ void load_batch(WBatch<R, META>& wb, const WSrc& src,
         const uint32_t base = __umul24(static_cast<uint32_t>(row), row_bytes) + static_cast<uint32_t>(c * 512 * BITS);
         const uint32_t off = base + static_cast<uint32_t>(lane * 16);
         const uint32_t moff = (__umul24(static_cast<uint32_t>(row), static_cast<uint32_t>(G)) + c * 64 + lane) *
-                              (META ? 8u : 4u);
+                              kMetaGroupBytes<META>;
         wb.a[i] = as_uint4(__builtin_amdgcn_raw_buffer_load_b128(src.nib, ok ? off : kOutOfRange, 0, kLoadNT));
         if constexpr (BITS == 4) {
             wb.b[i] = as_uint4(
@@ -341,10 +341,7 @@ __device__ __forceinline__ void load_batch(WBatch<R, META>& wb, const WSrc& src,
             const u32x2 h = __builtin_amdgcn_raw_buffer_load_b64(src.nib, ok ? hoff : kOutOfRange, 0, kLoadNT);
             wb.b[i] = make_uint4(h.x, h.y, 0u, 0u);
         }
-        if constexpr (META)
-            wb.m[i] = __builtin_amdgcn_raw_buffer_load_b64(src.meta, ok ? moff : kOutOfRange, 0, kLoadNT);
-        else
-            wb.m[i] = __builtin_amdgcn_raw_buffer_load_b32(src.meta, ok ? moff : kOutOfRange, 0, kLoadNT);
+        wb.m[i] = load_meta<META, kLoadNT>(src.meta, ok ? moff : kOutOfRange);
     }
 }
 
@@ -522,8 +519,12 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
                 //   v2: s sum qx + z sum x   = e (s D + (8 s + z) G)
                 const float df = static_cast<float>(Dg);
                 const float sc = meta_scale(cur.m[i]);
-                const float z = meta_zero(cur.m[i]);
-                acc[i] = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
+                if constexpr (META == 2) {  // zero 8, format v1: s e D (the v1 form with 8 - z = 0)
+                    acc[i] = (sc * ge) * df;
+                } else {
+                    const float z = meta_zero(cur.m[i]);
+                    acc[i] = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
+                }
                 acc[i] = wave_sum(acc[i]);
             }
         }
@@ -707,7 +708,9 @@ static hipError_t launch_tiled_bits(const GemvLaunch& p, hipStream_t s) {
     }
 }
 
-// TILED64 launches with fp32 metadata (gemv_w4a16_m32.hip).
+// TILED64 launches with fp32 metadata (gemv_w4a16_m32.hip) and with the fp16
+// scale alone, zero 8 (gemv_w4a16_s16.hip).
 hipError_t launch_gemv_tiled_m32(const GemvLaunch& p, hipStream_t s);
+hipError_t launch_gemv_tiled_s16(const GemvLaunch& p, hipStream_t s);
 
 }  // namespace xqhip

@@ -222,7 +222,8 @@ __device__ __forceinline__ half8 codes_to_h8(uint32_t w) {
 template <int WGR, int WGT, int TI, int TJ, int EPI, int META>
 __global__ void __launch_bounds__(kWave * WGR * WGT) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_w4_mfma_kernel(GemmArgs a) {
-    constexpr uint32_t kMetaBytes = META ? 8u : 4u;  // fp16 pair in a u32, or the fp32 pair
+    // fp16 (scale, zero) in a u32, the fp32 pair (the scale is its first word), or the fp16 scale alone
+    constexpr uint32_t kMetaBytes = kMetaGroupBytes<META>;
     using T = GemmTile<WGR, WGT, TI, TJ>;
     constexpr int BR = T::kBR, BT = T::kBT, XU = T::kXU, NT = T::kThreads;
     constexpr int kTokStep = NT / 16;  // tokens between a thread's x pieces
@@ -301,14 +302,15 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         const uint32_t g_ = static_cast<uint32_t>(gg);                                                       \
         _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) X[j_] =                                            \
             __builtin_amdgcn_raw_buffer_load_b128(x_r, xoff[j_], g_ * 128u, 0);                              \
-        M = __builtin_amdgcn_raw_buffer_load_b32(meta_r, moff, g_ * kMetaBytes, 0);                           \
+        M = META == 2 ? static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(meta_r, moff, g_ * kMetaBytes, 0)) \
+                      : __builtin_amdgcn_raw_buffer_load_b32(meta_r, moff, g_ * kMetaBytes, 0);                \
     }
 #define GEMM_STORE_X(X, M, st)                                                                               \
     {                                                                                                        \
         _Float16* d_ = xlds + (st) * T::kXStage + xdst;                                                      \
         _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) *reinterpret_cast<u32x4*>(d_ + j_ * kTokStep * kGemmXLd) = \
             X[j_];                                                                                           \
-        if (s_thread) slds[(st) * BR + threadIdx.x] = META ? __uint_as_float(M) : half_lo(M);                 \
+        if (s_thread) slds[(st) * BR + threadIdx.x] = META == 1 ? __uint_as_float(M) : half_lo(M);            \
     }
 // MFMAs of one group, each tile's four chained into a per-group sum that is scaled into acc
 #define GEMM_COMPUTE(st, W)                                                                                  \
@@ -392,10 +394,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const uint32_t o = g8 + e < g1 ? off + kMetaBytes * e : kBufOOB;
-                if constexpr (META)
-                    mw[i][e] = __builtin_amdgcn_raw_buffer_load_b64(meta_r, o, 0, 0);
-                else
-                    mw[i][e] = __builtin_amdgcn_raw_buffer_load_b32(meta_r, o, 0, 0);
+                mw[i][e] = load_meta<META, 0>(meta_r, o);
             }
         }
 #pragma unroll
@@ -514,7 +513,8 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(const float* __
 }
 
 bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro) {
-    if ((layout != 0 && layout != 2) || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0) return false;
+    if ((layout != 0 && layout != 2 && layout != 3) || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0)
+        return false;
     if (pro.mode == PRO_GATED)
         return pro.head_dim > 0 && pro.head_dim % 8 == 0 && cols % pro.head_dim == 0 &&
                cols / pro.head_dim <= kPrepMaxHeads;
@@ -552,12 +552,19 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.zero_is_8, xh, xs, ts,
                (G + splits - 1) / splits, part, p.m, m_pad, p.y, p.ldy};
     // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
-    const bool m32 = p.layout == 2;
+    // metadata form: 0 fp16 (scale, zero), 1 fp32 pair (layout 2), 2 fp16 scale, zero 8 (layout 3)
+    const int meta = p.layout == 2 ? 1 : (p.layout == 3 ? 2 : 0);
     hipError_t e = hipErrorInvalidValue;
-    switch (p.epi) {
-        case 0: e = m32 ? launch_gemm_cfg<4, 1, 2, 4, 0, 1>(a, splits, s) : launch_gemm_cfg<4, 1, 2, 4, 0, 0>(a, splits, s); break;
-        case 1: e = m32 ? launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, splits, s) : launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, splits, s); break;
-        case 2: e = m32 ? launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, splits, s) : launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, splits, s); break;
+    switch (p.epi * 3 + meta) {
+        case 0: e = launch_gemm_cfg<4, 1, 2, 4, 0, 0>(a, splits, s); break;
+        case 1: e = launch_gemm_cfg<4, 1, 2, 4, 0, 1>(a, splits, s); break;
+        case 2: e = launch_gemm_cfg<4, 1, 2, 4, 0, 2>(a, splits, s); break;
+        case 3: e = launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, splits, s); break;
+        case 4: e = launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, splits, s); break;
+        case 5: e = launch_gemm_cfg<4, 1, 2, 4, 1, 2>(a, splits, s); break;
+        case 6: e = launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, splits, s); break;
+        case 7: e = launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, splits, s); break;
+        case 8: e = launch_gemm_cfg<4, 1, 2, 4, 2, 2>(a, splits, s); break;
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess || splits == 1) return e;

@@ -254,7 +254,8 @@ static void pack_meta_f32(const float* scales, const float* zeros, size_t n, std
 // c*2048 + h*gc*16 + l*16: one wave-wide 16-byte load per half is 1 KiB
 // contiguous.  Nibble order inside each 16 bytes is unchanged (even column in
 // the low nibble); every code q is stored as q ^ 8.  Metadata becomes one u32
-// per group: fp16 scale | fp16 zero<<16.
+// per group: fp16 scale | fp16 zero<<16; the fp16 scale alone (u16) when every
+// zero is 8 (format v1); the fp32 pair when fp16 cannot hold a value.
 int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols, int group,
                     int affine, xqhip_w4* out) {
     if (!packed || !scales || !zeros || !out || rows <= 0 || cols <= 0 || group <= 0)
@@ -273,6 +274,7 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
     out->nib_bytes = row_bytes * rows;
     std::vector<uint8_t> nib_host;
     std::vector<uint32_t> meta_u32;
+    std::vector<uint16_t> meta_u16;
     std::vector<float> meta_f32;
     const void* nib_src = packed;
     const void* meta_src = nullptr;
@@ -298,9 +300,17 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
         if (out->inexact_meta > 0) {  // keep the reference's fp32 values
             pack_meta_f32(scales, zeros, n_meta, &meta_u32);
             out->layout = XQHIP_LAYOUT_TILED64_F32META;
+            out->meta_bytes = meta_u32.size() * 4;
+        } else if (out->zero_is_8) {  // the zero point is implied: the fp16 scales alone
+            meta_u16.resize(n_meta);
+            for (size_t i = 0; i < n_meta; ++i) meta_u16[i] = static_cast<uint16_t>(meta_u32[i] & 0xFFFFu);
+            out->layout = XQHIP_LAYOUT_TILED64_SCALE16;
+            out->meta_bytes = meta_u16.size() * 2;
+        } else {
+            out->meta_bytes = meta_u32.size() * 4;
         }
-        out->meta_bytes = meta_u32.size() * 4;
-        meta_src = meta_u32.data();
+        meta_src = out->layout == XQHIP_LAYOUT_TILED64_SCALE16 ? static_cast<const void*>(meta_u16.data())
+                                                                : static_cast<const void*>(meta_u32.data());
     } else {
         meta_f32.resize(static_cast<size_t>(rows) * G * 2);
         std::memcpy(meta_f32.data(), scales, static_cast<size_t>(rows) * G * 4);
@@ -406,8 +416,10 @@ static int validate_w4(const xqhip_w4* w, const char* who) {
     if (!w || !w->nib || !w->meta || w->rows <= 0 || w->cols <= 0)
         return fail(XQHIP_EINVAL, "%s: matrix is not uploaded", who);
     if (w->layout != XQHIP_LAYOUT_TILED64 && w->layout != XQHIP_LAYOUT_GENERIC &&
-        w->layout != XQHIP_LAYOUT_TILED64_F32META)
+        w->layout != XQHIP_LAYOUT_TILED64_F32META && w->layout != XQHIP_LAYOUT_TILED64_SCALE16)
         return fail(XQHIP_EINVAL, "%s: unknown layout %d", who, w->layout);
+    if (w->layout == XQHIP_LAYOUT_TILED64_SCALE16 && (w->bits != 4 || w->affine || !w->zero_is_8))
+        return fail(XQHIP_EINVAL, "%s: the scale-only layout holds 4-bit format-v1 matrices with zero 8", who);
     if (w->layout != XQHIP_LAYOUT_GENERIC && (w->group != 64 || w->cols % 64 != 0 || w->cols / 64 > 256))
         return fail(XQHIP_EINVAL, "%s: inconsistent TILED64 matrix %dx%d g%d", who, w->rows, w->cols, w->group);
     if (w->bits != 4 && w->bits != 3 && w->bits != 2)

@@ -51,14 +51,35 @@ __device__ __forceinline__ float half_hi(uint32_t u) {
 }
 
 // Group metadata word of a TILED64 matrix: fp16 (scale, zero) in one u32
-// (META 0) or the fp32 (scale, zero) pair in two (META 1, matrices whose values
-// fp16 cannot hold exactly).
+// (META 0), the fp32 (scale, zero) pair in two (META 1, matrices whose values
+// fp16 cannot hold exactly), or the fp16 scale alone with the zero point 8
+// implied (META 2, format-v1 matrices whose zeros are all 8).
+struct Scale16 {
+    uint32_t v;  // fp16 scale in the low half
+};
 template <int META>
-using MetaWord = typename std::conditional<META != 0, u32x2, uint32_t>::type;
+using MetaWord = typename std::conditional<META == 1, u32x2,
+                                           typename std::conditional<META == 2, Scale16, uint32_t>::type>::type;
+template <int META>
+constexpr uint32_t kMetaGroupBytes = META == 1 ? 8u : (META == 2 ? 2u : 4u);  // per group
 __device__ __forceinline__ float meta_scale(uint32_t m) { return half_lo(m); }
 __device__ __forceinline__ float meta_zero(uint32_t m) { return half_hi(m); }
 __device__ __forceinline__ float meta_scale(u32x2 m) { return __uint_as_float(m.x); }
 __device__ __forceinline__ float meta_zero(u32x2 m) { return __uint_as_float(m.y); }
+__device__ __forceinline__ float meta_scale(Scale16 m) { return half_lo(m.v); }
+__device__ __forceinline__ float meta_zero(Scale16) { return 8.0f; }
+// A group's metadata from a buffer resource at byte offset off.
+// (AUX: the load's cache-policy bits)
+template <int META, int AUX>
+__device__ __forceinline__ MetaWord<META> load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (META == 1) {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX);
+    } else if constexpr (META == 2) {
+        return Scale16{static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX))};
+    } else {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
+    }
+}
 
 // Range-checked buffer loads: an offset at or past the resource's byte range
 // returns 0 without a memory access, so a load can be issued unconditionally
