@@ -1256,82 +1256,104 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
     const int j = j0 + col;
     const bool active = j < dv;
     float* S = p.state + static_cast<size_t>(vh) * DK * dv;
+    const __amdgpu_buffer_rsrc_t r_state = buf_rsrc(S, static_cast<uint32_t>(DK * dv) * 4u);
     float sreg[RS];
 #pragma unroll
-    for (int r = 0; r < RS; ++r) sreg[r] = active ? S[static_cast<size_t>(ig + 16 * r) * dv + j] : 0.0f;
+    for (int r = 0; r < RS; ++r)
+        sreg[r] = buf_load_f32(r_state, active ? (static_cast<uint32_t>(ig + 16 * r) * dv + j) * 4u : kBufOOB);
     const float rdk = 1.0f / sqrtf(static_cast<float>(DK));
-    const float* conv = p.ws;
-    const float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim;
-    // staging: thread th loads q/k floats th, th + 256, ... of a group, v and (beta, decay)
+    // staging: thread th loads q/k floats th, th + 256, ... of a group, v and (beta, decay).
+    // Every load is a range-checked buffer load over the group's tokens (tokens past
+    // the end read 0) with no branch around it, so each wait covers exactly the loads
+    // it needs and the token loop's LDS reads are not held behind a branch.
     constexpr int QK = TG * 2 * DK / 256;  // per thread
-    float rq[QK], rv = 0.0f, rg = 0.0f;
+    float rq[QK], rv, rg;
+    const size_t aux0 = static_cast<size_t>(p.tokens) * conv_dim;
     auto load_stage = [&](int g0) {
+        // (uniform: readfirstlane keeps the descriptor in scalar registers)
+        const uint32_t nt = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(max(0, min(TG, p.tokens - g0))));
+        const __amdgpu_buffer_rsrc_t r_c = buf_rsrc(p.ws + static_cast<size_t>(g0) * conv_dim, nt * conv_dim * 4u);
+        const __amdgpu_buffer_rsrc_t r_g =
+            buf_rsrc(p.ws + aux0 + static_cast<size_t>(g0) * p.lv_n * 2, nt * p.lv_n * 8u);
 #pragma unroll
         for (int u = 0; u < QK; ++u) {
             const int e = threadIdx.x + u * 256;
             const int tk = e / (2 * DK), ch = e % (2 * DK);
-            const int tok = min(g0 + tk, p.tokens - 1);
             const int cc = (ch >= DK ? p.lk_n * DK : 0) + kh * DK + (ch % DK);
-            rq[u] = conv[static_cast<size_t>(tok) * conv_dim + cc];
+            rq[u] = buf_load_f32(r_c, (static_cast<uint32_t>(tk) * conv_dim + cc) * 4u);
         }
-        {
-            const int tk = threadIdx.x >> 4, cl = threadIdx.x & 15;  // TG x 16 values
-            const int tok = min(g0 + tk, p.tokens - 1);
-            rv = j0 + cl < dv ? conv[static_cast<size_t>(tok) * conv_dim + 2 * p.lk_n * DK + vh * dv + j0 + cl] : 0.0f;
-        }
-        if (threadIdx.x < 2 * TG) {
-            const int tok = min(g0 + static_cast<int>(threadIdx.x >> 1), p.tokens - 1);
-            rg = aux[(static_cast<size_t>(tok) * p.lv_n + vh) * 2 + (threadIdx.x & 1)];
-        }
+        const int tk = threadIdx.x >> 4, cl = threadIdx.x & 15;  // TG x 16 values
+        rv = buf_load_f32(r_c, j0 + cl < dv ? (static_cast<uint32_t>(tk) * conv_dim + 2 * p.lk_n * DK + vh * dv + j0 + cl) * 4u
+                                            : kBufOOB);
+        rg = buf_load_f32(r_g, threadIdx.x < 2 * TG ? ((threadIdx.x >> 1) * p.lv_n * 2u + vh * 2u + (threadIdx.x & 1)) * 4u
+                                                     : kBufOOB);
     };
-    auto store_stage = [&](int buf) {
+    // tokens past the end get beta 0 and decay 1 (their q / k / v read 0): the state
+    // passes through them unchanged
+    auto store_stage = [&](int buf, int g0) {
 #pragma unroll
         for (int u = 0; u < QK; ++u) {
             const int e = threadIdx.x + u * 256;
             const int tk = e / (2 * DK), ch = e % (2 * DK);
-            if (ch < DK) qs[buf][tk][ch] = rq[u]; else ks[buf][tk][ch - DK] = rq[u];
+            *(ch < DK ? &qs[buf][tk][ch] : &ks[buf][tk][ch - DK]) = rq[u];
         }
         vs[buf][threadIdx.x >> 4][threadIdx.x & 15] = rv;
-        if (threadIdx.x < 2 * TG) gs[buf][threadIdx.x >> 1][threadIdx.x & 1] = rg;
+        if (threadIdx.x < 2 * TG) {
+            const bool live = g0 + static_cast<int>(threadIdx.x >> 1) < p.tokens;
+            gs[buf][threadIdx.x >> 1][threadIdx.x & 1] = live ? rg : static_cast<float>(threadIdx.x & 1);
+        }
     };
     load_stage(0);
     for (int g0 = 0, buf = 0; g0 < p.tokens; g0 += TG, buf ^= 1) {
-        store_stage(buf);
+        store_stage(buf, g0);
         __syncthreads();  // this buffer is complete; the other one is no longer read
-        if (g0 + TG < p.tokens) load_stage(g0 + TG);
+        load_stage(g0 + TG);  // past the last group: every load reads 0
         const int nt = min(TG, p.tokens - g0);
-        // A fixed, unrolled TG-token loop (so the LDS reads of later tokens are issued
-        // early); tokens past the end run with beta 0 and decay 1, leaving the state as
-        // is.  Each token's output is kept by lane ig == k and stored after the loop.
+        // A fixed, unrolled TG-token loop; each token's output is kept by lane ig == k
+        // and stored after the loop.
         float my_o = 0.0f;
-#pragma unroll
-        for (int k = 0; k < TG; ++k) {
-            const bool live = k < nt;
-            const float beta = live ? gs[buf][k][0] : 0.0f, decay = live ? gs[buf][k][1] : 1.0f;
-            const float vj = vs[buf][k][col];
-            float kr[RS], qr[RS];
+        // k / q / v / beta / decay of token k + 2 are read from LDS right after token
+        // k's state update (a three-slot register ring; the scheduling barrier keeps
+        // the reads there), so their latency hides behind token k's output and token
+        // k + 1's update, which the scheduler interleaves after the barrier
+        float kb[3][RS], qb[3][RS], vb[3], bb[3], db[3];
+        auto read_token = [&](int k, float (&kk)[RS], float (&qq)[RS], float& v, float& b, float& d) {
 #pragma unroll
             for (int r = 0; r < RS; ++r) {
-                kr[r] = ks[buf][k][ig + 16 * r];
-                qr[r] = qs[buf][k][ig + 16 * r];
+                kk[r] = ks[buf][k][ig + 16 * r];
+                qq[r] = qs[buf][k][ig + 16 * r];
             }
+            v = vs[buf][k][col];
+            b = gs[buf][k][0];
+            d = gs[buf][k][1];
+        };
+        read_token(0, kb[0], qb[0], vb[0], bb[0], db[0]);
+        read_token(1, kb[1], qb[1], vb[1], bb[1], db[1]);
+#pragma unroll
+        for (int k = 0; k < TG; ++k) {
+            const int c = k % 3;
             float pa = 0.0f, pb = 0.0f;  // two chains
 #pragma unroll
             for (int r = 0; r < RS; r += 2) {
-                sreg[r] *= decay;
-                sreg[r + 1] *= decay;
-                pa = fmaf(sreg[r], kr[r], pa);
-                pb = fmaf(sreg[r + 1], kr[r + 1], pb);
+                sreg[r] *= db[c];
+                sreg[r + 1] *= db[c];
+                pa = fmaf(sreg[r], kb[c][r], pa);
+                pb = fmaf(sreg[r + 1], kb[c][r + 1], pb);
             }
             const float pred = lanes_sum<16>(pa + pb);
-            const float delta = beta * (vj - pred);
+            const float delta = bb[c] * (vb[c] - pred);
+#pragma unroll
+            for (int r = 0; r < RS; ++r) sreg[r] = fmaf(kb[c][r], delta, sreg[r]);
+            if (k + 2 < TG) {
+                const int n = (k + 2) % 3;
+                read_token(k + 2, kb[n], qb[n], vb[n], bb[n], db[n]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
             float oa = 0.0f, ob = 0.0f;
 #pragma unroll
             for (int r = 0; r < RS; r += 2) {
-                sreg[r] = fmaf(kr[r], delta, sreg[r]);
-                sreg[r + 1] = fmaf(kr[r + 1], delta, sreg[r + 1]);
-                oa = fmaf(sreg[r], qr[r], oa);
-                ob = fmaf(sreg[r + 1], qr[r + 1], ob);
+                oa = fmaf(sreg[r], qb[c][r], oa);
+                ob = fmaf(sreg[r + 1], qb[c][r + 1], ob);
             }
             const float o = lanes_sum<16>(oa + ob);
             if (ig == k) my_o = o;
