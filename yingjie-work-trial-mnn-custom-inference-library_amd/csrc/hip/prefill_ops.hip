@@ -142,6 +142,153 @@ __global__ void __launch_bounds__(256) prep_x_kernel(const float* __restrict__ x
     }
 }
 
+// The same for rows of NK * 2048 columns with 16-byte aligned rows, weights and
+// gates, the prologue mode a template argument: thread i owns the 8-column
+// pieces i, i + 256, ... of its token's row and loads each once, as 16-byte
+// loads with no branch around them (the generic kernel reads the row three
+// times, one float per load); the gated norm's per-head sums stay inside the
+// 16 lanes that own a 128-column head.
+template <int NK, int MODE>
+__global__ void __launch_bounds__(256) prep_x_vec_kernel(const float* __restrict__ x, int ldx, int m, Prologue pro,
+                                                         int ldz, _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                         float* __restrict__ xs, float* __restrict__ ts) {
+    constexpr int kCols = NK * 2048, kG = kCols / 64;
+    __shared__ float red_s[4], red_m[4];
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    uint4* oh = reinterpret_cast<uint4*>(xh + static_cast<size_t>(t) * kCols);
+    uint4* ol = reinterpret_cast<uint4*>(xl + static_cast<size_t>(t) * kCols);
+    float* os = xs + static_cast<size_t>(t) * kG;
+    if (t >= m) {  // block-uniform
+#pragma unroll
+        for (int k = 0; k < NK; ++k) oh[threadIdx.x + 256 * k] = ol[threadIdx.x + 256 * k] = make_uint4(0u, 0u, 0u, 0u);
+        for (int g = threadIdx.x; g < kG; g += 256) os[g] = 0.0f;
+        if (threadIdx.x == 0) ts[t] = 1.0f;
+        return;
+    }
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * ldx);
+    float4 xv[NK][2], wv[NK][2], zv[NK][2];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int c4 = 2 * (threadIdx.x + 256 * k);  // float4 index of the piece
+        xv[k][0] = xr[c4];
+        xv[k][1] = xr[c4 + 1];
+        if constexpr (MODE == PRO_RMS) {
+            wv[k][0] = reinterpret_cast<const float4*>(pro.w)[c4];
+            wv[k][1] = reinterpret_cast<const float4*>(pro.w)[c4 + 1];
+        } else if constexpr (MODE == PRO_GATED) {
+            // head_dim 128: the piece's offset in its head is 8 (i mod 16)
+            const int d4 = 2 * (threadIdx.x & 15);
+            wv[k][0] = reinterpret_cast<const float4*>(pro.w)[d4];
+            wv[k][1] = reinterpret_cast<const float4*>(pro.w)[d4 + 1];
+            const float4* zr = reinterpret_cast<const float4*>(pro.z + static_cast<size_t>(t) * ldz);
+            zv[k][0] = zr[c4];
+            zv[k][1] = zr[c4 + 1];
+        }
+    }
+    float v[NK][8];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const float4 a = xv[k][0], b = xv[k][1];
+        v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+        v[k][4] = b.x; v[k][5] = b.y; v[k][6] = b.z; v[k][7] = b.w;
+    }
+    if constexpr (MODE == PRO_RMS) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NK; ++k)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += v[k][e] * v[k][e];
+        ss = wave_sum(ss);
+        if (lane == 0) red_s[wid] = ss;
+        __syncthreads();
+        ss = (red_s[0] + red_s[1]) + (red_s[2] + red_s[3]);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(kCols) + pro.eps);
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const float w8[8] = {wv[k][0].x, wv[k][0].y, wv[k][0].z, wv[k][0].w,
+                                 wv[k][1].x, wv[k][1].y, wv[k][1].z, wv[k][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[k][e] = v[k][e] * inv * w8[e];
+        }
+    } else if constexpr (MODE == PRO_GATED) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += v[k][e] * v[k][e];
+            ss = lanes_sum<16>(ss);  // the head's 16 pieces
+            const float ih = 1.0f / sqrtf(ss / 128.0f + pro.eps);
+            const float w8[8] = {wv[k][0].x, wv[k][0].y, wv[k][0].z, wv[k][0].w,
+                                 wv[k][1].x, wv[k][1].y, wv[k][1].z, wv[k][1].w};
+            const float z8[8] = {zv[k][0].x, zv[k][0].y, zv[k][0].z, zv[k][0].w,
+                                 zv[k][1].x, zv[k][1].y, zv[k][1].z, zv[k][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[k][e] = v[k][e] * ih * w8[e] * silu_dev(z8[e]);
+        }
+    }
+    // the row's power-of-two scale from its largest magnitude
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[k][e]));
+    mx = wave_max(mx);
+    if (lane == 0) red_m[wid] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    int ex = 0;
+    frexpf(mx, &ex);
+    const float down = mx > 0.0f ? ldexpf(1.0f, 13 - ex) : 1.0f;
+    if (threadIdx.x == 0) ts[t] = mx > 0.0f ? ldexpf(1.0f, ex - 13) : 1.0f;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int c8 = threadIdx.x + 256 * k;
+        uint32_t ph[4], pl[4];
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] *= down;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // positions 2q, 2q + 1 <- columns q, q + 4
+            const float va = v[k][q], vb = v[k][q + 4];
+            const _Float16 ha = static_cast<_Float16>(va), hb = static_cast<_Float16>(vb);
+            ph[q] = pack_h2(ha, hb);
+            pl[q] = pack_h2(static_cast<_Float16>(va - static_cast<float>(ha)),
+                            static_cast<_Float16>(vb - static_cast<float>(hb)));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += v[k][e];
+        oh[c8] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+        ol[c8] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+        sum = lanes_sum<8>(sum);
+        if ((c8 & 7) == 0) os[c8 >> 3] = sum;
+    }
+}
+
+// the vectorised form's launch, or false when the shape or alignment needs the generic kernel
+template <int NK>
+static bool launch_prep_vec(const GemmLaunch& p, int m_pad, _Float16* xh, _Float16* xl, float* xs, float* ts,
+                            hipStream_t s) {
+    if (p.pro.mode == PRO_RMS)
+        hipLaunchKernelGGL((prep_x_vec_kernel<NK, PRO_RMS>), dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.pro,
+                           p.ldz, xh, xl, xs, ts);
+    else if (p.pro.mode == PRO_GATED)
+        hipLaunchKernelGGL((prep_x_vec_kernel<NK, PRO_GATED>), dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.pro,
+                           p.ldz, xh, xl, xs, ts);
+    else
+        hipLaunchKernelGGL((prep_x_vec_kernel<NK, PRO_NONE>), dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.pro,
+                           p.ldz, xh, xl, xs, ts);
+    return true;
+}
+
+static bool prep_vec_ok(const GemmLaunch& p) {
+    auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    if (p.cols % 2048 != 0 || !al16(p.x) || p.ldx % 4 != 0) return false;
+    if (p.pro.mode == PRO_RMS) return al16(p.pro.w);
+    if (p.pro.mode == PRO_GATED) return p.pro.head_dim == 128 && al16(p.pro.w) && al16(p.pro.z) && p.ldz % 4 == 0;
+    return p.pro.mode == PRO_NONE;
+}
+
 // ---------------------------------------------------------------------------
 // W4A16 GEMM, y[t][r] (op)= sum_k w[r][k] x[t][k] for a prompt chunk.
 //
@@ -542,8 +689,14 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     _Float16* xl = xh + static_cast<size_t>(m_pad) * p.cols;
     float* xs = reinterpret_cast<float*>(xl + static_cast<size_t>(m_pad) * p.cols);
     float* ts = xs + static_cast<size_t>(m_pad) * (p.cols / 64);
-    hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
-                       xs, ts);
+    const int nk = p.cols / 2048;
+    const bool vec = prep_vec_ok(p) && (nk == 1 || nk == 2 || nk == 6) &&
+                     (nk == 1 ? launch_prep_vec<1>(p, m_pad, xh, xl, xs, ts, s)
+                              : nk == 2 ? launch_prep_vec<2>(p, m_pad, xh, xl, xs, ts, s)
+                                        : launch_prep_vec<6>(p, m_pad, xh, xl, xs, ts, s));
+    if (!vec)
+        hipLaunchKernelGGL(prep_x_kernel, dim3(m_pad), dim3(256), 0, s, p.x, p.ldx, p.m, p.cols, p.pro, p.ldz, xh, xl,
+                           xs, ts);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const int splits = gemm_splits(p.rows, p.m, p.cols, p.epi);
     const int G = p.cols / 64;

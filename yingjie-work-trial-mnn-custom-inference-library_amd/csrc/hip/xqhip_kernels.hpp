@@ -159,7 +159,7 @@ struct GemmLaunch {
     const uint8_t* nib;  // TILED64 matrix
     const void* meta;
     int rows, cols, affine;
-    int layout;      // 0 TILED64 (fp16 metadata), 2 TILED64_F32META
+    int layout;      // 0 TILED64 (fp16 metadata), 2 TILED64_F32META, 3 TILED64_SCALE16
     int zero_is_8;   // w = (q - 8) s everywhere: no zero-point term
     const float* x;  // [m][ldx]
     int ldx, m;
