@@ -1390,6 +1390,88 @@ __global__ void __launch_bounds__(256) linear_conv_prefill_kernel(LinearScanLaun
     if (ok) p.ws[static_cast<size_t>(t) * conv_dim + c] = y;
 }
 
+// The same pass for 128-channel heads and a conv kernel of KS taps, one block
+// per (head, kConvTokens tokens): each thread keeps its channel's inputs for
+// the tokens and the KS - 1 before them in registers (every input read once,
+// range-checked buffer loads with no branch around them), and the q / k norms
+// of the block's tokens share one barrier.  Same arithmetic and order as
+// linear_conv_prefill_kernel.
+constexpr int kConvTokens = 16;
+
+template <int KS>
+__global__ void __launch_bounds__(128) linear_conv_prefill_tg_kernel(LinearScanLaunch p) {
+    constexpr int H = KS - 1, TG = kConvTokens, W = TG + H;
+    __shared__ float red[2][TG];
+    const int hb = blockIdx.x, g0 = blockIdx.y * TG;
+    const int conv_dim = 2 * p.lk_n * 128 + p.lv_n * 128;
+    const bool is_qk = hb < 2 * p.lk_n;
+    const int c = (is_qk ? hb * 128 : 2 * p.lk_n * 128 + (hb - 2 * p.lk_n) * 128) + static_cast<int>(threadIdx.x);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    // window slot i holds the input of token g0 - H + i: rows [r0, r1) of the
+    // chunk, the history before token 0 (only the first group reaches it)
+    const int r0 = max(0, g0 - H), r1 = min(p.tokens, g0 + TG);
+    const uint32_t stride4 = static_cast<uint32_t>(p.mixed_stride) * 4u;
+    const __amdgpu_buffer_rsrc_t r_x =
+        buf_rsrc(p.mixed + static_cast<size_t>(r0) * p.mixed_stride, static_cast<uint32_t>(r1 - r0) * stride4);
+    const __amdgpu_buffer_rsrc_t r_h = buf_rsrc(p.hist_in, static_cast<uint32_t>(conv_dim * H) * 4u);
+    float xw[W], w[KS];
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+        const int tau = g0 - H + i;
+        float v = buf_load_f32(r_x, tau >= r0 ? static_cast<uint32_t>(tau - r0) * stride4 + c * 4u : kBufOOB);
+        if (i < H) v += buf_load_f32(r_h, tau < 0 ? static_cast<uint32_t>(c * H + H + tau) * 4u : kBufOOB);
+        xw[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < KS; ++i) w[i] = p.conv_w[static_cast<size_t>(c) * KS + i];
+    float y[TG];
+#pragma unroll
+    for (int k = 0; k < TG; ++k) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < H; ++i) acc += xw[k + i] * w[i];
+        acc += xw[k + H] * w[H];
+        y[k] = silu_dev(acc);
+    }
+    if (is_qk) {  // block-uniform; l2NormalizeHeads: x / sqrt(sum x^2 + 1e-6)
+#pragma unroll
+        for (int k = 0; k < TG; ++k) {
+            const float ss = wave_sum(y[k] * y[k]);
+            if (lane == 0) red[wid][k] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < TG; ++k) {
+            float ss = 0.0f;
+            ss += red[0][k];
+            ss += red[1][k];
+            y[k] *= 1.0f / sqrtf(ss + 1.0e-6f);
+        }
+    } else if (threadIdx.x < TG && g0 + static_cast<int>(threadIdx.x) < p.tokens) {
+        const int t = g0 + threadIdx.x, vh = hb - 2 * p.lk_n;
+        const size_t row = static_cast<size_t>(t) * p.mixed_stride + vh;
+        float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim + (static_cast<size_t>(t) * p.lv_n + vh) * 2;
+        aux[0] = sigmoid_dev(p.b[row]);
+        aux[1] = expf(-expf(p.a_log[vh]) * softplus_dev(p.a[row] + p.dt_bias[vh]));
+    }
+#pragma unroll
+    for (int k = 0; k < TG; ++k)
+        if (g0 + k < p.tokens) p.ws[static_cast<size_t>(g0 + k) * conv_dim + c] = y[k];
+    // the history after the chunk: inputs of tokens tokens - H .. tokens - 1, slots
+    // tokens - g0 + i of the group that holds the last token
+    if (g0 <= p.tokens - 1 && p.tokens - 1 < g0 + TG) {
+        const int base = p.tokens - g0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; ++j)
+                if (j == base + i) v = xw[j];
+            p.hist_out[static_cast<size_t>(c) * H + i] = v;
+        }
+    }
+}
+
 constexpr int kRecurTokens = 16;  // tokens staged in LDS per barrier
 
 template <int DK>
@@ -1526,9 +1608,14 @@ bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) 
 
 hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
     if (p.ws && p.lk_hd == 128 && p.lv_hd <= 256) {
-        const int width = max(p.lk_hd, p.lv_hd);
-        hipLaunchKernelGGL(linear_conv_prefill_kernel, dim3(p.tokens, 2 * p.lk_n + p.lv_n),
-                           dim3((width + kWave - 1) / kWave * kWave), 0, s, p);
+        if (p.lv_hd == 128 && p.ksize == 4) {
+            hipLaunchKernelGGL(linear_conv_prefill_tg_kernel<4>,
+                               dim3(2 * p.lk_n + p.lv_n, (p.tokens + kConvTokens - 1) / kConvTokens), dim3(128), 0, s, p);
+        } else {
+            const int width = max(p.lk_hd, p.lv_hd);
+            hipLaunchKernelGGL(linear_conv_prefill_kernel, dim3(p.tokens, 2 * p.lk_n + p.lv_n),
+                               dim3((width + kWave - 1) / kWave * kWave), 0, s, p);
+        }
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
         hipLaunchKernelGGL(linear_scan_recur_kernel<128>, dim3(p.lv_n, (p.lv_hd + 15) / 16), dim3(256), 0, s, p);
         return hipGetLastError();
