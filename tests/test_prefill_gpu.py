@@ -147,7 +147,8 @@ def test_attn_prep_batch_matches_single_token_calls():
     assert np.array_equal(vc_b.download(np.float16, cap * nkv * hd), vc_s.download(np.float16, cap * nkv * hd))
 
 
-@pytest.mark.parametrize("nq,nkv,hd,T,pos0", [(32, 8, 128, 70, 0), (32, 8, 128, 9, 500), (4, 2, 8, 5, 3)])
+@pytest.mark.parametrize("nq,nkv,hd,T,pos0", [(32, 8, 128, 70, 0), (32, 8, 128, 9, 500), (32, 8, 128, 33, 130),
+                                              (4, 2, 8, 5, 3)])
 def test_prefill_attention_vs_causal_oracle(nq, nkv, hd, T, pos0):
     rng = np.random.default_rng(T + pos0)
     ctx = pos0 + T

@@ -12,7 +12,7 @@
 //                        x hi / lo on v_mfma_f32_16x16x32_f16, group sums scaled
 //                        by the group scale; the zero-point term as a K = G
 //                        MFMA contraction after the group loop
-//   prefill_attn_tile_kernel / prefill_attn_kernel   causal GQA over the cache
+//   prefill_attn_mfma_kernel / prefill_attn_kernel   causal GQA over the cache
 //   linear_conv_prefill_kernel + linear_scan_recur_kernel   conv1d + norms +
 //                        gates for all tokens, then the gated-delta recurrence
 //                        with the state in registers (one-pass kernels
@@ -813,149 +813,181 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnLaunch p) 
     }
 }
 
-// Tiled form for head_dim 128 and 4 query heads per kv head (the 9B shape):
-// block (16-token tile, kv head) holds the tile's 64 query rows (token, head)
-// in LDS and streams the keys in 64-key chunks through LDS (fp32), so every
-// key is read once per tile instead of once per token.  Thread (rq, kq) =
-// (threadIdx / 16, threadIdx % 16) owns the 4 rows of token rq: the scores of
-// keys 4kq..4kq+3 (row max / sum over a chunk are reductions over the 16 lanes
-// of one DPP row) and output dims 8kq..8kq+7.  Online softmax over chunks
-// (rescale by exp(m_old - m_new)), then the output is multiplied by 1/l and by
-// the sigmoid gate, as in prefill_attn_kernel.
-constexpr int kTQ = 16;         // tokens per tile
-constexpr int kTHd = 128;       // head dim of the tiled kernel
-constexpr int kTGroup = 4;      // query heads per kv head of the tiled kernel
-constexpr int kTRows = kTQ * kTGroup;
-constexpr int kTLdq = kTHd + 4;  // fp32 row stride of Q / K / V in LDS
-constexpr int kTLdp = kPAttnChunk + 4;
+// Matrix-core form for head_dim 128 and 4 query heads per kv head (the 9B
+// shape): block (16-token tile, kv head), wave h = query head h of the kv head,
+// keys in 64-key chunks with a running max / sum (rescaled by
+// exp(m_old - m_new)), then 1/l and the sigmoid gate, as prefill_attn_kernel.
+// Scores are formed transposed, S^T = K Q^T (keys are the MFMA rows), so a
+// lane holds 16 keys of one token: the token's max and sum are over the lane's
+// own values and the lanes 16 and 32 away, and its probabilities are already
+// the B operand of O^T = V^T P^T.  q and p are split into fp16 hi + lo (about
+// 22 bits together; k and v are fp16 in the cache), two
+// v_mfma_f32_16x16x32_f16 per product, fp32 accumulation.  The k index of an
+// MFMA may be any permutation of the keys as long as both operands use it:
+// lane group g (lanes 16g..16g+15) feeds keys 32s + 4g + 0..3 and
+// 32s + 16 + 4g + 0..3 of step s, the keys its score tiles hold.  A chunk's K
+// (rows of 128 dims) and V (transposed: rows of 64 keys) go through LDS; the
+// next chunk is loaded into registers while the current one is used.
+constexpr int kFT = 16;        // tokens per tile
+constexpr int kFLdk = 136;     // halves per K row in LDS
+constexpr int kFLdv = 72;      // halves per V^T row in LDS
+constexpr int kFHd = 128, kFGroup = 4;
 
-constexpr size_t prefill_attn_tile_lds() {
-    return sizeof(float) * (static_cast<size_t>(kTRows) * kTLdq + 2 * static_cast<size_t>(kPAttnChunk) * kTLdq +
-                            static_cast<size_t>(kTRows) * kTLdp);
+template <int M>
+__device__ __forceinline__ float xor_pair_max(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+                     __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+    } else {
+        static_assert(M == 32, "pair distance");
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+                     __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+    }
 }
 
-__global__ void __launch_bounds__(256) prefill_attn_tile_kernel(PrefillAttnLaunch p) {
-    extern __shared__ float4 attn_lds[];
-    float* Qs = reinterpret_cast<float*>(attn_lds);   // [64 rows][kTLdq]
-    float* Ks = Qs + kTRows * kTLdq;                  // [64 keys][kTLdq]
-    float* Vs = Ks + kPAttnChunk * kTLdq;             // [64 keys][kTLdq]
-    float* Ps = Vs + kPAttnChunk * kTLdq;             // [64 rows][kTLdp]
-    const int t0 = blockIdx.x * kTQ, kh = blockIdx.y;
-    const int rq = threadIdx.x >> 4, kq = threadIdx.x & 15;
+// fp32 -> fp16 hi + fp16 lo (x - hi) of 8 values
+__device__ __forceinline__ void split_h8(const float (&x)[8], half8& hi, half8& lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const _Float16 h = static_cast<_Float16>(x[e]);
+        hi[e] = h;
+        lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(h));
+    }
+}
+
+__global__ void __launch_bounds__(256) prefill_attn_mfma_kernel(PrefillAttnLaunch p) {
+    __shared__ _Float16 Ks[kPAttnChunk * kFLdk];
+    __shared__ _Float16 Vt[kFHd * kFLdv];
+    const int t0 = blockIdx.x * kFT, kh = blockIdx.y;
+    const int lane = threadIdx.x & (kWave - 1), h = threadIdx.x / kWave;
+    const int tl = lane & 15, g = lane >> 4;
     const int pos0 = *p.pos0;
-    const int ntok = min(kTQ, p.tokens - t0);
-    const int qpos = pos0 + t0 + rq;                      // this thread's token
-    const int last = pos0 + t0 + ntok - 1;                // last key any row of the tile sees
-    // Q: row r = token * 4 + head; thread loads 32 floats (8 float4)
-    for (int i = threadIdx.x; i < kTRows * kTHd / 4; i += 256) {
-        const int r = i / (kTHd / 4), d4 = i % (kTHd / 4);
-        const int tok = r / kTGroup, h = r % kTGroup;
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (tok < ntok)
-            v = *reinterpret_cast<const float4*>(p.q + static_cast<size_t>(t0 + tok) * p.q_stride +
-                                                 static_cast<size_t>(kh * kTGroup + h) * kTHd + 4 * d4);
-        *reinterpret_cast<float4*>(Qs + r * kTLdq + 4 * d4) = v;
-    }
-    float m[4], l[4], o[4][8];
+    const int ntok = min(kFT, p.tokens - t0);
+    const int qpos = pos0 + t0 + tl;        // this lane's token
+    const int last = pos0 + t0 + ntok - 1;  // last key any token of the tile sees
+    const int qh = kh * kFGroup + h;
+    const float rscale = 1.0f / sqrtf(static_cast<float>(kFHd));
+    // q fragments: lane supplies Q[token tl][dims 32 s + 8 g .. + 7] (tokens past ntok read 0)
+    const uint32_t qrow = static_cast<uint32_t>(p.q_stride) * 4u;
+    const __amdgpu_buffer_rsrc_t r_q = buf_rsrc(p.q + static_cast<size_t>(t0) * p.q_stride, ntok * qrow);
+    half8 qhi[4], qlo[4];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+    for (int s = 0; s < 4; ++s) {
+        const uint32_t off = static_cast<uint32_t>(tl) * qrow + (static_cast<uint32_t>(qh) * kFHd + 32 * s + 8 * g) * 4u;
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(r_q, off, 0, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b128(r_q, off + 16u, 0, 0);
+        const float x[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]),
+                            __uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(b[2]), __uint_as_float(b[3])};
+        split_h8(x, qhi[s], qlo[s]);
     }
-    const float rscale = 1.0f / sqrtf(static_cast<float>(kTHd));
-    for (int c0 = 0; c0 <= last; c0 += kPAttnChunk) {
-        __syncthreads();  // the previous chunk's K, V and P have been read
-        // K and V of keys c0..c0+63 as fp32; keys past `last` are zero (never read as data)
-        for (int i = threadIdx.x; i < kPAttnChunk * kTHd / 8; i += 256) {
-            const int kk = i / (kTHd / 8), d8 = i % (kTHd / 8);
-            uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-            if (c0 + kk <= last) {
-                const size_t off = (static_cast<size_t>(c0 + kk) * p.nkv + kh) * kTHd + 8 * d8;
-                kw = *reinterpret_cast<const uint4*>(p.k_cache + off);
-                vw = *reinterpret_cast<const uint4*>(p.v_cache + off);
-            }
-            float* kd = Ks + kk * kTLdq + 8 * d8;
-            float* vd = Vs + kk * kTLdq + 8 * d8;
-            *reinterpret_cast<float4*>(kd) = make_float4(half_lo(kw.x), half_hi(kw.x), half_lo(kw.y), half_hi(kw.y));
-            *reinterpret_cast<float4*>(kd + 4) = make_float4(half_lo(kw.z), half_hi(kw.z), half_lo(kw.w), half_hi(kw.w));
-            *reinterpret_cast<float4*>(vd) = make_float4(half_lo(vw.x), half_hi(vw.x), half_lo(vw.y), half_hi(vw.y));
-            *reinterpret_cast<float4*>(vd + 4) = make_float4(half_lo(vw.z), half_hi(vw.z), half_lo(vw.w), half_hi(vw.w));
+    // chunk loads: piece i = threadIdx + 256 u is key i & 63, dims 8 (i >> 6) .. + 7
+    const uint32_t krow = static_cast<uint32_t>(p.nkv) * kFHd * 2u;  // bytes per cache position
+    u32x4 kr[4], vr[4];
+    auto load_chunk = [&](int c0) {
+        const uint32_t range = static_cast<uint32_t>(max(0, min(kPAttnChunk, last - c0 + 1))) * krow;
+        const size_t base = static_cast<size_t>(max(0, min(c0, last))) * p.nkv * kFHd + static_cast<size_t>(kh) * kFHd;
+        const __amdgpu_buffer_rsrc_t rk = buf_rsrc(p.k_cache + base, range), rv = buf_rsrc(p.v_cache + base, range);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = static_cast<int>(threadIdx.x) + 256 * u;
+            const uint32_t off = static_cast<uint32_t>(i & 63) * krow + static_cast<uint32_t>(i >> 6) * 16u;
+            kr[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+            vr[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+        }
+    };
+    float m = -INFINITY, l = 0.0f;
+    floatx4 o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const floatx4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    load_chunk(0);
+    for (int c0 = 0; c0 <= last; c0 += kPAttnChunk) {  // block-uniform
+        __syncthreads();  // the previous chunk's K and V have been read
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = static_cast<int>(threadIdx.x) + 256 * u, key = i & 63, d8 = i >> 6;
+            *reinterpret_cast<u32x4*>(Ks + key * kFLdk + 8 * d8) = kr[u];
+            const uint32_t w[4] = {vr[u][0], vr[u][1], vr[u][2], vr[u][3]};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                Vt[(8 * d8 + e) * kFLdv + key] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1))));
         }
         __syncthreads();
-        // scores of rows (rq, h) x keys 4kq + j
-        float sc[4][4];
+        load_chunk(c0 + kPAttnChunk);  // past `last`: reads 0, never stored as data
+        // S^T tiles c: keys c0 + 16 c + 4 g + v of token tl
+        floatx4 sc[4];
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
+        for (int c = 0; c < 4; ++c) {
+            sc[c] = zero4;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[h][j] = 0.0f;
-        const float* qr = Qs + (rq * kTGroup) * kTLdq;
-        const float* kr = Ks + (4 * kq) * kTLdq;
-#pragma unroll 4
-        for (int d = 0; d < kTHd; d += 4) {
-            float4 qv[4], kv[4];
-#pragma unroll
-            for (int h = 0; h < 4; ++h) qv[h] = *reinterpret_cast<const float4*>(qr + h * kTLdq + d);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) kv[j] = *reinterpret_cast<const float4*>(kr + j * kTLdq + d);
-#pragma unroll
-            for (int h = 0; h < 4; ++h)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    sc[h][j] += qv[h].x * kv[j].x + qv[h].y * kv[j].y + qv[h].z * kv[j].z + qv[h].w * kv[j].w;
-        }
-        // causal mask, chunk max / sum per row (16 lanes), online rescale
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            float mc = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bool ok = c0 + 4 * kq + j <= qpos;
-                sc[h][j] = ok ? sc[h][j] * rscale : -INFINITY;
-                mc = fmaxf(mc, sc[h][j]);
+            for (int s = 0; s < 4; ++s) {
+                const half8 a = *reinterpret_cast<const half8*>(Ks + (16 * c + tl) * kFLdk + 32 * s + 8 * g);
+                sc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qhi[s], sc[c], 0, 0, 0);
+                sc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qlo[s], sc[c], 0, 0, 0);
             }
-            mc = lanes_max<16>(mc);
-            const float m_new = fmaxf(m[h], mc);
-            float ls = 0.0f;
+        }
+        // causal mask, the token's chunk max and sum, online rescale
+        float mc = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float e = sc[h][j] == -INFINITY ? 0.0f : expf(sc[h][j] - m_new);
-                sc[h][j] = e;
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const bool ok = c0 + 16 * c + 4 * g + v <= qpos;
+                sc[c][v] = ok ? sc[c][v] * rscale : -INFINITY;
+                mc = fmaxf(mc, sc[c][v]);
+            }
+        mc = xor_pair_max<32>(xor_pair_max<16>(mc));
+        const float m_new = fmaxf(m, mc);
+        float ls = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float e = sc[c][v] == -INFINITY ? 0.0f : expf(sc[c][v] - m_new);
+                sc[c][v] = e;
                 ls += e;
             }
-            ls = lanes_sum<16>(ls);
-            const float f = m[h] == -INFINITY ? 0.0f : expf(m[h] - m_new);
-            m[h] = m_new;
-            l[h] = l[h] * f + ls;
+        ls = xor_pair_sum<32>(xor_pair_sum<16>(ls));
+        const float f = m == -INFINITY ? 0.0f : expf(m - m_new);
+        m = m_new;
+        l = l * f + ls;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[h][e] *= f;
-            *reinterpret_cast<float4*>(Ps + (rq * kTGroup + h) * kTLdp + 4 * kq) =
-                make_float4(sc[h][0], sc[h][1], sc[h][2], sc[h][3]);
+        for (int j = 0; j < 8; ++j) o[j] *= f;
+        // P^T fragments of key steps s2 (keys 32 s2 + 4 g + v, then 32 s2 + 16 + 4 g + v)
+        half8 phi[2], plo[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const float x[8] = {sc[2 * s2][0], sc[2 * s2][1], sc[2 * s2][2], sc[2 * s2][3],
+                                sc[2 * s2 + 1][0], sc[2 * s2 + 1][1], sc[2 * s2 + 1][2], sc[2 * s2 + 1][3]};
+            split_h8(x, phi[s2], plo[s2]);
         }
-        __syncthreads();
-        // o[rows of token rq][dims 8kq..] += P . V over the chunk's keys
-        const int nk = min(kPAttnChunk, last - c0 + 1);
-        for (int k = 0; k < nk; ++k) {
-            const float4 v0 = *reinterpret_cast<const float4*>(Vs + k * kTLdq + 8 * kq);
-            const float4 v1 = *reinterpret_cast<const float4*>(Vs + k * kTLdq + 8 * kq + 4);
+        // O^T tiles j: dims 16 j + 4 g + v of token tl
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const float pk = Ps[(rq * kTGroup + h) * kTLdp + k];
-                o[h][0] += pk * v0.x; o[h][1] += pk * v0.y; o[h][2] += pk * v0.z; o[h][3] += pk * v0.w;
-                o[h][4] += pk * v1.x; o[h][5] += pk * v1.y; o[h][6] += pk * v1.z; o[h][7] += pk * v1.w;
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const _Float16* vrow = Vt + (16 * j + tl) * kFLdv + 32 * s2 + 4 * g;
+                const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow);
+                const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + 16);
+                const half8 a = __builtin_bit_cast(half8, u32x4{lo4[0], lo4[1], hi4[0], hi4[1]});
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, phi[s2], o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, plo[s2], o[j], 0, 0, 0);
             }
-        }
     }
-    if (rq >= ntok) return;
+    if (tl >= ntok) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const size_t head = static_cast<size_t>(qh) * kFHd + 4 * g;
+    const float* gr = p.gate + static_cast<size_t>(t0 + tl) * p.q_stride + head;
+    float* orow = p.out + static_cast<size_t>(t0 + tl) * p.out_stride + head;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        const float inv = l[h] > 0.0f ? 1.0f / l[h] : 0.0f;
-        const size_t head = static_cast<size_t>(kh * kTGroup + h) * kTHd + 8 * kq;
-        const float* gr = p.gate + static_cast<size_t>(t0 + rq) * p.q_stride + head;
-        float* orow = p.out + static_cast<size_t>(t0 + rq) * p.out_stride + head;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) orow[e] = (o[h][e] * inv) * sigmoid_dev(gr[e]);
+    for (int j = 0; j < 8; ++j) {
+        const float4 gv = *reinterpret_cast<const float4*>(gr + 16 * j);
+        *reinterpret_cast<float4*>(orow + 16 * j) =
+            make_float4((o[j][0] * inv) * sigmoid_dev(gv.x), (o[j][1] * inv) * sigmoid_dev(gv.y),
+                        (o[j][2] * inv) * sigmoid_dev(gv.z), (o[j][3] * inv) * sigmoid_dev(gv.w));
     }
 }
 
@@ -966,17 +998,11 @@ bool prefill_attn_supported(int nq, int nkv, int head_dim) {
 
 hipError_t launch_prefill_attn(const PrefillAttnLaunch& p, hipStream_t s) {
     const int group = p.nq / p.nkv;
-    if (p.head_dim == kTHd && group == kTGroup) {
-        static bool attr_set = false;
-        constexpr size_t lds = prefill_attn_tile_lds();
-        if (!attr_set) {
-            if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_tile_kernel),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-                e != hipSuccess)
-                return e;
-            attr_set = true;
-        }
-        hipLaunchKernelGGL(prefill_attn_tile_kernel, dim3((p.tokens + kTQ - 1) / kTQ, p.nkv), dim3(256), lds, s, p);
+    // the matrix-core kernel reads q, the gate and the output as 16-byte pieces
+    const bool al16 = ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.gate) |
+                        reinterpret_cast<uintptr_t>(p.out)) & 15u) == 0 && p.q_stride % 4 == 0 && p.out_stride % 4 == 0;
+    if (p.head_dim == kFHd && group == kFGroup && al16) {
+        hipLaunchKernelGGL(prefill_attn_mfma_kernel, dim3((p.tokens + kFT - 1) / kFT, p.nkv), dim3(256), 0, s, p);
         return hipGetLastError();
     }
     const size_t lds = sizeof(float) * (2 * static_cast<size_t>(group) * p.head_dim + group * (kPAttnChunk + 3));
