@@ -1500,20 +1500,22 @@ __global__ void __launch_bounds__(128) linear_conv_prefill_tg_kernel(LinearScanL
 
 constexpr int kRecurTokens = 16;  // tokens staged in LDS per barrier
 
-template <int DK>
+// LPC lanes per value column (LPC / 64 of a wave), RS = DK / LPC state rows per lane
+template <int DK, int LPC>
 __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch p) {
-    constexpr int RS = DK / 16;  // state rows per lane
-    static_assert(RS % 2 == 0, "two accumulation chains");
+    constexpr int RS = DK / LPC;
+    static_assert(RS % 2 == 0 && (LPC == 16 || LPC == 32), "two accumulation chains, DPP / permlane row sums");
+    constexpr int CPB = 4 * (kWave / LPC);  // value columns per block (four waves)
     constexpr int TG = kRecurTokens;
-    __shared__ float qs[2][TG][DK], ks[2][TG][DK], vs[2][TG][16], gs[2][TG][2];
+    __shared__ float qs[2][TG][DK], ks[2][TG][DK], vs[2][TG][CPB], gs[2][TG][2];
     const int vh = blockIdx.x;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     const int factor = max(1, p.lv_n / max(1, p.lk_n));
     const int kh = min(p.lk_n - 1, vh / factor);
     const int dv = p.lv_hd;
     const int conv_dim = 2 * p.lk_n * DK + p.lv_n * dv;
-    const int ig = lane & 15, col = wid * 4 + (lane >> 4);
-    const int j0 = blockIdx.y * 16;
+    const int ig = lane % LPC, col = wid * (kWave / LPC) + lane / LPC;
+    const int j0 = blockIdx.y * CPB;
     const int j = j0 + col;
     const bool active = j < dv;
     float* S = p.state + static_cast<size_t>(vh) * DK * dv;
@@ -1521,8 +1523,14 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
     float sreg[RS];
 #pragma unroll
     for (int r = 0; r < RS; ++r)
-        sreg[r] = buf_load_f32(r_state, active ? (static_cast<uint32_t>(ig + 16 * r) * dv + j) * 4u : kBufOOB);
+        sreg[r] = buf_load_f32(r_state, active ? (static_cast<uint32_t>(ig + LPC * r) * dv + j) * 4u : kBufOOB);
     const float rdk = 1.0f / sqrtf(static_cast<float>(DK));
+    // sum over the LPC lanes of a column
+    auto col_sum = [](float v) {
+        v = lanes_sum<16>(v);
+        if constexpr (LPC == 32) v = xor_pair_sum<16>(v);
+        return v;
+    };
     // staging: thread th loads q/k floats th, th + 256, ... of a group, v and (beta, decay).
     // Every load is a range-checked buffer load over the group's tokens (tokens past
     // the end read 0) with no branch around it, so each wait covers exactly the loads
@@ -1543,9 +1551,10 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
             const int cc = (ch >= DK ? p.lk_n * DK : 0) + kh * DK + (ch % DK);
             rq[u] = buf_load_f32(r_c, (static_cast<uint32_t>(tk) * conv_dim + cc) * 4u);
         }
-        const int tk = threadIdx.x >> 4, cl = threadIdx.x & 15;  // TG x 16 values
-        rv = buf_load_f32(r_c, j0 + cl < dv ? (static_cast<uint32_t>(tk) * conv_dim + 2 * p.lk_n * DK + vh * dv + j0 + cl) * 4u
-                                            : kBufOOB);
+        const int tk = threadIdx.x / CPB, cl = threadIdx.x % CPB;  // TG x CPB values
+        rv = buf_load_f32(r_c, threadIdx.x < TG * CPB && j0 + cl < dv
+                                   ? (static_cast<uint32_t>(tk) * conv_dim + 2 * p.lk_n * DK + vh * dv + j0 + cl) * 4u
+                                   : kBufOOB);
         rg = buf_load_f32(r_g, threadIdx.x < 2 * TG ? ((threadIdx.x >> 1) * p.lv_n * 2u + vh * 2u + (threadIdx.x & 1)) * 4u
                                                      : kBufOOB);
     };
@@ -1558,7 +1567,7 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
             const int tk = e / (2 * DK), ch = e % (2 * DK);
             *(ch < DK ? &qs[buf][tk][ch] : &ks[buf][tk][ch - DK]) = rq[u];
         }
-        vs[buf][threadIdx.x >> 4][threadIdx.x & 15] = rv;
+        if (threadIdx.x < TG * CPB) vs[buf][threadIdx.x / CPB][threadIdx.x % CPB] = rv;
         if (threadIdx.x < 2 * TG) {
             const bool live = g0 + static_cast<int>(threadIdx.x >> 1) < p.tokens;
             gs[buf][threadIdx.x >> 1][threadIdx.x & 1] = live ? rg : static_cast<float>(threadIdx.x & 1);
@@ -1581,8 +1590,8 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
         auto read_token = [&](int k, float (&kk)[RS], float (&qq)[RS], float& v, float& b, float& d) {
 #pragma unroll
             for (int r = 0; r < RS; ++r) {
-                kk[r] = ks[buf][k][ig + 16 * r];
-                qq[r] = qs[buf][k][ig + 16 * r];
+                kk[r] = ks[buf][k][ig + LPC * r];
+                qq[r] = qs[buf][k][ig + LPC * r];
             }
             v = vs[buf][k][col];
             b = gs[buf][k][0];
@@ -1601,7 +1610,7 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
                 pa = fmaf(sreg[r], kb[c][r], pa);
                 pb = fmaf(sreg[r + 1], kb[c][r + 1], pb);
             }
-            const float pred = lanes_sum<16>(pa + pb);
+            const float pred = col_sum(pa + pb);
             const float delta = bb[c] * (vb[c] - pred);
 #pragma unroll
             for (int r = 0; r < RS; ++r) sreg[r] = fmaf(kb[c][r], delta, sreg[r]);
@@ -1616,7 +1625,7 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
                 oa = fmaf(sreg[r], qb[c][r], oa);
                 ob = fmaf(sreg[r + 1], qb[c][r + 1], ob);
             }
-            const float o = lanes_sum<16>(oa + ob);
+            const float o = col_sum(oa + ob);
             if (ig == k) my_o = o;
         }
         if (active && ig < nt)
@@ -1624,7 +1633,7 @@ __global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch
     }
 #pragma unroll
     for (int r = 0; r < RS; ++r)
-        if (active) S[static_cast<size_t>(ig + 16 * r) * dv + j] = sreg[r];
+        if (active) S[static_cast<size_t>(ig + LPC * r) * dv + j] = sreg[r];
 }
 
 bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
@@ -1643,7 +1652,10 @@ hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
                                dim3((width + kWave - 1) / kWave * kWave), 0, s, p);
         }
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-        hipLaunchKernelGGL(linear_scan_recur_kernel<128>, dim3(p.lv_n, (p.lv_hd + 15) / 16), dim3(256), 0, s, p);
+        // 16 lanes per value column, 16 columns per block, one wave per SIMD (32 lanes
+        // per column, two waves per SIMD whose per-token chains interleave, measured
+        // slower: 99.7 against 86-89 us per layer at 512 tokens)
+        hipLaunchKernelGGL((linear_scan_recur_kernel<128, 16>), dim3(p.lv_n, (p.lv_hd + 15) / 16), dim3(256), 0, s, p);
         return hipGetLastError();
     }
     const dim3 grid(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols);
