@@ -323,10 +323,13 @@ XQHIP_API int xqhip_linear_attn_scan(const float* mixed, const float* a, const f
                                      int ksize, int tokens, float* out, int out_stride, void* stream);
 /* xqhip_linear_attn_scan with a workspace of xqhip_linear_scan_workspace_bytes()
  * (16-byte aligned): the conv1d + SiLU, q/k L2 norms and gates of all tokens
- * run first as one token-parallel pass, leaving only the state recurrence
- * sequential (same results up to the fp32 summation order of the norms). No
- * counterpart in the reference (which prefills token by token,
- * custom_model.cpp:610-640); same contract as xqhip_linear_attn_scan. */
+ * run first as one token-parallel pass; for key heads of 128 dims the state
+ * recurrence then runs in 64-token chunks (the per-token update unrolled over a
+ * chunk into products with a triangular solve, parallel over chunks except one
+ * pass per value head and 16 columns).  Same mathematics as the per-token scan,
+ * a different fp32 summation order.  No counterpart in the reference (which
+ * prefills token by token, custom_model.cpp:610-640); same contract as
+ * xqhip_linear_attn_scan. */
 XQHIP_API size_t xqhip_linear_scan_workspace_bytes(int tokens, int lk_n, int lk_hd, int lv_n, int lv_hd);
 XQHIP_API int xqhip_linear_attn_scan_ws(const float* mixed, const float* a, const float* b, int stride,
                                         float* conv_state, int pos0, const float* conv_w, const float* a_log,

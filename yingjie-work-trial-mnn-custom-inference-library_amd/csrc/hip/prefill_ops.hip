@@ -13,7 +13,7 @@
 //                        by the group scale; the zero-point term as a K = G
 //                        MFMA contraction after the group loop
 //   prefill_attn_mfma_kernel / prefill_attn_kernel   causal GQA over the cache
-//   linear_conv_prefill_kernel + linear_scan_recur_kernel   conv1d + norms +
+//   linear_conv_prefill_tg_kernel + scan_chunk_prep_kernel + scan_chunk_state_kernel   conv1d + norms +
 //                        gates for all tokens, then the gated-delta recurrence
 //                        with the state in registers (one-pass kernels
 //                        linear_scan_wave_kernel / linear_scan_kernel otherwise)
@@ -864,8 +864,11 @@ __global__ void __launch_bounds__(256) prefill_attn_mfma_kernel(PrefillAttnLaunc
     const int t0 = blockIdx.x * kFT, kh = blockIdx.y;
     const int lane = threadIdx.x & (kWave - 1), h = threadIdx.x / kWave;
     const int tl = lane & 15, g = lane >> 4;
+    // block-uniform values computed with vector ops are made scalar with
+    // readfirstlane: a buffer descriptor built from a vector register becomes a
+    // loop over the distinct values of the wave
     const int pos0 = *p.pos0;
-    const int ntok = min(kFT, p.tokens - t0);
+    const int ntok = __builtin_amdgcn_readfirstlane(min(kFT, p.tokens - t0));
     const int qpos = pos0 + t0 + tl;        // this lane's token
     const int last = pos0 + t0 + ntok - 1;  // last key any token of the tile sees
     const int qh = kh * kFGroup + h;
@@ -887,8 +890,10 @@ __global__ void __launch_bounds__(256) prefill_attn_mfma_kernel(PrefillAttnLaunc
     const uint32_t krow = static_cast<uint32_t>(p.nkv) * kFHd * 2u;  // bytes per cache position
     u32x4 kr[4], vr[4];
     auto load_chunk = [&](int c0) {
-        const uint32_t range = static_cast<uint32_t>(max(0, min(kPAttnChunk, last - c0 + 1))) * krow;
-        const size_t base = static_cast<size_t>(max(0, min(c0, last))) * p.nkv * kFHd + static_cast<size_t>(kh) * kFHd;
+        const uint32_t range =
+            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(max(0, min(kPAttnChunk, last - c0 + 1)))) * krow;
+        const size_t base = static_cast<size_t>(__builtin_amdgcn_readfirstlane(max(0, min(c0, last)))) * p.nkv * kFHd +
+                            static_cast<size_t>(kh) * kFHd;
         const __amdgpu_buffer_rsrc_t rk = buf_rsrc(p.k_cache + base, range), rv = buf_rsrc(p.v_cache + base, range);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -1357,21 +1362,29 @@ __global__ void __launch_bounds__(256) linear_scan_wave_kernel(LinearScanLaunch 
 }
 
 // ---------------------------------------------------------------------------
-// Two-pass form of the prefill linear-attention scan (with a workspace):
-// 1. linear_conv_prefill_kernel, parallel over (token, head): the causal conv1d
-//    + SiLU of every channel for every token of the chunk (inputs of earlier
-//    tokens from the chunk, before the chunk from hist_in), the L2 norm of the
-//    q and k heads, the per-(token, value head) beta = sigmoid(b) and
-//    decay = exp(-exp(A_log) softplus(a + dt_bias)), and the final history.
-// 2. linear_scan_recur_kernel: only the state recurrence stays sequential; a
-//    block stages 16 tokens of normalised q/k, v, beta and decay in LDS at a
-//    time (double-buffered, one barrier per 16 tokens) and each wave updates
-//    its 4 value columns per token exactly as the fused decode step does.
-// Workspace: conv output [tokens][conv_dim] and (beta, decay) [tokens][lv_n][2].
+// Two-pass form of the prefill linear-attention scan (with a workspace, key
+// heads of 128 dims):
+// 1. linear_conv_prefill_tg_kernel / linear_conv_prefill_kernel, parallel over
+//    tokens and heads: the causal conv1d + SiLU of every channel for every
+//    token of the chunk (inputs of earlier tokens from the chunk, before the
+//    chunk from hist_in), the L2 norm of the q and k heads, the per-(token,
+//    value head) beta = sigmoid(b) and log decay g = -exp(A_log) softplus(a +
+//    dt_bias), and the final history.
+// 2. the chunked recurrence (scan_chunk_prep_kernel, scan_chunk_state_kernel,
+//    below): parallel over 64-token chunks except for one pass over the chunks
+//    per (value head, 16 columns).
+// Workspace: conv output [tokens][conv_dim], (beta, g) [tokens][lv_n][2], then
+// per (chunk, value head) the record T [64][64], Wq [64][64], gamma [64],
+// gamma_last / gamma [64].
 // ---------------------------------------------------------------------------
+constexpr int kChunkTokens = 64;
+constexpr int kChunkRecord = 2 * kChunkTokens * kChunkTokens + 2 * kChunkTokens;
+
 size_t linear_scan_workspace_bytes(int tokens, int lk_n, int lk_hd, int lv_n, int lv_hd) {
     const size_t conv_dim = 2 * static_cast<size_t>(lk_n) * lk_hd + static_cast<size_t>(lv_n) * lv_hd;
-    return sizeof(float) * static_cast<size_t>(tokens) * (conv_dim + 2 * static_cast<size_t>(lv_n));
+    const size_t chunks = (static_cast<size_t>(tokens) + kChunkTokens - 1) / kChunkTokens;
+    return sizeof(float) * (static_cast<size_t>(tokens) * (conv_dim + 2 * static_cast<size_t>(lv_n)) +
+                            chunks * lv_n * kChunkRecord);
 }
 
 __global__ void __launch_bounds__(256) linear_conv_prefill_kernel(LinearScanLaunch p) {
@@ -1411,7 +1424,7 @@ __global__ void __launch_bounds__(256) linear_conv_prefill_kernel(LinearScanLaun
         const size_t row = static_cast<size_t>(t) * p.mixed_stride + vh;
         float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim + (static_cast<size_t>(t) * p.lv_n + vh) * 2;
         aux[0] = sigmoid_dev(p.b[row]);
-        aux[1] = expf(-expf(p.a_log[vh]) * softplus_dev(p.a[row] + p.dt_bias[vh]));
+        aux[1] = -expf(p.a_log[vh]) * softplus_dev(p.a[row] + p.dt_bias[vh]);  // log of the decay
     }
     if (ok) p.ws[static_cast<size_t>(t) * conv_dim + c] = y;
 }
@@ -1478,7 +1491,7 @@ __global__ void __launch_bounds__(128) linear_conv_prefill_tg_kernel(LinearScanL
         const size_t row = static_cast<size_t>(t) * p.mixed_stride + vh;
         float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim + (static_cast<size_t>(t) * p.lv_n + vh) * 2;
         aux[0] = sigmoid_dev(p.b[row]);
-        aux[1] = expf(-expf(p.a_log[vh]) * softplus_dev(p.a[row] + p.dt_bias[vh]));
+        aux[1] = -expf(p.a_log[vh]) * softplus_dev(p.a[row] + p.dt_bias[vh]);  // log of the decay
     }
 #pragma unroll
     for (int k = 0; k < TG; ++k)
@@ -1498,142 +1511,415 @@ __global__ void __launch_bounds__(128) linear_conv_prefill_tg_kernel(LinearScanL
     }
 }
 
-constexpr int kRecurTokens = 16;  // tokens staged in LDS per barrier
+// Chunked (parallel-in-time) form of the gated-delta recurrence over a prompt
+// chunk, for key heads of 128 dims.  Within a chunk of C = 64 tokens
+// (local i, decay a_i = exp(g_i), cumulative log decay G_i = g_0 + .. + g_i,
+// gamma_i = exp(G_i)), the per-token update
+//     S_i = a_i (I - b_i k_i k_i^T) S_{i-1} + b_i k_i v_i^T,   o_i = S_i^T q_i
+// unrolls (by induction on i) to S_i = gamma_i S_0 + sum_{j<=i} exp(G_i - G_j) k_j u_j^T
+// with the rows u_j^T of U solving the unit lower-triangular system
+//     (I + A) U = R,   A_ij = b_i exp(G_i - G_j) (k_i . k_j) (j < i),
+//     R_i = b_i (v_i - gamma_i S_0^T k_i),
+// so that
+//     o_i = gamma_i S_0^T q_i + sum_{j<=i} exp(G_i - G_j) (q_i . k_j) u_j,
+//     S_C = gamma_{C-1} S_0 + sum_j exp(G_{C-1} - G_j) k_j u_j^T.
+// scan_chunk_prep_kernel, parallel over (value head, chunk): the Gram products
+// K K^T and Q K^T, T = (I + A)^{-1} (forward substitution, row by row) and
+// Wq_ij = exp(G_i - G_j) (q_i . k_j) (j <= i); scan_chunk_state_kernel, one block
+// per (value head, 16 value columns), walks the chunks in order with the state
+// slice in LDS and the products on v_mfma_f32_16x16x4_f32 (fp32 operands, fp32
+// accumulation).  Same mathematics as the per-token recurrence
+// (custom_model.cpp:1074-1096), a different fp32 summation order.
+constexpr int kChunk = kChunkTokens;  // tokens per chunk
+constexpr int kChLd = 132;   // floats per 128-dim row in LDS (16-byte aligned rows)
+constexpr int kChLdT = 68;   // floats per 64-wide row in LDS
+constexpr int kChRec = kChunkRecord;  // floats per (value head, chunk) record
 
-// LPC lanes per value column (LPC / 64 of a wave), RS = DK / LPC state rows per lane
-template <int DK, int LPC>
-__global__ void __launch_bounds__(256) linear_scan_recur_kernel(LinearScanLaunch p) {
-    constexpr int RS = DK / LPC;
-    static_assert(RS % 2 == 0 && (LPC == 16 || LPC == 32), "two accumulation chains, DPP / permlane row sums");
-    constexpr int CPB = 4 * (kWave / LPC);  // value columns per block (four waves)
-    constexpr int TG = kRecurTokens;
-    __shared__ float qs[2][TG][DK], ks[2][TG][DK], vs[2][TG][CPB], gs[2][TG][2];
-    const int vh = blockIdx.x;
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    const int factor = max(1, p.lv_n / max(1, p.lk_n));
-    const int kh = min(p.lk_n - 1, vh / factor);
-    const int dv = p.lv_hd;
-    const int conv_dim = 2 * p.lk_n * DK + p.lv_n * dv;
-    const int ig = lane % LPC, col = wid * (kWave / LPC) + lane / LPC;
-    const int j0 = blockIdx.y * CPB;
-    const int j = j0 + col;
-    const bool active = j < dv;
-    float* S = p.state + static_cast<size_t>(vh) * DK * dv;
-    const __amdgpu_buffer_rsrc_t r_state = buf_rsrc(S, static_cast<uint32_t>(DK * dv) * 4u);
-    float sreg[RS];
+static size_t scan_chunk_prep_lds() {
+    return sizeof(float) * (2 * static_cast<size_t>(kChunk) * kChLd + 2 * kChunk * kChLdT + 4 * 16 * 17 + 3 * kChunk);
+}
+static size_t scan_chunk_state_lds() {
+    return sizeof(float) * (2 * static_cast<size_t>(kChunk) * kChLd + 2 * kChunk * kChLdT + 2 * 16 * kChLdT +
+                            16 * kChLd + kChunk * 16 + 3 * kChunk);
+}
+
+// q and k rows of key head kh for the chunk's tokens [t0, t0 + n) -> LDS rows of
+// kChLd floats (rows past n are 0)
+__device__ __forceinline__ void stage_qk_rows(const LinearScanLaunch& p, int conv_dim, int kh, int t0, int n,
+                                              float* Ks, float* Qs) {
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(p.ws + static_cast<size_t>(t0) * conv_dim,
+                                              static_cast<uint32_t>(max(0, n)) * conv_dim * 4u);
+    const uint32_t kc = static_cast<uint32_t>(p.lk_n * 128 + kh * 128), qc = static_cast<uint32_t>(kh * 128);
+    u32x4 kv[8], qv[8];  // all loads in flight before the first store
 #pragma unroll
-    for (int r = 0; r < RS; ++r)
-        sreg[r] = buf_load_f32(r_state, active ? (static_cast<uint32_t>(ig + LPC * r) * dv + j) * 4u : kBufOOB);
-    const float rdk = 1.0f / sqrtf(static_cast<float>(DK));
-    // sum over the LPC lanes of a column
-    auto col_sum = [](float v) {
-        v = lanes_sum<16>(v);
-        if constexpr (LPC == 32) v = xor_pair_sum<16>(v);
-        return v;
-    };
-    // staging: thread th loads q/k floats th, th + 256, ... of a group, v and (beta, decay).
-    // Every load is a range-checked buffer load over the group's tokens (tokens past
-    // the end read 0) with no branch around it, so each wait covers exactly the loads
-    // it needs and the token loop's LDS reads are not held behind a branch.
-    constexpr int QK = TG * 2 * DK / 256;  // per thread
-    float rq[QK], rv, rg;
-    const size_t aux0 = static_cast<size_t>(p.tokens) * conv_dim;
-    auto load_stage = [&](int g0) {
-        // (uniform: readfirstlane keeps the descriptor in scalar registers)
-        const uint32_t nt = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(max(0, min(TG, p.tokens - g0))));
-        const __amdgpu_buffer_rsrc_t r_c = buf_rsrc(p.ws + static_cast<size_t>(g0) * conv_dim, nt * conv_dim * 4u);
-        const __amdgpu_buffer_rsrc_t r_g =
-            buf_rsrc(p.ws + aux0 + static_cast<size_t>(g0) * p.lv_n * 2, nt * p.lv_n * 8u);
-#pragma unroll
-        for (int u = 0; u < QK; ++u) {
-            const int e = threadIdx.x + u * 256;
-            const int tk = e / (2 * DK), ch = e % (2 * DK);
-            const int cc = (ch >= DK ? p.lk_n * DK : 0) + kh * DK + (ch % DK);
-            rq[u] = buf_load_f32(r_c, (static_cast<uint32_t>(tk) * conv_dim + cc) * 4u);
-        }
-        const int tk = threadIdx.x / CPB, cl = threadIdx.x % CPB;  // TG x CPB values
-        rv = buf_load_f32(r_c, threadIdx.x < TG * CPB && j0 + cl < dv
-                                   ? (static_cast<uint32_t>(tk) * conv_dim + 2 * p.lk_n * DK + vh * dv + j0 + cl) * 4u
-                                   : kBufOOB);
-        rg = buf_load_f32(r_g, threadIdx.x < 2 * TG ? ((threadIdx.x >> 1) * p.lv_n * 2u + vh * 2u + (threadIdx.x & 1)) * 4u
-                                                     : kBufOOB);
-    };
-    // tokens past the end get beta 0 and decay 1 (their q / k / v read 0): the state
-    // passes through them unchanged
-    auto store_stage = [&](int buf, int g0) {
-#pragma unroll
-        for (int u = 0; u < QK; ++u) {
-            const int e = threadIdx.x + u * 256;
-            const int tk = e / (2 * DK), ch = e % (2 * DK);
-            *(ch < DK ? &qs[buf][tk][ch] : &ks[buf][tk][ch - DK]) = rq[u];
-        }
-        if (threadIdx.x < TG * CPB) vs[buf][threadIdx.x / CPB][threadIdx.x % CPB] = rv;
-        if (threadIdx.x < 2 * TG) {
-            const bool live = g0 + static_cast<int>(threadIdx.x >> 1) < p.tokens;
-            gs[buf][threadIdx.x >> 1][threadIdx.x & 1] = live ? rg : static_cast<float>(threadIdx.x & 1);
-        }
-    };
-    load_stage(0);
-    for (int g0 = 0, buf = 0; g0 < p.tokens; g0 += TG, buf ^= 1) {
-        store_stage(buf, g0);
-        __syncthreads();  // this buffer is complete; the other one is no longer read
-        load_stage(g0 + TG);  // past the last group: every load reads 0
-        const int nt = min(TG, p.tokens - g0);
-        // A fixed, unrolled TG-token loop; each token's output is kept by lane ig == k
-        // and stored after the loop.
-        float my_o = 0.0f;
-        // k / q / v / beta / decay of token k + 2 are read from LDS right after token
-        // k's state update (a three-slot register ring; the scheduling barrier keeps
-        // the reads there), so their latency hides behind token k's output and token
-        // k + 1's update, which the scheduler interleaves after the barrier
-        float kb[3][RS], qb[3][RS], vb[3], bb[3], db[3];
-        auto read_token = [&](int k, float (&kk)[RS], float (&qq)[RS], float& v, float& b, float& d) {
-#pragma unroll
-            for (int r = 0; r < RS; ++r) {
-                kk[r] = ks[buf][k][ig + LPC * r];
-                qq[r] = qs[buf][k][ig + LPC * r];
-            }
-            v = vs[buf][k][col];
-            b = gs[buf][k][0];
-            d = gs[buf][k][1];
-        };
-        read_token(0, kb[0], qb[0], vb[0], bb[0], db[0]);
-        read_token(1, kb[1], qb[1], vb[1], bb[1], db[1]);
-#pragma unroll
-        for (int k = 0; k < TG; ++k) {
-            const int c = k % 3;
-            float pa = 0.0f, pb = 0.0f;  // two chains
-#pragma unroll
-            for (int r = 0; r < RS; r += 2) {
-                sreg[r] *= db[c];
-                sreg[r + 1] *= db[c];
-                pa = fmaf(sreg[r], kb[c][r], pa);
-                pb = fmaf(sreg[r + 1], kb[c][r + 1], pb);
-            }
-            const float pred = col_sum(pa + pb);
-            const float delta = bb[c] * (vb[c] - pred);
-#pragma unroll
-            for (int r = 0; r < RS; ++r) sreg[r] = fmaf(kb[c][r], delta, sreg[r]);
-            if (k + 2 < TG) {
-                const int n = (k + 2) % 3;
-                read_token(k + 2, kb[n], qb[n], vb[n], bb[n], db[n]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            float oa = 0.0f, ob = 0.0f;
-#pragma unroll
-            for (int r = 0; r < RS; r += 2) {
-                oa = fmaf(sreg[r], qb[c][r], oa);
-                ob = fmaf(sreg[r + 1], qb[c][r + 1], ob);
-            }
-            const float o = col_sum(oa + ob);
-            if (ig == k) my_o = o;
-        }
-        if (active && ig < nt)
-            p.out[static_cast<size_t>(g0 + ig) * p.out_stride + static_cast<size_t>(vh) * dv + j] = my_o * rdk;
+    for (int u = 0; u < 8; ++u) {
+        const int e = static_cast<int>(threadIdx.x) + 256 * u, row = e >> 5, d4 = e & 31;
+        const uint32_t base = static_cast<uint32_t>(row) * conv_dim + 4u * d4;
+        kv[u] = __builtin_amdgcn_raw_buffer_load_b128(r, (base + kc) * 4u, 0, 0);
+        qv[u] = __builtin_amdgcn_raw_buffer_load_b128(r, (base + qc) * 4u, 0, 0);
     }
 #pragma unroll
-    for (int r = 0; r < RS; ++r)
-        if (active) S[static_cast<size_t>(ig + LPC * r) * dv + j] = sreg[r];
+    for (int u = 0; u < 8; ++u) {
+        const int e = static_cast<int>(threadIdx.x) + 256 * u, row = e >> 5, d4 = e & 31;
+        *reinterpret_cast<u32x4*>(Ks + row * kChLd + 4 * d4) = kv[u];
+        *reinterpret_cast<u32x4*>(Qs + row * kChLd + 4 * d4) = qv[u];
+    }
+}
+
+__global__ void __launch_bounds__(256) scan_chunk_prep_kernel(LinearScanLaunch p) {
+    extern __shared__ float4 scan_lds[];
+    float* Ks = reinterpret_cast<float*>(scan_lds);  // [64][kChLd]
+    float* Qs = Ks + kChunk * kChLd;                 // [64][kChLd]
+    float* Am = Qs + kChunk * kChLd;                 // [64][kChLdT] A (strictly lower)
+    float* Tm = Am + kChunk * kChLdT;                // [64][kChLdT] T = (I + A)^{-1}, by 16 x 16 blocks
+    float* Mw = Tm + kChunk * kChLdT;                // [4 waves][16][17] block products
+    float* Gc = Mw + 4 * 16 * 17;                    // [64] cumulative log decay
+    float* Bt = Gc + kChunk;                         // [64] beta
+    float* gl = Bt + kChunk;                         // [64] log decay
+    const int vh = blockIdx.x, ch = blockIdx.y, t0 = ch * kChunk;
+    const int n = __builtin_amdgcn_readfirstlane(min(kChunk, p.tokens - t0));  // scalar: buffer descriptors use it
+    const int factor = max(1, p.lv_n / max(1, p.lk_n));
+    const int kh = __builtin_amdgcn_readfirstlane(min(p.lk_n - 1, vh / factor));
+    const int conv_dim = 2 * p.lk_n * 128 + p.lv_n * p.lv_hd;
+    const int tid = threadIdx.x;
+    stage_qk_rows(p, conv_dim, kh, t0, n, Ks, Qs);
+    if (tid < kChunk) {  // tokens past n: beta 0, log decay 0 (the state passes unchanged)
+        const float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim;
+        const size_t ai = (static_cast<size_t>(t0 + tid) * p.lv_n + vh) * 2;
+        Bt[tid] = tid < n ? aux[ai] : 0.0f;
+        gl[tid] = tid < n ? aux[ai + 1] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < kChunk) {
+        float acc = 0.0f;
+        for (int l = 0; l <= tid; ++l) acc += gl[l];
+        Gc[tid] = acc;
+    }
+    // K K^T and Q K^T on v_mfma_f32_16x16x4_f32: wave w takes rows 16 w .. 16 w + 15
+    // against the four 16-key column tiles; lane (li, lq) feeds dims 32 lq + s at
+    // step s (the same permutation of the contraction for both operands)
+    const int lane = tid & (kWave - 1), w = tid / kWave, li = lane & 15, lq = lane >> 4;
+    float ka[32], qa[32];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const float4 kv = *reinterpret_cast<const float4*>(Ks + (16 * w + li) * kChLd + 32 * lq + 4 * u);
+        const float4 qv = *reinterpret_cast<const float4*>(Qs + (16 * w + li) * kChLd + 32 * lq + 4 * u);
+        ka[4 * u] = kv.x; ka[4 * u + 1] = kv.y; ka[4 * u + 2] = kv.z; ka[4 * u + 3] = kv.w;
+        qa[4 * u] = qv.x; qa[4 * u + 1] = qv.y; qa[4 * u + 2] = qv.z; qa[4 * u + 3] = qv.w;
+    }
+    floatx4 kk[4], qk[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) kk[ct] = qk[ct] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // eight independent accumulation chains, four dims of every column tile per round
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        float kb[4][4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const float4 v = *reinterpret_cast<const float4*>(Ks + (16 * ct + li) * kChLd + 32 * lq + 4 * u);
+            kb[ct][0] = v.x; kb[ct][1] = v.y; kb[ct][2] = v.z; kb[ct][3] = v.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                kk[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[4 * u + e], kb[ct][e], kk[ct], 0, 0, 0);
+                qk[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * u + e], kb[ct][e], qk[ct], 0, 0, 0);
+            }
+    }
+    __syncthreads();  // Gc is complete
+    float* rec = p.ws + static_cast<size_t>(p.tokens) * (conv_dim + 2 * p.lv_n) +
+                 (static_cast<size_t>(ch) * p.lv_n + vh) * kChRec;
+    float* Wq = rec + kChunk * kChunk;
+    // lane holds rows 16 w + 4 lq + v, column 16 ct + li of each product
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = 16 * w + 4 * lq + v, j = 16 * ct + li;
+            const float dec = j <= i ? expf(Gc[i] - Gc[j]) : 0.0f;
+            Am[i * kChLdT + j] = j < i ? Bt[i] * dec * kk[ct][v] : 0.0f;
+            Wq[i * kChunk + j] = dec * qk[ct][v];
+        }
+    __syncthreads();
+    // T = (I + A)^{-1} by 16 x 16 blocks (A is strictly lower, so T is unit lower
+    // triangular).  Diagonal blocks D_k = (I + A_kk)^{-1}, wave k: lane column c
+    // keeps column c of D_k in registers, row r = e_r - sum_{j<r} A_rj D_j.
+    const int c16 = lane & 15;
+    {
+        float dc[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < r; ++j) acc += Am[(16 * w + r) * kChLdT + 16 * w + j] * dc[j];
+            dc[r] = (c16 == r ? 1.0f : 0.0f) - acc;
+        }
+        if (lane < 16)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) Tm[(16 * w + r) * kChLdT + 16 * w + c16] = dc[r];
+    }
+    __syncthreads();
+    // off-diagonal blocks by distance: T_ij = -D_i sum_{k=j}^{i-1} A_ik T_kj (wave j
+    // takes block (j + dist, j)); lane: row lane / 4, columns 4 (lane % 4) .. + 3
+    const int br = lane >> 2, bc = 4 * (lane & 3);
+    for (int dist = 1; dist < 4; ++dist) {  // block-uniform
+        const int bi = w + dist, bj = w;
+        const bool task = bi < 4;
+        float m4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (task)
+            for (int k = bj; k < bi; ++k)
+#pragma unroll
+                for (int mm = 0; mm < 16; ++mm) {
+                    const float a = Am[(16 * bi + br) * kChLdT + 16 * k + mm];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) m4[e] += a * Tm[(16 * k + mm) * kChLdT + 16 * bj + bc + e];
+                }
+        float* mw = Mw + w * 16 * 17;
+        if (task)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mw[br * 17 + bc + e] = m4[e];
+        __syncthreads();
+        if (task) {
+            float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int mm = 0; mm < 16; ++mm) {
+                const float d = Tm[(16 * bi + br) * kChLdT + 16 * bi + mm];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t4[e] += d * mw[mm * 17 + bc + e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Tm[(16 * bi + br) * kChLdT + 16 * bj + bc + e] = -t4[e];
+        }
+        __syncthreads();
+    }
+    for (int e = tid; e < kChunk * kChunk; e += 256) {
+        const int i = e >> 6, j = e & 63;
+        rec[e] = (j >> 4) <= (i >> 4) ? Tm[i * kChLdT + j] : 0.0f;  // blocks above the diagonal are 0
+    }
+    if (tid < kChunk) {
+        rec[2 * kChunk * kChunk + tid] = expf(Gc[tid]);                          // gamma_i
+        rec[2 * kChunk * kChunk + kChunk + tid] = expf(Gc[kChunk - 1] - Gc[tid]);  // gamma_last / gamma_j
+    }
+}
+
+// a chunk's inputs in registers: q / k rows, T, Wq, the value slice, beta and
+// the decay factors (loaded for chunk c + 1 while chunk c is computed)
+struct ChunkRegs {
+    u32x4 k[8], q[8], t[4], wq[4];
+    float v[4], bet, gam, del;
+};
+
+__global__ void __launch_bounds__(256) scan_chunk_state_kernel(LinearScanLaunch p) {
+    extern __shared__ float4 scan_lds[];
+    float* Kc = reinterpret_cast<float*>(scan_lds);  // [64][kChLd]
+    float* Qc = Kc + kChunk * kChLd;                 // [64][kChLd]
+    float* Tc = Qc + kChunk * kChLd;                 // [64][kChLdT]
+    float* Wc = Tc + kChunk * kChLdT;                // [64][kChLdT]
+    // R, U and the state slice are kept transposed (column-major in the value
+    // column): the MFMA operand a lane needs is then a contiguous run
+    float* Rt = Wc + kChunk * kChLdT;                // [16][kChLdT] R^T
+    float* Ut = Rt + 16 * kChLdT;                    // [16][kChLdT] U^T
+    float* St = Ut + 16 * kChLdT;                    // [16][kChLd] the state slice, transposed
+    float* Vc = St + 16 * kChLd;                     // [64][16]
+    float* gam = Vc + kChunk * 16;                   // [64]
+    float* del = gam + kChunk;                       // [64]
+    float* bet = del + kChunk;                       // [64]
+    const int vh = blockIdx.x, j0 = blockIdx.y * 16;
+    const int factor = max(1, p.lv_n / max(1, p.lk_n));
+    const int kh = __builtin_amdgcn_readfirstlane(min(p.lk_n - 1, vh / factor));
+    const int dv = p.lv_hd;
+    const int conv_dim = 2 * p.lk_n * 128 + p.lv_n * dv;
+    const int chunks = __builtin_amdgcn_readfirstlane((p.tokens + kChunk - 1) / kChunk);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+    const int li = lane & 15, lq = lane >> 4;  // MFMA operand row / column li, k slot lq
+    const bool cact = j0 + li < dv;
+    const float rdk = 1.0f / sqrtf(128.0f);
+    float* S = p.state + static_cast<size_t>(vh) * 128 * dv;
+    const float* aux = p.ws + static_cast<size_t>(p.tokens) * conv_dim;
+    const float* recs = aux + static_cast<size_t>(p.tokens) * p.lv_n * 2;
+    const uint32_t kcol = static_cast<uint32_t>(p.lk_n * 128 + kh * 128), qcol = static_cast<uint32_t>(kh * 128);
+    const uint32_t vcol = static_cast<uint32_t>(2 * p.lk_n * 128 + vh * dv + j0);
+    // every load is a range-checked buffer load issued back to back: tokens past
+    // the prompt and chunks past the last read 0
+    // (sizes and bases through readfirstlane: scalar buffer descriptors)
+    auto load_chunk = [&](int ch, ChunkRegs& r) {
+        const int t0 = __builtin_amdgcn_readfirstlane(min(ch * kChunk, p.tokens));
+        const int n = __builtin_amdgcn_readfirstlane(max(0, min(kChunk, p.tokens - t0)));
+        const int cr = __builtin_amdgcn_readfirstlane(min(ch, chunks - 1));
+        const uint32_t rbytes = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(ch < chunks ? kChRec * 4 : 0));
+        const __amdgpu_buffer_rsrc_t rc =
+            buf_rsrc(p.ws + static_cast<size_t>(t0) * conv_dim, static_cast<uint32_t>(n) * conv_dim * 4u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = tid + 256 * u, row = e >> 5, d4 = e & 31;
+            const uint32_t base = static_cast<uint32_t>(row) * conv_dim + 4u * d4;
+            r.k[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, (base + kcol) * 4u, 0, 0);
+            r.q[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, (base + qcol) * 4u, 0, 0);
+        }
+        const __amdgpu_buffer_rsrc_t rr = buf_rsrc(recs + static_cast<size_t>(cr * p.lv_n + vh) * kChRec, rbytes);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t e4 = static_cast<uint32_t>(tid + 256 * u);
+            r.t[u] = __builtin_amdgcn_raw_buffer_load_b128(rr, e4 * 16u, 0, 0);
+            r.wq[u] = __builtin_amdgcn_raw_buffer_load_b128(rr, kChunk * kChunk * 4u + e4 * 16u, 0, 0);
+        }
+        const int vi = tid >> 2, vc = 4 * (tid & 3);  // value rows x 4 columns
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            r.v[e] = buf_load_f32(rc, j0 + vc + e < dv ? (static_cast<uint32_t>(vi) * conv_dim + vcol + vc + e) * 4u : kBufOOB);
+        const __amdgpu_buffer_rsrc_t ra =
+            buf_rsrc(aux + static_cast<size_t>(t0) * p.lv_n * 2, static_cast<uint32_t>(n) * p.lv_n * 8u);
+        r.bet = buf_load_f32(ra, tid < kChunk ? (static_cast<uint32_t>(tid) * p.lv_n * 2 + vh * 2) * 4u : kBufOOB);
+        r.gam = buf_load_f32(rr, tid < kChunk ? (2 * kChunk * kChunk + tid) * 4u : kBufOOB);
+        r.del = buf_load_f32(rr, tid < kChunk ? (2 * kChunk * kChunk + kChunk + tid) * 4u : kBufOOB);
+    };
+    auto store_chunk = [&](const ChunkRegs& r) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = tid + 256 * u, row = e >> 5, d4 = e & 31;
+            *reinterpret_cast<u32x4*>(Kc + row * kChLd + 4 * d4) = r.k[u];
+            *reinterpret_cast<u32x4*>(Qc + row * kChLd + 4 * d4) = r.q[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e4 = tid + 256 * u, i = e4 >> 4, j4 = e4 & 15;
+            *reinterpret_cast<u32x4*>(Tc + i * kChLdT + 4 * j4) = r.t[u];
+            *reinterpret_cast<u32x4*>(Wc + i * kChLdT + 4 * j4) = r.wq[u];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Vc[(tid >> 2) * 16 + 4 * (tid & 3) + e] = r.v[e];
+        if (tid < kChunk) {
+            bet[tid] = r.bet;
+            gam[tid] = r.gam;
+            del[tid] = r.del;
+        }
+    };
+    for (int e = tid; e < 128 * 16; e += 256) {
+        const int d = e >> 4, cc = e & 15;
+        St[cc * kChLd + d] = j0 + cc < dv ? S[static_cast<size_t>(d) * dv + j0 + cc] : 0.0f;
+    }
+    // a float4 of LDS into four registers
+    auto ld4 = [](const float* q, float* d) {
+        const float4 v = *reinterpret_cast<const float4*>(q);
+        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+    };
+    ChunkRegs nx;
+    load_chunk(0, nx);
+    const floatx4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ch = 0; ch < chunks; ++ch) {  // block-uniform
+        const int t0 = ch * kChunk, n = min(kChunk, p.tokens - t0);
+        __syncthreads();  // the previous chunk's LDS data have been read
+        store_chunk(nx);
+        __syncthreads();
+        load_chunk(ch + 1, nx);  // in flight during this chunk's products
+        // The contraction index of every product below is a permutation shared by
+        // both operands: lane (li, lq) feeds dims 32 lq + s (K S, Q S) or tokens
+        // 16 lq + s (T R, Wq U, K^T U) at step s, so its operands are contiguous.
+        // X = K S_0, Y = Q S_0 for the wave's 16 tokens
+        floatx4 X = zero4, Y = zero4;
+        {
+            float ka[32], qa[32], sp[32];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ld4(Kc + (16 * w + li) * kChLd + 32 * lq + 4 * u, ka + 4 * u);
+                ld4(Qc + (16 * w + li) * kChLd + 32 * lq + 4 * u, qa + 4 * u);
+                ld4(St + li * kChLd + 32 * lq + 4 * u, sp + 4 * u);
+            }
+            floatx4 X1 = zero4, Y1 = zero4;  // two chains each (even / odd steps)
+#pragma unroll
+            for (int st = 0; st < 32; st += 2) {
+                X = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[st], sp[st], X, 0, 0, 0);
+                Y = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], sp[st], Y, 0, 0, 0);
+                X1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[st + 1], sp[st + 1], X1, 0, 0, 0);
+                Y1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st + 1], sp[st + 1], Y1, 0, 0, 0);
+            }
+            X += X1;
+            Y += Y1;
+        }
+        // R_i = b_i (v_i - gamma_i X_i) (rows 16 w + 4 lq + v, column li), stored transposed
+        {
+            float r4[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int i = 16 * w + 4 * lq + v;
+                r4[v] = bet[i] * (Vc[i * 16 + li] - gam[i] * X[v]);
+            }
+            *reinterpret_cast<float4*>(Rt + li * kChLdT + 16 * w + 4 * lq) = make_float4(r4[0], r4[1], r4[2], r4[3]);
+        }
+        __syncthreads();
+        // U = T R for the wave's 16 tokens
+        floatx4 U = zero4;
+        {
+            float ta[16], rb[16];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                ld4(Tc + (16 * w + li) * kChLdT + 16 * lq + 4 * u, ta + 4 * u);
+                ld4(Rt + li * kChLdT + 16 * lq + 4 * u, rb + 4 * u);
+            }
+            floatx4 U1 = zero4;
+#pragma unroll
+            for (int st = 0; st < 16; st += 2) {
+                U = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[st], rb[st], U, 0, 0, 0);
+                U1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[st + 1], rb[st + 1], U1, 0, 0, 0);
+            }
+            U += U1;
+        }
+        *reinterpret_cast<float4*>(Ut + li * kChLdT + 16 * w + 4 * lq) = make_float4(U[0], U[1], U[2], U[3]);
+        __syncthreads();
+        // O = diag(gamma) Y + Wq U; the state update's U operand, scaled by del
+        floatx4 O = zero4;
+        float ub[16];
+        {
+            float wa[16], dl[16];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                ld4(Wc + (16 * w + li) * kChLdT + 16 * lq + 4 * u, wa + 4 * u);
+                ld4(Ut + li * kChLdT + 16 * lq + 4 * u, ub + 4 * u);
+                ld4(del + 16 * lq + 4 * u, dl + 4 * u);
+            }
+            floatx4 O1 = zero4;
+#pragma unroll
+            for (int st = 0; st < 16; st += 2) {
+                O = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[st], ub[st], O, 0, 0, 0);
+                O1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[st + 1], ub[st + 1], O1, 0, 0, 0);
+            }
+            O += O1;
+#pragma unroll
+            for (int st = 0; st < 16; ++st) ub[st] *= dl[st];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = 16 * w + 4 * lq + v;
+            if (i < n && cact)
+                p.out[static_cast<size_t>(t0 + i) * p.out_stride + static_cast<size_t>(vh) * dv + j0 + li] =
+                    (gam[i] * Y[v] + O[v]) * rdk;
+        }
+        // S_C = gamma_last S_0 + K^T diag(del) U: the wave's state rows 32 w .. 32 w + 31
+        floatx4 Sn[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int rt = 2 * w + rr;
+            float s4[4], kt[16];
+            ld4(St + li * kChLd + 16 * rt + 4 * lq, s4);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) Sn[rr][v] = gam[kChunk - 1] * s4[v];
+#pragma unroll
+            for (int st = 0; st < 16; ++st) kt[st] = Kc[(16 * lq + st) * kChLd + 16 * rt + li];
+#pragma unroll
+            for (int st = 0; st < 16; ++st) Sn[rr] = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[st], ub[st], Sn[rr], 0, 0, 0);
+        }
+        __syncthreads();  // every wave has read the old state
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+            *reinterpret_cast<float4*>(St + li * kChLd + 16 * (2 * w + rr) + 4 * lq) =
+                make_float4(Sn[rr][0], Sn[rr][1], Sn[rr][2], Sn[rr][3]);
+    }
+    __syncthreads();
+    for (int e = tid; e < 128 * 16; e += 256) {
+        const int d = e >> 4, cc = e & 15;
+        if (j0 + cc < dv) S[static_cast<size_t>(d) * dv + j0 + cc] = St[cc * kChLd + d];
+    }
 }
 
 bool linear_scan_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
@@ -1652,10 +1938,25 @@ hipError_t launch_linear_scan(const LinearScanLaunch& p, hipStream_t s) {
                                dim3((width + kWave - 1) / kWave * kWave), 0, s, p);
         }
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-        // 16 lanes per value column, 16 columns per block, one wave per SIMD (32 lanes
-        // per column, two waves per SIMD whose per-token chains interleave, measured
-        // slower: 99.7 against 86-89 us per layer at 512 tokens)
-        hipLaunchKernelGGL((linear_scan_recur_kernel<128, 16>), dim3(p.lv_n, (p.lv_hd + 15) / 16), dim3(256), 0, s, p);
+        static bool attr_set = false;
+        if (!attr_set) {
+            if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_chunk_prep_kernel),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   static_cast<int>(scan_chunk_prep_lds()));
+                e != hipSuccess)
+                return e;
+            if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_chunk_state_kernel),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   static_cast<int>(scan_chunk_state_lds()));
+                e != hipSuccess)
+                return e;
+            attr_set = true;
+        }
+        const int chunks = (p.tokens + kChunk - 1) / kChunk;
+        hipLaunchKernelGGL(scan_chunk_prep_kernel, dim3(p.lv_n, chunks), dim3(256), scan_chunk_prep_lds(), s, p);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        hipLaunchKernelGGL(scan_chunk_state_kernel, dim3(p.lv_n, (p.lv_hd + 15) / 16), dim3(256), scan_chunk_state_lds(),
+                           s, p);
         return hipGetLastError();
     }
     const dim3 grid(p.lv_n, (p.lv_hd + kScanCols - 1) / kScanCols);
