@@ -173,11 +173,15 @@ def test_prefill_attention_vs_causal_oracle(nq, nkv, hd, T, pos0):
 @pytest.mark.parametrize("with_ws", [False, True])
 @pytest.mark.parametrize("shape,T,pos0", [((16, 32, 128, 128, 4), 12, 0), ((16, 32, 128, 128, 4), 7, 5),
                                           ((16, 32, 128, 128, 4), 37, 3), ((3, 6, 64, 32, 3), 9, 2),
-                                          ((2, 2, 256, 40, 4), 4, 1), ((2, 4, 128, 24, 2), 2, 0)])
+                                          ((2, 2, 256, 40, 4), 4, 1), ((2, 4, 128, 24, 2), 2, 0),
+                                          ((16, 32, 128, 128, 4), 64, 0), ((16, 32, 128, 128, 4), 130, 7),
+                                          ((2, 4, 128, 24, 2), 100, 1)])
 def test_linear_scan_matches_consecutive_steps(shape, T, pos0, with_ws):
     """The prefill scan (fused per-token kernel, or with a workspace the
-    token-parallel conv pass + recurrence kernel) against consecutive decode
-    steps; 37 tokens cross the 16-token staging groups."""
+    token-parallel conv pass + the chunked recurrence for 128-dim key heads)
+    against consecutive decode steps; 37 tokens cross the 16-token staging
+    groups, 64 fill one 64-token chunk exactly, 130 and 100 span several
+    chunks with a short last one (100 with value heads of 24 columns)."""
     lk_n, lv_n, lk_hd, lv_hd, ks = shape
     rng = np.random.default_rng(T * 7 + pos0)
     _, cstate, cw = linear_inputs(lk_n, lv_n, lk_hd, lv_hd, ks, seed=41)
