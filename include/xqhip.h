@@ -246,6 +246,27 @@ XQHIP_API int xqhip_attn_decode_head(const float* q_src, const float* k_src, con
                                      int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
                                      float eps, const float* rope_cs, const int32_t* pos, void* k_cache,
                                      void* v_cache, float* out, void* stream);
+/* The same step with the cached context split over `splits` (1..4) blocks per
+ * query head: split s takes the positions [s per, (s + 1) per), per =
+ * ceil(pos / splits), the last split also the new token (appended as above).
+ * Each block writes its partial (running max, exp sum, exp-weighted value
+ * sums) to the workspace and counts itself on its head's counter; the block
+ * completing the count merges the head's partials and writes the gated output
+ * to `out` (no block waits for another, no merge kernel).  One split gives
+ * xqhip_attn_decode_head's result bit for bit.  workspace:
+ * xqhip_attn_split_workspace_bytes(nq) bytes, 16-byte aligned, zero-filled
+ * once before the first call: partials [XQHIP_ATTN_MAX_SPLITS][nq]
+ * [XQHIP_ATTN_PART_STRIDE] floats, then one counter per head 128 bytes apart;
+ * every call leaves the counters at zero again, and calls that overlap on one
+ * device race on them.  Replaces the same reference code as
+ * xqhip_attn_decode_head (custom_model.cpp:740-951). */
+#define XQHIP_ATTN_PART_STRIDE 132 /* floats per (split, head): m, l, 2 pad, o[128] */
+#define XQHIP_ATTN_MAX_SPLITS 4
+XQHIP_API size_t xqhip_attn_split_workspace_bytes(int nq);
+XQHIP_API int xqhip_attn_decode_split(const float* q_src, const float* k_src, const float* v_src, int gated, int nq,
+                                      int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
+                                      float eps, const float* rope_cs, const int32_t* pos, void* k_cache,
+                                      void* v_cache, int splits, void* workspace, float* out, void* stream);
 
 /* Linear attention: conv1d + SiLU over the mixed q|k|v channels with the
  * [channels][ksize-1] history updated in place, then L2-normalised q and k

@@ -18,6 +18,7 @@ import pytest
 
 import oracle_bind as ob
 import xqbind as xb
+from synth import w4_matrix
 
 pytestmark = pytest.mark.gpu
 O = ob.oracle
@@ -282,6 +283,81 @@ def test_head_attention_rejects_other_head_sizes():
     rc = xb.hip().xqhip_attn_decode_head(z.ptr, z.ptr, z.ptr, 1, 8, 2, 64, 32, z.ptr, z.ptr, 1e-6, z.ptr, z.ptr,
                                          z.ptr, z.ptr, z.ptr, None)
     assert rc == -1 and b"head_dim 128" in xb.hip().xqhip_last_error()  # XQHIP_EINVAL
+
+
+# The per-head attention split over 1, 2 or 4 context ranges per query head
+# and merged by the last block of each head: the new token alone, fewer cached
+# positions than splits (empty ranges), the 512-token point, a range of exactly
+# one 1024-token pass and ranges past it, group sizes 1, 4 and 8, gated and not.
+PART_CASES = [(32, 8, 128, 32, 0, 64, True), (32, 8, 128, 32, 2, 64, True), (32, 8, 128, 32, 511, 1024, True),
+              (32, 8, 128, 64, 540, 1024, False), (16, 2, 128, 32, 1023, 2048, True),
+              (8, 8, 128, 128, 4095, 4160, True), (4, 1, 128, 32, 9000, 9216, False)]
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4])
+@pytest.mark.parametrize("case", PART_CASES, ids=lambda c: "nq%d_nkv%d_hd%d_rd%d_pos%d" % c[:5])
+def test_split_attention_merged_in_kernel(case, splits):
+    """xqhip_attn_decode_split (partials merged by the last block of each query
+    head) against the oracle and against xqhip_attn_decode_head on its own copy
+    of the caches: bit-identical with one split, within 1e-5 otherwise; three
+    consecutive positions on one workspace, zero-filled once (each call must
+    leave its counters at zero)."""
+    nq, nkv, hd, rd, pos, max_ctx, gated = case
+    theta, eps = 1e7, 1e-6
+    print(f"split attention case {case} splits {splits}", flush=True)
+    assert pos + 3 <= max_ctx
+    qsrc, k, v, qn, kn, kc, vc = attn_layer_inputs(nq, nkv, hd, pos, seed=pos + 13, gated=gated)
+    tab = np.empty(max_ctx * rd, np.float32)
+    xb.ck(xb.hip().xqhip_rope_table(theta, rd, max_ctx, xb.ptr(tab)))
+    kcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    vcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    kcache[:pos], vcache[:pos] = kc, vc
+    kd, vd = dev(kcache), dev(vcache)    # split kernel
+    kd2, vd2 = dev(kcache), dev(vcache)  # single-block kernel
+    qn_d, kn_d, tab_d = dev(qn), dev(kn), dev(tab)
+    nbytes = xb.hip().xqhip_attn_split_workspace_bytes(nq)
+    ws = dev(np.zeros(nbytes, np.uint8))
+    out, out2 = xb.DeviceBuffer(nq * hd * 4), xb.DeviceBuffer(nq * hd * 4)
+    rng = np.random.default_rng(pos + 4)
+    for step in range(3):
+        p = pos + step
+        if step:
+            qsrc = rng.normal(0, 1, qsrc.size).astype(np.float32)
+            k = rng.normal(0, 1, k.size).astype(np.float32)
+            v = rng.normal(0, 1, v.size).astype(np.float32)
+        qs_d, k_d, v_d = dev(qsrc), dev(k), dev(v)
+        pos_d = dev(np.array([p], np.int32))
+        xb.ck(xb.hip().xqhip_attn_decode_split(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr,
+                                               kn_d.ptr, eps, tab_d.ptr, pos_d.ptr, kd.ptr, vd.ptr, splits, ws.ptr,
+                                               out.ptr, None))
+        xb.ck(xb.hip().xqhip_attn_decode_head(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr,
+                                              kn_d.ptr, eps, tab_d.ptr, pos_d.ptr, kd2.ptr, vd2.ptr, out2.ptr, None))
+        kc_got = kd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        vc_got = vd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+        assert np.array_equal(kc_got, kd2.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd))
+        assert np.array_equal(vc_got, vd2.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd))
+        assert np.array_equal(vc_got[p].reshape(-1), v.astype(np.float16))
+        assert not kc_got[p + 1:].any() and not vc_got[p + 1:].any()  # later slots untouched
+        _, want = oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, p, theta, eps, kc_got, vc_got)
+        got, ref = out.download(np.float32, nq * hd), out2.download(np.float32, nq * hd)
+        close(got, want, f"split attention pos {p}")
+        if splits == 1:
+            assert np.array_equal(got, ref), "one split must match the single-block kernel bit for bit"
+        else:
+            close(got, ref, f"split vs single-block pos {p}", atol=1e-5, rtol=1e-5)
+    cnt = ws.download(np.uint32, nbytes // 4)[xb.ATTN_MAX_SPLITS * nq * xb.ATTN_PART_STRIDE:]
+    assert not cnt.any()  # the counters are back at zero
+
+
+def test_split_attention_rejections():
+    z = dev(np.zeros(64, np.float32))
+    assert xb.hip().xqhip_attn_split_workspace_bytes(0) == 0
+    ws = dev(np.zeros(xb.hip().xqhip_attn_split_workspace_bytes(32), np.uint8))
+    for splits, hd in ((0, 128), (5, 128), (2, 64)):
+        rc = xb.hip().xqhip_attn_decode_split(z.ptr, z.ptr, z.ptr, 1, 32, 8, hd, 32, z.ptr, z.ptr, 1e-6, z.ptr, z.ptr,
+                                              z.ptr, z.ptr, splits, ws.ptr, z.ptr, None)
+        assert rc == -1  # XQHIP_EINVAL
+    assert b"head_dim 128" in xb.hip().xqhip_last_error()
 
 
 @pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 100])

@@ -776,10 +776,15 @@ __device__ __forceinline__ uint4 buf_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t 
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// One query head with first-pass sub-passes KS (later passes, for contexts
-// past kHeadPass, use all kHeadKSubs).
-template <int HD, int KS>
-__device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSmem<HD>& sm, int pos) {
+// One query head over the cached positions [c0, c1) and, when `fresh`, the new
+// token at `pos` (appended to the caches by the first query head of each kv
+// head), with first-pass sub-passes KS (later passes, for ranges past
+// kHeadPass, use all kHeadKSubs).  PART: the unnormalised result goes to
+// part_out (running max, exp sum, sum of exp-weighted values; the consumer
+// merges the ranges and applies 1/l and the gate); otherwise the gated output.
+template <int HD, int KS, bool PART>
+__device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSmem<HD>& sm, int pos, int c0, int c1,
+                                               bool fresh, float* part_out) {
     static_assert(HD == 128, "4 score lanes x 32 dims, 16 value lanes x 8 dims");
     constexpr int kWaves = kHeadThreads / kWave;
     const GqaLaunch& p = a.g;
@@ -789,7 +794,7 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
     // a kv head's blocks share one XCD's L2 and its K / V come from memory once
     const int kh = static_cast<int>(blockIdx.x) % p.nkv;
     const int qh = kh * group + static_cast<int>(blockIdx.x) / p.nkv;
-    const bool owner = qh % group == 0;  // appends the new key / value of kv head kh
+    const bool owner = fresh && qh % group == 0;  // appends the new key / value of kv head kh
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int sub = tid & 3, tt = tid >> 2;   // score lanes: dims 32 u + 8 sub + e of token tt
     const int dsl = tid & 15, ts = tid >> 4;  // value lanes: dims 8 dsl + e of token ts
@@ -813,7 +818,7 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
     const __amdgpu_buffer_rsrc_t r_gate =
         buf_rsrc(p.gate, p.gate ? static_cast<uint32_t>(p.nq) * p.gate_stride * 4u : 0u);
     const float gv = buf_load_f32(
-        r_gate, tid < HD ? (static_cast<uint32_t>(qh) * p.gate_stride + tid) * 4u : kBufOOB);
+        r_gate, !PART && tid < HD ? (static_cast<uint32_t>(qh) * p.gate_stride + tid) * 4u : kBufOOB);
     // the keys of a pass: cached positions [t0, t0 + nc), rows past nc read 0
     auto load_k = [&](int t0, int nc, auto& kr) {
         constexpr int J = sizeof(kr) / sizeof(kr[0]);
@@ -826,7 +831,7 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
                 kr[j][u] = buf_load_u4(r, static_cast<uint32_t>(tt + kHeadKSub * j) * row_bytes + sub * 16u + u * 64u);
     };
     uint4 kr[KS][4];
-    load_k(0, min(kHeadPass, pos), kr);
+    load_k(c0, min(kHeadPass, c1 - c0), kr);
     // per-head RMSNorm (custom_model.cpp:301-313) of q and k; v as it is
     if (wid < 2) {
         float ss = hv0 * hv0 + hv1 * hv1;
@@ -880,8 +885,8 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
     // the new token when it falls in this pass)
     auto pass = [&](int t0, const auto& kp) {
         constexpr int J = sizeof(kp) / sizeof(kp[0]);
-        const int nc = min(kHeadPass, pos - t0);
-        const bool last = pos - t0 < kHeadPass;
+        const int nc = min(kHeadPass, c1 - t0);
+        const bool last = fresh && c1 - t0 < kHeadPass;
         const __amdgpu_buffer_rsrc_t r_v = buf_rsrc(p.v_cache + static_cast<size_t>(t0) * kv_stride + kh * HD,
                                                     static_cast<uint32_t>(nc) * row_bytes);
         float m = -INFINITY;
@@ -948,13 +953,13 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
         }
         __syncthreads();  // sc and red are rewritten by the next pass
     };
-    pass(0, kr);
-    // longer contexts: further passes of kHeadKSubs sub-passes, each loading its
+    pass(c0, kr);
+    // longer ranges: further passes of kHeadKSubs sub-passes, each loading its
     // keys first (kept apart from the first pass so that no key register lives
-    // across a value phase)
-    for (int t0 = kHeadPass; t0 <= pos; t0 += kHeadPass) {
+    // across a value phase); the new token may open a pass of its own
+    for (int t0 = c0 + kHeadPass; fresh ? t0 <= c1 : t0 < c1; t0 += kHeadPass) {
         uint4 kr2[kHeadKSubs][4];
-        load_k(t0, min(kHeadPass, pos - t0), kr2);
+        load_k(t0, min(kHeadPass, c1 - t0), kr2);
         pass(t0, kr2);
     }
     // lanes with the same dsl: 4 per wave (16 apart), then the waves through LDS;
@@ -975,7 +980,15 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
             acc += sm.ored[w][tid];
             lt += sm.ored[w][HD];
         }
-        p.out[static_cast<size_t>(qh) * HD + tid] = (acc * (1.0f / lt)) * sigmoid_dev(sm.gate[tid]);
+        if constexpr (PART) {  // written through to memory: the merging block may run on another XCD
+            __hip_atomic_store(part_out + kAttnPartO + tid, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) {
+                __hip_atomic_store(part_out, run_m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(part_out + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else {
+            p.out[static_cast<size_t>(qh) * HD + tid] = (acc * (1.0f / lt)) * sigmoid_dev(sm.gate[tid]);
+        }
     }
 }
 
@@ -986,15 +999,96 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDeco
     // 128-token sub-passes holding the first pass's cached positions
     const int ks = max(1, (min(pos, kHeadPass) + kHeadKSub - 1) / kHeadKSub);
     switch (ks) {
-        case 1: head_attention<HD, 1>(a, sm, pos); break;
-        case 2: head_attention<HD, 2>(a, sm, pos); break;
-        case 3: head_attention<HD, 3>(a, sm, pos); break;
-        case 4: head_attention<HD, 4>(a, sm, pos); break;
-        case 5: head_attention<HD, 5>(a, sm, pos); break;
-        case 6: head_attention<HD, 6>(a, sm, pos); break;
-        case 7: head_attention<HD, 7>(a, sm, pos); break;
-        default: head_attention<HD, 8>(a, sm, pos); break;
+        case 1: head_attention<HD, 1, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        case 2: head_attention<HD, 2, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        case 3: head_attention<HD, 3, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        case 4: head_attention<HD, 4, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        case 5: head_attention<HD, 5, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        case 6: head_attention<HD, 6, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        case 7: head_attention<HD, 7, false>(a, sm, pos, 0, pos, true, nullptr); break;
+        default: head_attention<HD, 8, false>(a, sm, pos, 0, pos, true, nullptr); break;
     }
+}
+
+// The context split over gridDim.y blocks per query head: split s takes the
+// cached positions [s per, (s + 1) per) (per = ceil(pos / splits)), the last
+// split also the new token, and each writes its partial to
+// part[s][query head][kAttnPartStride] with write-through stores.  Once they
+// are complete the block counts itself on the query head's counter
+// (cnt[head * 32], zero before the launch), and the block that completes the
+// count merges the head's partials (loads that bypass the per-XCD L2: the
+// splits may run on other XCDs), weights exp(m_s - max m), multiplies by 1 / l
+// (custom_model.cpp:901-904) and the sigmoid gate, writes a.g.out and sets the
+// counter back to 0; no block waits for another.  With one split the result is
+// the single-block kernel's, bit for bit.
+template <int HD>
+__global__ void __launch_bounds__(kHeadThreads) attn_decode_part_kernel(AttnDecodeLaunch a, float* part,
+                                                                        uint32_t* cnt) {
+    __shared__ HeadSmem<HD> sm;
+    const int pos = *a.g.pos;
+    const int splits = static_cast<int>(gridDim.y), sp = static_cast<int>(blockIdx.y);
+    const int per = (pos + splits - 1) / splits;
+    const int c0 = min(pos, sp * per), c1 = min(pos, c0 + per);
+    const bool fresh = sp == splits - 1;
+    const int kh = static_cast<int>(blockIdx.x) % a.g.nkv;
+    const int qh = kh * (a.g.nq / a.g.nkv) + static_cast<int>(blockIdx.x) / a.g.nkv;
+    float* out = part + (static_cast<size_t>(sp) * a.g.nq + qh) * kAttnPartStride;
+    if (!fresh && c0 == c1) {  // nothing cached in this range (block-uniform): an empty partial
+        if (threadIdx.x < HD)
+            __hip_atomic_store(out + kAttnPartO + threadIdx.x, 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(out, -INFINITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(out + 1, 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else {
+        const int ks = max(1, (min(c1 - c0, kHeadPass) + kHeadKSub - 1) / kHeadKSub);
+        switch (ks) {
+            case 1: head_attention<HD, 1, true>(a, sm, pos, c0, c1, fresh, out); break;
+            case 2: head_attention<HD, 2, true>(a, sm, pos, c0, c1, fresh, out); break;
+            case 3: head_attention<HD, 3, true>(a, sm, pos, c0, c1, fresh, out); break;
+            case 4: head_attention<HD, 4, true>(a, sm, pos, c0, c1, fresh, out); break;
+            case 5: head_attention<HD, 5, true>(a, sm, pos, c0, c1, fresh, out); break;
+            case 6: head_attention<HD, 6, true>(a, sm, pos, c0, c1, fresh, out); break;
+            case 7: head_attention<HD, 7, true>(a, sm, pos, c0, c1, fresh, out); break;
+            default: head_attention<HD, 8, true>(a, sm, pos, c0, c1, fresh, out); break;
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
+    __syncthreads();
+    __shared__ int last;
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(cnt + qh * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               static_cast<uint32_t>(splits - 1);
+    __syncthreads();
+    if (!last) return;  // block-uniform
+    if (threadIdx.x < HD) {
+        const int tid = threadIdx.x;
+        // no gate projection: the reference's zero gate, sigmoid(0) (custom_model.cpp:750-753)
+        const float g = a.g.gate ? a.g.gate[static_cast<size_t>(qh) * a.g.gate_stride + tid] : 0.0f;
+        float mv[kAttnMaxSplits], lv[kAttnMaxSplits], ov[kAttnMaxSplits];
+        float M = -INFINITY;
+#pragma unroll
+        for (int s2 = 0; s2 < kAttnMaxSplits; ++s2) {
+            const float* q2 = part + (static_cast<size_t>(min(s2, splits - 1)) * a.g.nq + qh) * kAttnPartStride;
+            mv[s2] = __hip_atomic_load(q2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lv[s2] = __hip_atomic_load(q2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ov[s2] = __hip_atomic_load(q2 + kAttnPartO + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < kAttnMaxSplits; ++s2) {
+            if (s2 >= splits) mv[s2] = -INFINITY;  // re-read of the last split: weight 0
+            M = fmaxf(M, mv[s2]);
+        }
+        float L = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < kAttnMaxSplits; ++s2) {
+            const float wgt = expf(mv[s2] - M);  // an empty range (m = -inf): 0
+            L += wgt * lv[s2];
+            acc += wgt * ov[s2];
+        }
+        a.g.out[static_cast<size_t>(qh) * HD + tid] = (acc * (1.0f / L)) * sigmoid_dev(g);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt + qh * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 bool attn_head_supported(int nq, int nkv, int head_dim) {
@@ -1003,6 +1097,11 @@ bool attn_head_supported(int nq, int nkv, int head_dim) {
 
 hipError_t launch_attn_decode_head(const AttnDecodeLaunch& a, hipStream_t s) {
     hipLaunchKernelGGL(attn_decode_head_kernel<128>, dim3(a.g.nq), dim3(kHeadThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_decode_part(const AttnDecodeLaunch& a, int splits, float* part, uint32_t* cnt, hipStream_t s) {
+    hipLaunchKernelGGL(attn_decode_part_kernel<128>, dim3(a.g.nq, splits), dim3(kHeadThreads), 0, s, a, part, cnt);
     return hipGetLastError();
 }
 

@@ -684,6 +684,40 @@ int xqhip_attn_decode_head(const float* q_src, const float* k_src, const float* 
     return check(xqhip::launch_attn_decode_head(a, as_stream(stream)), "attn_decode_head launch");
 }
 
+static_assert(XQHIP_ATTN_PART_STRIDE == xqhip::kAttnPartStride && XQHIP_ATTN_MAX_SPLITS == xqhip::kAttnMaxSplits,
+              "split attention workspace layout");
+
+size_t xqhip_attn_split_workspace_bytes(int nq) {
+    if (nq <= 0) return 0;
+    // partials [XQHIP_ATTN_MAX_SPLITS][nq][stride] floats, then one counter per head, 128 bytes apart
+    return sizeof(float) * static_cast<size_t>(XQHIP_ATTN_MAX_SPLITS) * nq * XQHIP_ATTN_PART_STRIDE +
+           static_cast<size_t>(nq) * 128;
+}
+
+int xqhip_attn_decode_split(const float* q_src, const float* k_src, const float* v_src, int gated, int nq, int nkv,
+                            int head_dim, int rotary_dim, const float* q_norm, const float* k_norm, float eps,
+                            const float* rope_cs, const int32_t* pos, void* k_cache, void* v_cache, int splits,
+                            void* workspace, float* out, void* stream) {
+    if (!q_src || !k_src || !v_src || !q_norm || !k_norm || !pos || !k_cache || !v_cache || !workspace || !out ||
+        (rotary_dim > 0 && !rope_cs))
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode_split: null argument");
+    if (!xqhip::attn_head_supported(nq, nkv, head_dim))
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode_split: unsupported shape nq=%d nkv=%d hd=%d (head_dim 128 only)",
+                    nq, nkv, head_dim);
+    if (splits < 1 || splits > XQHIP_ATTN_MAX_SPLITS)
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode_split: splits %d outside 1..%d", splits, XQHIP_ATTN_MAX_SPLITS);
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(XQHIP_EINVAL, "xqhip_attn_decode_split: workspace not 16-byte aligned");
+    float* part = static_cast<float*>(workspace);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(part + static_cast<size_t>(XQHIP_ATTN_MAX_SPLITS) * nq *
+                                                           XQHIP_ATTN_PART_STRIDE);
+    const xqhip::AttnDecodeLaunch a = attn_decode_args(q_src, k_src, v_src, gated, nq, nkv, head_dim, rotary_dim,
+                                                       q_norm, k_norm, eps, rope_cs, pos, k_cache, v_cache, 0, out,
+                                                       nullptr);
+    return check(xqhip::launch_attn_decode_part(a, splits, part, cnt, as_stream(stream)),
+                 "attn_decode_split launch");
+}
+
 int xqhip_linear_conv(const float* mixed, float* conv_state, const float* conv_w, int lk_n, int lk_hd, int lv_n,
                       int lv_hd, int ksize, float* out, void* stream) {
     if (!mixed || !conv_state || !conv_w || !out || lk_n <= 0 || lv_n <= 0 || ksize < 1 ||

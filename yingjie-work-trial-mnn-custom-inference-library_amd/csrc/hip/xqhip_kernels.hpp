@@ -8,6 +8,10 @@ namespace xqhip {
 
 enum { PRO_NONE = 0, PRO_RMS = 1, PRO_GATED = 2 };
 constexpr int kMaxNormHeads = 256;
+// Split decode attention partials (attn_decode_part_kernel): per split and
+// query head, the running max at 0, the exp sum at 1 and the head_dim (128)
+// exp-weighted value sums from kAttnPartO (16-byte aligned rows).
+constexpr int kAttnPartO = 4, kAttnPartStride = kAttnPartO + 128, kAttnMaxSplits = 4;
 
 // Normalisation applied to the GEMV input inside the kernel prologue.
 struct Prologue {
@@ -105,6 +109,10 @@ hipError_t launch_attn_decode(const AttnDecodeLaunch& a, hipStream_t s);
 // one block per query head, no merge kernel (head_dim 128)
 bool attn_head_supported(int nq, int nkv, int head_dim);
 hipError_t launch_attn_decode_head(const AttnDecodeLaunch& a, hipStream_t s);
+// the same over `splits` context ranges per query head, merged by the last
+// block of each head (cnt: a zeroed counter per head, 128 bytes apart, left
+// zeroed) into the gated output a.g.out
+hipError_t launch_attn_decode_part(const AttnDecodeLaunch& a, int splits, float* part, uint32_t* cnt, hipStream_t s);
 size_t gqa_workspace_bytes(int nq, int nkv, int head_dim);
 bool gqa_supported(int nq, int nkv, int head_dim, int max_ctx);
 hipError_t launch_gqa(const GqaLaunch& p, hipStream_t s);

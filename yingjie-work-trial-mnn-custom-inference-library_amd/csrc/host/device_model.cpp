@@ -256,18 +256,22 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     const int attn_n = std::max({nq_ * hd_, lv_dim_, hidden_});
     size_t ws_argmax = xqhip_argmax_workspace_bytes(lm_head_.rows);
     size_t ws_gqa = any_full ? xqhip_gqa_workspace_bytes(nq_, nkv_, hd_) : 1;
-    uint8_t *wa = nullptr, *wg = nullptr;
+    size_t ws_split = any_full ? std::max<size_t>(1, xqhip_attn_split_workspace_bytes(nq_)) : 1;
+    uint8_t *wa = nullptr, *wg = nullptr, *wsp = nullptr;
     if (!alloc(&resid_, hidden_, error) || !alloc(&normed_, hidden_, error) || !alloc(&proj_, max_proj, error) ||
         !alloc(&attn_, attn_n, error) ||
+
         !alloc(&ffn_, inter_, error) || !alloc(&best_val_, 1, error) || !alloc(&d_ctrl_, 4, error) ||
-        !alloc(&wa, ws_argmax, error) || !alloc(&wg, ws_gqa, error))
+        !alloc(&wa, ws_argmax, error) || !alloc(&wg, ws_gqa, error) || !alloc(&wsp, ws_split, error))
         return false;
     argmax_ws_ = wa;
     gqa_ws_ = wg;
+    attn_split_ws_ = wsp;
     if (xqhip_stream_create(&stream_) != 0) return fail_hip(error, "stream");
     xqhip_fill_u8(resid_, 0, sizeof(float) * hidden_, stream_);  // hidden_ starts at zero (custom_model.cpp:478)
     xqhip_fill_u8(argmax_ws_, 0, ws_argmax, stream_);
     xqhip_fill_u8(gqa_ws_, 0, ws_gqa, stream_);
+    xqhip_fill_u8(attn_split_ws_, 0, ws_split, stream_);  // the split attention's counters start (and stay) at 0
     xqhip_fill_u8(d_ctrl_, 0, 16, stream_);
     if (any_full && !build_rope_table(error)) return false;
     (void)any_linear;
@@ -340,15 +344,30 @@ static bool head_attention_enabled() {
     return !(v && v[0] == '0');
 }
 
+// Context splits of the split attention; XQ_ATTN_SPLITS overrides the default
+// (0: no split attention, for measurements).
+static int attn_splits(int dflt) {
+    const char* v = std::getenv("XQ_ATTN_SPLITS");
+    if (!v || !*v) return dflt;
+    const int n = std::atoi(v);
+    return n < 0 ? 0 : (n > XQHIP_ATTN_MAX_SPLITS ? XQHIP_ATTN_MAX_SPLITS : n);
+}
+
 // Picks the attention kernel of the full-attention layers for a step whose
-// context is `ctx` tokens.  Both kernels give the same results; the graphs
-// that hold the other one are dropped after the queued steps have finished.
+// context is `ctx` tokens.  The kernels give the same results within fp32
+// rounding; the graphs that hold another one are dropped after the queued
+// steps have finished.
 bool DeviceModel::select_attention(size_t ctx, KernelTrace* trace, std::string* error) {
-    const bool want = head_attention_enabled() && hd_ == 128 && nq_ % nkv_ == 0 &&
-                      ctx <= static_cast<size_t>(kHeadAttnMaxCtx);
-    if (want == attn_head_) return true;
+    const bool per_head = head_attention_enabled() && hd_ == 128 && nq_ % nkv_ == 0;
+    const bool split = per_head && attn_splits(kAttnSplits) > 0;
+    AttnMode want = AttnMode::kSlot;
+    if (split && ctx >= static_cast<size_t>(kSplitMinCtx) && ctx <= static_cast<size_t>(kSplitMaxCtx))
+        want = AttnMode::kSplit;
+    else if (per_head && ctx <= static_cast<size_t>(split ? kSplitMinCtx : kHeadAttnMaxCtx))
+        want = AttnMode::kHead;
+    if (want == attn_mode_) return true;
     if (!sync(trace, error)) return false;
-    attn_head_ = want;
+    attn_mode_ = want;
     for (void** g : {&g_prefill_, &g_forward_}) {
         if (*g) xqhip_graph_destroy(*g);
         *g = nullptr;
@@ -433,7 +452,12 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
                      {"prefill_kv_build_custom", "attention_score_custom", "attention_softmax_custom",
                       "attention_v_reduce_custom"},
                      4);
-            if (attn_head_) {
+            if (attn_mode_ == AttnMode::kSplit) {
+                XQ_CALL(xqhip_attn_decode_split(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm,
+                                                L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache,
+                                                attn_splits(kAttnSplits), attn_split_ws_, attn_, stream_),
+                        "attention decode");
+            } else if (attn_mode_ == AttnMode::kHead) {
                 XQ_CALL(xqhip_attn_decode_head(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm,
                                                L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache, attn_, stream_),
                         "attention decode");

@@ -111,11 +111,19 @@ private:
     float eps_ = 1.0e-6f, theta_ = 10000000.0f;
     static constexpr int kMaxContext = 1 << 20;  // the attention kernels' limit
     int max_ctx_ = 8192;                          // KV capacity (positions), grows on demand
-    // Full-attention layers attend with one block per query head (one launch,
-    // no merge) up to this context, with the slot kernel + merge beyond it;
-    // the step graphs hold one of the two and are captured again on a switch.
-    static constexpr int kHeadAttnMaxCtx = 1024;  // measured crossover: 11.4 vs 12.4 us at 1024, 17.5 vs 13.3 at 1536
-    bool attn_head_ = false;
+    // Decode attention of the full-attention layers, by context (attention +
+    // o_proj GEMV per layer, 32q/8kv d128, measured in step graphs): one block
+    // per query head below kSplitMinCtx (9.8 against 10.7 us at 256 tokens);
+    // kAttnSplits context splits per query head merged by each head's last
+    // block up to kSplitMaxCtx (10.9 / 11.7 / 13.5 / 28.7 us at 512 / 1024 /
+    // 2048 / 8191 tokens against 11.6 / 15.3 / 22.5 / 79.4 for one block per
+    // head and 16.4 / 17.0 / 18.8 / 38.0 for the slot kernel + merge); the
+    // slot kernel + merge beyond.  The step graphs hold one of them and are
+    // captured again on a switch.
+    enum class AttnMode { kSlot, kHead, kSplit };
+    static constexpr int kSplitMinCtx = 384, kSplitMaxCtx = 8192, kAttnSplits = 4;
+    static constexpr int kHeadAttnMaxCtx = 1024;  // without splits (XQ_ATTN_SPLITS=0): one block per head up to here
+    AttnMode attn_mode_ = AttnMode::kSlot;
     std::string model_dir_, backend_request_, device_name_;
     uint64_t weight_bytes_ = 0;
     int inexact_meta_ = 0;
@@ -131,6 +139,7 @@ private:
     float* normed_ = nullptr;    // final-normed hidden (exposed hidden state)
     float* proj_ = nullptr;      // fused input projection output
     float* attn_ = nullptr;      // attention / delta output
+    void* attn_split_ws_ = nullptr;  // split attention partials + per-head counters (zeroed once)
     float* ffn_ = nullptr;
     float* logits_ = nullptr;    // debug_json only
     float* best_val_ = nullptr;

@@ -19,6 +19,7 @@ c_uint64, c_int32, c_uint8 = ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint8
 
 F32, F16 = 0, 1
 PRO_NONE, PRO_RMS, PRO_GATED_HEAD = 0, 1, 2
+ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 132, 4  # split attention workspace: partials, then counters
 EPI_STORE, EPI_ADD, EPI_SILU_PAIR = 0, 1, 2
 LAYOUT_TILED64, LAYOUT_GENERIC, LAYOUT_TILED64_F32META, LAYOUT_TILED64_SCALE16 = 0, 1, 2, 3
 
@@ -81,6 +82,10 @@ _HIP_SIGS = {
     "xqhip_attn_decode_head": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                        c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p]),
+    "xqhip_attn_split_workspace_bytes": (c_size_t, [c_int]),
+    "xqhip_attn_decode_split": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                        c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                                        c_void_p, c_void_p]),
     "xqhip_linear_conv": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                   c_void_p]),
     "xqhip_gated_delta": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
