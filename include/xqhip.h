@@ -246,7 +246,7 @@ XQHIP_API int xqhip_attn_decode_head(const float* q_src, const float* k_src, con
                                      int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,
                                      float eps, const float* rope_cs, const int32_t* pos, void* k_cache,
                                      void* v_cache, float* out, void* stream);
-/* The same step with the cached context split over `splits` (1..4) blocks per
+/* The same step with the cached context split over `splits` (1..8) blocks per
  * query head: split s takes the positions [s per, (s + 1) per), per =
  * ceil(pos / splits), the last split also the new token (appended as above).
  * Each block writes its partial (running max, exp sum, exp-weighted value
@@ -261,7 +261,7 @@ XQHIP_API int xqhip_attn_decode_head(const float* q_src, const float* k_src, con
  * device race on them.  Replaces the same reference code as
  * xqhip_attn_decode_head (custom_model.cpp:740-951). */
 #define XQHIP_ATTN_PART_STRIDE 132 /* floats per (split, head): m, l, 2 pad, o[128] */
-#define XQHIP_ATTN_MAX_SPLITS 4
+#define XQHIP_ATTN_MAX_SPLITS 8
 XQHIP_API size_t xqhip_attn_split_workspace_bytes(int nq);
 XQHIP_API int xqhip_attn_decode_split(const float* q_src, const float* k_src, const float* v_src, int gated, int nq,
                                       int nkv, int head_dim, int rotary_dim, const float* q_norm, const float* k_norm,

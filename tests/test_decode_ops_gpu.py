@@ -294,7 +294,7 @@ PART_CASES = [(32, 8, 128, 32, 0, 64, True), (32, 8, 128, 32, 2, 64, True), (32,
               (8, 8, 128, 128, 4095, 4160, True), (4, 1, 128, 32, 9000, 9216, False)]
 
 
-@pytest.mark.parametrize("splits", [1, 2, 4])
+@pytest.mark.parametrize("splits", [1, 2, 4, 8])
 @pytest.mark.parametrize("case", PART_CASES, ids=lambda c: "nq%d_nkv%d_hd%d_rd%d_pos%d" % c[:5])
 def test_split_attention_merged_in_kernel(case, splits):
     """xqhip_attn_decode_split (partials merged by the last block of each query
@@ -353,7 +353,7 @@ def test_split_attention_rejections():
     z = dev(np.zeros(64, np.float32))
     assert xb.hip().xqhip_attn_split_workspace_bytes(0) == 0
     ws = dev(np.zeros(xb.hip().xqhip_attn_split_workspace_bytes(32), np.uint8))
-    for splits, hd in ((0, 128), (5, 128), (2, 64)):
+    for splits, hd in ((0, 128), (9, 128), (2, 64)):
         rc = xb.hip().xqhip_attn_decode_split(z.ptr, z.ptr, z.ptr, 1, 32, 8, hd, 32, z.ptr, z.ptr, 1e-6, z.ptr, z.ptr,
                                               z.ptr, z.ptr, splits, ws.ptr, z.ptr, None)
         assert rc == -1  # XQHIP_EINVAL

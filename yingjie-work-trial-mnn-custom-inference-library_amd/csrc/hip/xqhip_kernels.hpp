@@ -11,7 +11,7 @@ constexpr int kMaxNormHeads = 256;
 // Split decode attention partials (attn_decode_part_kernel): per split and
 // query head, the running max at 0, the exp sum at 1 and the head_dim (128)
 // exp-weighted value sums from kAttnPartO (16-byte aligned rows).
-constexpr int kAttnPartO = 4, kAttnPartStride = kAttnPartO + 128, kAttnMaxSplits = 4;
+constexpr int kAttnPartO = 4, kAttnPartStride = kAttnPartO + 128, kAttnMaxSplits = 8;
 
 // Normalisation applied to the GEMV input inside the kernel prologue.
 struct Prologue {

@@ -361,7 +361,7 @@ bool DeviceModel::select_attention(size_t ctx, KernelTrace* trace, std::string* 
     const bool per_head = head_attention_enabled() && hd_ == 128 && nq_ % nkv_ == 0;
     const bool split = per_head && attn_splits(kAttnSplits) > 0;
     AttnMode want = AttnMode::kSlot;
-    if (split && ctx >= static_cast<size_t>(kSplitMinCtx) && ctx <= static_cast<size_t>(kSplitMaxCtx))
+    if (split && ctx >= static_cast<size_t>(kSplitMinCtx))
         want = AttnMode::kSplit;
     else if (per_head && ctx <= static_cast<size_t>(split ? kSplitMinCtx : kHeadAttnMaxCtx))
         want = AttnMode::kHead;

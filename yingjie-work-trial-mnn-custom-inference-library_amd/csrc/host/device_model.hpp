@@ -111,17 +111,18 @@ private:
     float eps_ = 1.0e-6f, theta_ = 10000000.0f;
     static constexpr int kMaxContext = 1 << 20;  // the attention kernels' limit
     int max_ctx_ = 8192;                          // KV capacity (positions), grows on demand
-    // Decode attention of the full-attention layers, by context (attention +
-    // o_proj GEMV per layer, 32q/8kv d128, measured in step graphs): one block
-    // per query head below kSplitMinCtx (9.8 against 10.7 us at 256 tokens);
-    // kAttnSplits context splits per query head merged by each head's last
-    // block up to kSplitMaxCtx (10.9 / 11.7 / 13.5 / 28.7 us at 512 / 1024 /
-    // 2048 / 8191 tokens against 11.6 / 15.3 / 22.5 / 79.4 for one block per
-    // head and 16.4 / 17.0 / 18.8 / 38.0 for the slot kernel + merge); the
-    // slot kernel + merge beyond.  The step graphs hold one of them and are
+    // Decode attention of the full-attention layers at head_dim 128, by
+    // context (attention + o_proj GEMV per layer, 32q/8kv, measured in step
+    // graphs): one block per query head below kSplitMinCtx (9.9 against 10.8
+    // us at 256 tokens, 10.7 / 10.9 at 384); kAttnSplits context splits per
+    // query head merged by each head's last block from there on (10.9 / 11.0
+    // / 11.8 / 19.7 / 53.1 us at 512 / 1024 / 2048 / 8191 / 32767 tokens
+    // against 11.6 / 15.3 / 22.5 / 80.1 / 314.6 for one block per head and
+    // 16.4 / 17.1 / 18.8 / 38.0 / 109.1 for the slot kernel + merge, which
+    // serves other head sizes).  The step graphs hold one of them and are
     // captured again on a switch.
     enum class AttnMode { kSlot, kHead, kSplit };
-    static constexpr int kSplitMinCtx = 384, kSplitMaxCtx = 8192, kAttnSplits = 4;
+    static constexpr int kSplitMinCtx = 400, kAttnSplits = 8;
     static constexpr int kHeadAttnMaxCtx = 1024;  // without splits (XQ_ATTN_SPLITS=0): one block per head up to here
     AttnMode attn_mode_ = AttnMode::kSlot;
     std::string model_dir_, backend_request_, device_name_;

@@ -19,7 +19,7 @@ c_uint64, c_int32, c_uint8 = ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint8
 
 F32, F16 = 0, 1
 PRO_NONE, PRO_RMS, PRO_GATED_HEAD = 0, 1, 2
-ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 132, 4  # split attention workspace: partials, then counters
+ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 132, 8  # split attention workspace: partials, then counters
 EPI_STORE, EPI_ADD, EPI_SILU_PAIR = 0, 1, 2
 LAYOUT_TILED64, LAYOUT_GENERIC, LAYOUT_TILED64_F32META, LAYOUT_TILED64_SCALE16 = 0, 1, 2, 3
 
