@@ -211,21 +211,27 @@ def test_decode_before_prefill_and_context_capacity(small_dir):
     assert st == xb.XQ_ERR_NOT_READY and b"prefill" in m.error
 
 
-def test_attention_kernel_switch_matches_oracle(small_dir, monkeypatch):
+@pytest.mark.parametrize("n_prompt", [396, 1020])
+def test_attention_kernel_switch_matches_oracle(small_dir, monkeypatch, n_prompt):
     """Full-attention layers with head_dim 128 attend with one block per query
-    head up to 1024 context tokens and with the slot kernel + merge beyond;
-    decoding from a 1020-token prompt crosses the switch (contexts 1021 ..
-    1028).  Greedy ids against the oracle under the margin rule, hidden states
-    within tolerance at every step, and against a session that keeps the slot
-    kernel throughout (XQ_HEAD_ATTENTION=0): same ids, hidden states within
-    1e-5 abs + 1e-4 rel (the two kernels sum in different orders)."""
-    prompt = [int(t) for t in np.random.default_rng(1020).integers(0, 4096, 1020)]
+    head below 400 context tokens and with the context split over eight blocks
+    per query head from there on.  A 396-token prompt decodes across that
+    switch (contexts 397 .. 404); a 1020-token prompt decodes split past 1024
+    (where the per-head kernel alone would hand over to the slot kernel).
+    Greedy ids against the oracle under the margin rule, hidden states within
+    tolerance at every step, and against sessions that keep the slot kernel
+    throughout (XQ_HEAD_ATTENTION=0) or never split (XQ_ATTN_SPLITS=0): same
+    ids, hidden states within 1e-5 abs + 1e-4 rel (the kernels sum in
+    different orders)."""
+    prompt = [int(t) for t in np.random.default_rng(n_prompt).integers(0, 4096, n_prompt)]
     n_new = 8
     want, margins, hiddens = oracle_run(small_dir, prompt, n_new)
     runs = {}
-    for mode in ("switch", "slot"):
-        if mode == "slot":
-            monkeypatch.setenv("XQ_HEAD_ATTENTION", "0")
+    for mode, env in (("default", {}), ("slot", {"XQ_HEAD_ATTENTION": "0"}), ("unsplit", {"XQ_ATTN_SPLITS": "0"})):
+        monkeypatch.delenv("XQ_HEAD_ATTENTION", raising=False)
+        monkeypatch.delenv("XQ_ATTN_SPLITS", raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
         s = xb.Session(small_dir, xb.options())
         st, _ = s.prefill(prompt)
         assert st == 0
@@ -240,10 +246,11 @@ def test_attention_kernel_switch_matches_oracle(small_dir, monkeypatch):
         compare_tokens(toks, want, margins)
         runs[mode] = (toks, hs)
         s.close()
-    assert runs["switch"][0] == runs["slot"][0]
-    for i, (a, b) in enumerate(zip(runs["switch"][1], runs["slot"][1])):
-        err = np.abs(a.astype(np.float64) - b)
-        assert (err <= 1e-5 + 1e-4 * np.abs(b)).all(), (i, err.max())
+    for other in ("slot", "unsplit"):
+        assert runs["default"][0] == runs[other][0], other
+        for i, (a, b) in enumerate(zip(runs["default"][1], runs[other][1])):
+            err = np.abs(a.astype(np.float64) - b)
+            assert (err <= 1e-5 + 1e-4 * np.abs(b)).all(), (other, i, err.max())
 
 
 def test_kv_cache_growth_keeps_results(small_dir):
