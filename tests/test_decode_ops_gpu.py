@@ -288,10 +288,12 @@ def test_head_attention_rejects_other_head_sizes():
 # The per-head attention split over 1, 2 or 4 context ranges per query head
 # and merged by the last block of each head: the new token alone, fewer cached
 # positions than splits (empty ranges), the 512-token point, a range of exactly
-# one 1024-token pass and ranges past it, group sizes 1, 4 and 8, gated and not.
+# one 1024-token pass and ranges past it (up to 20000 cached positions), group
+# sizes 1, 4 and 8, gated and not.
 PART_CASES = [(32, 8, 128, 32, 0, 64, True), (32, 8, 128, 32, 2, 64, True), (32, 8, 128, 32, 511, 1024, True),
               (32, 8, 128, 64, 540, 1024, False), (16, 2, 128, 32, 1023, 2048, True),
-              (8, 8, 128, 128, 4095, 4160, True), (4, 1, 128, 32, 9000, 9216, False)]
+              (8, 8, 128, 128, 4095, 4160, True), (4, 1, 128, 32, 9000, 9216, False),
+              (4, 1, 128, 32, 20000, 20480, True)]
 
 
 @pytest.mark.parametrize("splits", [1, 2, 4, 8])
