@@ -203,7 +203,7 @@ PROJECTIONS = [
     ("down", 4096, 12288, "none", "add"),
     ("in_proj_linear", 12352, 4096, "rms", "store"),   # qkv 8192 | a 32 | b 32 | z 4096
     ("in_proj_full", 10240, 4096, "rms", "store"),     # q 8192 (gated) | k 1024 | v 1024
-    ("out_proj_linear", 4096, 4096, "gated", "add"),   # gated head RMSNorm prologue
+    ("out_proj_linear", 4096, 4096, "gated", "add"),   # gated head RMSNorm prologue (gate activated by the step)
     ("o_proj_full", 4096, 4096, "none", "add"),
     ("lm_head", 248320, 4096, "rms", "argmax"),
 ]
@@ -238,7 +238,7 @@ def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6
     ws = xb.DeviceBuffer(hip.xqhip_argmax_workspace_bytes(rows))
     idx, val = xb.DeviceBuffer(4), xb.DeviceBuffer(4)
     pro = {"none": None, "rms": xb.prologue(xb.PRO_RMS, nw, eps=1e-6),
-           "gated": xb.prologue(xb.PRO_GATED_HEAD, hw, z, head_dim=128, eps=1e-6)}[pro_kind]
+           "gated": xb.prologue(xb.PRO_GATED_HEAD_ACT, hw, z, head_dim=128, eps=1e-6)}[pro_kind]
     pro_ref = ctypes.byref(pro) if pro is not None else None
     epi_code = {"store": xb.EPI_STORE, "add": xb.EPI_ADD, "silu": xb.EPI_SILU_PAIR}.get(epi)
 

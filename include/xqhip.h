@@ -144,9 +144,12 @@ enum {
     XQHIP_PRO_NONE = 0,
     XQHIP_PRO_RMS = 1,        /* x * inv * weight[c], inv = 1/sqrt(mean(x^2) + eps)
                                  (rmsnormReference, ref_rmsnorm.cpp:8-17)          */
-    XQHIP_PRO_GATED_HEAD = 2  /* per head of head_dim values:
+    XQHIP_PRO_GATED_HEAD = 2, /* per head of head_dim values:
                                  x * inv_h * weight[c % head_dim] * silu(gate[c])
                                  (applyGatedHeadRms, custom_model.cpp:329-349)     */
+    XQHIP_PRO_GATED_HEAD_ACT = 3 /* GATED_HEAD with gate[c] already holding
+                                 silu(gate[c]) (as xqhip_linear_attn_step_act
+                                 leaves it): the GEMV entry points only        */
 };
 typedef struct xqhip_prologue {
     int32_t mode;
@@ -291,6 +294,14 @@ XQHIP_API int xqhip_linear_attn_step(const float* mixed, float* conv_state, cons
                                      const float* b, const float* a_log, const float* dt_bias, float* state, int lk_n,
                                      int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos, float* out,
                                      void* stream);
+/* The same step that also replaces `gate` (lv_n * lv_hd, the gated output
+ * norm's z) by silu(gate) in place, once per step, so that the output
+ * projection's XQHIP_PRO_GATED_HEAD_ACT prologue reads it instead of every one
+ * of its blocks evaluating the 4096 SiLUs (custom_model.cpp:329-349). */
+XQHIP_API int xqhip_linear_attn_step_act(const float* mixed, float* conv_state, const float* conv_w, const float* a,
+                                         const float* b, const float* a_log, const float* dt_bias, float* state,
+                                         int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos,
+                                         float* out, float* gate, void* stream);
 /* y = x * inv * w (rmsnormReference, ref_rmsnorm.cpp:8-17). */
 XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream);
 

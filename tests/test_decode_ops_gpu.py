@@ -509,6 +509,68 @@ def test_fused_linear_attn_step_two_positions(shape):
     assert np.array_equal(got_hist[hist:], st_o)  # the second step wrote copy 1 again; shifts are exact
 
 
+@pytest.mark.parametrize("shape", [(16, 32, 128, 128, 4), (3, 6, 64, 32, 3), (2, 2, 256, 40, 4)])
+def test_linear_step_act_matches_step_and_activates_gate(shape):
+    """xqhip_linear_attn_step_act: bit-identical outputs, state and conv history
+    to xqhip_linear_attn_step, and the gate vector replaced by silu(gate); the
+    gated-norm GEMV on that activated gate (XQHIP_PRO_GATED_HEAD_ACT) gives the
+    XQHIP_PRO_GATED_HEAD result on the raw gate bit for bit, and both match the
+    oracle's applyGatedHeadRms + GEMV (custom_model.cpp:329-349)."""
+    lk_n, lv_n, lk_hd, lv_hd, ks = shape
+    rng = np.random.default_rng(41)
+    mixed, cstate, cw = linear_inputs(lk_n, lv_n, lk_hd, lv_hd, ks, seed=43)
+    hist = cstate.size
+    a = rng.normal(0, 1, lv_n).astype(np.float32)
+    b = rng.normal(0, 1, lv_n).astype(np.float32)
+    a_log = rng.normal(-1, 0.5, lv_n).astype(np.float32)
+    dt = rng.normal(0, 0.5, lv_n).astype(np.float32)
+    S0 = rng.normal(0, 0.1, lv_n * lk_hd * lv_hd).astype(np.float32)
+    z = rng.normal(0, 2, lv_n * lv_hd).astype(np.float32)
+    two = np.concatenate([cstate, np.full(hist, 5.0, np.float32)])
+    md, wd, ad, bd, ald, dtd = dev(mixed), dev(cw), dev(a), dev(b), dev(a_log), dev(dt)
+    pd = dev(np.array([8], np.int32))
+    res = []
+    for act in (False, True):
+        sd, Sd, zd = dev(two), dev(S0), dev(z)
+        od = xb.DeviceBuffer(lv_n * lv_hd * 4)
+        args = (md.ptr, sd.ptr, wd.ptr, ad.ptr, bd.ptr, ald.ptr, dtd.ptr, Sd.ptr, lk_n, lk_hd, lv_n, lv_hd, ks, pd.ptr,
+                od.ptr)
+        if act:
+            xb.ck(xb.hip().xqhip_linear_attn_step_act(*args, zd.ptr, None))
+        else:
+            xb.ck(xb.hip().xqhip_linear_attn_step(*args, None))
+        res.append((od.download(np.float32, lv_n * lv_hd), Sd.download(np.float32, S0.size),
+                    sd.download(np.float32, 2 * hist), zd))
+    (o0, s0, h0, z_raw), (o1, s1, h1, z_act) = res
+    assert np.array_equal(o0, o1) and np.array_equal(s0, s1) and np.array_equal(h0, h1)
+    assert np.array_equal(z_raw.download(np.float32, z.size), z)  # the plain step leaves the gate alone
+    zz = z.astype(np.float64)
+    close(z_act.download(np.float32, z.size), zz / (1 + np.exp(-zz)), "activated gate", atol=1e-6, rtol=1e-6)
+    # the output projection of the step output, gate raw (silu in the prologue) or activated
+    if lv_hd % 8 or (lv_hd // 8) & (lv_hd // 8 - 1):
+        return  # the tiled GEMV's gated prologue needs head_dim / 8 a power of two
+    hidden = 256
+    q = w4_matrix(hidden, lv_n * lv_hd, 17)
+    w4 = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols)
+    nw = dev(rng.normal(1, 0.1, lv_hd).astype(np.float32))
+    xo = dev(o0)
+    ys = []
+    for mode, gate in ((xb.PRO_GATED_HEAD, z_raw), (xb.PRO_GATED_HEAD_ACT, z_act)):
+        y = xb.DeviceBuffer(hidden * 4)
+        pro = xb.prologue(mode, nw, gate, head_dim=lv_hd, eps=1e-6)
+        xb.ck(xb.hip().xqhip_gemv_w4a16(w4.ref, xo.ptr, xb.F32, ctypes.byref(pro), y.ptr, xb.F32, xb.EPI_STORE, None))
+        ys.append(y.download(np.float32, hidden))
+    assert np.array_equal(ys[0], ys[1])
+    normed = np.empty_like(o0)
+    O().orc_gated_head_rms(ob.p(o0), ob.p(nw.download(np.float32, lv_hd)), ob.p(z), lv_n, lv_hd, 1e-6, ob.p(normed))
+    close(ys[1], ob.gemv(q, normed), "gated-norm GEMV on the activated gate")
+    # the prefill GEMM prepares its own gate: the activated form is refused there
+    ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(4, lv_n * lv_hd, hidden))
+    pro = xb.prologue(xb.PRO_GATED_HEAD_ACT, nw, z_act, head_dim=lv_hd, eps=1e-6)
+    assert xb.hip().xqhip_gemm_w4a16(w4.ref, xo.ptr, 1, lv_n * lv_hd, ctypes.byref(pro), lv_n * lv_hd, y.ptr,
+                                     hidden, xb.EPI_STORE, ws.ptr, None) == -1
+
+
 def test_rmsnorm_kernel():
     rng = np.random.default_rng(3)
     x = rng.normal(0, 5, 4096).astype(np.float32)

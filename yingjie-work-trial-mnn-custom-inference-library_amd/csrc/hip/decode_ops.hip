@@ -1363,6 +1363,12 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
     }
     const bool has_v = threadIdx.x < kDeltaCols && j0 + static_cast<int>(threadIdx.x) < dv;
     load_taps(has_v ? 2 * p.lk_n * dk + vh * dv + j0 + static_cast<int>(threadIdx.x) : -1, tv);
+    // the gated norm's gate of this block's columns, activated here once instead
+    // of in every block of the output projection (read now, written at the end)
+    const bool has_z = p.z_act != nullptr && has_v;
+    const float zraw = buf_load_f32(buf_rsrc(p.z_act, p.z_act ? static_cast<uint32_t>(p.lv_n * dv) * 4u : 0u),
+                                    has_z ? static_cast<uint32_t>(vh * dv + j0 + static_cast<int>(threadIdx.x)) * 4u
+                                          : kBufOOB);
     const __amdgpu_buffer_rsrc_t r_state = buf_rsrc(S, static_cast<uint32_t>(dk * dv) * 4u);
     float sreg[kDeltaMaxKPerThread];
 #pragma unroll
@@ -1445,6 +1451,7 @@ __global__ void __launch_bounds__(256) linear_step_kernel(LinearStepLaunch p) {
         }
     }
     if (has_v) write_history(st_out, 2 * p.lk_n * dk + vh * dv + j0 + threadIdx.x, tv);
+    if (has_z) p.z_act[vh * dv + j0 + threadIdx.x] = silu_dev(zraw);
 }
 
 bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {

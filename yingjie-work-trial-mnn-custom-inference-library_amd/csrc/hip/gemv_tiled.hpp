@@ -98,7 +98,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
     // All activation and prologue loads are unconditional range-checked buffer
     // loads (an unused vector has range 0 and reads as zeros without a memory
     // access): straight-line code, so no wait is forced before the barrier.
-    const bool gated = pro.mode == PRO_GATED;
+    const bool gated = pro.mode == PRO_GATED || pro.mode == PRO_GATED_ACT;
     const __amdgpu_buffer_rsrc_t xr = vec_rsrc(x, static_cast<uint32_t>(cols) * (x_f16 ? 2u : 4u));
     const __amdgpu_buffer_rsrc_t wr =
         vec_rsrc(pro.w, pro.mode == PRO_RMS ? cols * 4u : (gated ? static_cast<uint32_t>(pro.head_dim) * 4u : 0u));
@@ -163,7 +163,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * wl[i];
         }
-    } else if (pro.mode == PRO_GATED) {
+    } else if (gated) {
         // head_dim % 8 == 0 and head_dim / 8 a power of two <= 64: the items of a
         // head are head_dim/8 consecutive lanes of one wave
         const int per_head = pro.head_dim >> 3;
@@ -192,8 +192,13 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
                 as_floats8(load16(wr, woff), load16(wr, woff + 16u), wl);
                 as_floats8(load16(zr, item * 32u), load16(zr, item * 32u + 16u), zl);
             }
+            if (pro.mode == PRO_GATED_ACT) {  // the gate holds silu(gate) already (uniform branch)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i] * silu_dev(zl[i]);
+                for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i] * zl[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * wl[i] * silu_dev(zl[i]);
+            }
         }
     }
     uint32_t* xw = reinterpret_cast<uint32_t*>(xs);
@@ -242,7 +247,7 @@ __device__ __forceinline__ float rms_factor(const float* red, int cols, float ep
 
 inline bool stage_supported(int cols, const Prologue& pro) {
     if (cols % 64 != 0 || cols > kMaxStageCols) return false;
-    if (pro.mode == PRO_GATED) {
+    if (pro.mode == PRO_GATED || pro.mode == PRO_GATED_ACT) {
         const int per = pro.head_dim / 8;
         return pro.head_dim % 8 == 0 && per >= 1 && per <= 64 && (per & (per - 1)) == 0;
     }

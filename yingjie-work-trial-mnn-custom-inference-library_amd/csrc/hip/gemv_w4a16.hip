@@ -50,7 +50,8 @@ __device__ __forceinline__ float load_act(const void* x, int x_f16, int i) {
 // Normalisation prologues fused into the GEMV (computed by every block from x):
 //   PRO_RMS   x * inv * w[c], inv = 1/sqrt(mean(x^2)+eps)        (ref_rmsnorm.cpp:8-17)
 //   PRO_GATED per head h of head_dim values: x * inv_h * w[c % head_dim] * silu(z[c])
-//             (applyGatedHeadRms, custom_model.cpp:329-349)
+//             (applyGatedHeadRms, custom_model.cpp:329-349); PRO_GATED_ACT the same
+//             with z holding silu(z) already
 // inv_lds receives inv (PRO_RMS) or inv_h for every head (PRO_GATED).
 __device__ void prologue_factors(const void* x, int x_f16, int n, const Prologue& pro, float* inv_lds, float* red) {
     if (pro.mode == PRO_RMS) {
@@ -61,7 +62,7 @@ __device__ void prologue_factors(const void* x, int x_f16, int n, const Prologue
         }
         ss = block_sum(ss, red);
         if (threadIdx.x == 0) inv_lds[0] = 1.0f / sqrtf(ss / static_cast<float>(n) + pro.eps);
-    } else if (pro.mode == PRO_GATED) {
+    } else if (pro.mode == PRO_GATED || pro.mode == PRO_GATED_ACT) {
         const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = blockDim.x / kWave;
         const int heads = n / pro.head_dim;
         for (int h = wid; h < heads; h += nw) {
@@ -79,9 +80,10 @@ __device__ void prologue_factors(const void* x, int x_f16, int n, const Prologue
 
 __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& pro, const float* inv_lds) {
     if (pro.mode == PRO_RMS) return v * inv_lds[0] * pro.w[c];
-    if (pro.mode == PRO_GATED) {
+    if (pro.mode == PRO_GATED || pro.mode == PRO_GATED_ACT) {
         const int h = c / pro.head_dim;
-        return v * inv_lds[h] * pro.w[c - h * pro.head_dim] * silu_dev(pro.z[c]);
+        const float g = pro.mode == PRO_GATED_ACT ? pro.z[c] : silu_dev(pro.z[c]);
+        return v * inv_lds[h] * pro.w[c - h * pro.head_dim] * g;
     }
     return v;
 }

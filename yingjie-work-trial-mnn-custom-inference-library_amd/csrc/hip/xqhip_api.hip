@@ -439,11 +439,16 @@ static xqhip::Prologue make_prologue(const xqhip_prologue* pro) {
     return p;
 }
 
-static int validate_prologue(const xqhip_prologue* pro, int cols, const char* who) {
+static_assert(XQHIP_PRO_GATED_HEAD_ACT == xqhip::PRO_GATED_ACT && XQHIP_PRO_GATED_HEAD == xqhip::PRO_GATED,
+              "prologue modes");
+
+// gated_act: whether the entry point takes XQHIP_PRO_GATED_HEAD_ACT (the GEMVs; the
+// prefill GEMM prepares its activations with the reference's own silu)
+static int validate_prologue(const xqhip_prologue* pro, int cols, const char* who, bool gated_act = true) {
     if (!pro || pro->mode == XQHIP_PRO_NONE) return XQHIP_OK;
     if (pro->mode == XQHIP_PRO_RMS && pro->weight) return XQHIP_OK;
-    if (pro->mode == XQHIP_PRO_GATED_HEAD && pro->weight && pro->gate && pro->head_dim > 0 &&
-        cols % pro->head_dim == 0 && cols / pro->head_dim <= xqhip::kMaxNormHeads)
+    if ((pro->mode == XQHIP_PRO_GATED_HEAD || (gated_act && pro->mode == XQHIP_PRO_GATED_HEAD_ACT)) && pro->weight &&
+        pro->gate && pro->head_dim > 0 && cols % pro->head_dim == 0 && cols / pro->head_dim <= xqhip::kMaxNormHeads)
         return XQHIP_OK;
     return fail(XQHIP_EINVAL, "%s: bad prologue (mode %d)", who, pro->mode);
 }
@@ -455,7 +460,7 @@ static int validate_alignment(const xqhip_w4* w, const void* x, const xqhip_prol
     if (!a16(x)) return fail(XQHIP_EINVAL, "%s: x must be 16-byte aligned", who);
     if (pro && pro->mode != XQHIP_PRO_NONE && !a16(pro->weight))
         return fail(XQHIP_EINVAL, "%s: prologue weight must be 16-byte aligned", who);
-    if (pro && pro->mode == XQHIP_PRO_GATED_HEAD && !a16(pro->gate))
+    if (pro && (pro->mode == XQHIP_PRO_GATED_HEAD || pro->mode == XQHIP_PRO_GATED_HEAD_ACT) && !a16(pro->gate))
         return fail(XQHIP_EINVAL, "%s: prologue gate must be 16-byte aligned", who);
     return XQHIP_OK;
 }
@@ -745,7 +750,22 @@ int xqhip_linear_attn_step(const float* mixed, float* conv_state, const float* c
         return fail(XQHIP_EINVAL, "xqhip_linear_attn_step: unsupported shape lk=%dx%d lv=%dx%d k=%d", lk_n, lk_hd, lv_n,
                     lv_hd, ksize);
     xqhip::LinearStepLaunch p{mixed, conv_state, conv_w, a, b, a_log, dt_bias, state,
-                              lk_n, lk_hd, lv_n, lv_hd, ksize, pos, out};
+                              lk_n, lk_hd, lv_n, lv_hd, ksize, pos, out, nullptr};
+    return check(xqhip::launch_linear_step(p, as_stream(stream)), "linear step launch");
+}
+
+int xqhip_linear_attn_step_act(const float* mixed, float* conv_state, const float* conv_w, const float* a,
+                               const float* b, const float* a_log, const float* dt_bias, float* state, int lk_n,
+                               int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos, float* out,
+                               float* gate, void* stream) {
+    if (!gate) return fail(XQHIP_EINVAL, "xqhip_linear_attn_step_act: null gate");
+    if (!mixed || !conv_state || !conv_w || !a || !b || !a_log || !dt_bias || !state || !pos || !out)
+        return fail(XQHIP_EINVAL, "xqhip_linear_attn_step_act: null argument");
+    if (!xqhip::linear_step_supported(lk_n, lk_hd, lv_n, lv_hd, ksize))
+        return fail(XQHIP_EINVAL, "xqhip_linear_attn_step_act: unsupported shape lk=%dx%d lv=%dx%d k=%d", lk_n, lk_hd,
+                    lv_n, lv_hd, ksize);
+    xqhip::LinearStepLaunch p{mixed, conv_state, conv_w, a, b, a_log, dt_bias, state,
+                              lk_n, lk_hd, lv_n, lv_hd, ksize, pos, out, gate};
     return check(xqhip::launch_linear_step(p, as_stream(stream)), "linear step launch");
 }
 
@@ -759,7 +779,7 @@ int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xq
                      float* y, int ldy, int epilogue, void* workspace, void* stream) {
     if (int rc = validate_w4(w, "xqhip_gemm_w4a16")) return rc;
     if (w->bits != 4) return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: 4-bit matrices only (got %d bits)", w->bits);
-    if (int rc = validate_prologue(pro, w->cols, "xqhip_gemm_w4a16")) return rc;
+    if (int rc = validate_prologue(pro, w->cols, "xqhip_gemm_w4a16", false)) return rc;
     if (!x || !y || !workspace || m <= 0 || ldx < w->cols)
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: bad vectors (m=%d ldx=%d)", m, ldx);
     if (epilogue < XQHIP_EPI_STORE || epilogue > XQHIP_EPI_SILU_PAIR)

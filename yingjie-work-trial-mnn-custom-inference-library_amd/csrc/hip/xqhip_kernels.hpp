@@ -6,7 +6,8 @@
 
 namespace xqhip {
 
-enum { PRO_NONE = 0, PRO_RMS = 1, PRO_GATED = 2 };
+// PRO_GATED_ACT: PRO_GATED whose gate vector already holds silu(gate)
+enum { PRO_NONE = 0, PRO_RMS = 1, PRO_GATED = 2, PRO_GATED_ACT = 3 };
 constexpr int kMaxNormHeads = 256;
 // Split decode attention partials (attn_decode_part_kernel): per split and
 // query head, the running max at 0, the exp sum at 1 and the head_dim (128)
@@ -155,7 +156,8 @@ struct LinearStepLaunch {
     float* state;  // [lv_n][lk_hd][lv_hd]
     int lk_n, lk_hd, lv_n, lv_hd, ksize;
     const int32_t* pos;
-    float* out;  // lv_n * lv_hd
+    float* out;    // lv_n * lv_hd
+    float* z_act;  // optional: the gated norm's gate (lv_n * lv_hd), replaced by silu(gate) in place
 };
 bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
 hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s);

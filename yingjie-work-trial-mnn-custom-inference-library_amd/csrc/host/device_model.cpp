@@ -479,14 +479,15 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
             op_end(timed);
             const float* a = proj_ + conv_dim_;
             const float* b = a + lv_n_;
-            const float* z = b + lv_n_;
+            float* z = proj_ + conv_dim_ + 2 * lv_n_;
+            // the step also replaces z by silu(z) once, for the output norm's prologue
             op_begin(timed, "linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
                      {"linear_attention_conv1d_custom"}, 2);
-            XQ_CALL(xqhip_linear_attn_step(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias, L.rec_state,
-                                           lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_, stream_),
+            XQ_CALL(xqhip_linear_attn_step_act(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias, L.rec_state,
+                                               lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_, z, stream_),
                     "linear-attention step");
             op_end(timed);
-            xqhip_prologue gated{XQHIP_PRO_GATED_HEAD, lv_hd_, L.lin_norm, z, eps_};
+            xqhip_prologue gated{XQHIP_PRO_GATED_HEAD_ACT, lv_hd_, L.lin_norm, z, eps_};
             op_begin(timed, "linear_attn_out_proj_w4a16(fused:linear_attention_gated_rmsnorm,residual_add_attention)");
             XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, &gated, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),
                     "out projection");

@@ -18,7 +18,7 @@ c_int, c_float, c_size_t, c_void_p, c_char_p = ctypes.c_int, ctypes.c_float, cty
 c_uint64, c_int32, c_uint8 = ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint8
 
 F32, F16 = 0, 1
-PRO_NONE, PRO_RMS, PRO_GATED_HEAD = 0, 1, 2
+PRO_NONE, PRO_RMS, PRO_GATED_HEAD, PRO_GATED_HEAD_ACT = 0, 1, 2, 3
 ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 132, 8  # split attention workspace: partials, then counters
 EPI_STORE, EPI_ADD, EPI_SILU_PAIR = 0, 1, 2
 LAYOUT_TILED64, LAYOUT_GENERIC, LAYOUT_TILED64_F32META, LAYOUT_TILED64_SCALE16 = 0, 1, 2, 3
@@ -92,6 +92,9 @@ _HIP_SIGS = {
                                   c_int, c_void_p, c_void_p]),
     "xqhip_linear_attn_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "xqhip_linear_attn_step_act": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                                           c_void_p]),
     "xqhip_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "xqhip_gemm_w4a16": (c_int, [_P(W4), c_void_p, c_int, c_int, _P(Prologue), c_int, c_void_p, c_int, c_int,
                                  c_void_p, c_void_p]),
