@@ -98,6 +98,10 @@ XQHIP_API int xqhip_memcpy_d2h_async(void* dst, const void* src, size_t bytes, v
 /* Pinned host memory (hipHostMalloc). */
 XQHIP_API int xqhip_host_alloc(void** ptr, size_t bytes);
 XQHIP_API int xqhip_host_free(void* ptr);
+/* Pinned host memory that kernels may store to directly (hipHostMalloc,
+ * mapped and coherent): a kernel's system-scope store reaches the host
+ * without a copy on the stream. */
+XQHIP_API int xqhip_host_alloc_coherent(void** ptr, size_t bytes);
 /* Byte fill done by a kernel (safe inside captured graphs). */
 XQHIP_API int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream);
 /* Device-to-device copy as one plain kernel dispatch (graph-capturable; also
@@ -112,6 +116,9 @@ XQHIP_API int xqhip_event_record(void* ev, void* stream);
 /* Blocks the host until the work recorded before `ev` has finished. */
 XQHIP_API int xqhip_event_synchronize(void* ev);
 XQHIP_API int xqhip_event_elapsed_ms(void* start, void* stop, float* ms);
+/* 1 once the work recorded before `ev` has finished, 0 while it is pending,
+ * a negative XQHIP_E* code on a device error.  Does not block. */
+XQHIP_API int xqhip_event_query(void* ev);
 
 /* ---- W4A16 weights ----------------------------------------------------- */
 /* Repack a reference-format matrix (packed[rows][ceil(cols/2)], fp32
@@ -178,6 +185,19 @@ XQHIP_API size_t xqhip_argmax_workspace_bytes(int rows);
  * initialisation needed.  out_index / out_value: device. */
 XQHIP_API int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
                                       void* workspace, int32_t* out_index, float* out_value, void* stream);
+
+/* xqhip_gemv_w4a16_argmax that also advances a device position and hands the
+ * result to the host without a copy: no counterpart in the reference, whose
+ * decodeOne samples on the calling thread (custom_model.cpp:1281-1356).  After
+ * the argmax, the finishing kernel adds 1 to *position (device int32) and
+ * stores ((uint64_t)(uint32_t)new_position << 32) | (uint32_t)index to
+ * *host_slot (8-byte aligned memory from xqhip_host_alloc_coherent) in one
+ * system-scope store.  A host thread polls the slot for the position it
+ * expects, so sampling, the next token's position and its forward pass can be
+ * one captured graph with no copies between them. */
+XQHIP_API int xqhip_gemv_w4a16_argmax_publish(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
+                                              void* workspace, int32_t* out_index, float* out_value,
+                                              int32_t* position, uint64_t* host_slot, void* stream);
 
 /* xqhip_gemv_w4a16_argmax without a workspace argument and without any
  * allocation: no counterpart in the reference.  For callers that cannot

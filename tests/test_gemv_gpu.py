@@ -194,6 +194,44 @@ def test_argmax_fused_final_norm():
         assert got_idx == want_idx
 
 
+@pytest.mark.parametrize("rows,cols,seed,start", [(248320, 4096, 91, 511), (4099, 1024, 92, -1)])
+def test_argmax_publish_advances_position_and_publishes(rows, cols, seed, start):
+    """xqhip_gemv_w4a16_argmax_publish: the same index and value as
+    xqhip_gemv_w4a16_argmax, *position + 1 on the device, and
+    (new position << 32) | index in the coherent host slot, on three calls in
+    a row (the host clears the slot before each)."""
+    q = w4_matrix(rows, cols, seed)
+    x = np.random.default_rng(seed + 1).normal(0, 1, cols).astype(np.float32)
+    want = run_argmax(q, x)[0]
+    w = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols, q.group, q.affine)
+    xd = xb.DeviceBuffer.from_array(x)
+    ws = xb.DeviceBuffer(xb.hip().xqhip_argmax_workspace_bytes(q.rows))
+    idx, val = xb.DeviceBuffer(4), xb.DeviceBuffer(4)
+    posd = xb.DeviceBuffer.from_array(np.array([start], np.int32))
+    slot_p = ctypes.c_void_p()
+    xb.ck(xb.hip().xqhip_host_alloc_coherent(ctypes.byref(slot_p), 8))
+    try:
+        slot = ctypes.cast(slot_p, ctypes.POINTER(ctypes.c_uint64))
+        for call in range(3):
+            slot[0] = 0xFFFFFFFFFFFFFFFF
+            xb.ck(xb.hip().xqhip_gemv_w4a16_argmax_publish(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr, val.ptr,
+                                                           posd.ptr, slot_p, None))
+            xb.ck(xb.hip().xqhip_device_synchronize())
+            pos = start + call + 1
+            assert int(posd.download(np.int32, 1)[0]) == pos
+            got = (int(idx.download(np.int32, 1)[0]), float(val.download(np.float32, 1)[0]))
+            assert got == want
+            assert slot[0] == ((pos & 0xFFFFFFFF) << 32) | want[0]
+        rc = xb.hip().xqhip_gemv_w4a16_argmax_publish(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr, val.ptr, None,
+                                                      slot_p, None)
+        assert rc == -1  # XQHIP_EINVAL
+        rc = xb.hip().xqhip_gemv_w4a16_argmax_publish(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr, val.ptr,
+                                                      posd.ptr, ctypes.c_void_p(slot_p.value + 4), None)
+        assert rc == -1 and b"8-byte aligned" in xb.hip().xqhip_last_error()
+    finally:
+        xb.ck(xb.hip().xqhip_host_free(slot_p))
+
+
 def test_gemv_gated_head_prologue():
     """out_proj input of the linear-attention layer: per-head gated RMSNorm fused
     into the GEMV prologue (applyGatedHeadRms, custom_model.cpp:329-349)."""

@@ -88,9 +88,13 @@ __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& 
     return v;
 }
 
+// position != nullptr: also advances *position by one and publishes
+// (new position << 32 | index) to host_slot (coherent pinned host memory) in
+// one system-scope store, which a host thread polls for.
 __global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __restrict__ partial, int n,
                                                             int32_t* __restrict__ out_idx,
-                                                            float* __restrict__ out_val) {
+                                                            float* __restrict__ out_val, int32_t* position,
+                                                            uint64_t* host_slot) {
     __shared__ uint64_t keys[4];
     uint64_t best = 0;
     for (int i = threadIdx.x; i < n; i += 256) best = u64_max(best, partial[i]);
@@ -100,13 +104,21 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __re
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint64_t b = u64_max(u64_max(keys[0], keys[1]), u64_max(keys[2], keys[3]));
-        *out_idx = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(b));
+        const uint32_t idx = 0xffffffffu - static_cast<uint32_t>(b);
+        *out_idx = static_cast<int32_t>(idx);
         *out_val = float_from_order_key(static_cast<uint32_t>(b >> 32));
+        if (position) {
+            const int32_t np = *position + 1;
+            *position = np;
+            __hip_atomic_store(host_slot, (static_cast<uint64_t>(static_cast<uint32_t>(np)) << 32) | idx,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
 hipError_t launch_argmax_finish(const GemvLaunch& p, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, s, p.partial, blocks, p.out_idx, p.out_val);
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, s, p.partial, blocks, p.out_idx, p.out_val,
+                       p.position, p.host_slot);
     return hipGetLastError();
 }
 

@@ -170,6 +170,12 @@ int xqhip_host_alloc(void** ptr, size_t bytes) {
     return check(hipHostMalloc(ptr, bytes == 0 ? 1 : bytes, hipHostMallocDefault), "hipHostMalloc");
 }
 
+int xqhip_host_alloc_coherent(void** ptr, size_t bytes) {
+    if (!ptr) return fail(XQHIP_EINVAL, "xqhip_host_alloc_coherent: null out pointer");
+    return check(hipHostMalloc(ptr, bytes == 0 ? 1 : bytes, hipHostMallocMapped | hipHostMallocCoherent),
+                 "hipHostMalloc(coherent)");
+}
+
 int xqhip_host_free(void* ptr) { return ptr ? check(hipHostFree(ptr), "hipHostFree") : XQHIP_OK; }
 
 int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream) {
@@ -208,6 +214,13 @@ int xqhip_event_record(void* ev, void* stream) {
 }
 int xqhip_event_synchronize(void* ev) {
     return check(hipEventSynchronize(static_cast<hipEvent_t>(ev)), "hipEventSynchronize");
+}
+
+int xqhip_event_query(void* ev) {
+    const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(ev));
+    if (e == hipSuccess) return 1;
+    if (e == hipErrorNotReady) return 0;
+    return check(e, "hipEventQuery");
 }
 
 int xqhip_event_elapsed_ms(void* start, void* stop, float* ms) {
@@ -521,6 +534,28 @@ int xqhip_gemv_w4a16_argmax(const xqhip_w4* w, const void* x, int x_type, const 
     p.out_val = out_value;
     p.max_blocks = gemv_block_cap() > 0 ? std::min(kArgmaxMaxBlocks, gemv_block_cap()) : 0;
     return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax launch");
+}
+
+int xqhip_gemv_w4a16_argmax_publish(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
+                                    void* workspace, int32_t* out_index, float* out_value, int32_t* position,
+                                    uint64_t* host_slot, void* stream) {
+    if (!position || !host_slot) return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax_publish: null argument");
+    if (reinterpret_cast<uintptr_t>(host_slot) % alignof(uint64_t) != 0)
+        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax_publish: host_slot is not 8-byte aligned");
+    if (int rc = validate_w4(w, "xqhip_gemv_w4a16_argmax_publish")) return rc;
+    if (int rc = validate_prologue(pro, w->cols, "xqhip_gemv_w4a16_argmax_publish")) return rc;
+    if (!x || !workspace || !out_index || !out_value)
+        return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax_publish: null argument");
+    if (int rc = validate_alignment(w, x, pro, "xqhip_gemv_w4a16_argmax_publish")) return rc;
+    xqhip::GemvLaunch p = base_launch(w, x, x_type, pro);
+    p.epi = 3;
+    p.partial = static_cast<uint64_t*>(workspace);
+    p.out_idx = out_index;
+    p.out_val = out_value;
+    p.position = position;
+    p.host_slot = host_slot;
+    p.max_blocks = gemv_block_cap() > 0 ? std::min(kArgmaxMaxBlocks, gemv_block_cap()) : 0;
+    return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax_publish launch");
 }
 
 int xqhip_gemv_w4a16_argmax_static(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,

@@ -39,6 +39,8 @@ struct GemvLaunch {
     uint64_t* partial;  // argmax: one key per block
     int32_t* out_idx;
     float* out_val;
+    int32_t* position;    // argmax: advanced by one after the argmax (nullptr: untouched)
+    uint64_t* host_slot;  // argmax with position: receives (new position << 32) | index
     int max_blocks;  // <= 0: as many blocks as are resident on the device at once
 };
 

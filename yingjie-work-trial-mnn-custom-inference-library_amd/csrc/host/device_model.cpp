@@ -34,9 +34,7 @@ double elapsed_ms(void* a, void* b) {
 DeviceModel::~DeviceModel() {
     if (stream_) xqhip_stream_synchronize(stream_);
     if (g_prefill_) xqhip_graph_destroy(g_prefill_);
-    if (g_sample_) xqhip_graph_destroy(g_sample_);
-    if (g_forward_) xqhip_graph_destroy(g_forward_);
-    if (ev_token_) xqhip_event_destroy(ev_token_);
+    if (g_step_) xqhip_graph_destroy(g_step_);
     for (auto& pair : step_ev_)
         for (void* e : pair)
             if (e) xqhip_event_destroy(e);
@@ -45,6 +43,7 @@ DeviceModel::~DeviceModel() {
     for (void* e : event_pool_) xqhip_event_destroy(e);
     if (h_ctrl_) xqhip_host_free(h_ctrl_);
     if (h_tok_) xqhip_host_free(h_tok_);
+    if (h_slot_) xqhip_host_free(h_slot_);
     if (stream_) xqhip_stream_destroy(stream_);
 }
 
@@ -281,7 +280,9 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     void* pinned = nullptr;
     if (xqhip_host_alloc(&pinned, 4 * sizeof(int32_t)) != 0) return fail_hip(error, "pinned memory");
     h_tok_ = static_cast<int32_t*>(pinned);
-    if (xqhip_event_create(&ev_token_) != 0) return fail_hip(error, "event");
+    if (xqhip_host_alloc_coherent(&pinned, sizeof(uint64_t)) != 0) return fail_hip(error, "coherent host memory");
+    h_slot_ = static_cast<uint64_t*>(pinned);
+    *h_slot_ = ~0ull;
     for (auto& pair : step_ev_)
         for (void*& e : pair)
             if (xqhip_event_create(&e) != 0) return fail_hip(error, "event");
@@ -332,7 +333,7 @@ bool DeviceModel::ensure_capacity(size_t positions, std::string* error) {
     }
     max_ctx_ = new_ctx;
     if (!build_rope_table(error)) return false;
-    for (void** g : {&g_prefill_, &g_sample_, &g_forward_}) {
+    for (void** g : {&g_prefill_, &g_step_}) {
         if (*g) xqhip_graph_destroy(*g);
         *g = nullptr;
     }
@@ -368,7 +369,7 @@ bool DeviceModel::select_attention(size_t ctx, KernelTrace* trace, std::string* 
     if (want == attn_mode_) return true;
     if (!sync(trace, error)) return false;
     attn_mode_ = want;
-    for (void** g : {&g_prefill_, &g_forward_}) {
+    for (void** g : {&g_prefill_, &g_step_}) {
         if (*g) xqhip_graph_destroy(*g);
         *g = nullptr;
     }
@@ -384,6 +385,7 @@ void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past th
         xqhip_fill_u8(L.rec_state, 0, sizeof(float) * lv_n_ * lk_hd_ * lv_hd_, stream_);
     }
     detail_prefill_ = detail_decode_ = true;
+    dev_pos_ = kPosUnknown;
 }
 
 bool DeviceModel::op_begin(bool timed, const std::string& name, std::vector<std::string> extra, int split) {
@@ -431,7 +433,10 @@ bool DeviceModel::enqueue_embed(const int32_t* token_dev, bool timed, std::strin
 bool DeviceModel::enqueue_lm_head(bool timed, std::string* error) {
     xqhip_prologue fin{XQHIP_PRO_RMS, 0, final_norm_, nullptr, eps_};
     op_begin(timed, "lm_head_custom(fused:rmsnorm_final,argmax)", {"sampling_greedy_custom"});
-    XQ_CALL(xqhip_gemv_w4a16_argmax(&lm_head_, resid_, XQHIP_F32, &fin, argmax_ws_, d_ctrl_ + 2, best_val_, stream_),
+    // the sampled token is the input of the next position: the kernel advances
+    // d_ctrl_[0] and publishes (position, token) to h_slot_
+    XQ_CALL(xqhip_gemv_w4a16_argmax_publish(&lm_head_, resid_, XQHIP_F32, &fin, argmax_ws_, d_ctrl_ + 2, best_val_,
+                                            d_ctrl_, h_slot_, stream_),
             "lm_head argmax");
     op_end(timed);
     return true;
@@ -513,7 +518,7 @@ static bool graphs_enabled() {
 
 bool DeviceModel::ensure_graphs(std::string* error) {
     if (!graphs_enabled()) return true;  // eager launches of the same kernels
-    if (g_prefill_ && g_sample_ && g_forward_) return true;
+    if (g_prefill_ && g_step_) return true;
     auto capture = [&](void** out, auto&& enqueue) {
         XQ_CALL(xqhip_graph_begin(stream_), "graph capture");
         const bool ok = enqueue();
@@ -523,8 +528,10 @@ bool DeviceModel::ensure_graphs(std::string* error) {
         return true;
     };
     return capture(&g_prefill_, [&] { return enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error); }) &&
-           capture(&g_sample_, [&] { return enqueue_lm_head(false, error); }) &&
-           capture(&g_forward_, [&] { return enqueue_embed(d_ctrl_ + 2, false, error) && enqueue_layers(false, error); });
+           capture(&g_step_, [&] {
+               return enqueue_lm_head(false, error) && enqueue_embed(d_ctrl_ + 2, false, error) &&
+                      enqueue_layers(false, error);
+           });
 }
 
 // Batched prefill needs every matrix in the TILED64 layout (group 64) and the
@@ -570,6 +577,7 @@ bool DeviceModel::alloc_prefill_buffers(std::string* error) {
 bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, int n, int pos0, bool timed,
                                 std::string* error) {
     XQ_CALL(xqhip_memcpy_h2d_async(tok_dev_, h_tokens, sizeof(int32_t) * n, stream_), "prompt upload");
+    dev_pos_ = kPosUnknown;
     XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_pos, sizeof(int32_t), stream_), "position upload");
     const int32_t* pos = d_ctrl_;
     op_begin(timed, "prefill_embedding_bf16_rows");
@@ -704,6 +712,7 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
     for (size_t i = 0; i < n_tokens; ++i) {
         h_ctrl_[2 * i] = static_cast<int32_t>(i);
         h_ctrl_[2 * i + 1] = token_ids[i];
+        dev_pos_ = kPosUnknown;
         XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_ctrl_ + 2 * i, 2 * sizeof(int32_t), stream_), "control upload");
         if ((i == 0 && detail_prefill_) || !g_prefill_) {
             const bool timed = i == 0 && detail_prefill_;
@@ -736,36 +745,55 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     if (!ensure_capacity(position + 1, error)) return false;
     if (!select_attention(position + 1, trace, error)) return false;
     if (!ensure_graphs(error)) return false;
-    // The previous step's forward pass may still be running: h_tok_[0..1] are
-    // free again because their upload preceded that step's sampling, which the
-    // previous call waited for.
-    h_tok_[0] = static_cast<int32_t>(position);
-    h_tok_[1] = 0;
-    XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
-    if (detail_decode_ || !g_sample_ || !g_forward_) {
+    // The sampling kernel adds 1 to d_ctrl_[0] before the forward pass reads
+    // it, so the device must hold position - 1: after a step at position - 1
+    // it does, otherwise it is uploaded.  The previous step's forward pass may
+    // still be running: h_tok_[0..1] are free again because their upload
+    // preceded that step's sampling, which the previous call waited for, and
+    // so is h_slot_, which only sampling kernels store to.
+    const long long want = static_cast<long long>(position);
+    const bool upload = dev_pos_ != want - 1;
+    dev_pos_ = kPosUnknown;
+    *h_slot_ = ~0ull;
+    if (upload) {
+        h_tok_[0] = static_cast<int32_t>(want - 1);
+        h_tok_[1] = 0;
+        XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
+    }
+    if (detail_decode_ || !g_step_) {
         // per-op events: the whole step is waited for before its times are read
         const bool timed = detail_decode_;
         if (!sync(trace, error)) return false;
         if (!enqueue_lm_head(timed, error)) return false;
-        XQ_CALL(xqhip_memcpy_d2h_async(h_tok_ + 2, d_ctrl_ + 2, sizeof(int32_t), stream_), "token readback");
         if (!enqueue_embed(d_ctrl_ + 2, timed, error) || !enqueue_layers(timed, error)) return false;
         XQ_CALL(xqhip_stream_synchronize(stream_), "decode");
-        *token_id = h_tok_[2];
+        if (!read_slot(want, token_id, error)) return false;
+        dev_pos_ = want;
         detail_decode_ = false;
         flush_timed(trace);
         return true;
     }
-    // sample, hand the token to the host, then enqueue the forward pass and
-    // return once the token is known
+    // one graph samples, publishes the token, advances the position and runs
+    // the forward pass; return once the token is published
     void** ev = step_ev_[step_slot_];
     XQ_CALL(xqhip_event_record(ev[0], stream_), "step event");
-    XQ_CALL(xqhip_graph_launch(g_sample_, stream_), "sampling graph");
-    XQ_CALL(xqhip_memcpy_d2h_async(h_tok_ + 2, d_ctrl_ + 2, sizeof(int32_t), stream_), "token readback");
-    XQ_CALL(xqhip_event_record(ev_token_, stream_), "token event");
-    XQ_CALL(xqhip_graph_launch(g_forward_, stream_), "forward graph");
+    XQ_CALL(xqhip_graph_launch(g_step_, stream_), "decode step graph");
     XQ_CALL(xqhip_event_record(ev[1], stream_), "step event");
-    XQ_CALL(xqhip_event_synchronize(ev_token_), "decode");
-    *token_id = h_tok_[2];
+    for (uint32_t spin = 1;; ++spin) {
+        if (static_cast<uint32_t>(__atomic_load_n(h_slot_, __ATOMIC_ACQUIRE) >> 32) == static_cast<uint32_t>(want))
+            break;
+        if ((spin & 1023u) == 0) {  // the step ended (or failed) without publishing: report it
+            const int q = xqhip_event_query(ev[1]);
+            if (q < 0) return fail_hip(error, "decode step");
+            if (q == 1 && static_cast<uint32_t>(__atomic_load_n(h_slot_, __ATOMIC_ACQUIRE) >> 32) !=
+                              static_cast<uint32_t>(want)) {
+                *error = "decode step ended without publishing the sampled token";
+                return false;
+            }
+        }
+    }
+    if (!read_slot(want, token_id, error)) return false;
+    dev_pos_ = want;
     // the previous step's forward pass preceded this step's sampling: complete
     if (step_pending_ && trace) {
         void** prev = step_ev_[step_slot_ ^ 1];
@@ -773,6 +801,17 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     }
     step_pending_ = true;
     step_slot_ ^= 1;
+    return true;
+}
+
+// The slot the sampling kernel published: (position << 32) | token.
+bool DeviceModel::read_slot(long long want, int32_t* token_id, std::string* error) const {
+    const uint64_t v = __atomic_load_n(h_slot_, __ATOMIC_ACQUIRE);
+    if (static_cast<uint32_t>(v >> 32) != static_cast<uint32_t>(want)) {
+        *error = "sampled token published for another position";
+        return false;
+    }
+    *token_id = static_cast<int32_t>(static_cast<uint32_t>(v));
     return true;
 }
 

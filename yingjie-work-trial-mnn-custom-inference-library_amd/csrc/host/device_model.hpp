@@ -94,6 +94,7 @@ private:
     bool enqueue_layers(bool timed, std::string* error);
     bool enqueue_embed(const int32_t* token_dev, bool timed, std::string* error);
     bool enqueue_lm_head(bool timed, std::string* error);
+    bool read_slot(long long want, int32_t* token_id, std::string* error) const;
     bool op_begin(bool timed, const std::string& name, std::vector<std::string> extra = {}, int split = 1);
     void op_end(bool timed);
     void flush_timed(KernelTrace* trace);
@@ -149,12 +150,15 @@ private:
     int32_t* d_ctrl_ = nullptr;  // [0] position, [1] input token, [2] sampled token
     int32_t* h_ctrl_ = nullptr;  // pinned staging, 2 ints per queued token
     size_t h_ctrl_cap_ = 0;
-    int32_t* h_tok_ = nullptr;   // pinned sampled-token readback
+    int32_t* h_tok_ = nullptr;   // pinned control staging of the decode step
+    uint64_t* h_slot_ = nullptr; // coherent pinned: (position << 32) | sampled token, stored by the sampling kernel
+    static constexpr long long kPosUnknown = -(1LL << 40);
+    long long dev_pos_ = kPosUnknown;  // d_ctrl_[0] once the queued work has run, if known
     void* stream_ = nullptr;
     void* g_prefill_ = nullptr;  // graph: embed(input token) + layers
-    void* g_sample_ = nullptr;   // graph: lm_head argmax -> sampled token (d_ctrl_[2])
-    void* g_forward_ = nullptr;  // graph: embed(sampled token) + layers
-    void* ev_token_ = nullptr;   // recorded once the sampled token reached h_tok_[2]
+    // graph: lm_head argmax -> sampled token (d_ctrl_[2]), d_ctrl_[0] + 1 and the
+    // published slot, then embed(sampled token) + layers at the new position
+    void* g_step_ = nullptr;
     void* step_ev_[2][2] = {};   // (start, end) of the last two graph steps
     int step_slot_ = 0;          // slot of the next graph step
     bool step_pending_ = false;  // slot step_slot_ ^ 1 holds a step not yet credited to the trace

@@ -58,6 +58,9 @@ _HIP_SIGS = {
     "xqhip_event_record": (c_int, [c_void_p, c_void_p]),
     "xqhip_event_synchronize": (c_int, [c_void_p]),
     "xqhip_event_elapsed_ms": (c_int, [c_void_p, c_void_p, ctypes.POINTER(c_float)]),
+    "xqhip_event_query": (c_int, [c_void_p]),
+    "xqhip_host_alloc_coherent": (c_int, [ctypes.POINTER(c_void_p), c_size_t]),
+    "xqhip_host_free": (c_int, [c_void_p]),
     "xqhip_w4_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, ctypes.POINTER(W4)]),
     "xqhip_wlb_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                  ctypes.POINTER(W4)]),
@@ -67,6 +70,8 @@ _HIP_SIGS = {
     "xqhip_argmax_workspace_bytes": (c_size_t, [c_int]),
     "xqhip_gemv_w4a16_argmax": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p, c_void_p,
                                         c_void_p]),
+    "xqhip_gemv_w4a16_argmax_publish": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p, c_void_p,
+                                                c_void_p, c_void_p, c_void_p]),
     "xqhip_gemv_w4a16_argmax_static": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p,
                                                c_void_p]),
     "xqhip_embed_bf16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
