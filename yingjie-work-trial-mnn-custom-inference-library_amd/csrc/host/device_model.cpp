@@ -782,6 +782,9 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     for (uint32_t spin = 1;; ++spin) {
         if (static_cast<uint32_t>(__atomic_load_n(h_slot_, __ATOMIC_ACQUIRE) >> 32) == static_cast<uint32_t>(want))
             break;
+#if defined(__x86_64__) || defined(__i386__)
+        __builtin_ia32_pause();  // spin-wait hint: yields the core's pipeline to its sibling thread
+#endif
         if ((spin & 1023u) == 0) {  // the step ended (or failed) without publishing: report it
             const int q = xqhip_event_query(ev[1]);
             if (q < 0) return fail_hip(error, "decode step");
