@@ -386,6 +386,7 @@ void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past th
     }
     detail_prefill_ = detail_decode_ = true;
     dev_pos_ = kPosUnknown;
+    chained_ = false;
 }
 
 bool DeviceModel::op_begin(bool timed, const std::string& name, std::vector<std::string> extra, int split) {
@@ -578,6 +579,7 @@ bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, i
                                 std::string* error) {
     XQ_CALL(xqhip_memcpy_h2d_async(tok_dev_, h_tokens, sizeof(int32_t) * n, stream_), "prompt upload");
     dev_pos_ = kPosUnknown;
+    chained_ = false;
     XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_pos, sizeof(int32_t), stream_), "position upload");
     const int32_t* pos = d_ctrl_;
     op_begin(timed, "prefill_embedding_bf16_rows");
@@ -713,6 +715,7 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
         h_ctrl_[2 * i] = static_cast<int32_t>(i);
         h_ctrl_[2 * i + 1] = token_ids[i];
         dev_pos_ = kPosUnknown;
+    chained_ = false;
         XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_ctrl_ + 2 * i, 2 * sizeof(int32_t), stream_), "control upload");
         if ((i == 0 && detail_prefill_) || !g_prefill_) {
             const bool timed = i == 0 && detail_prefill_;
@@ -761,6 +764,7 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
     }
     if (detail_decode_ || !g_step_) {
+        chained_ = false;
         // per-op events: the whole step is waited for before its times are read
         const bool timed = detail_decode_;
         if (!sync(trace, error)) return false;
@@ -775,8 +779,18 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     }
     // one graph samples, publishes the token, advances the position and runs
     // the forward pass; return once the token is published
+    // A step that directly follows the previous graph step starts at that
+    // step's end event (one marker fewer between the graphs); the ring of
+    // three keeps both events of the step still to be credited intact.
     void** ev = step_ev_[step_slot_];
-    XQ_CALL(xqhip_event_record(ev[0], stream_), "step event");
+    const int prev = (step_slot_ + 2) % 3;
+    if (chained_ && !upload) {
+        step_start_[step_slot_] = step_ev_[prev][1];
+    } else {
+        XQ_CALL(xqhip_event_record(ev[0], stream_), "step event");
+        step_start_[step_slot_] = ev[0];
+    }
+    chained_ = false;
     XQ_CALL(xqhip_graph_launch(g_step_, stream_), "decode step graph");
     XQ_CALL(xqhip_event_record(ev[1], stream_), "step event");
     for (uint32_t spin = 1;; ++spin) {
@@ -798,12 +812,11 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     if (!read_slot(want, token_id, error)) return false;
     dev_pos_ = want;
     // the previous step's forward pass preceded this step's sampling: complete
-    if (step_pending_ && trace) {
-        void** prev = step_ev_[step_slot_ ^ 1];
-        trace->add("decode_step_graph_custom", elapsed_ms(prev[0], prev[1]), kTraceBackend);
-    }
+    if (step_pending_ && trace)
+        trace->add("decode_step_graph_custom", elapsed_ms(step_start_[prev], step_ev_[prev][1]), kTraceBackend);
     step_pending_ = true;
-    step_slot_ ^= 1;
+    chained_ = true;
+    step_slot_ = (step_slot_ + 1) % 3;
     return true;
 }
 
@@ -819,11 +832,12 @@ bool DeviceModel::read_slot(long long want, int32_t* token_id, std::string* erro
 }
 
 bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
+    chained_ = false;  // whatever the caller enqueues next runs between the steps
     if (!stream_) return true;
     if (xqhip_stream_synchronize(stream_) != 0) return fail_hip(error, "decode step");
     if (step_pending_ && trace) {
-        void** prev = step_ev_[step_slot_ ^ 1];
-        trace->add("decode_step_graph_custom", elapsed_ms(prev[0], prev[1]), kTraceBackend);
+        const int prev = (step_slot_ + 2) % 3;
+        trace->add("decode_step_graph_custom", elapsed_ms(step_start_[prev], step_ev_[prev][1]), kTraceBackend);
     }
     step_pending_ = false;
     return true;

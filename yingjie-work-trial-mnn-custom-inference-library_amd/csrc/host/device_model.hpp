@@ -159,9 +159,11 @@ private:
     // graph: lm_head argmax -> sampled token (d_ctrl_[2]), d_ctrl_[0] + 1 and the
     // published slot, then embed(sampled token) + layers at the new position
     void* g_step_ = nullptr;
-    void* step_ev_[2][2] = {};   // (start, end) of the last two graph steps
+    void* step_ev_[3][2] = {};   // (start, end) events of the last three graph steps
+    void* step_start_[3] = {};   // a step's start: its own start event or the previous step's end
     int step_slot_ = 0;          // slot of the next graph step
-    bool step_pending_ = false;  // slot step_slot_ ^ 1 holds a step not yet credited to the trace
+    bool step_pending_ = false;  // slot (step_slot_ + 2) % 3 holds a step not yet credited to the trace
+    bool chained_ = false;       // the last work enqueued is a graph step (its end event starts the next)
     bool detail_prefill_ = true, detail_decode_ = true;
     // prompt-chunk buffers, [token][...] rows (allocated when every matrix is TILED64)
     bool batched_prefill_ = false;
