@@ -109,6 +109,9 @@ XQHIP_API int xqhip_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream
  * aligned pointers. */
 XQHIP_API int xqhip_copy(void* dst, const void* src, size_t bytes, void* stream);
 XQHIP_API int xqhip_stream_synchronize(void* stream);
+/* 1 once all work enqueued on `stream` has finished, 0 while some is pending,
+ * a negative XQHIP_E* code on a device error.  Does not block. */
+XQHIP_API int xqhip_stream_query(void* stream);
 XQHIP_API int xqhip_device_synchronize(void);
 XQHIP_API int xqhip_event_create(void** ev);
 XQHIP_API int xqhip_event_destroy(void* ev);

@@ -216,6 +216,13 @@ int xqhip_event_synchronize(void* ev) {
     return check(hipEventSynchronize(static_cast<hipEvent_t>(ev)), "hipEventSynchronize");
 }
 
+int xqhip_stream_query(void* stream) {
+    const hipError_t e = hipStreamQuery(as_stream(stream));
+    if (e == hipSuccess) return 1;
+    if (e == hipErrorNotReady) return 0;
+    return check(e, "hipStreamQuery");
+}
+
 int xqhip_event_query(void* ev) {
     const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(ev));
     if (e == hipSuccess) return 1;

@@ -779,28 +779,29 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     }
     // one graph samples, publishes the token, advances the position and runs
     // the forward pass; return once the token is published
-    // A step that directly follows the previous graph step starts at that
-    // step's end event (one marker fewer between the graphs); the ring of
-    // three keeps both events of the step still to be credited intact.
-    void** ev = step_ev_[step_slot_];
-    const int prev = (step_slot_ + 2) % 3;
-    if (chained_ && !upload) {
-        step_start_[step_slot_] = step_ev_[prev][1];
-    } else {
-        XQ_CALL(xqhip_event_record(ev[0], stream_), "step event");
-        step_start_[step_slot_] = ev[0];
+    // Step timing: consecutive graph steps form a segment that starts at an
+    // event (its own, or the end event of the segment before it) and ends at
+    // the event recorded after its kStepsPerEvent-th step, so most steps
+    // carry no marker packet between their graphs; each of a segment's steps
+    // is credited the segment's time / its steps.
+    if (!chained_ || upload) {
+        if (seg_steps_ > 0 && !sync(trace, error)) return false;  // closes the open segment
+        seg_start_ = step_ev_[seg_slot_][0];
+        XQ_CALL(xqhip_event_record(seg_start_, stream_), "step event");
+        seg_steps_ = 0;
     }
     chained_ = false;
     XQ_CALL(xqhip_graph_launch(g_step_, stream_), "decode step graph");
-    XQ_CALL(xqhip_event_record(ev[1], stream_), "step event");
+    const bool closes = ++seg_steps_ == kStepsPerEvent;
+    if (closes) XQ_CALL(xqhip_event_record(step_ev_[seg_slot_][1], stream_), "step event");
     for (uint32_t spin = 1;; ++spin) {
         if (static_cast<uint32_t>(__atomic_load_n(h_slot_, __ATOMIC_ACQUIRE) >> 32) == static_cast<uint32_t>(want))
             break;
 #if defined(__x86_64__) || defined(__i386__)
         __builtin_ia32_pause();  // spin-wait hint: yields the core's pipeline to its sibling thread
 #endif
-        if ((spin & 1023u) == 0) {  // the step ended (or failed) without publishing: report it
-            const int q = xqhip_event_query(ev[1]);
+        if ((spin & 1023u) == 0) {  // the stream drained (or failed) without publishing: report it
+            const int q = xqhip_stream_query(stream_);
             if (q < 0) return fail_hip(error, "decode step");
             if (q == 1 && static_cast<uint32_t>(__atomic_load_n(h_slot_, __ATOMIC_ACQUIRE) >> 32) !=
                               static_cast<uint32_t>(want)) {
@@ -811,13 +812,27 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     }
     if (!read_slot(want, token_id, error)) return false;
     dev_pos_ = want;
-    // the previous step's forward pass preceded this step's sampling: complete
-    if (step_pending_ && trace)
-        trace->add("decode_step_graph_custom", elapsed_ms(step_start_[prev], step_ev_[prev][1]), kTraceBackend);
-    step_pending_ = true;
+    // a segment closed by an earlier call ended before this step's sampling: complete
+    credit_segment(trace);
+    if (closes) {
+        pend_start_ = seg_start_;
+        pend_end_ = step_ev_[seg_slot_][1];
+        pend_steps_ = seg_steps_;
+        seg_start_ = pend_end_;  // the next segment starts where this one ended
+        seg_steps_ = 0;
+        seg_slot_ = (seg_slot_ + 1) % 3;
+    }
     chained_ = true;
-    step_slot_ = (step_slot_ + 1) % 3;
     return true;
+}
+
+// Credits the closed segment (if any) to the trace, one row per step.
+void DeviceModel::credit_segment(KernelTrace* trace) {
+    if (pend_steps_ > 0 && trace) {
+        const double ms = elapsed_ms(pend_start_, pend_end_) / pend_steps_;
+        for (int i = 0; i < pend_steps_; ++i) trace->add("decode_step_graph_custom", ms, kTraceBackend);
+    }
+    pend_steps_ = 0;
 }
 
 // The slot the sampling kernel published: (position << 32) | token.
@@ -834,12 +849,18 @@ bool DeviceModel::read_slot(long long want, int32_t* token_id, std::string* erro
 bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
     chained_ = false;  // whatever the caller enqueues next runs between the steps
     if (!stream_) return true;
+    const bool open = seg_steps_ > 0;  // steps enqueued since the last segment event: close the segment
+    if (open && xqhip_event_record(step_ev_[seg_slot_][1], stream_) != 0) return fail_hip(error, "step event");
     if (xqhip_stream_synchronize(stream_) != 0) return fail_hip(error, "decode step");
-    if (step_pending_ && trace) {
-        const int prev = (step_slot_ + 2) % 3;
-        trace->add("decode_step_graph_custom", elapsed_ms(step_start_[prev], step_ev_[prev][1]), kTraceBackend);
+    credit_segment(trace);
+    if (open) {
+        pend_start_ = seg_start_;
+        pend_end_ = step_ev_[seg_slot_][1];
+        pend_steps_ = seg_steps_;
+        seg_steps_ = 0;
+        seg_slot_ = (seg_slot_ + 1) % 3;
+        credit_segment(trace);
     }
-    step_pending_ = false;
     return true;
 }
 

@@ -95,6 +95,7 @@ private:
     bool enqueue_embed(const int32_t* token_dev, bool timed, std::string* error);
     bool enqueue_lm_head(bool timed, std::string* error);
     bool read_slot(long long want, int32_t* token_id, std::string* error) const;
+    void credit_segment(KernelTrace* trace);
     bool op_begin(bool timed, const std::string& name, std::vector<std::string> extra = {}, int split = 1);
     void op_end(bool timed);
     void flush_timed(KernelTrace* trace);
@@ -159,11 +160,16 @@ private:
     // graph: lm_head argmax -> sampled token (d_ctrl_[2]), d_ctrl_[0] + 1 and the
     // published slot, then embed(sampled token) + layers at the new position
     void* g_step_ = nullptr;
-    void* step_ev_[3][2] = {};   // (start, end) events of the last three graph steps
-    void* step_start_[3] = {};   // a step's start: its own start event or the previous step's end
-    int step_slot_ = 0;          // slot of the next graph step
-    bool step_pending_ = false;  // slot (step_slot_ + 2) % 3 holds a step not yet credited to the trace
-    bool chained_ = false;       // the last work enqueued is a graph step (its end event starts the next)
+    // decode-step timing by segments of consecutive graph steps
+    static constexpr int kStepsPerEvent = 8;
+    void* step_ev_[3][2] = {};   // (start, end) events of three segments
+    int seg_slot_ = 0;           // slot of the open segment
+    void* seg_start_ = nullptr;  // start event of the open segment
+    int seg_steps_ = 0;          // graph steps enqueued in the open segment
+    void* pend_start_ = nullptr;  // a closed segment not yet credited to the trace
+    void* pend_end_ = nullptr;
+    int pend_steps_ = 0;
+    bool chained_ = false;       // the last work enqueued is a graph step (the open segment continues)
     bool detail_prefill_ = true, detail_decode_ = true;
     // prompt-chunk buffers, [token][...] rows (allocated when every matrix is TILED64)
     bool batched_prefill_ = false;
