@@ -402,13 +402,21 @@ bool DeviceModel::op_begin(bool timed, const std::string& name, std::vector<std:
     op.split = split;
     op.ev0 = event_pool_[event_next_++];
     op.ev1 = event_pool_[event_next_++];
-    xqhip_event_record(op.ev0, stream_);
+    // an op that directly follows the previous one starts at its end event:
+    // one event recorded on the stream per op instead of two
+    if (op_chained_ && !ops_.empty())
+        op.ev0 = ops_.back().ev1;
+    else
+        xqhip_event_record(op.ev0, stream_);
+    op_chained_ = false;
     ops_.push_back(std::move(op));
     return true;
 }
 
 void DeviceModel::op_end(bool timed) {
-    if (timed && !ops_.empty()) xqhip_event_record(ops_.back().ev1, stream_);
+    if (!timed || ops_.empty()) return;
+    xqhip_event_record(ops_.back().ev1, stream_);
+    op_chained_ = true;
 }
 
 void DeviceModel::flush_timed(KernelTrace* trace) {
@@ -421,6 +429,7 @@ void DeviceModel::flush_timed(KernelTrace* trace) {
     }
     ops_.clear();
     event_next_ = 0;
+    op_chained_ = false;
 }
 
 

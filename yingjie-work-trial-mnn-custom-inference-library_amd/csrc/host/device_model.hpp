@@ -187,6 +187,7 @@ private:
     std::vector<TimedOp> ops_;
     std::vector<void*> event_pool_;
     size_t event_next_ = 0;
+    bool op_chained_ = false;  // the last event recorded on the stream ended the last timed op
     std::vector<void*> allocations_;
     std::vector<xqhip_w4*> matrices_;
 };
