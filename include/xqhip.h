@@ -392,6 +392,61 @@ XQHIP_API int xqhip_linear_attn_scan_ws(const float* mixed, const float* a, cons
                                         int ksize, int tokens, float* out, int out_stride, void* workspace,
                                         void* stream);
 
+/* ---- decode chains: consecutive projections in one persistent launch --- */
+/* A chain runs a sequence of decode-step GEMVs (the projections between two
+ * non-GEMV ops of the reference's runLayer, customlib/runtime/custom_model.cpp
+ * :1138-1256: o/out_proj -> gate/up -> down -> the next layer's input
+ * projection) as one launch of one block per CU.  Each CU keeps streaming
+ * weights across the op boundaries (the next op's first weights are requested
+ * before the current op's output is complete), and an op reads its input
+ * vector from the previous op through a hand-off arena of 8-byte records
+ * (value, launch sequence number) stored write-through, polled with bounded
+ * waits: no kernel boundary and no grid barrier between the ops.  Results are
+ * those of xqhip_gemv_w4a16 on the same operands, bit for bit.
+ *
+ * Every matrix of a chain must be a 4-bit TILED64 matrix and all must share
+ * one metadata layout; cols <= 16384. */
+typedef struct xqhip_chain_src {
+    const float* plain; /* a device fp32 vector complete before the launch, or */
+    int32_t op;         /* (plain == NULL) the output of op `op` of the chain */
+    int32_t offset;     /* first element taken from that output */
+} xqhip_chain_src;
+
+typedef struct xqhip_chain_op {
+    const xqhip_w4* w;
+    int32_t epi;          /* XQHIP_EPI_STORE / ADD / SILU_PAIR                  */
+    int32_t pro;          /* XQHIP_PRO_NONE / RMS / GATED_HEAD_ACT              */
+    const float* pro_w;   /* RMS: [cols]; GATED_HEAD_ACT: [head_dim]            */
+    int32_t head_dim;     /* GATED_HEAD_ACT                                     */
+    float eps;
+    xqhip_chain_src x;    /* input, cols values                                */
+    xqhip_chain_src gate; /* GATED_HEAD_ACT: silu(gate), cols values            */
+    xqhip_chain_src res;  /* ADD: the residual added to                         */
+    float* y_plain;       /* also store the output here (NULL: later ops only)  */
+} xqhip_chain_op;
+
+/* Validates the ops and uploads a device description; *chain receives an
+ * opaque handle.  XQHIP_EINVAL when a matrix or shape is not supported. */
+XQHIP_API int xqhip_chain_create(const xqhip_chain_op* ops, int n_ops, void** chain);
+XQHIP_API int xqhip_chain_destroy(void* chain);
+/* Hand-off records a launch of this chain needs (8 bytes each). */
+XQHIP_API size_t xqhip_chain_arena_records(const void* chain);
+/* Bytes of the synchronisation block shared by the chains of one stream
+ * (zero-filled once before the first launch, then left alone). */
+XQHIP_API size_t xqhip_chain_sync_bytes(void);
+/* One launch: arena of at least xqhip_chain_arena_records records (zero-filled
+ * once before first use), sync block as above.  Graph-capturable.  Launches
+ * sharing an arena or sync block must be ordered (one stream). */
+XQHIP_API int xqhip_chain_launch(const void* chain, void* arena, void* sync, void* stream);
+/* The same launch recording per op and block the device's 100 MHz realtime
+ * counter when the op's input is staged and when its last output is stored:
+ * stamps[(op * grid + block) * 2 + {0, 1}] (uint64), grid = xqhip_chain_grid. */
+XQHIP_API int xqhip_chain_launch_stamped(const void* chain, void* arena, void* sync, void* stamps, void* stream);
+XQHIP_API int xqhip_chain_grid(const void* chain);
+/* Reads the sync block's error word (synchronous copy): 0, or nonzero after a
+ * launch whose hand-off wait gave up (its results are then invalid). */
+XQHIP_API int xqhip_chain_error(const void* sync, int* error);
+
 /* ---- streams and graphs ------------------------------------------------ */
 XQHIP_API int xqhip_stream_create(void** stream);
 XQHIP_API int xqhip_stream_destroy(void* stream);

@@ -298,3 +298,40 @@ def test_selftest_entry_point():
     bad = [r for r in j["vector_results"] if not r["pass"]]
     assert not bad, bad
     assert j["wall_clock_ms"] > 0
+
+
+@pytest.mark.parametrize("which", ["small", "heads9b"])
+def test_decode_chain_matches_per_op_launches(which, small_dir, heads9b_dir, monkeypatch):
+    """XQ_DECODE_CHAIN=1 runs each run of projections between two non-GEMV ops
+    (o/out_proj, gate/up, down, next input projection) as one persistent launch
+    (xqhip_chain_*).  Its arithmetic is the per-op GEMVs', so ids and hidden
+    states after the prefill and after every greedy step equal the default
+    session's bit for bit; both are checked against the oracle too."""
+    d = small_dir if which == "small" else heads9b_dir
+    prompt = [int(t) for t in np.random.default_rng(77).integers(0, 4096, 45)]
+    want, margins, hiddens = oracle_run(d, prompt, 6)
+    runs = {}
+    for mode in ("default", "chain"):
+        monkeypatch.delenv("XQ_DECODE_CHAIN", raising=False)
+        if mode == "chain":
+            monkeypatch.setenv("XQ_DECODE_CHAIN", "1")
+        s = xb.Session(d, xb.options())
+        assert s.status == xb.XQ_OK
+        info = s.json("xq_get_backend_info")[1]
+        assert ("decode_chain=on" in info) == (mode == "chain"), info
+        st, _ = s.prefill(prompt)
+        assert st == 0
+        toks, hs = [], [s.hidden()[1]]
+        for _ in range(6):
+            st, tok, m = s.decode_one()
+            assert st == 0, m.error
+            toks.append(tok)
+            hs.append(s.hidden()[1])
+        compare_tokens(toks, want, margins)
+        close(hs[-1], hiddens[-1], f"{mode}: hidden after 6 steps")
+        runs[mode] = (toks, hs, s.json("xq_get_kernel_trace_json")[1])
+        s.close()
+    assert runs["chain"][0] == runs["default"][0]
+    for a, b in zip(runs["chain"][1], runs["default"][1]):
+        assert np.array_equal(a, b)
+    assert "decode_chain_w4a16" in runs["chain"][2] and "decode_chain_w4a16" not in runs["default"][2]

@@ -140,13 +140,18 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
         // relative to each group's maximum, so the groups are staged from x * w
         // and the factor multiplies the group scales after the caller's barrier
         // (rms_factor): here each wave only leaves its sum of squares in red.
+        // explicit fused multiply-adds on selected operands: the rounding of
+        // the sum of squares does not depend on how the compiler contracts or
+        // if-converts it (the decode chains stage with the same sequence)
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
-            const int item = threadIdx.x + k * THREADS;
-            if (item < n_items)
+            const bool in = static_cast<int>(threadIdx.x) + k * THREADS < n_items;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
+            for (int i = 0; i < 8; ++i) {
+                const float a = in ? v[k][i] : 0.0f;
+                ss = fmaf(a, a, ss);
+            }
         }
         ss = wave_sum(ss);
         if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
@@ -171,7 +176,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
         for (int k = 0; k < ITEMS; ++k) {
             float hs = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) hs += v[k][i] * v[k][i];
+            for (int i = 0; i < 8; ++i) hs = fmaf(v[k][i], v[k][i], hs);
             if (per_head >= 2) hs += dpp_f32<kDppXor1>(hs);
             if (per_head >= 4) hs += dpp_f32<kDppXor2>(hs);
             if (per_head >= 8) hs += dpp_f32<kDppHalfMirror>(hs);

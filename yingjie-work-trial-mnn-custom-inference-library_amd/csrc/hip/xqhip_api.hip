@@ -57,6 +57,15 @@ int gemv_block_cap() {
 
 using xqhip::kArgmaxMaxBlocks;
 
+}  // namespace
+
+// Error text of entry points defined in other files of the library.
+namespace xqhip {
+void set_last_error(const std::string& msg) { g_err = msg; }
+}  // namespace xqhip
+
+namespace {
+
 uint16_t f32_to_f16_bits(float f, bool* exact) {
     const _Float16 h = static_cast<_Float16>(f);
     *exact = static_cast<float>(h) == f;

@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <mutex>
 #include <sstream>
 
 namespace xqh {
@@ -19,6 +20,29 @@ namespace {
 
 using Clock = std::chrono::steady_clock;
 const char* kTraceBackend = "hip";
+
+// One stream for every model of the process: the decode chains need all CUs
+// at once, so two models' steps must never run side by side (xq_decode_one
+// returns while the step's forward pass still runs).  Shared and counted;
+// destroyed with the last model.
+std::mutex g_stream_mu;
+void* g_stream = nullptr;
+int g_stream_users = 0;
+
+void* acquire_stream() {
+    std::lock_guard<std::mutex> lock(g_stream_mu);
+    if (!g_stream && xqhip_stream_create(&g_stream) != 0) return nullptr;
+    ++g_stream_users;
+    return g_stream;
+}
+
+void release_stream() {
+    std::lock_guard<std::mutex> lock(g_stream_mu);
+    if (--g_stream_users == 0 && g_stream) {
+        xqhip_stream_destroy(g_stream);
+        g_stream = nullptr;
+    }
+}
 
 double elapsed_ms(void* a, void* b) {
     float ms = 0.0f;
@@ -35,6 +59,7 @@ DeviceModel::~DeviceModel() {
     if (stream_) xqhip_stream_synchronize(stream_);
     if (g_prefill_) xqhip_graph_destroy(g_prefill_);
     if (g_step_) xqhip_graph_destroy(g_step_);
+    for (void* c : chains_) xqhip_chain_destroy(c);
     for (auto& pair : step_ev_)
         for (void* e : pair)
             if (e) xqhip_event_destroy(e);
@@ -44,7 +69,7 @@ DeviceModel::~DeviceModel() {
     if (h_ctrl_) xqhip_host_free(h_ctrl_);
     if (h_tok_) xqhip_host_free(h_tok_);
     if (h_slot_) xqhip_host_free(h_slot_);
-    if (stream_) xqhip_stream_destroy(stream_);
+    if (stream_) release_stream();
 }
 
 bool DeviceModel::fail_hip(std::string* error, const char* what) {
@@ -266,7 +291,8 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     argmax_ws_ = wa;
     gqa_ws_ = wg;
     attn_split_ws_ = wsp;
-    if (xqhip_stream_create(&stream_) != 0) return fail_hip(error, "stream");
+    stream_ = acquire_stream();
+    if (!stream_) return fail_hip(error, "stream");
     xqhip_fill_u8(resid_, 0, sizeof(float) * hidden_, stream_);  // hidden_ starts at zero (custom_model.cpp:478)
     xqhip_fill_u8(argmax_ws_, 0, ws_argmax, stream_);
     xqhip_fill_u8(gqa_ws_, 0, ws_gqa, stream_);
@@ -286,8 +312,133 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     for (auto& pair : step_ev_)
         for (void*& e : pair)
             if (xqhip_event_create(&e) != 0) return fail_hip(error, "event");
+    if (!build_chains(error)) return false;
     reset_state();
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "load sync");
+}
+
+// Decode chains are opt-in (XQ_DECODE_CHAIN=1): measured on the 9B shapes a
+// chain of out_proj, gate/up, down and the next in_proj takes 39.2 us against
+// 33.5 us for the four GEMV launches (every in-kernel hand-off costs 2-4 us,
+// as much as the kernel boundary it replaces), so the step graphs keep one
+// launch per projection by default.
+static bool chains_enabled() {
+    const char* v = std::getenv("XQ_DECODE_CHAIN");
+    return v && v[0] == '1';
+}
+
+bool DeviceModel::build_chains(std::string* error) {
+    if (!chains_enabled()) {
+        chain_note_ = "off";
+        return true;
+    }
+    const size_t n = layers_.size();
+    if (n == 0) return true;
+    std::vector<std::vector<xqhip_chain_op>> specs(n + 1);
+    std::vector<std::string> names(n + 1);
+    auto plain = [](const float* p) {
+        xqhip_chain_src s{};
+        s.plain = p;
+        return s;
+    };
+    auto from = [](int op, int offset) {
+        xqhip_chain_src s{};
+        s.plain = nullptr;
+        s.op = op;
+        s.offset = offset;
+        return s;
+    };
+    for (size_t k = 0; k <= n; ++k) {
+        std::vector<xqhip_chain_op>& ops = specs[k];
+        std::string& nm = names[k];
+        int down_op = -1;
+        if (k > 0) {  // layer k-1: output projection, gate/up, down
+            Layer& L = layers_[k - 1];
+            xqhip_chain_op o{};
+            o.w = &L.out_proj;
+            o.epi = XQHIP_EPI_ADD;
+            o.x = plain(attn_);
+            o.res = plain(resid_);
+            if (!L.full) {  // linear attention: gated head norm of the step output (gate already silu)
+                o.pro = XQHIP_PRO_GATED_HEAD_ACT;
+                o.pro_w = L.lin_norm;
+                o.head_dim = lv_hd_;
+                o.eps = eps_;
+                o.gate = plain(proj_ + conv_dim_ + 2 * lv_n_);
+            }
+            ops.push_back(o);
+            xqhip_chain_op g{};
+            g.w = &L.gate_up;
+            g.epi = XQHIP_EPI_SILU_PAIR;
+            g.pro = XQHIP_PRO_RMS;
+            g.pro_w = L.post_norm;
+            g.eps = eps_;
+            g.x = from(0, 0);
+            ops.push_back(g);
+            xqhip_chain_op dn{};
+            dn.w = &L.down;
+            dn.epi = XQHIP_EPI_ADD;
+            dn.x = from(1, 0);
+            dn.res = from(0, 0);
+            dn.y_plain = resid_;
+            ops.push_back(dn);
+            down_op = 2;
+            nm = L.full ? "decode_chain_w4a16(o_proj,residual_add_attention,gate_proj,up_proj,rmsnorm_post_attention,"
+                          "silu_gate_mul,down_proj,residual_add_mlp"
+                        : "decode_chain_w4a16(linear_attn_out_proj,linear_attention_gated_rmsnorm,residual_add_attention,"
+                          "gate_proj,up_proj,rmsnorm_post_attention,silu_gate_mul,down_proj,residual_add_mlp";
+        }
+        if (k < n) {  // layer k's input projection
+            Layer& L = layers_[k];
+            xqhip_chain_op q{};
+            q.w = &L.in_proj;
+            q.epi = XQHIP_EPI_STORE;
+            q.pro = XQHIP_PRO_RMS;
+            q.pro_w = L.in_norm;
+            q.eps = eps_;
+            q.x = down_op >= 0 ? from(down_op, 0) : plain(resid_);
+            q.y_plain = proj_;
+            ops.push_back(q);
+            nm += nm.empty() ? "decode_chain_w4a16(" : ",";
+            nm += L.full ? "q_proj,k_proj,v_proj,rmsnorm_input" : "in_proj_qkv,in_proj_a,in_proj_b,in_proj_z,rmsnorm_input";
+        }
+        nm += ")";
+    }
+    std::vector<void*> made;
+    size_t records = 0;
+    for (size_t k = 0; k <= n; ++k) {
+        void* c = nullptr;
+        if (xqhip_chain_create(specs[k].data(), static_cast<int>(specs[k].size()), &c) != 0) {
+            for (void* m : made) xqhip_chain_destroy(m);
+            std::string why = xqhip_last_error();
+            for (char& ch : why)
+                if (ch == ';' || ch == '=') ch = ' ';  // the summary is a ;-separated key=value list
+            chain_note_ = "off(" + why + ")";
+            return true;  // the per-op launches serve this model
+        }
+        made.push_back(c);
+        records = std::max(records, xqhip_chain_arena_records(c));
+    }
+    uint8_t *arena = nullptr, *sync = nullptr;
+    if (!alloc(&arena, records * 8, error) || !alloc(&sync, xqhip_chain_sync_bytes(), error)) {
+        for (void* m : made) xqhip_chain_destroy(m);
+        return false;
+    }
+    xqhip_fill_u8(arena, 0, records * 8, stream_);
+    xqhip_fill_u8(sync, 0, xqhip_chain_sync_bytes(), stream_);
+    chain_arena_ = arena;
+    chain_sync_ = sync;
+    chains_ = std::move(made);
+    chain_names_ = std::move(names);
+    chain_note_ = "on";
+    return true;
+}
+
+bool DeviceModel::enqueue_chain(size_t k, bool timed, std::string* error) {
+    op_begin(timed, chain_names_[k]);
+    XQ_CALL(xqhip_chain_launch(chains_[k], chain_arena_, chain_sync_, stream_), "decode chain");
+    op_end(timed);
+    return true;
 }
 
 bool DeviceModel::build_rope_table(std::string* error) {
@@ -454,8 +605,51 @@ bool DeviceModel::enqueue_lm_head(bool timed, std::string* error) {
 
 bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
     const int32_t* pos = d_ctrl_;
-    for (Layer& L : layers_) {
+    const bool chain = !chains_.empty();
+    if (chain && !enqueue_chain(0, timed, error)) return false;
+    for (size_t li = 0; li < layers_.size(); ++li) {
+        Layer& L = layers_[li];
         xqhip_prologue rms_in{XQHIP_PRO_RMS, 0, L.in_norm, nullptr, eps_};
+        if (chain) {  // the layer's attention or linear-attention step between two chains
+            if (L.full) {
+                const float* k_src = proj_ + static_cast<size_t>(nq_) * hd_ * (L.q_gated ? 2 : 1);
+                const float* v_src = k_src + static_cast<size_t>(nkv_) * hd_;
+                op_begin(timed, "attention_gqa_decode_custom(fused:q_norm,k_norm,rope_qk,kv_append,output_gate)",
+                         {"prefill_kv_build_custom", "attention_score_custom", "attention_softmax_custom",
+                          "attention_v_reduce_custom"},
+                         4);
+                if (attn_mode_ == AttnMode::kSplit) {
+                    XQ_CALL(xqhip_attn_decode_split(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_,
+                                                    L.q_norm, L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache,
+                                                    attn_splits(kAttnSplits), attn_split_ws_, attn_, stream_),
+                            "attention decode");
+                } else if (attn_mode_ == AttnMode::kHead) {
+                    XQ_CALL(xqhip_attn_decode_head(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_,
+                                                   L.q_norm, L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache, attn_,
+                                                   stream_),
+                            "attention decode");
+                } else {
+                    XQ_CALL(xqhip_attn_decode(proj_, k_src, v_src, L.q_gated ? 1 : 0, nq_, nkv_, hd_, rot_, L.q_norm,
+                                              L.k_norm, eps_, rope_cs_, pos, L.k_cache, L.v_cache, max_ctx_, attn_,
+                                              gqa_ws_, stream_),
+                            "attention decode");
+                }
+                op_end(timed);
+            } else {
+                const float* a = proj_ + conv_dim_;
+                const float* b = a + lv_n_;
+                float* z = proj_ + conv_dim_ + 2 * lv_n_;
+                op_begin(timed, "linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
+                         {"linear_attention_conv1d_custom"}, 2);
+                XQ_CALL(xqhip_linear_attn_step_act(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias,
+                                                   L.rec_state, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_, z,
+                                                   stream_),
+                        "linear-attention step");
+                op_end(timed);
+            }
+            if (!enqueue_chain(li + 1, timed, error)) return false;
+            continue;
+        }
         if (L.full) {
             op_begin(timed, "linear_q_proj_w4a16(fused:k_proj,v_proj,rmsnorm_input)");
             XQ_CALL(xqhip_gemv_w4a16(&L.in_proj, resid_, XQHIP_F32, &rms_in, proj_, XQHIP_F32, XQHIP_EPI_STORE, stream_),
@@ -861,6 +1055,15 @@ bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
     const bool open = seg_steps_ > 0;  // steps enqueued since the last segment event: close the segment
     if (open && xqhip_event_record(step_ev_[seg_slot_][1], stream_) != 0) return fail_hip(error, "step event");
     if (xqhip_stream_synchronize(stream_) != 0) return fail_hip(error, "decode step");
+    if (chain_sync_) {
+        int bad = 0;
+        if (xqhip_chain_error(chain_sync_, &bad) != 0) return fail_hip(error, "decode chain status");
+        if (bad) {
+            *error = "decode chain: a hand-off wait gave up (not every block of the chain launch was resident); "
+                     "results since the last check are invalid";
+            return false;
+        }
+    }
     credit_segment(trace);
     if (open) {
         pend_start_ = seg_start_;
@@ -884,7 +1087,7 @@ std::string DeviceModel::coverage_summary() const {  // fields of custom_model.c
       << "linear_attention_qk_norm=hip_fused_conv1d;linear_attention_gated_rmsnorm=hip_fused_gemv_prologue;"
       << "sampling=hip_fused_lm_head_argmax;prefill_kv_build=hip_fp16_append;decode_step=hip_graph;"
       << "weight_bytes_per_token=" << weight_bytes_ << ";fp16_meta_inexact=" << inexact_meta_
-      << ";kv_capacity=" << max_ctx_ << ";fallback_ops=none";
+      << ";kv_capacity=" << max_ctx_ << ";decode_chain=" << chain_note_ << ";fallback_ops=none";
     return o.str();
 }
 

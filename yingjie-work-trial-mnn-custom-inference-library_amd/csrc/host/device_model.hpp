@@ -100,6 +100,9 @@ private:
     void op_end(bool timed);
     void flush_timed(KernelTrace* trace);
     bool ensure_graphs(std::string* error);
+    // decode chains: the projections between two non-GEMV ops as one launch
+    bool build_chains(std::string* error);
+    bool enqueue_chain(size_t k, bool timed, std::string* error);
     // batched prefill of prompt chunks (GEMMs on the matrix cores)
     bool prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, int n, int pos0, bool timed,
                        std::string* error);
@@ -190,6 +193,17 @@ private:
     bool op_chained_ = false;  // the last event recorded on the stream ended the last timed op
     std::vector<void*> allocations_;
     std::vector<xqhip_w4*> matrices_;
+    // Decode chains (xqhip_chain_*): chain 0 = layer 0's input projection,
+    // chain k (1 <= k < layers) = layer k-1's output projection, gate/up and
+    // down and layer k's input projection, the last = the last layer's output
+    // projection, gate/up and down.  Between chains k and k+1 runs layer k's
+    // attention or linear-attention step.  Empty when a matrix does not fit
+    // (then every projection is its own GEMV launch).
+    std::vector<void*> chains_;
+    std::vector<std::string> chain_names_;
+    void* chain_arena_ = nullptr;
+    void* chain_sync_ = nullptr;
+    std::string chain_note_ = "off";  // why the chains are not used, or "on"
 };
 
 }  // namespace xqh

@@ -37,6 +37,19 @@ class Prologue(ctypes.Structure):
                 ("eps", c_float)]
 
 
+class ChainSrc(ctypes.Structure):
+    """Mirror of xqhip_chain_src (include/xqhip.h): a plain device vector, or
+    (plain NULL) element `offset` on of op `op`'s output in the same chain."""
+    _fields_ = [("plain", c_void_p), ("op", ctypes.c_int32), ("offset", ctypes.c_int32)]
+
+
+class ChainOp(ctypes.Structure):
+    """Mirror of xqhip_chain_op (include/xqhip.h)."""
+    _fields_ = [("w", ctypes.POINTER(W4)), ("epi", ctypes.c_int32), ("pro", ctypes.c_int32), ("pro_w", c_void_p),
+                ("head_dim", ctypes.c_int32), ("eps", c_float), ("x", ChainSrc), ("gate", ChainSrc),
+                ("res", ChainSrc), ("y_plain", c_void_p)]
+
+
 _P = ctypes.POINTER
 
 _HIP_SIGS = {
@@ -117,6 +130,14 @@ _HIP_SIGS = {
                                           c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                           c_int, c_void_p, c_void_p]),
     "xqhip_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]),
+    "xqhip_chain_create": (c_int, [_P(ChainOp), c_int, _P(c_void_p)]),
+    "xqhip_chain_destroy": (c_int, [c_void_p]),
+    "xqhip_chain_arena_records": (c_size_t, [c_void_p]),
+    "xqhip_chain_sync_bytes": (c_size_t, []),
+    "xqhip_chain_launch": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "xqhip_chain_launch_stamped": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "xqhip_chain_grid": (c_int, [c_void_p]),
+    "xqhip_chain_error": (c_int, [c_void_p, _P(c_int)]),
     "xqhip_stream_create": (c_int, [_P(c_void_p)]),
     "xqhip_stream_destroy": (c_int, [c_void_p]),
     "xqhip_graph_begin": (c_int, [c_void_p]),
