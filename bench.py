@@ -521,6 +521,7 @@ def cpu_baseline_decode(prompt, gpu_sess, runs=3):
         margins.append(round(top[0]["logit"] - top[1]["logit"], 5) if len(top) > 1 else None)
         st, tok, _ = gpu_sess.decode_one()
         gpu_toks.append(tok)
+    h_gpu = gpu_sess.hidden()[1].astype(np.float64)
     if ob.ref_available():
         ref = xb.bind_xq_abi(ctypes.CDLL(ob.REF_SO))
         t0 = time.perf_counter()
@@ -534,6 +535,7 @@ def cpu_baseline_decode(prompt, gpu_sess, runs=3):
             if r > 0:
                 tps.append(m.decode_tokens_per_second)
                 pre.append(m.prefill_tokens_per_second)
+        h_cpu = rs.hidden()[1].astype(np.float64)
         rs.close()
         kind = "reference"
     else:
@@ -550,8 +552,14 @@ def cpu_baseline_decode(prompt, gpu_sess, runs=3):
             if r > 0:
                 tps.append(n_new / (t3 - t2))
                 pre.append(n_prompt / (t2 - t1))
+        h_cpu = np.asarray(om.hidden_state(), np.float64)
         kind = "port"
     match = [int(a) == int(b) for a, b in zip(gpu_toks, toks)]
+    # the final-normed hidden after the sample's last step, GPU against CPU: ids
+    # alone repeat one token on this random-init model (see the full-size
+    # parity test for the per-state comparison)
+    herr = np.abs(h_gpu - h_cpu)
+    h_ok = bool(h_gpu.shape == h_cpu.shape and np.all(herr <= 1e-2 + 1e-3 * np.abs(h_cpu)))
     return {"value": round(float(np.mean(tps)), 4), "unit": "tokens/s", "cores": threads, "kind": kind,
             "sample": f"{n_prompt}-token prompt + {n_new} greedy decode steps on the same 9B-shaped model files, "
                       f"1 warmup + {runs} measured runs (reset + generate each), mean decode tok/s "
@@ -559,7 +567,9 @@ def cpu_baseline_decode(prompt, gpu_sess, runs=3):
                       f"{os.cpu_count()} host cores; load {load_s:.1f} s; prefill {np.mean(pre):.3f} tok/s",
             "runs_decode_tps": [round(t, 4) for t in tps],
             "greedy_ids_gpu": [int(t) for t in gpu_toks], "greedy_ids_cpu": [int(t) for t in toks],
-            "greedy_ids_match": all(match), "gpu_top2_margins": margins}
+            "greedy_ids_match": all(match), "gpu_top2_margins": margins,
+            "hidden_max_abs_err": float(herr.max()) if herr.size else None,
+            "hidden_within_1e-2_abs_1e-3_rel": h_ok}
 
 
 def main():

@@ -392,6 +392,13 @@ XQHIP_API int xqhip_linear_attn_scan_ws(const float* mixed, const float* a, cons
                                         int ksize, int tokens, float* out, int out_stride, void* workspace,
                                         void* stream);
 
+/* Test diagnostic, no counterpart in the reference: fills the LDS of every CU
+ * with `value` (blocks holding a CU's whole 160 KiB), so that a kernel
+ * launched next on the same stream finds that value wherever it reads LDS it
+ * has not written itself (LDS keeps its contents between kernels).  The
+ * attention tests run the decode attention right after it. */
+XQHIP_API int xqhip_lds_fill(float value, void* stream);
+
 /* ---- decode chains: consecutive projections in one persistent launch --- */
 /* A chain runs a sequence of decode-step GEMVs (the projections between two
  * non-GEMV ops of the reference's runLayer, customlib/runtime/custom_model.cpp

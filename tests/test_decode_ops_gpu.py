@@ -580,3 +580,41 @@ def test_rmsnorm_kernel():
     y = xb.DeviceBuffer(4096 * 4)
     xb.ck(xb.hip().xqhip_rmsnorm(dev(x).ptr, dev(w).ptr, 4096, 1e-6, y.ptr, None))
     close(y.download(np.float32, 4096), want, "rmsnorm", atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("fill", [1.0e30, -1.0e30])
+@pytest.mark.parametrize("kernel,pos", [("head", 511), ("head", 540), ("split", 511), ("split", 1100)])
+def test_attention_ignores_stale_lds(kernel, pos, fill):
+    """Regression guard for a fixed race: the per-head / split decode attention
+    must read no LDS word before its own block wrote it (the new token's score
+    once entered the pass maximum before the barrier that publishes it).  The
+    LDS of every CU is filled with a huge value right before the launch
+    (xqhip_lds_fill; LDS keeps its contents between kernels), then the output
+    is compared with the oracle (custom_model.cpp:840-951) at 32q/8kv d128."""
+    nq, nkv, hd, rd, gated = 32, 8, 128, 32, True
+    theta, eps, max_ctx = 1e7, 1e-6, 2048
+    print(f"stale-LDS attention case {kernel} pos {pos} fill {fill:g}", flush=True)
+    qsrc, k, v, qn, kn, kc, vc = attn_layer_inputs(nq, nkv, hd, pos, seed=pos + 29, gated=gated)
+    tab = np.empty(max_ctx * rd, np.float32)
+    xb.ck(xb.hip().xqhip_rope_table(theta, rd, max_ctx, xb.ptr(tab)))
+    kcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    vcache = np.zeros((max_ctx, nkv, hd), np.float16)
+    kcache[:pos], vcache[:pos] = kc, vc
+    kd, vd = dev(kcache), dev(vcache)
+    qs_d, k_d, v_d, qn_d, kn_d, tab_d = dev(qsrc), dev(k), dev(v), dev(qn), dev(kn), dev(tab)
+    pos_d = dev(np.array([pos], np.int32))
+    out = xb.DeviceBuffer(nq * hd * 4)
+    ws = dev(np.zeros(xb.hip().xqhip_attn_split_workspace_bytes(nq), np.uint8))
+    xb.ck(xb.hip().xqhip_device_synchronize())
+    xb.ck(xb.hip().xqhip_lds_fill(fill, None))
+    if kernel == "head":
+        xb.ck(xb.hip().xqhip_attn_decode_head(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr,
+                                              kn_d.ptr, eps, tab_d.ptr, pos_d.ptr, kd.ptr, vd.ptr, out.ptr, None))
+    else:
+        xb.ck(xb.hip().xqhip_attn_decode_split(qs_d.ptr, k_d.ptr, v_d.ptr, int(gated), nq, nkv, hd, rd, qn_d.ptr,
+                                               kn_d.ptr, eps, tab_d.ptr, pos_d.ptr, kd.ptr, vd.ptr, 8, ws.ptr,
+                                               out.ptr, None))
+    kc_got = kd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+    vc_got = vd.download(np.float16, max_ctx * nkv * hd).reshape(max_ctx, nkv, hd)
+    _, want = oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, pos, theta, eps, kc_got, vc_got)
+    close(out.download(np.float32, nq * hd), want, f"{kernel} attention after an LDS fill, pos {pos}")

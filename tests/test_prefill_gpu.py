@@ -223,3 +223,48 @@ def test_linear_scan_matches_consecutive_steps(shape, T, pos0, with_ws):
     hb = sd_b.download(np.float32, 2 * hist)[nxt * hist:(nxt + 1) * hist]
     hs = sd_s.download(np.float32, 2 * hist)[nxt * hist:(nxt + 1) * hist]
     assert np.array_equal(hb, hs)
+
+
+def test_linear_scan_130_tokens_matches_oracle():
+    """The chunked prefill recurrence (token-parallel conv pass, then 64-token
+    chunks: three chunks, the last one short) at the 9B shape (16 key heads,
+    32 value heads of 128 x 128, 4 taps) directly against the oracle's
+    per-token restatement: orc_conv1d_step + orc_l2norm_heads + the gate /
+    beta formulas + orc_gated_delta for each of 130 tokens
+    (custom_model.cpp:961-1096, ref_delta.cpp:8-41).  Outputs and the final
+    state within 1e-6 (outputs) or 5e-6 (state) abs + 1e-5 rel (measured 6e-8 and
+    7e-7; the chunked form sums in another fp32
+    order); the conv history the next decode position reads bit-exact."""
+    from test_decode_ops_gpu import oracle_linear_step
+    shape = lk_n, lv_n, lk_hd, lv_hd, ks = (16, 32, 128, 128, 4)
+    T, pos0 = 130, 7
+    rng = np.random.default_rng(130)
+    _, cstate, cw = linear_inputs(lk_n, lv_n, lk_hd, lv_hd, ks, seed=43)
+    conv_dim = 2 * lk_n * lk_hd + lv_n * lv_hd
+    stride = conv_dim + 2 * lv_n + 3
+    rows = rng.normal(0, 1, (T, stride)).astype(np.float32)
+    a_log = rng.normal(-1, 0.5, lv_n).astype(np.float32)
+    dt = rng.normal(0, 0.5, lv_n).astype(np.float32)
+    S0 = rng.normal(0, 0.1, lv_n * lk_hd * lv_hd).astype(np.float32)
+    hist = cstate.size
+    two = np.zeros(2 * hist, np.float32)
+    two[(pos0 & 1) * hist:((pos0 & 1) + 1) * hist] = cstate
+    sd, Sd, rd = dev(two), dev(S0), dev(rows)
+    out = xb.DeviceBuffer(T * lv_n * lv_hd * 4)
+    wsd = xb.DeviceBuffer(xb.hip().xqhip_linear_scan_workspace_bytes(T, lk_n, lk_hd, lv_n, lv_hd))
+    xb.ck(xb.hip().xqhip_linear_attn_scan_ws(rd.ptr, at(rd, conv_dim * 4), at(rd, (conv_dim + lv_n) * 4), stride,
+                                             sd.ptr, pos0, dev(cw).ptr, dev(a_log).ptr, dev(dt).ptr, Sd.ptr, lk_n,
+                                             lk_hd, lv_n, lv_hd, ks, T, out.ptr, lv_n * lv_hd, wsd.ptr, None))
+    got = out.download(np.float32, T * lv_n * lv_hd).reshape(T, -1)
+    st, S = cstate.copy(), S0.copy()
+    want = np.empty_like(got)
+    for t in range(T):
+        r = rows[t]
+        want[t] = oracle_linear_step(r[:conv_dim].copy(), st, cw, r[conv_dim:conv_dim + lv_n],
+                                     r[conv_dim + lv_n:conv_dim + 2 * lv_n], a_log, dt, S, shape)
+    print(f"scan vs oracle: max output err {np.abs(got - want).max():.3g}, "
+          f"max state err {np.abs(Sd.download(np.float32, S.size) - S).max():.3g}", flush=True)
+    close(got, want, "chunked scan vs oracle outputs", atol=1e-6, rtol=1e-5)
+    close(Sd.download(np.float32, S.size), S, "chunked scan vs oracle state", atol=5e-6, rtol=1e-5)
+    nxt = (pos0 + T) & 1
+    assert np.array_equal(sd.download(np.float32, 2 * hist)[nxt * hist:(nxt + 1) * hist], st)

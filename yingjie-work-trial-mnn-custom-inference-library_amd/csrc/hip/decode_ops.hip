@@ -1485,6 +1485,32 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = x[i] * inv * w[i];
 }
 
+// ---------------------------------------------------------------------------
+// LDS fill (a diagnostic for tests): every block writes `value` over the whole
+// LDS a block may hold, so a kernel launched next on the same stream finds it
+// wherever it reads LDS it has not written itself (LDS keeps its contents
+// between kernels).
+// ---------------------------------------------------------------------------
+constexpr int kLdsFillBytes = 160 * 1024;
+__global__ void __launch_bounds__(1024) lds_fill_kernel(float value) {
+    extern __shared__ float lds_all[];
+    volatile float* l = lds_all;  // stores nothing reads in this kernel stay
+    for (int i = threadIdx.x; i < kLdsFillBytes / 4; i += 1024) l[i] = value;
+}
+
+hipError_t launch_lds_fill(float value, hipStream_t s) {
+    const auto fn = reinterpret_cast<const void*>(&lds_fill_kernel);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsFillBytes);
+    if (e != hipSuccess) return e;
+    int dev = 0, cus = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    // one block fills a CU's whole LDS, so no two run on one CU at once; twice
+    // the CU count reaches every CU
+    hipLaunchKernelGGL(lds_fill_kernel, dim3(2 * cus), dim3(1024), kLdsFillBytes, s, value);
+    return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s) {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, x, w, n, eps, y);
     return hipGetLastError();

@@ -972,6 +972,10 @@ int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, vo
     return check(xqhip::launch_rmsnorm(x, w, n, eps, y, as_stream(stream)), "rmsnorm launch");
 }
 
+int xqhip_lds_fill(float value, void* stream) {
+    return check(xqhip::launch_lds_fill(value, as_stream(stream)), "lds fill launch");
+}
+
 int xqhip_stream_create(void** stream) {
     hipStream_t s;
     if (int rc = check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return rc;

@@ -165,6 +165,7 @@ bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
 hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s);
 
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
+hipError_t launch_lds_fill(float value, hipStream_t s);
 
 // prefill_ops.hip: multi-token kernels of a prompt chunk.
 struct GemmLaunch {

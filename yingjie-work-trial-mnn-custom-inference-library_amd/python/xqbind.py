@@ -130,6 +130,7 @@ _HIP_SIGS = {
                                           c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                           c_int, c_void_p, c_void_p]),
     "xqhip_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]),
+    "xqhip_lds_fill": (c_int, [c_float, c_void_p]),
     "xqhip_chain_create": (c_int, [_P(ChainOp), c_int, _P(c_void_p)]),
     "xqhip_chain_destroy": (c_int, [c_void_p]),
     "xqhip_chain_arena_records": (c_size_t, [c_void_p]),
