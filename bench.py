@@ -413,8 +413,9 @@ def bench_decode(args):
         st, tok, m = sess.decode_one()
         assert st == 0
     # timed: fresh prefill and the first decode step after it (untimed: that
-    # step launches its kernels one by one with per-op events for the kernel
-    # trace), then exactly K decode steps, each a pair of captured graphs
+    # step replays the traced copy of the step graph, timestamps between its
+    # ops for the kernel trace), then exactly K decode steps, each one graph
+    # launch (every 128th the traced copy)
     assert sess.lib.xq_reset(sess.h) == 0
     st, m = sess.prefill(prompt)
     assert st == 0, m.error
@@ -438,6 +439,9 @@ def bench_decode(args):
     dn = next((r for n, r in rows.items() if n.startswith("linear_down_proj")), None)
     lm = next((r for n, r in rows.items() if n.startswith("lm_head_custom")), None)
     step = rows.get("decode_step_graph_custom")
+    traced = rows.get("decode_step_graph_traced_custom")
+    st_tr, txt_tr = sess.json("xq_get_kernel_trace_json", 1 << 22)
+    trace_counts = {k: v for k, v in json.loads(txt_tr).items() if k != "rows"} if st_tr == 0 else {}
     bytes_gu = w4_bytes(2 * inter, hidden) + hidden * 4 + inter * 4
     bytes_dn = w4_bytes(hidden, inter) + inter * 4 + 2 * hidden * 4
     bytes_lm = w4_bytes(248320, hidden) + hidden * 4
@@ -464,6 +468,8 @@ def bench_decode(args):
                                "decode steps",
                    "prompt_tokens": prompt_len, "weight_bytes_per_token": wbytes,
                    "graph_step_ms": round(step_ms, 4), "decode_total_ms_from_xq_metrics": round(decode_ms, 3),
+                   "traced_graph_step_ms": round(traced["mean_ms"], 4) if traced else None,
+                   "kernel_trace_sampling": trace_counts,
                    "weight_stream_GBps": round(wbytes / (step_ms * 1e-3) / 1e9, 1),
                    "prefill_ms": round(prefill_ms, 2), "prefill_tokens_per_s": round(prompt_len / prefill_ms * 1e3, 1),
                    "model_write_s": round(gen_s, 1), "load_s": round(load_s, 1)},

@@ -209,8 +209,9 @@ XQHIP_API int xqhip_gemv_w4a16_argmax_publish(const xqhip_w4* w, const void* x, 
  * of the library's own device memory (one per GPU, held until the process
  * ends; any matrix size fits, the launch caps its blocks), which keeps the last
  * call's contents and needs no clearing.  Calls that overlap on one GPU (other
- * streams, other threads) race on that array: serialise them.  Same results as
- * xqhip_gemv_w4a16_argmax. */
+ * streams, other threads) race on that array: serialise them.  The array used
+ * is the current device's: a non-NULL `stream` must belong to that device
+ * (XQHIP_EINVAL otherwise).  Same results as xqhip_gemv_w4a16_argmax. */
 XQHIP_API int xqhip_gemv_w4a16_argmax_static(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
                                              int32_t* out_index, float* out_value, void* stream);
 
@@ -286,7 +287,8 @@ XQHIP_API int xqhip_attn_decode_head(const float* q_src, const float* k_src, con
  * every call leaves the counters at zero again, and calls that overlap on one
  * device race on them.  Replaces the same reference code as
  * xqhip_attn_decode_head (custom_model.cpp:740-951). */
-#define XQHIP_ATTN_PART_STRIDE 132 /* floats per (split, head): m, l, 2 pad, o[128] */
+#define XQHIP_ATTN_PART_STRIDE 160 /* floats per (split, head): m, l, 2 pad, o[128], pad to
+                                      five 128-byte lines (no line holds two records) */
 #define XQHIP_ATTN_MAX_SPLITS 8
 XQHIP_API size_t xqhip_attn_split_workspace_bytes(int nq);
 XQHIP_API int xqhip_attn_decode_split(const float* q_src, const float* k_src, const float* v_src, int gated, int nq,
@@ -347,10 +349,12 @@ XQHIP_API size_t xqhip_gemm_workspace_bytes(int m, int cols, int rows);
  * as fp16 hi + lo halves on fp16 MFMA with fp32 accumulation, the group sum is
  * scaled by the group scale, and the zero-point term is added as the product of
  * the per-group offsets with the per-token group sums of x.  GATED_HEAD reads the gate
- * of token t at pro->gate + t * ld_gate.  workspace: 16-byte aligned,
- * xqhip_gemm_workspace_bytes(m, cols, rows of w). */
+ * of token t at pro->gate + t * ld_gate.  workspace: 16-byte aligned, of
+ * workspace_bytes >= xqhip_gemm_workspace_bytes(m, cols, rows of w) (checked:
+ * XQHIP_EINVAL when smaller). */
 XQHIP_API int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro,
-                               int ld_gate, float* y, int ldy, int epilogue, void* workspace, void* stream);
+                               int ld_gate, float* y, int ldy, int epilogue, void* workspace, size_t workspace_bytes,
+                               void* stream);
 /* xqhip_embed_bf16 for n tokens (device ids) into out[n][hidden]. */
 XQHIP_API int xqhip_embed_bf16_batch(const uint16_t* table, int vocab, int hidden, const int32_t* tokens, int n,
                                      float* out, void* stream);
@@ -392,6 +396,13 @@ XQHIP_API int xqhip_linear_attn_scan_ws(const float* mixed, const float* a, cons
                                         int ksize, int tokens, float* out, int out_stride, void* workspace,
                                         void* stream);
 
+/* One kernel of one thread that stores the device's 100 MHz realtime counter
+ * (s_memrealtime) to *slot with a system-scope store; slot may be device or
+ * coherent host memory (xqhip_host_alloc_coherent).  Between two kernels on a
+ * stream it marks the end of the first; graph-capturable.  Times the ops of
+ * traced decode-step graphs (the kernel trace's per-op rows, after
+ * custom_model.cpp:374-417). */
+XQHIP_API int xqhip_timestamp(uint64_t* slot, void* stream);
 /* Test diagnostic, no counterpart in the reference: fills the LDS of every CU
  * with `value` (blocks holding a CU's whole 160 KiB), so that a kernel
  * launched next on the same stream finds that value wherever it reads LDS it

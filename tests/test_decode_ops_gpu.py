@@ -568,7 +568,7 @@ def test_linear_step_act_matches_step_and_activates_gate(shape):
     ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(4, lv_n * lv_hd, hidden))
     pro = xb.prologue(xb.PRO_GATED_HEAD_ACT, nw, z_act, head_dim=lv_hd, eps=1e-6)
     assert xb.hip().xqhip_gemm_w4a16(w4.ref, xo.ptr, 1, lv_n * lv_hd, ctypes.byref(pro), lv_n * lv_hd, y.ptr,
-                                     hidden, xb.EPI_STORE, ws.ptr, None) == -1
+                                     hidden, xb.EPI_STORE, ws.ptr, ws.nbytes, None) == -1
 
 
 def test_rmsnorm_kernel():

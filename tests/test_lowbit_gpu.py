@@ -120,7 +120,7 @@ def test_lowbit_rejected_by_prefill_gemm_and_bad_widths():
     x = xb.DeviceBuffer(4 * 256 * 4)
     y = xb.DeviceBuffer(4 * 64 * 4)
     ws = xb.DeviceBuffer(xb.hip().xqhip_gemm_workspace_bytes(4, 256, 64))
-    rc = xb.hip().xqhip_gemm_w4a16(w.ref, x.ptr, 4, 256, None, 0, y.ptr, 64, xb.EPI_STORE, ws.ptr, None)
+    rc = xb.hip().xqhip_gemm_w4a16(w.ref, x.ptr, 4, 256, None, 0, y.ptr, 64, xb.EPI_STORE, ws.ptr, ws.nbytes, None)
     assert rc != 0 and b"4-bit" in xb.hip().xqhip_last_error()
     bad = xb.W4()
     rc = xb.hip().xqhip_wlb_upload(ob.p(q.packed), ob.p(q.scales), ob.p(q.zeros), 64, 256, 64, 5, 0,

@@ -335,3 +335,36 @@ def test_decode_chain_matches_per_op_launches(which, small_dir, heads9b_dir, mon
     for a, b in zip(runs["chain"][1], runs["default"][1]):
         assert np.array_equal(a, b)
     assert "decode_chain_w4a16" in runs["chain"][2] and "decode_chain_w4a16" not in runs["default"][2]
+
+
+def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch):
+    """Kernel-trace rows of decode (the reference times every op of every step,
+    custom_model.cpp:374-417, and exports them through session.cpp:556-566):
+    every step is one graph launch timed on its own (decode_step_graph_custom,
+    one row entry per untraced step), and the first step after the prefill
+    plus every XQ_TRACE_EVERY-th step replay the traced copy of the step graph
+    whose per-op events give the per-op rows (each op one call per traced
+    step); the JSON says how many steps the rows were sampled from."""
+    monkeypatch.setenv("XQ_TRACE_EVERY", "16")
+    s = xb.Session(small_dir, xb.options())
+    assert s.status == xb.XQ_OK
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, 4096, 20)]
+    st, toks, m = s.generate(prompt, 40)
+    assert st == 0, m.error
+    tr = json.loads(s.json("xq_get_kernel_trace_json")[1])
+    rows = {r["name"]: r for r in tr["rows"]}
+    traced = 1 + 40 // 16  # the first step after the prefill, then steps 16 and 32
+    assert tr["decode_graph_steps"] == 40 and tr["decode_op_traced_graph_steps"] == traced
+    assert tr["decode_op_trace_every"] == 16
+    assert rows["decode_step_graph_custom"]["calls"] == 40 - traced
+    assert rows["decode_step_graph_traced_custom"]["calls"] == traced
+    assert rows["lm_head_custom(fused:rmsnorm_final,argmax)"]["calls"] == traced
+    assert rows["sampling_greedy_custom"]["calls"] == traced
+    step = rows["decode_step_graph_custom"]
+    assert 0 < step["min_ms"] < step["max_ms"]  # per-step times, not an average spread over steps
+    for name in ("linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
+                 "attention_score_custom"):
+        assert rows[name]["calls"] % traced == 0 and rows[name]["calls"] > 0, name
+    info = s.json("xq_get_backend_info")[1]
+    assert "kernel_trace=per_op_every_16_graph_steps" in info
+    s.close()

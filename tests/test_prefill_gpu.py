@@ -60,7 +60,7 @@ def run_gemm(q, X, epi, pro=None, gamma=None, z=None, head_dim=0, y0=None):
         pr = xb.prologue(xb.PRO_GATED_HEAD, dev(gamma), gate=zd, head_dim=head_dim, eps=1e-6)
         ld_gate = z.shape[1]
     xb.ck(xb.hip().xqhip_gemm_w4a16(w.ref, dev(X).ptr, m, cols, ctypes.byref(pr) if pr else None, ld_gate,
-                                    ydev.ptr, out_cols, epi, ws.ptr, None))
+                                    ydev.ptr, out_cols, epi, ws.ptr, ws.nbytes, None))
     return ydev.download(np.float32, m * out_cols).reshape(m, out_cols)
 
 
@@ -268,3 +268,21 @@ def test_linear_scan_130_tokens_matches_oracle():
     close(Sd.download(np.float32, S.size), S, "chunked scan vs oracle state", atol=5e-6, rtol=1e-5)
     nxt = (pos0 + T) & 1
     assert np.array_equal(sd.download(np.float32, 2 * hist)[nxt * hist:(nxt + 1) * hist], st)
+
+
+def test_gemm_rejects_a_short_workspace():
+    """The workspace holds the staged x and, for launches split over the columns,
+    the partial products of every row: one sized for fewer rows is refused
+    (XQHIP_EINVAL) instead of being written past its end."""
+    rows, cols, m = 4096, 4096, 64
+    q = w4_matrix(rows, cols, 3)
+    w = xb.DeviceW4(q.packed, q.scales, q.zeros, rows, cols)
+    x, y = dev(np.zeros((m, cols), np.float32)), xb.DeviceBuffer(m * rows * 4)
+    need = xb.hip().xqhip_gemm_workspace_bytes(m, cols, rows)
+    short = xb.hip().xqhip_gemm_workspace_bytes(m, cols, 0)
+    ws = xb.DeviceBuffer(need)
+    if short < need:  # a split launch: the partial products need room
+        assert xb.hip().xqhip_gemm_w4a16(w.ref, x.ptr, m, cols, None, 0, y.ptr, rows, xb.EPI_STORE, ws.ptr, short,
+                                         None) == -1
+        assert b"workspace" in xb.hip().xqhip_last_error()
+    xb.ck(xb.hip().xqhip_gemm_w4a16(w.ref, x.ptr, m, cols, None, 0, y.ptr, rows, xb.EPI_STORE, ws.ptr, need, None))

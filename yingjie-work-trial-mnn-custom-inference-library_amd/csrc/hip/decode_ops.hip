@@ -1053,6 +1053,15 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_part_kernel(AttnDeco
             default: head_attention<HD, 8, true>(a, sm, pos, c0, c1, fresh, out); break;
         }
     }
+    // Ordering without fences: every partial store above is an agent-scope
+    // store (written through the L2) and this wait completes them, so they
+    // are visible device-wide before the counter's atomic is issued; the
+    // merging block reads them with agent-scope loads (which bypass the L2)
+    // after its atomic has returned the final count.  That is the release /
+    // acquire sequence of the target's memory model minus its L2 write-back
+    // and invalidate, which only non-agent-scope accesses would need (and
+    // which cost 22-32 us per launch when measured).  Records are padded to
+    // whole 128-byte lines.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
     __syncthreads();
     __shared__ int last;
@@ -1483,6 +1492,23 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
     for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = x[i] * inv * w[i];
+}
+
+// ---------------------------------------------------------------------------
+// Timestamp: one thread stores the device's 100 MHz realtime counter to *slot
+// with a system-scope store (a slot in coherent host memory is read by the
+// host without a copy).  Between two kernels of a stream it marks the end of
+// the first and the start of the second; used to time the ops of a traced
+// decode-step graph, where event-record nodes give no timings.
+// ---------------------------------------------------------------------------
+__global__ void timestamp_kernel(uint64_t* slot) {
+    __hip_atomic_store(slot, static_cast<uint64_t>(__builtin_amdgcn_s_memrealtime()), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+hipError_t launch_timestamp(uint64_t* slot, hipStream_t s) {
+    hipLaunchKernelGGL(timestamp_kernel, dim3(1), dim3(1), 0, s, slot);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

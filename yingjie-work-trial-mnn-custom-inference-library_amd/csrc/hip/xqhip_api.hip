@@ -88,13 +88,23 @@ __global__ void copy_u32x4_kernel(uint4* __restrict__ dst, const uint4* __restri
 }
 
 // Address of `scratch` on the current device, resolved once per device with
-// that device current.  nullptr (and the error set) on failure.
+// that device current.  A launch stream must belong to that device (its
+// kernels would otherwise write another device's copy).  nullptr (and the
+// error set) on failure.
 constexpr int kMaxDevices = 64;
-void* static_scratch() {
+void* static_scratch(hipStream_t stream = nullptr) {
     static std::mutex mu;
     static void* addr[kMaxDevices] = {};
     int dev = 0;
     if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (stream) {
+        int sdev = 0;
+        if (check(hipStreamGetDevice(stream, &sdev), "hipStreamGetDevice")) return nullptr;
+        if (sdev != dev) {
+            fail(XQHIP_EINVAL, "the stream belongs to device %d, the current device is %d", sdev, dev);
+            return nullptr;
+        }
+    }
     if (dev < 0 || dev >= kMaxDevices) {
         fail(XQHIP_EDEVICE, "device %d beyond the %d devices the static scratch covers", dev, kMaxDevices);
         return nullptr;
@@ -241,8 +251,14 @@ int xqhip_event_query(void* ev) {
 
 int xqhip_event_elapsed_ms(void* start, void* stop, float* ms) {
     if (int rc = check(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize")) return rc;
-    return check(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
-                 "hipEventElapsedTime");
+    const hipError_t e = hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));
+    if (e != hipSuccess) (void)hipGetLastError();  // not left behind for the next launch's error check
+    return check(e, "hipEventElapsedTime");
+}
+
+int xqhip_timestamp(uint64_t* slot, void* stream) {
+    if (!slot) return fail(XQHIP_EINVAL, "xqhip_timestamp: null slot");
+    return check(xqhip::launch_timestamp(slot, as_stream(stream)), "timestamp launch");
 }
 
 // fp16 (scale, zero) pairs of the TILED64 layout; returns the count of inexact values.
@@ -580,8 +596,8 @@ int xqhip_gemv_w4a16_argmax_static(const xqhip_w4* w, const void* x, int x_type,
     if (need > sizeof(scratch))
         return fail(XQHIP_EINVAL, "xqhip_gemv_w4a16_argmax_static: needs %zu bytes of scratch, the library holds %zu",
                     need, sizeof(scratch));
-    void* ptr = static_scratch();
-    if (!ptr) return XQHIP_EDEVICE;
+    void* ptr = static_scratch(as_stream(stream));
+    if (!ptr) return std::strstr(g_err.c_str(), "the stream belongs") ? XQHIP_EINVAL : XQHIP_EDEVICE;
     // the keys need no clearing: every block of the launch writes its own
     // before the finishing kernel reads exactly those
     return xqhip_gemv_w4a16_argmax(w, x, x_type, pro, ptr, out_index, out_value, stream);
@@ -827,7 +843,7 @@ size_t xqhip_gemm_workspace_bytes(int m, int cols, int rows) {
 }
 
 int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xqhip_prologue* pro, int ld_gate,
-                     float* y, int ldy, int epilogue, void* workspace, void* stream) {
+                     float* y, int ldy, int epilogue, void* workspace, size_t workspace_bytes, void* stream) {
     if (int rc = validate_w4(w, "xqhip_gemm_w4a16")) return rc;
     if (w->bits != 4) return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: 4-bit matrices only (got %d bits)", w->bits);
     if (int rc = validate_prologue(pro, w->cols, "xqhip_gemm_w4a16", false)) return rc;
@@ -845,6 +861,9 @@ int xqhip_gemm_w4a16(const xqhip_w4* w, const float* x, int m, int ldx, const xq
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: needs a TILED64 matrix (%dx%d g%d)", w->rows, w->cols, w->group);
     if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: workspace must be 16-byte aligned");
+    // the staged x and, for launches split over the columns, the partial products
+    if (const size_t need = xqhip::gemm_workspace_bytes(m, w->cols, w->rows); workspace_bytes < need)
+        return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: workspace of %zu bytes, %zu needed", workspace_bytes, need);
     // the kernels address the staged x (hi and lo halves) with 32-bit buffer offsets
     if (xqhip::gemm_workspace_bytes(m, w->cols, 0) >= (size_t{1} << 31))
         return fail(XQHIP_EINVAL, "xqhip_gemm_w4a16: %d tokens of %d columns exceed one call (2 GiB of staged x)", m,

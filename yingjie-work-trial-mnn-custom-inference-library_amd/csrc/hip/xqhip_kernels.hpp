@@ -12,7 +12,7 @@ constexpr int kMaxNormHeads = 256;
 // Split decode attention partials (attn_decode_part_kernel): per split and
 // query head, the running max at 0, the exp sum at 1 and the head_dim (128)
 // exp-weighted value sums from kAttnPartO (16-byte aligned rows).
-constexpr int kAttnPartO = 4, kAttnPartStride = kAttnPartO + 128, kAttnMaxSplits = 8;
+constexpr int kAttnPartO = 4, kAttnPartStride = 160, kAttnMaxSplits = 8;  // a record fills five 128-byte lines
 
 // Normalisation applied to the GEMV input inside the kernel prologue.
 struct Prologue {
@@ -166,6 +166,7 @@ hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s);
 
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
 hipError_t launch_lds_fill(float value, hipStream_t s);
+hipError_t launch_timestamp(uint64_t* slot, hipStream_t s);
 
 // prefill_ops.hip: multi-token kernels of a prompt chunk.
 struct GemmLaunch {

@@ -60,15 +60,16 @@ DeviceModel::~DeviceModel() {
     if (g_prefill_) xqhip_graph_destroy(g_prefill_);
     if (g_step_) xqhip_graph_destroy(g_step_);
     for (void* c : chains_) xqhip_chain_destroy(c);
-    for (auto& pair : step_ev_)
-        for (void* e : pair)
-            if (e) xqhip_event_destroy(e);
+    if (g_step_traced_) xqhip_graph_destroy(g_step_traced_);
+    for (void* e : step_ev_)
+        if (e) xqhip_event_destroy(e);
     for (xqhip_w4* m : matrices_) xqhip_w4_free(m);
     for (void* p : allocations_) xqhip_free(p);
     for (void* e : event_pool_) xqhip_event_destroy(e);
     if (h_ctrl_) xqhip_host_free(h_ctrl_);
     if (h_tok_) xqhip_host_free(h_tok_);
     if (h_slot_) xqhip_host_free(h_slot_);
+    if (h_ts_) xqhip_host_free(h_ts_);
     if (stream_) release_stream();
 }
 
@@ -309,9 +310,14 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     if (xqhip_host_alloc_coherent(&pinned, sizeof(uint64_t)) != 0) return fail_hip(error, "coherent host memory");
     h_slot_ = static_cast<uint64_t*>(pinned);
     *h_slot_ = ~0ull;
-    for (auto& pair : step_ev_)
-        for (void*& e : pair)
-            if (xqhip_event_create(&e) != 0) return fail_hip(error, "event");
+    if (xqhip_host_alloc_coherent(&pinned, sizeof(uint64_t) * kMaxTimestamps) != 0)
+        return fail_hip(error, "coherent host memory");
+    h_ts_ = static_cast<uint64_t*>(pinned);
+    for (void*& e : step_ev_)
+        if (xqhip_event_create(&e) != 0) return fail_hip(error, "event");
+    if (const char* v = std::getenv("XQ_TRACE_EVERY")) trace_every_ = std::max(0, std::atoi(v));
+    trace_note_ = trace_every_ > 0 ? "per_op_every_" + std::to_string(trace_every_) + "_graph_steps"
+                                   : std::string("per_op_first_step_after_prefill");
     if (!build_chains(error)) return false;
     reset_state();
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "load sync");
@@ -484,10 +490,7 @@ bool DeviceModel::ensure_capacity(size_t positions, std::string* error) {
     }
     max_ctx_ = new_ctx;
     if (!build_rope_table(error)) return false;
-    for (void** g : {&g_prefill_, &g_step_}) {
-        if (*g) xqhip_graph_destroy(*g);
-        *g = nullptr;
-    }
+    drop_graphs();
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "KV cache growth");
 }
 
@@ -520,10 +523,7 @@ bool DeviceModel::select_attention(size_t ctx, KernelTrace* trace, std::string* 
     if (want == attn_mode_) return true;
     if (!sync(trace, error)) return false;
     attn_mode_ = want;
-    for (void** g : {&g_prefill_, &g_step_}) {
-        if (*g) xqhip_graph_destroy(*g);
-        *g = nullptr;
-    }
+    drop_graphs();
     return true;
 }
 
@@ -542,15 +542,26 @@ void DeviceModel::reset_state() {  // custom_model.cpp:555-567 (KV slots past th
 
 bool DeviceModel::op_begin(bool timed, const std::string& name, std::vector<std::string> extra, int split) {
     if (!timed) return true;
+    TimedOp op;
+    op.name = name;
+    op.extra_names = std::move(extra);
+    op.split = split;
+    if (ts_mode_) {  // traced graph: a timestamp kernel before the op (unless the previous op's end marks it)
+        if (op_chained_ && !ops_.empty()) {
+            op.ts0 = ops_.back().ts1;
+        } else {
+            if (ts_next_ >= kMaxTimestamps || xqhip_timestamp(h_ts_ + ts_next_, stream_) != 0) return false;
+            op.ts0 = ts_next_++;
+        }
+        op_chained_ = false;
+        ops_.push_back(std::move(op));
+        return true;
+    }
     while (event_pool_.size() < event_next_ + 2) {
         void* e = nullptr;
         if (xqhip_event_create(&e) != 0) return false;
         event_pool_.push_back(e);
     }
-    TimedOp op;
-    op.name = name;
-    op.extra_names = std::move(extra);
-    op.split = split;
     op.ev0 = event_pool_[event_next_++];
     op.ev1 = event_pool_[event_next_++];
     // an op that directly follows the previous one starts at its end event:
@@ -566,7 +577,11 @@ bool DeviceModel::op_begin(bool timed, const std::string& name, std::vector<std:
 
 void DeviceModel::op_end(bool timed) {
     if (!timed || ops_.empty()) return;
-    xqhip_event_record(ops_.back().ev1, stream_);
+    if (ts_mode_) {
+        if (ts_next_ < kMaxTimestamps && xqhip_timestamp(h_ts_ + ts_next_, stream_) == 0) ops_.back().ts1 = ts_next_++;
+    } else {
+        xqhip_event_record(ops_.back().ev1, stream_);
+    }
     op_chained_ = true;
 }
 
@@ -720,6 +735,14 @@ static bool graphs_enabled() {
     return !(v && v[0] == '0');
 }
 
+void DeviceModel::drop_graphs() {
+    for (void** g : {&g_prefill_, &g_step_, &g_step_traced_}) {
+        if (*g) xqhip_graph_destroy(*g);
+        *g = nullptr;
+    }
+    traced_ops_.clear();
+}
+
 bool DeviceModel::ensure_graphs(std::string* error) {
     if (!graphs_enabled()) return true;  // eager launches of the same kernels
     if (g_prefill_ && g_step_) return true;
@@ -731,11 +754,40 @@ bool DeviceModel::ensure_graphs(std::string* error) {
         *out = g;
         return true;
     };
-    return capture(&g_prefill_, [&] { return enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error); }) &&
-           capture(&g_step_, [&] {
-               return enqueue_lm_head(false, error) && enqueue_embed(d_ctrl_ + 2, false, error) &&
-                      enqueue_layers(false, error);
-           });
+    if (!capture(&g_prefill_, [&] { return enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error); }) ||
+        !capture(&g_step_, [&] {
+            return enqueue_lm_head(false, error) && enqueue_embed(d_ctrl_ + 2, false, error) &&
+                   enqueue_layers(false, error);
+        }))
+        return false;
+    // the traced step: the same launches with a timestamp kernel after every
+    // op (event-record nodes of a graph give no timings here)
+    ops_.clear();
+    event_next_ = 0;
+    op_chained_ = false;
+    ts_next_ = 0;
+    ts_mode_ = true;
+    void* g = nullptr;
+    std::string ignored;
+    bool ok = xqhip_graph_begin(stream_) == 0;
+    if (ok) {
+        const bool enq = enqueue_lm_head(true, &ignored) && enqueue_embed(d_ctrl_ + 2, true, &ignored) &&
+                         enqueue_layers(true, &ignored);
+        ok = xqhip_graph_end(stream_, &g) == 0 && enq;
+    }
+    ts_mode_ = false;
+    for (const TimedOp& op : ops_) ok = ok && op.ts0 >= 0 && op.ts1 >= 0;
+    if (ok) {
+        g_step_traced_ = g;
+        traced_ops_ = std::move(ops_);
+    } else {
+        if (g) xqhip_graph_destroy(g);
+        trace_note_ = "per_op_first_eager_step_after_prefill(traced_graph_unavailable)";
+    }
+    ops_.clear();
+    event_next_ = 0;
+    op_chained_ = false;
+    return true;
 }
 
 // Batched prefill needs every matrix in the TILED64 layout (group 64) and the
@@ -764,6 +816,7 @@ bool DeviceModel::alloc_prefill_buffers(std::string* error) {
         !alloc(&ws, ws_bytes, error) || !alloc(&tok_dev_, c, error))
         return false;
     gemm_ws_ = ws;
+    gemm_ws_bytes_ = ws_bytes;
     bool any_linear = false;
     for (const Layer& L : layers_) any_linear |= !L.full;
     if (any_linear) {
@@ -781,8 +834,6 @@ bool DeviceModel::alloc_prefill_buffers(std::string* error) {
 bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, int n, int pos0, bool timed,
                                 std::string* error) {
     XQ_CALL(xqhip_memcpy_h2d_async(tok_dev_, h_tokens, sizeof(int32_t) * n, stream_), "prompt upload");
-    dev_pos_ = kPosUnknown;
-    chained_ = false;
     XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_pos, sizeof(int32_t), stream_), "position upload");
     const int32_t* pos = d_ctrl_;
     op_begin(timed, "prefill_embedding_bf16_rows");
@@ -794,7 +845,7 @@ bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, i
         op_begin(timed, L.full ? "prefill_gemm_w4a16_mfma(q_proj,k_proj,v_proj,rmsnorm_input)"
                                : "prefill_gemm_w4a16_mfma(in_proj_qkv,in_proj_a,in_proj_b,in_proj_z,rmsnorm_input)");
         XQ_CALL(xqhip_gemm_w4a16(&L.in_proj, x_all_, n, hidden_, &rms_in, 0, proj_all_, max_proj_, XQHIP_EPI_STORE,
-                                 gemm_ws_, stream_),
+                                 gemm_ws_, gemm_ws_bytes_, stream_),
                 "prefill input projection");
         op_end(timed);
         if (L.full) {
@@ -813,7 +864,7 @@ bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, i
             op_end(timed);
             op_begin(timed, "prefill_gemm_w4a16_mfma(o_proj,residual_add)");
             XQ_CALL(xqhip_gemm_w4a16(&L.out_proj, attn_all_, n, attn_n_, nullptr, 0, x_all_, hidden_, XQHIP_EPI_ADD,
-                                     gemm_ws_, stream_),
+                                     gemm_ws_, gemm_ws_bytes_, stream_),
                     "prefill o projection");
             op_end(timed);
         } else {
@@ -829,19 +880,19 @@ bool DeviceModel::prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, i
             xqhip_prologue gated{XQHIP_PRO_GATED_HEAD, lv_hd_, L.lin_norm, z, eps_};
             op_begin(timed, "prefill_gemm_w4a16_mfma(out_proj,gated_rmsnorm,residual_add)");
             XQ_CALL(xqhip_gemm_w4a16(&L.out_proj, attn_all_, n, attn_n_, &gated, max_proj_, x_all_, hidden_,
-                                     XQHIP_EPI_ADD, gemm_ws_, stream_),
+                                     XQHIP_EPI_ADD, gemm_ws_, gemm_ws_bytes_, stream_),
                     "prefill out projection");
             op_end(timed);
         }
         xqhip_prologue rms_post{XQHIP_PRO_RMS, 0, L.post_norm, nullptr, eps_};
         op_begin(timed, "prefill_gemm_w4a16_mfma(gate_proj,up_proj,rmsnorm_post_attention,silu_gate_mul)");
         XQ_CALL(xqhip_gemm_w4a16(&L.gate_up, x_all_, n, hidden_, &rms_post, 0, ffn_all_, inter_, XQHIP_EPI_SILU_PAIR,
-                                 gemm_ws_, stream_),
+                                 gemm_ws_, gemm_ws_bytes_, stream_),
                 "prefill gate/up projection");
         op_end(timed);
         op_begin(timed, "prefill_gemm_w4a16_mfma(down_proj,residual_add)");
         XQ_CALL(xqhip_gemm_w4a16(&L.down, ffn_all_, n, inter_, nullptr, 0, x_all_, hidden_, XQHIP_EPI_ADD, gemm_ws_,
-                                 stream_),
+                                 gemm_ws_bytes_, stream_),
                 "prefill down projection");
         op_end(timed);
     }
@@ -917,8 +968,6 @@ bool DeviceModel::prefill(const int32_t* token_ids, size_t n_tokens, KernelTrace
     for (size_t i = 0; i < n_tokens; ++i) {
         h_ctrl_[2 * i] = static_cast<int32_t>(i);
         h_ctrl_[2 * i + 1] = token_ids[i];
-        dev_pos_ = kPosUnknown;
-    chained_ = false;
         XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_ctrl_ + 2 * i, 2 * sizeof(int32_t), stream_), "control upload");
         if ((i == 0 && detail_prefill_) || !g_prefill_) {
             const bool timed = i == 0 && detail_prefill_;
@@ -966,9 +1015,11 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         h_tok_[1] = 0;
         XQ_CALL(xqhip_memcpy_h2d_async(d_ctrl_, h_tok_, 2 * sizeof(int32_t), stream_), "control upload");
     }
-    if (detail_decode_ || !g_step_) {
+    if (trace) trace_ = trace;
+    if (!g_step_ || (detail_decode_ && !g_step_traced_)) {
+        // eager launches (graphs off, or no traced graph for the first step
+        // after a prefill): per-op events, the whole step waited for
         chained_ = false;
-        // per-op events: the whole step is waited for before its times are read
         const bool timed = detail_decode_;
         if (!sync(trace, error)) return false;
         if (!enqueue_lm_head(timed, error)) return false;
@@ -980,23 +1031,26 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         flush_timed(trace);
         return true;
     }
-    // one graph samples, publishes the token, advances the position and runs
-    // the forward pass; return once the token is published
-    // Step timing: consecutive graph steps form a segment that starts at an
-    // event (its own, or the end event of the segment before it) and ends at
-    // the event recorded after its kStepsPerEvent-th step, so most steps
-    // carry no marker packet between their graphs; each of a segment's steps
-    // is credited the segment's time / its steps.
-    if (!chained_ || upload) {
-        if (seg_steps_ > 0 && !sync(trace, error)) return false;  // closes the open segment
-        seg_start_ = step_ev_[seg_slot_][0];
-        XQ_CALL(xqhip_event_record(seg_start_, stream_), "step event");
-        seg_steps_ = 0;
+    // One graph samples, publishes the token, advances the position and runs
+    // the forward pass; the call returns once the token is published.  The
+    // step is timed from the previous graph step's end event (or an event of
+    // its own when it does not follow one) to its own end event; the traced
+    // graph (an event after every op) replaces it on the first step after a
+    // prefill and on every trace_every_-th graph step.
+    ++graph_steps_;
+    const bool traced = g_step_traced_ &&
+                        (detail_decode_ || (trace_every_ > 0 && graph_steps_ % static_cast<uint64_t>(trace_every_) == 0));
+    void* start = last_end_;
+    if (!chained_ || upload || !start) {
+        start = next_step_event();
+        XQ_CALL(xqhip_event_record(start, stream_), "step event");
     }
     chained_ = false;
-    XQ_CALL(xqhip_graph_launch(g_step_, stream_), "decode step graph");
-    const bool closes = ++seg_steps_ == kStepsPerEvent;
-    if (closes) XQ_CALL(xqhip_event_record(step_ev_[seg_slot_][1], stream_), "step event");
+    XQ_CALL(xqhip_graph_launch(traced ? g_step_traced_ : g_step_, stream_), "decode step graph");
+    void* end = next_step_event();
+    XQ_CALL(xqhip_event_record(end, stream_), "step event");
+    pending_.push_back(PendingStep{start, end, traced});
+    detail_decode_ = false;
     for (uint32_t spin = 1;; ++spin) {
         if (static_cast<uint32_t>(__atomic_load_n(h_slot_, __ATOMIC_ACQUIRE) >> 32) == static_cast<uint32_t>(want))
             break;
@@ -1015,27 +1069,44 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     }
     if (!read_slot(want, token_id, error)) return false;
     dev_pos_ = want;
-    // a segment closed by an earlier call ended before this step's sampling: complete
-    credit_segment(trace);
-    if (closes) {
-        pend_start_ = seg_start_;
-        pend_end_ = step_ev_[seg_slot_][1];
-        pend_steps_ = seg_steps_;
-        seg_start_ = pend_end_;  // the next segment starts where this one ended
-        seg_steps_ = 0;
-        seg_slot_ = (seg_slot_ + 1) % 3;
-    }
+    // this step's sampling ran after every earlier step had finished
+    credit_steps(trace, pending_.size() - 1);
+    last_end_ = end;
     chained_ = true;
     return true;
 }
 
-// Credits the closed segment (if any) to the trace, one row per step.
-void DeviceModel::credit_segment(KernelTrace* trace) {
-    if (pend_steps_ > 0 && trace) {
-        const double ms = elapsed_ms(pend_start_, pend_end_) / pend_steps_;
-        for (int i = 0; i < pend_steps_; ++i) trace->add("decode_step_graph_custom", ms, kTraceBackend);
+void* DeviceModel::next_step_event() {
+    void* e = step_ev_[step_ev_next_];
+    step_ev_next_ = (step_ev_next_ + 1) % kStepEvents;
+    return e;
+}
+
+// One row per graph step (decode_step_graph_custom; a traced step under
+// decode_step_graph_traced_custom, its time including its events), and the
+// traced steps' per-op rows.
+void DeviceModel::credit_steps(KernelTrace* trace, size_t n) {
+    n = std::min(n, pending_.size());
+    for (size_t i = 0; i < n && trace; ++i) {
+        const PendingStep& st = pending_[i];
+        trace->add(st.traced ? "decode_step_graph_traced_custom" : "decode_step_graph_custom",
+                   elapsed_ms(st.start, st.end), kTraceBackend);
+        if (st.traced) {
+            ++traced_steps_;
+            for (const TimedOp& op : traced_ops_) {
+                // 100 MHz counter: 1e5 ticks per ms
+                const double ms = static_cast<double>(static_cast<int64_t>(h_ts_[op.ts1] - h_ts_[op.ts0])) * 1e-5;
+                trace->add(op.name, ms, kTraceBackend);
+                for (const std::string& e : op.extra_names) trace->add(e, ms / op.split, kTraceBackend);
+            }
+        }
     }
-    pend_steps_ = 0;
+    if (trace) {
+        trace->set_count("decode_graph_steps", static_cast<int64_t>(graph_steps_));
+        trace->set_count("decode_op_traced_graph_steps", static_cast<int64_t>(traced_steps_));
+        trace->set_count("decode_op_trace_every", trace_every_);
+    }
+    pending_.erase(pending_.begin(), pending_.begin() + static_cast<std::ptrdiff_t>(n));
 }
 
 // The slot the sampling kernel published: (position << 32) | token.
@@ -1052,8 +1123,7 @@ bool DeviceModel::read_slot(long long want, int32_t* token_id, std::string* erro
 bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
     chained_ = false;  // whatever the caller enqueues next runs between the steps
     if (!stream_) return true;
-    const bool open = seg_steps_ > 0;  // steps enqueued since the last segment event: close the segment
-    if (open && xqhip_event_record(step_ev_[seg_slot_][1], stream_) != 0) return fail_hip(error, "step event");
+    if (trace) trace_ = trace;
     if (xqhip_stream_synchronize(stream_) != 0) return fail_hip(error, "decode step");
     if (chain_sync_) {
         int bad = 0;
@@ -1064,15 +1134,7 @@ bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
             return false;
         }
     }
-    credit_segment(trace);
-    if (open) {
-        pend_start_ = seg_start_;
-        pend_end_ = step_ev_[seg_slot_][1];
-        pend_steps_ = seg_steps_;
-        seg_steps_ = 0;
-        seg_slot_ = (seg_slot_ + 1) % 3;
-        credit_segment(trace);
-    }
+    credit_steps(trace, pending_.size());
     return true;
 }
 
@@ -1087,19 +1149,27 @@ std::string DeviceModel::coverage_summary() const {  // fields of custom_model.c
       << "linear_attention_qk_norm=hip_fused_conv1d;linear_attention_gated_rmsnorm=hip_fused_gemv_prologue;"
       << "sampling=hip_fused_lm_head_argmax;prefill_kv_build=hip_fp16_append;decode_step=hip_graph;"
       << "weight_bytes_per_token=" << weight_bytes_ << ";fp16_meta_inexact=" << inexact_meta_
-      << ";kv_capacity=" << max_ctx_ << ";decode_chain=" << chain_note_ << ";fallback_ops=none";
+      << ";kv_capacity=" << max_ctx_ << ";decode_chain=" << chain_note_ << ";kernel_trace=" << trace_note_
+      << ";fallback_ops=none";
     return o.str();
 }
 
 bool DeviceModel::copy_hidden(float* out_values, size_t value_capacity, size_t* out_size) {
     if (out_size) *out_size = static_cast<size_t>(hidden_);
     if (!out_values || value_capacity < static_cast<size_t>(hidden_)) return false;
+    // the queued steps are credited to the trace first: this work runs between them
+    std::string err;
+    if (!sync(trace_, &err)) return false;
     if (xqhip_rmsnorm(resid_, final_norm_, hidden_, eps_, normed_, stream_) != 0) return false;
     return xqhip_memcpy_d2h(out_values, normed_, sizeof(float) * hidden_, stream_) == 0;
 }
 
 std::string DeviceModel::debug_json(int top_k) {  // custom_model.cpp:1382-1436
     const int k = std::max(1, std::min(top_k, 16));
+    {
+        std::string err;
+        sync(trace_, &err);  // (copy_hidden below waits too; the steps are credited first)
+    }
     std::vector<float> h(static_cast<size_t>(hidden_), 0.0f);
     size_t n_h = 0;
     copy_hidden(h.data(), h.size(), &n_h);

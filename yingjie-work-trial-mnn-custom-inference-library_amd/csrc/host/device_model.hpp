@@ -78,6 +78,7 @@ private:
         int split = 1;                         // time divided over extra rows (fused attention)
         void* ev0 = nullptr;
         void* ev1 = nullptr;
+        int ts0 = -1, ts1 = -1;  // traced graph: slots of h_ts_ (timestamp kernels) instead of events
     };
 
     bool upload_matrix(const HostMatrix& m, xqhip_w4* out, std::string* error);
@@ -95,11 +96,14 @@ private:
     bool enqueue_embed(const int32_t* token_dev, bool timed, std::string* error);
     bool enqueue_lm_head(bool timed, std::string* error);
     bool read_slot(long long want, int32_t* token_id, std::string* error) const;
-    void credit_segment(KernelTrace* trace);
+    // credits the first n enqueued graph steps (complete by then) to `trace`
+    void credit_steps(KernelTrace* trace, size_t n);
+    void* next_step_event();
     bool op_begin(bool timed, const std::string& name, std::vector<std::string> extra = {}, int split = 1);
     void op_end(bool timed);
     void flush_timed(KernelTrace* trace);
     bool ensure_graphs(std::string* error);
+    void drop_graphs();
     // decode chains: the projections between two non-GEMV ops as one launch
     bool build_chains(std::string* error);
     bool enqueue_chain(size_t k, bool timed, std::string* error);
@@ -163,16 +167,38 @@ private:
     // graph: lm_head argmax -> sampled token (d_ctrl_[2]), d_ctrl_[0] + 1 and the
     // published slot, then embed(sampled token) + layers at the new position
     void* g_step_ = nullptr;
-    // decode-step timing by segments of consecutive graph steps
-    static constexpr int kStepsPerEvent = 8;
-    void* step_ev_[3][2] = {};   // (start, end) events of three segments
-    int seg_slot_ = 0;           // slot of the open segment
-    void* seg_start_ = nullptr;  // start event of the open segment
-    int seg_steps_ = 0;          // graph steps enqueued in the open segment
-    void* pend_start_ = nullptr;  // a closed segment not yet credited to the trace
-    void* pend_end_ = nullptr;
-    int pend_steps_ = 0;
-    bool chained_ = false;       // the last work enqueued is a graph step (the open segment continues)
+    // Decode-step timing: every graph step records an end event, and a step
+    // that follows the previous one is timed from that step's end event (one
+    // event per step between the graphs); steps are credited once a later
+    // step has started (its sampling ran after them) or at a sync.
+    static constexpr int kStepEvents = 8;  // ring: at most two steps (four events) are ever pending
+    void* step_ev_[kStepEvents] = {};
+    int step_ev_next_ = 0;
+    void* last_end_ = nullptr;  // end event of the last graph step
+    struct PendingStep {
+        void* start;
+        void* end;
+        bool traced;
+    };
+    std::vector<PendingStep> pending_;
+    // The traced step graph: the same kernels with a timestamp after every op,
+    // replayed instead of g_step_ on the first step after each prefill and on
+    // every trace_every_-th graph step (XQ_TRACE_EVERY; 0: only after a
+    // prefill), so the trace has per-op rows of graph steps all along.
+    void* g_step_traced_ = nullptr;
+    std::vector<TimedOp> traced_ops_;
+    // timestamps of the traced graph (xqhip_timestamp kernels between its ops,
+    // 100 MHz counter) in coherent host memory; ts_mode_ while it is captured
+    static constexpr int kMaxTimestamps = 1024;
+    uint64_t* h_ts_ = nullptr;
+    int ts_next_ = 0;
+    bool ts_mode_ = false;
+    int trace_every_ = 128;
+    uint64_t graph_steps_ = 0, traced_steps_ = 0;
+    bool trace_next_ = true;
+    std::string trace_note_ = "per_op_every_128_graph_steps";
+    KernelTrace* trace_ = nullptr;  // the trace passed with the last prefill / decode / sync
+    bool chained_ = false;          // the last work enqueued is a graph step
     bool detail_prefill_ = true, detail_decode_ = true;
     // prompt-chunk buffers, [token][...] rows (allocated when every matrix is TILED64)
     bool batched_prefill_ = false;
@@ -185,6 +211,7 @@ private:
     float* attn_all_ = nullptr;  // [chunk][attn_n] attention / delta output
     float* ffn_all_ = nullptr;   // [chunk][inter]
     void* gemm_ws_ = nullptr;
+    size_t gemm_ws_bytes_ = 0;
     void* scan_ws_ = nullptr;  // linear-attention scan workspace (token-parallel conv pass)
     int32_t* tok_dev_ = nullptr;  // [chunk]
     std::vector<TimedOp> ops_;

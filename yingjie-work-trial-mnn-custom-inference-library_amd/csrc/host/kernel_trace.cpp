@@ -80,7 +80,9 @@ std::string KernelTrace::to_json() const {
           << ",\"min_ms\":" << s.min_ms << ",\"max_ms\":" << s.max_ms << "}";
         first = false;
     }
-    o << "]}";
+    o << "]";
+    for (const auto& kv : counts_) o << ",\"" << json_escape(kv.first) << "\":" << kv.second;
+    o << "}";
     return o.str();
 }
 

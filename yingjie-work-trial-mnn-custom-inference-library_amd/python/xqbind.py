@@ -19,7 +19,7 @@ c_uint64, c_int32, c_uint8 = ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint8
 
 F32, F16 = 0, 1
 PRO_NONE, PRO_RMS, PRO_GATED_HEAD, PRO_GATED_HEAD_ACT = 0, 1, 2, 3
-ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 132, 8  # split attention workspace: partials, then counters
+ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 160, 8  # split attention workspace: partials, then counters
 EPI_STORE, EPI_ADD, EPI_SILU_PAIR = 0, 1, 2
 LAYOUT_TILED64, LAYOUT_GENERIC, LAYOUT_TILED64_F32META, LAYOUT_TILED64_SCALE16 = 0, 1, 2, 3
 
@@ -115,7 +115,7 @@ _HIP_SIGS = {
                                            c_void_p]),
     "xqhip_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "xqhip_gemm_w4a16": (c_int, [_P(W4), c_void_p, c_int, c_int, _P(Prologue), c_int, c_void_p, c_int, c_int,
-                                 c_void_p, c_void_p]),
+                                 c_void_p, c_size_t, c_void_p]),
     "xqhip_embed_bf16_batch": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p]),
     "xqhip_attn_prep_batch": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                       c_void_p, c_float, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
@@ -131,6 +131,7 @@ _HIP_SIGS = {
                                           c_int, c_void_p, c_void_p]),
     "xqhip_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p, c_void_p]),
     "xqhip_lds_fill": (c_int, [c_float, c_void_p]),
+    "xqhip_timestamp": (c_int, [c_void_p, c_void_p]),
     "xqhip_chain_create": (c_int, [_P(ChainOp), c_int, _P(c_void_p)]),
     "xqhip_chain_destroy": (c_int, [c_void_p]),
     "xqhip_chain_arena_records": (c_size_t, [c_void_p]),
