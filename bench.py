@@ -6,7 +6,10 @@ Prints ONE JSON line.  Workloads (--workload):
          full attention, hidden 4096, MLP 12288, vocab 248320, W4A16 g64) run
          through the xqwen35.h ABI: a 512-token prefill of random token ids,
          then K greedy decode steps.  value = decode tokens/s (generated tokens
-         / decode wall time, as xq_metrics reports it).
+         / decode wall time, as xq_metrics reports it).  A second run on the
+         same shape written with the asymmetric quantiser's metadata (fp32
+         scales, integer zeros; --no-asymmetric skips it) is reported under
+         "asymmetric_metadata".
   mlp    decode MLP block, hidden 4096 -> 12288 -> 4096, W4A16 g64: fused
          RMSNorm + gate/up GEMV + SiLU*up, then down GEMV + residual add.
          value = algorithmic HBM GB/s of the block (the GEMV bandwidth metric).
@@ -212,22 +215,43 @@ PROJ_PER_STEP = {"gate_up": 32, "down": 32, "in_proj_linear": 24, "in_proj_full"
                  "o_proj_full": 8, "lm_head": 1}
 
 
-def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6):
+# group metadata of the synthetic matrices (time_projection):
+#   sym   fp16 scales, every zero point 2^(bits-1) (8 for 4-bit codes): the
+#         upload keeps the fp16 scale alone (2 B per group; 3 and 2 bits: the
+#         fp16 (scale, zero) pair, 4 B)
+#   asym  the asymmetric packer's metadata: fp32 scales, integer zeros 0..15:
+#         the fp32 scale and a 4-bit zero code (4.5 B per group)
+#   pair  fp32 scales, non-integer zeros: the fp32 (scale, zero) pair (8 B)
+META_KINDS = ("sym", "asym", "pair")
+
+
+def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6, meta="sym"):
     """Average duration of n back-to-back launches of one projection (HIP events
     on the default stream around the loop), weights rotated over enough copies
     (> 2x the 256 MB last-level cache) that every launch streams from HBM.
-    Algorithmic bytes = the uploaded matrix (codes + group metadata: the fp16
-    scale alone here, every zero point being 2^(bits-1) = 8 for 4-bit codes;
-    fp16 (scale, zero) for the 3- and 2-bit widths) + x + y."""
+    Algorithmic bytes = the uploaded matrix (codes + group metadata in the
+    layout the upload picks for `meta`) + x + y."""
     hip = xb.hip()
     rng = np.random.default_rng(rows + cols + bits)
     g = cols // 64
     packed = rng.integers(0, 256, (rows * cols * bits + 7) // 8, dtype=np.uint8)
-    scales = np.abs(rng.normal(0.0, 0.02, rows * g)).astype(np.float16).astype(np.float32)
-    zeros = np.full(rows * g, float(1 << (bits - 1)), np.float32)
-    one = w4_bytes(rows, cols) if bits == 4 else rows * cols * bits // 8 + rows * g * 4
+    scales32 = np.abs(rng.normal(0.0, 0.02, rows * g)).astype(np.float32)
+    if meta == "sym":
+        scales = scales32.astype(np.float16).astype(np.float32)
+        zeros = np.full(rows * g, float(1 << (bits - 1)), np.float32)
+    elif meta == "asym":
+        scales = scales32
+        zeros = np.clip(np.rint(7.5 + rng.normal(0.0, 1.0, rows * g)), 0, 15).astype(np.float32)
+    else:
+        scales = scales32
+        zeros = (7.5 + rng.normal(0.0, 1.0, rows * g)).astype(np.float32)
+    meta_bytes = {"sym": rows * g * (2 if bits == 4 else 4), "asym": rows * g * 4 + rows * ((g + 7) // 8) * 4,
+                  "pair": rows * g * 8}[meta]
+    one = rows * cols * bits // 8 + meta_bytes
     ncopy = max(2, min(64, int(np.ceil(budget / one))))
     copies = [xb.DeviceW4(packed, scales, zeros, rows, cols, 64, 0, bits=bits) for _ in range(ncopy)]
+    assert copies[0].weight_bytes() == one, (name, meta, copies[0].weight_bytes(), one)
+    layout = int(copies[0].w.layout)
     x = xb.DeviceBuffer.from_array(rng.normal(0, 1, cols).astype(np.float32))
     nw = xb.DeviceBuffer.from_array(rng.normal(1.0, 0.1, cols).astype(np.float32))
     hw = xb.DeviceBuffer.from_array(rng.normal(1.0, 0.1, 128).astype(np.float32))
@@ -264,16 +288,19 @@ def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6
     for c in copies:
         c.free()
     return {"name": name, "bits": bits, "rows": rows, "cols": cols, "prologue": pro_kind, "epilogue": epi,
+            "meta": meta, "layout": layout,
             "launches": n, "weight_copies": ncopy, "avg_us": round(us, 2), "bytes": int(algo),
             "GBps": round(algo / us / 1e3, 1), "frac": round(algo / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
 
-def projection_table(bits=4, n=200):
+def projection_table(bits=4, n=200, meta="sym", names=None):
     rows = []
     for name, r, c, pro, epi in PROJECTIONS:
-        rows.append(time_projection(name, r, c, pro, epi, bits=bits, n=n))
+        if names is not None and name not in names:
+            continue
+        rows.append(time_projection(name, r, c, pro, epi, bits=bits, n=n, meta=meta))
         t = rows[-1]
-        log(f"[bench] W{bits} {name:16s} {r}x{c} {t['avg_us']:8.2f} us {t['bytes'] / 1e6:8.2f} MB "
+        log(f"[bench] W{bits} {meta:4s} {name:16s} {r}x{c} {t['avg_us']:8.2f} us {t['bytes'] / 1e6:8.2f} MB "
             f"{t['GBps']:7.1f} GB/s frac {t['frac']:.3f}")
     return rows
 
@@ -378,13 +405,13 @@ def measure_traffic():
             "bench.py --workload pmc-probe, calibrated on a 64 MiB one-dispatch device copy (xqhip_copy)"}
 
 
-def ensure_model(path):
+def ensure_model(path, **overrides):
     marker = os.path.join(path, ".complete")
     if os.path.exists(marker):
         return 0.0
     t0 = time.perf_counter()
-    log(f"[bench] writing the synthetic 9B-shaped model to {path} ...")
-    xb.write_synth_model(path, threads=min(16, os.cpu_count() or 1))
+    log(f"[bench] writing the synthetic 9B-shaped model to {path} ({overrides or 'default metadata'}) ...")
+    xb.write_synth_model(path, threads=min(16, os.cpu_count() or 1), **overrides)
     open(marker, "w").write("ok")
     dt = time.perf_counter() - t0
     log(f"[bench] model written in {dt:.1f} s")
@@ -396,26 +423,21 @@ def trace_rows(sess):
     return {r["name"]: r for r in json.loads(txt)["rows"]} if st == 0 else {}
 
 
-def bench_decode(args):
-    prompt_len, hidden, inter = 512, 4096, 12288
-    gen_s = ensure_model(MODEL_DIR)
-    rng = np.random.default_rng(4)
-    prompt = rng.integers(0, 248320, prompt_len, dtype=np.int32)
-    t0 = time.perf_counter()
-    sess = xb.Session(MODEL_DIR, xb.options(backend=b"hip", max_context=8192))
-    if not sess.ok():
-        raise RuntimeError(f"xq_create failed: {sess.status}")
-    load_s = time.perf_counter() - t0
-    log(f"[bench] model loaded in {load_s:.1f} s: {sess.json('xq_get_backend_info')[1][:300]}")
-    # warmup: one prefill + W decode steps (captures the step graphs)
+def backend_field(info, key):
+    return info.split(key + "=")[1].split(";")[0] if key + "=" in info else None
+
+
+def timed_decode(sess, prompt, args):
+    """Warmup (one prefill + W decode steps, which capture the step graphs),
+    then the timed run: a fresh prefill and the first decode step after it
+    (untimed: that step replays the traced copy of the step graph, timestamps
+    between its ops for the kernel trace), then exactly K decode steps, each
+    one graph launch (every 128th the traced copy)."""
     st, m = sess.prefill(prompt)
+    assert st == 0, m.error
     for _ in range(args.warmup):
         st, tok, m = sess.decode_one()
         assert st == 0
-    # timed: fresh prefill and the first decode step after it (untimed: that
-    # step replays the traced copy of the step graph, timestamps between its
-    # ops for the kernel trace), then exactly K decode steps, each one graph
-    # launch (every 128th the traced copy)
     assert sess.lib.xq_reset(sess.h) == 0
     st, m = sess.prefill(prompt)
     assert st == 0, m.error
@@ -431,9 +453,23 @@ def bench_decode(args):
         toks.append(tok)
     xb.ck(xb.hip().xqhip_device_synchronize())
     wall = time.perf_counter() - t0
-    decode_ms = m.decode_total_ms
-    ms_per_step = wall * 1e3 / args.steps
-    tps = args.steps / wall
+    return {"wall_s": wall, "ms_per_step": wall * 1e3 / args.steps, "tps": args.steps / wall,
+            "prefill_ms": prefill_ms, "decode_ms": m.decode_total_ms, "tokens": toks}
+
+
+def bench_decode(args):
+    prompt_len, hidden, inter = 512, 4096, 12288
+    gen_s = ensure_model(MODEL_DIR)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 248320, prompt_len, dtype=np.int32)
+    t0 = time.perf_counter()
+    sess = xb.Session(MODEL_DIR, xb.options(backend=b"hip", max_context=8192))
+    if not sess.ok():
+        raise RuntimeError(f"xq_create failed: {sess.status}")
+    load_s = time.perf_counter() - t0
+    log(f"[bench] model loaded in {load_s:.1f} s: {sess.json('xq_get_backend_info')[1][:300]}")
+    run = timed_decode(sess, prompt, args)
+    prefill_ms, decode_ms, ms_per_step, tps = run["prefill_ms"], run["decode_ms"], run["ms_per_step"], run["tps"]
     rows = trace_rows(sess)
     gu = next((r for n, r in rows.items() if n.startswith("linear_gate_proj")), None)
     dn = next((r for n, r in rows.items() if n.startswith("linear_down_proj")), None)
@@ -446,7 +482,7 @@ def bench_decode(args):
     bytes_dn = w4_bytes(hidden, inter) + inter * 4 + 2 * hidden * 4
     bytes_lm = w4_bytes(248320, hidden) + hidden * 4
     info = sess.json("xq_get_backend_info")[1]
-    wbytes = int(info.split("weight_bytes_per_token=")[1].split(";")[0]) if "weight_bytes_per_token=" in info else 0
+    wbytes = int(backend_field(info, "weight_bytes_per_token") or 0)
     # --no-projections (profiling runs: only the decode path's own kernels in
     # the trace) leaves the roofline fields null
     proj = [] if args.no_projections else projection_table(4, n=200)
@@ -495,6 +531,8 @@ def bench_decode(args):
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_decode(prompt, sess)
     sess.close()
+    if not args.no_asymmetric:
+        result["asymmetric_metadata"] = bench_decode_asymmetric(args, prompt, tps, proj)
     if not args.no_traffic:
         t = measure_traffic()
         if t:
@@ -502,6 +540,55 @@ def bench_decode(args):
             result["roofline"]["traffic_detail"] = t
             log(f"[bench] gate/up traffic {t['bytes']} B per launch (algorithmic {bytes_gu})")
     return result
+
+
+ASYM_DIR = MODEL_DIR.rstrip("/") + "_asym"
+
+
+def bench_decode_asymmetric(args, prompt, sym_tps, sym_proj):
+    """The same decode workload on the same 9B shape written with the metadata
+    of the reference packer's asymmetric quantiser (fp32 scales, integer zeros
+    0..15, pack_qwen35_xq4_numpy.py:218-247): every matrix uploads in the
+    fp32-scale + 4-bit-zero layout (4.5 B per group).  Reports decode tok/s,
+    the weight bytes per token and the per-projection GEMV table of that
+    layout, and gate/up in the fp32-pair layout (8 B per group, what these
+    matrices would need without the 4-bit zero) for comparison."""
+    gen_s = ensure_model(ASYM_DIR, asymmetric=1)
+    t0 = time.perf_counter()
+    sess = xb.Session(ASYM_DIR, xb.options(backend=b"hip", max_context=8192))
+    if not sess.ok():
+        raise RuntimeError(f"xq_create failed (asymmetric model): {sess.status}")
+    load_s = time.perf_counter() - t0
+    info = sess.json("xq_get_backend_info")[1]
+    wbytes = int(backend_field(info, "weight_bytes_per_token") or 0)
+    run = timed_decode(sess, prompt, args)
+    rows = trace_rows(sess)
+    sess.close()
+    step = rows.get("decode_step_graph_custom")
+    step_ms = step["mean_ms"] if step else run["ms_per_step"]
+    log(f"[bench] asymmetric metadata: {run['ms_per_step']:.3f} ms/token wall ({run['tps']:.1f} tok/s), graph step "
+        f"{step_ms:.3f} ms, weights {wbytes / 1e9:.3f} GB/token; layouts {backend_field(info, 'weight_layouts')}")
+    out = {"model": "the same 9B shape and seed, XQ4 v1 files with fp32 scales |N(0, 0.02)| and integer zeros "
+                    "clamp(round(7.5 + N(0, 1)), 0, 15) per group (xqsynth asymmetric=1)",
+           "tokens_per_s": round(run["tps"], 2), "ms_per_step": round(run["ms_per_step"], 4),
+           "graph_step_ms": round(step_ms, 4), "vs_symmetric": round(run["tps"] / sym_tps, 4) if sym_tps else None,
+           "weight_bytes_per_token": wbytes, "weight_layouts": backend_field(info, "weight_layouts"),
+           "prefill_ms": round(run["prefill_ms"], 2), "model_write_s": round(gen_s, 1), "load_s": round(load_s, 1),
+           "layout": "TILED64_F32S_Z4: fp32 scale + 4-bit zero code per group (4.5 B), exact for these values"}
+    if not args.no_projections:
+        proj = projection_table(4, n=200, meta="asym")
+        pair = projection_table(4, n=200, meta="pair", names=("gate_up",))
+        gemv_us = sum(p["avg_us"] * PROJ_PER_STEP[p["name"]] for p in proj)
+        gemv_bytes = sum(p["bytes"] * PROJ_PER_STEP[p["name"]] for p in proj)
+        keys = ("name", "rows", "cols", "prologue", "epilogue", "layout", "avg_us", "bytes", "GBps", "frac")
+        out["per_projection"] = [{k: p[k] for k in keys} for p in proj]
+        out["projections_per_step"] = {"bytes": gemv_bytes, "sum_avg_us": round(gemv_us, 1),
+                                       "frac": round(gemv_bytes / (gemv_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+        out["gate_up_f32_pair_layout"] = {k: pair[0][k] for k in keys}
+        sym_gu = next((p for p in sym_proj if p["name"] == "gate_up"), None)
+        if sym_gu:
+            out["gate_up_fp16_scale_layout_us"] = sym_gu["avg_us"]
+    return out
 
 
 def cpu_baseline_decode(prompt, gpu_sess, runs=3):
@@ -590,6 +677,8 @@ def main():
     ap.add_argument("--no-projections", action="store_true",
                     help="decode: skip the per-projection GEMV table (roofline fields null; for kernel traces)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-asymmetric", action="store_true",
+                    help="decode: skip the second run on the model written with asymmetric-quantiser metadata")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are not part of "

@@ -53,11 +53,19 @@ enum {
                                  (scale, zero) per group (8 bytes): chosen when a
                                  value is not exact in fp16 (e.g. asymmetric scales
                                  (max - min) / 15)                                  */
-    XQHIP_LAYOUT_TILED64_SCALE16 = 3 /* TILED64 codes with one fp16 scale per group
+    XQHIP_LAYOUT_TILED64_SCALE16 = 3, /* TILED64 codes with one fp16 scale per group
                                  (2 bytes): chosen for 4-bit format-v1 matrices whose
                                  zeros are all 8 (the symmetric quantiser, the
                                  synthetic weights) and whose scales fp16 holds; the
                                  zero point is implied                              */
+    XQHIP_LAYOUT_TILED64_F32S_Z4 = 4 /* TILED64 codes with the fp32 scale and a 4-bit
+                                 zero code per group (4.5 bytes: fp32 scales
+                                 [rows][G], then per row ceil(G/8) u32 words, nibble
+                                 k of word j = zero of group 8j+k): chosen for 4-bit
+                                 format-v1 matrices whose zeros are integers 0..15
+                                 and whose scales fp16 cannot hold (the reference
+                                 packer's asymmetric quantiser,
+                                 pack_qwen35_xq4_numpy.py:218-247)                  */
 };
 
 /* A W4A16 matrix resident in HBM.  Semantics of the reference QuantizedMatrix
@@ -72,7 +80,7 @@ typedef struct xqhip_w4 {
     int32_t affine;
     int32_t layout;
     int32_t inexact_meta; /* scales/zeros fp16 cannot hold exactly: kept in fp32
-                             (layout TILED64_F32META)                            */
+                             (layouts TILED64_F32META, TILED64_F32S_Z4)          */
     int32_t bits;         /* code width: 4 (xqhip_w4_upload), 3 or 2 (xqhip_wlb_upload) */
     int32_t zero_is_8;    /* affine == 0 and every zero is 8: w = (q - 8) s, so the
                              zero-point term of the prefill GEMM vanishes          */
@@ -126,8 +134,11 @@ XQHIP_API int xqhip_event_query(void* ev);
 /* ---- W4A16 weights ----------------------------------------------------- */
 /* Repack a reference-format matrix (packed[rows][ceil(cols/2)], fp32
  * scales/zeros[rows][ceil(cols/group)], as read by custom_model.cpp:218-262)
- * into the device layout and upload it.  Chooses TILED64 when group == 64 and
- * cols % 64 == 0, else GENERIC. */
+ * into the device layout and upload it.  group == 64 and cols % 64 == 0 give a
+ * TILED64 layout, with the smallest metadata that holds every scale and zero
+ * exactly: SCALE16 (format v1, zeros all 8, fp16 scales), TILED64 (fp16 scale
+ * and zero), F32S_Z4 (format v1, integer zeros 0..15, fp32 scales) or
+ * F32META (fp32 pair); anything else gives GENERIC. */
 XQHIP_API int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols,
                               int group, int affine, xqhip_w4* out);
 /* 3- and 2-bit matrices (W3A16 / W2A16): the reference's low-bit format

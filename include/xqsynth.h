@@ -10,6 +10,10 @@
  *   4-bit codes uniform in 0..15, two per byte, even column in the low nibble;
  *   scales |N(0, scale_std)| rounded to fp16 and stored as fp32; zeros = `zero`
  *   (XQ4 version 1, w = (q - zero) * scale);
+ *   with `asymmetric` set, the metadata of the reference packer's asymmetric
+ *   quantiser (pack_qwen35_xq4_numpy.py:218-247: fp32 scales, integer zeros
+ *   0..15) instead: scales |N(0, scale_std)| in fp32, not rounded, and zeros
+ *   clamp(round(7.5 + N(0, 1)), 0, 15) per group (`zero` unused);
  *   embeddings N(0, embed_std) as bf16;
  *   norm weights with effective value N(1, norm_std) rounded to fp16 (stored
  *   minus one where the reader adds one);
@@ -51,6 +55,7 @@ typedef struct xqsynth_config {
     float embed_std;
     float norm_std;
     int32_t threads;
+    int32_t asymmetric;
 } xqsynth_config;
 
 /* Fills `cfg` with the 9B-shaped hybrid model of the benchmark workload:

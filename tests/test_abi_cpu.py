@@ -151,3 +151,35 @@ def test_synthetic_writer_is_deterministic(tmp_path):
     assert 0.01 < scales.mean() < 0.025 and np.all(scales >= 0)
     codes = np.concatenate([packed & 15, packed >> 4])
     assert abs(codes.mean() - 7.5) < 0.3
+
+
+def read_xq4(path):
+    """Header fields, codes, scales and zeros of an XQ4 file (custom_model.cpp:218-262)."""
+    raw = open(path, "rb").read()
+    assert raw[:7] == b"XQW4A16"
+    version, rows, cols, group, bits = np.frombuffer(raw, np.uint32, 5, 8)
+    n_packed, n_scales, n_zeros = np.frombuffer(raw, np.uint64, 3, 28)
+    off = 52 + int(n_packed)
+    scales = np.frombuffer(raw, np.float32, int(n_scales), off)
+    zeros = np.frombuffer(raw, np.float32, int(n_zeros), off + 4 * int(n_scales))
+    return int(version), int(rows), int(cols), scales, zeros
+
+
+@pytest.mark.parametrize("asymmetric", [0, 1])
+def test_synth_writer_metadata(tmp_path, asymmetric):
+    """Default: fp16 scales, every zero 8.  asymmetric=1: the metadata of the
+    asymmetric packer (fp32 scales, integer zeros 0..15 centred near 7.5)."""
+    from tiny_model import SMALL
+    xb.write_synth_model(str(tmp_path), **SMALL, asymmetric=asymmetric)
+    files = sorted(p for p in os.listdir(tmp_path) if p.endswith(".xq4"))
+    assert files
+    for name in files[:6]:
+        version, rows, cols, scales, zeros = read_xq4(os.path.join(tmp_path, name))
+        assert version == 1 and scales.size == zeros.size == rows * ((cols + 63) // 64)
+        f16_exact = scales.astype(np.float16).astype(np.float32) == scales
+        if asymmetric:
+            assert np.all(zeros == np.floor(zeros)) and zeros.min() >= 0 and zeros.max() <= 15
+            assert 7.0 <= zeros.mean() <= 8.0 and np.unique(zeros).size >= 4
+            assert f16_exact.mean() < 0.01
+        else:
+            assert np.all(zeros == 8.0) and f16_exact.all()

@@ -154,10 +154,10 @@ __device__ __forceinline__ float unit_dot(const Unit<META>& w, const uint32_t (&
     const float sc = meta_scale(w.m);
     float acc;
     if constexpr (META == 2) {
-        acc = (sc * ge) * df;
+        acc = mul_rn(sc * ge, df);
     } else {
         const float z = meta_zero(w.m);
-        acc = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
+        acc = affine ? mul_rn(ge, fmaf(sc, df, fmaf(8.0f, sc, z) * gg)) : mul_rn(sc * ge, fmaf(8.0f - z, gg, df));
     }
     return wave_sum(acc);
 }
@@ -686,7 +686,9 @@ XQHIP_API int xqhip_chain_create(const xqhip_chain_op* ops, int n_ops, void** ch
         const std::string at = "xqhip_chain_create op " + std::to_string(i) + ": ";
         if (!o.w || o.w->bits != 4) return chain_fail_host(XQHIP_EINVAL, at + "needs a 4-bit matrix");
         const int m = meta_of(o.w->layout);
-        if (m < 0) return chain_fail_host(XQHIP_EINVAL, at + "needs a TILED64 matrix");
+        if (m < 0)
+            return chain_fail_host(XQHIP_EINVAL, at + "needs a TILED64 matrix with fp16, fp32-pair or fp16-scale "
+                                                      "metadata (layout " + std::to_string(o.w->layout) + ")");
         if (meta >= 0 && m != meta) return chain_fail_host(XQHIP_EINVAL, at + "metadata layout differs from op 0");
         meta = m;
         const int rows = o.w->rows, cols = o.w->cols;

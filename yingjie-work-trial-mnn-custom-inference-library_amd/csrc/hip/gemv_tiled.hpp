@@ -312,7 +312,7 @@ __host__ __device__ constexpr uint32_t tiled_row_bytes(int cols) {
 template <int BITS, int META>
 __device__ __forceinline__ WSrc make_wsrc(const uint8_t* nib, const uint32_t* meta, int rows, int cols) {
     const uint32_t nib_bytes = static_cast<uint32_t>(rows) * tiled_row_bytes<BITS>(cols);
-    const uint32_t meta_bytes = static_cast<uint32_t>(rows) * static_cast<uint32_t>(cols >> 6) * kMetaGroupBytes<META>;
+    const uint32_t meta_bytes = meta_total_bytes<META>(static_cast<uint32_t>(rows), static_cast<uint32_t>(cols >> 6));
     WSrc s;
     s.nib = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(nib), 0, nib_bytes, kRsrcWord3);
     s.meta = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(meta), 0, meta_bytes, kRsrcWord3);
@@ -351,7 +351,12 @@ __device__ __forceinline__ void load_batch(WBatch<R, META>& wb, const WSrc& src,
             const u32x2 h = __builtin_amdgcn_raw_buffer_load_b64(src.nib, ok ? hoff : kOutOfRange, 0, kLoadNT);
             wb.b[i] = make_uint4(h.x, h.y, 0u, 0u);
         }
-        wb.m[i] = load_meta<META, kLoadNT>(src.meta, ok ? moff : kOutOfRange);
+        uint32_t zoff = 0;
+        if constexpr (META == 3)
+            zoff = ok ? z4_offset(static_cast<uint32_t>(rows), static_cast<uint32_t>(G), static_cast<uint32_t>(row),
+                                  static_cast<uint32_t>(c * 64 + lane))
+                      : kOutOfRange;
+        wb.m[i] = load_meta<META, kLoadNT>(src.meta, ok ? moff : kOutOfRange, zoff);
     }
 }
 
@@ -527,13 +532,19 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
                 // sum_c q_c x_c = e (D + 8 G), sum_c x_c = e G, so
                 //   v1: s (sum qx - z sum x) = s e (D + (8 - z) G)   (exact cancellation for z = 8)
                 //   v2: s sum qx + z sum x   = e (s D + (8 s + z) G)
+                // (the group's term is rounded on its own before the row sum, mul_rn,
+                // so every metadata form and the decode chains round alike)
                 const float df = static_cast<float>(Dg);
                 const float sc = meta_scale(cur.m[i]);
                 if constexpr (META == 2) {  // zero 8, format v1: s e D (the v1 form with 8 - z = 0)
-                    acc[i] = (sc * ge) * df;
+                    acc[i] = mul_rn(sc * ge, df);
+                } else if constexpr (META == 3) {  // format v1, integer zero (group g = 64 c + lane: nibble lane % 8)
+                    const float z = meta_zero_at(cur.m[i], static_cast<uint32_t>(lane & 7) * 4u);
+                    acc[i] = mul_rn(sc * ge, fmaf(8.0f - z, gg, df));
                 } else {
                     const float z = meta_zero(cur.m[i]);
-                    acc[i] = affine ? ge * fmaf(sc, df, fmaf(8.0f, sc, z) * gg) : (sc * ge) * fmaf(8.0f - z, gg, df);
+                    acc[i] = affine ? mul_rn(ge, fmaf(sc, df, fmaf(8.0f, sc, z) * gg))
+                                    : mul_rn(sc * ge, fmaf(8.0f - z, gg, df));
                 }
                 acc[i] = wave_sum(acc[i]);
             }
@@ -718,9 +729,11 @@ static hipError_t launch_tiled_bits(const GemvLaunch& p, hipStream_t s) {
     }
 }
 
-// TILED64 launches with fp32 metadata (gemv_w4a16_m32.hip) and with the fp16
-// scale alone, zero 8 (gemv_w4a16_s16.hip).
+// TILED64 launches with fp32 metadata (gemv_w4a16_m32.hip), with the fp16
+// scale alone, zero 8 (gemv_w4a16_s16.hip), and with the fp32 scale and a
+// 4-bit zero (gemv_w4a16_z4.hip).
 hipError_t launch_gemv_tiled_m32(const GemvLaunch& p, hipStream_t s);
 hipError_t launch_gemv_tiled_s16(const GemvLaunch& p, hipStream_t s);
+hipError_t launch_gemv_tiled_z4(const GemvLaunch& p, hipStream_t s);
 
 }  // namespace xqhip

@@ -230,6 +230,7 @@ static hipError_t launch_generic_t(const GemvLaunch& p, hipStream_t s) {
 hipError_t launch_gemv(const GemvLaunch& p, hipStream_t s) {
     if (p.layout == 2) return launch_gemv_tiled_m32(p, s);
     if (p.layout == 3) return launch_gemv_tiled_s16(p, s);
+    if (p.layout == 4) return launch_gemv_tiled_z4(p, s);
     if (p.layout == 0) {
         switch (p.bits) {
             case 4: return launch_tiled_bits<4, 0>(p, s);

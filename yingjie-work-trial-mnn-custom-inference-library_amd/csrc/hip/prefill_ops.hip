@@ -369,7 +369,8 @@ __device__ __forceinline__ half8 codes_to_h8(uint32_t w) {
 template <int WGR, int WGT, int TI, int TJ, int EPI, int META>
 __global__ void __launch_bounds__(kWave * WGR * WGT) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_w4_mfma_kernel(GemmArgs a) {
-    // fp16 (scale, zero) in a u32, the fp32 pair (the scale is its first word), or the fp16 scale alone
+    // fp16 (scale, zero) in a u32, the fp32 pair (the scale is its first word), the fp16 scale alone,
+    // or the fp32 scale (its zero in the separate array of 4-bit codes)
     constexpr uint32_t kMetaBytes = kMetaGroupBytes<META>;
     using T = GemmTile<WGR, WGT, TI, TJ>;
     constexpr int BR = T::kBR, BT = T::kBT, XU = T::kXU, NT = T::kThreads;
@@ -431,7 +432,8 @@ gemm_w4_mfma_kernel(GemmArgs a) {
                    (c16 & 7) * 8u) * 2u;
     const int xdst = xtok * kGemmXLd + c16 * 8;
     // scales: thread < BR stages row r0 + tid (the others load out of range: zero, no branch)
-    const __amdgpu_buffer_rsrc_t meta_r = buf_rsrc(a.meta, static_cast<uint32_t>(a.rows) * G * kMetaBytes);
+    const __amdgpu_buffer_rsrc_t meta_r =
+        buf_rsrc(a.meta, meta_total_bytes<META>(static_cast<uint32_t>(a.rows), static_cast<uint32_t>(G)));
     const bool s_thread = threadIdx.x < BR;
     const uint32_t moff =
         s_thread ? static_cast<uint32_t>(min(r0 + static_cast<int>(threadIdx.x), a.rows - 1)) * G * kMetaBytes : kBufOOB;
@@ -457,7 +459,7 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         _Float16* d_ = xlds + (st) * T::kXStage + xdst;                                                      \
         _Pragma("unroll") for (int j_ = 0; j_ < XU; ++j_) *reinterpret_cast<u32x4*>(d_ + j_ * kTokStep * kGemmXLd) = \
             X[j_];                                                                                           \
-        if (s_thread) slds[(st) * BR + threadIdx.x] = META == 1 ? __uint_as_float(M) : half_lo(M);            \
+        if (s_thread) slds[(st) * BR + threadIdx.x] = META == 1 || META == 3 ? __uint_as_float(M) : half_lo(M); \
     }
 // MFMAs of one group, each tile's four chained into a per-group sum that is scaled into acc
 #define GEMM_COMPUTE(st, W)                                                                                  \
@@ -536,12 +538,17 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         uint32_t xw[TJ][8];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
-            const uint32_t off = (static_cast<uint32_t>(min(r0 + wr + 16 * i + lr, a.rows - 1)) * G +
-                                  static_cast<uint32_t>(g8)) * kMetaBytes;
+            const uint32_t row = static_cast<uint32_t>(min(r0 + wr + 16 * i + lr, a.rows - 1));
+            const uint32_t off = (row * G + static_cast<uint32_t>(g8)) * kMetaBytes;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const uint32_t o = g8 + e < g1 ? off + kMetaBytes * e : kBufOOB;
-                mw[i][e] = load_meta<META, 0>(meta_r, o);
+                const bool in = g8 + e < g1;
+                const uint32_t o = in ? off + kMetaBytes * e : kBufOOB;
+                const uint32_t zo =
+                    META == 3 && in ? z4_offset(static_cast<uint32_t>(a.rows), static_cast<uint32_t>(G), row,
+                                                static_cast<uint32_t>(g8 + e))
+                                    : kBufOOB;
+                mw[i][e] = load_meta<META, 0>(meta_r, o, zo);
             }
         }
 #pragma unroll
@@ -556,7 +563,8 @@ gemm_w4_mfma_kernel(GemmArgs a) {
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float sc = meta_scale(mw[i][e]), z = meta_zero(mw[i][e]);
+                const float sc = meta_scale(mw[i][e]);
+                const float z = meta_zero_at(mw[i][e], static_cast<uint32_t>((g8 + e) & 7) * 4u);
                 const float c0 = 64.0f * (a.affine ? fmaf(8.0f, sc, z) : (8.0f - z) * sc);
                 ch[i][e] = static_cast<_Float16>(c0);
                 cl[i][e] = static_cast<_Float16>(c0 - static_cast<float>(ch[i][e]));
@@ -660,7 +668,8 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce_kernel(const float* __
 }
 
 bool gemm_supported(int rows, int cols, int group, int layout, const Prologue& pro) {
-    if ((layout != 0 && layout != 2 && layout != 3) || group != 64 || cols % 64 != 0 || cols / 64 > 256 || rows <= 0)
+    if ((layout != 0 && layout != 2 && layout != 3 && layout != 4) || group != 64 || cols % 64 != 0 || cols / 64 > 256 ||
+        rows <= 0)
         return false;
     if (pro.mode == PRO_GATED)
         return pro.head_dim > 0 && pro.head_dim % 8 == 0 && cols % pro.head_dim == 0 &&
@@ -705,19 +714,23 @@ hipError_t launch_gemm(const GemmLaunch& p, hipStream_t s) {
     GemmArgs a{p.nib, static_cast<const uint32_t*>(p.meta), p.rows, p.cols, p.affine, p.zero_is_8, xh, xs, ts,
                (G + splits - 1) / splits, part, p.m, m_pad, p.y, p.ldy};
     // 128 rows x 64 tokens per block: four waves of 32 rows x 64 tokens
-    // metadata form: 0 fp16 (scale, zero), 1 fp32 pair (layout 2), 2 fp16 scale, zero 8 (layout 3)
-    const int meta = p.layout == 2 ? 1 : (p.layout == 3 ? 2 : 0);
+    // metadata form: 0 fp16 (scale, zero), 1 fp32 pair (layout 2), 2 fp16 scale, zero 8 (layout 3),
+    // 3 fp32 scale and 4-bit zero (layout 4)
+    const int meta = p.layout == 2 ? 1 : (p.layout == 3 ? 2 : (p.layout == 4 ? 3 : 0));
     hipError_t e = hipErrorInvalidValue;
-    switch (p.epi * 3 + meta) {
+    switch (p.epi * 4 + meta) {
         case 0: e = launch_gemm_cfg<4, 1, 2, 4, 0, 0>(a, splits, s); break;
         case 1: e = launch_gemm_cfg<4, 1, 2, 4, 0, 1>(a, splits, s); break;
         case 2: e = launch_gemm_cfg<4, 1, 2, 4, 0, 2>(a, splits, s); break;
-        case 3: e = launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, splits, s); break;
-        case 4: e = launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, splits, s); break;
-        case 5: e = launch_gemm_cfg<4, 1, 2, 4, 1, 2>(a, splits, s); break;
-        case 6: e = launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, splits, s); break;
-        case 7: e = launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, splits, s); break;
-        case 8: e = launch_gemm_cfg<4, 1, 2, 4, 2, 2>(a, splits, s); break;
+        case 3: e = launch_gemm_cfg<4, 1, 2, 4, 0, 3>(a, splits, s); break;
+        case 4: e = launch_gemm_cfg<4, 1, 2, 4, 1, 0>(a, splits, s); break;
+        case 5: e = launch_gemm_cfg<4, 1, 2, 4, 1, 1>(a, splits, s); break;
+        case 6: e = launch_gemm_cfg<4, 1, 2, 4, 1, 2>(a, splits, s); break;
+        case 7: e = launch_gemm_cfg<4, 1, 2, 4, 1, 3>(a, splits, s); break;
+        case 8: e = launch_gemm_cfg<4, 1, 2, 4, 2, 0>(a, splits, s); break;
+        case 9: e = launch_gemm_cfg<4, 1, 2, 4, 2, 1>(a, splits, s); break;
+        case 10: e = launch_gemm_cfg<4, 1, 2, 4, 2, 2>(a, splits, s); break;
+        case 11: e = launch_gemm_cfg<4, 1, 2, 4, 2, 3>(a, splits, s); break;
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess || splits == 1) return e;

@@ -284,6 +284,29 @@ static int32_t zero_is_8(const float* zeros, size_t n, int affine) {
     return 1;
 }
 
+// 1 when every zero is an integer 0..15 in format v1 (the reference packer's
+// asymmetric quantiser, pack_qwen35_xq4_numpy.py:218-247): the zero then fits
+// a 4-bit code exactly.
+static bool zeros_are_codes(const float* zeros, size_t n, int affine) {
+    if (affine) return false;
+    for (size_t i = 0; i < n; ++i)
+        if (!(zeros[i] >= 0.0f && zeros[i] <= 15.0f && zeros[i] == std::floor(zeros[i]))) return false;
+    return true;
+}
+
+// TILED64_F32S_Z4 metadata: the fp32 scales [rows][G], then per row
+// ceil(G / 8) u32 words of 4-bit zero codes (nibble k of word j = group 8 j + k).
+static void pack_meta_z4(const float* scales, const float* zeros, int rows, int G, std::vector<uint32_t>* out) {
+    const size_t n = static_cast<size_t>(rows) * G, zw = (static_cast<size_t>(G) + 7) / 8;
+    out->assign(n + static_cast<size_t>(rows) * zw, 0u);
+    std::memcpy(out->data(), scales, n * 4);
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g) {
+            const uint32_t z = static_cast<uint32_t>(zeros[static_cast<size_t>(r) * G + g]);
+            (*out)[n + r * zw + g / 8] |= z << (4 * (g % 8));
+        }
+}
+
 // fp32 (scale, zero) pairs of the TILED64_F32META layout, two words per group.
 static void pack_meta_f32(const float* scales, const float* zeros, size_t n, std::vector<uint32_t>* out) {
     out->resize(2 * n);
@@ -300,7 +323,9 @@ static void pack_meta_f32(const float* scales, const float* zeros, size_t n, std
 // contiguous.  Nibble order inside each 16 bytes is unchanged (even column in
 // the low nibble); every code q is stored as q ^ 8.  Metadata becomes one u32
 // per group: fp16 scale | fp16 zero<<16; the fp16 scale alone (u16) when every
-// zero is 8 (format v1); the fp32 pair when fp16 cannot hold a value.
+// zero is 8 (format v1); when fp16 cannot hold a value, the fp32 scale with a
+// 4-bit zero code if every zero is an integer 0..15 (format v1), else the fp32
+// pair.
 int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zeros, int rows, int cols, int group,
                     int affine, xqhip_w4* out) {
     if (!packed || !scales || !zeros || !out || rows <= 0 || cols <= 0 || group <= 0)
@@ -342,7 +367,12 @@ int xqhip_w4_upload(const uint8_t* packed, const float* scales, const float* zer
         nib_src = nib_host.data();
         const size_t n_meta = static_cast<size_t>(rows) * G;
         out->inexact_meta = pack_meta_f16(scales, zeros, n_meta, &meta_u32);
-        if (out->inexact_meta > 0) {  // keep the reference's fp32 values
+        if (out->inexact_meta > 0 && zeros_are_codes(zeros, n_meta, out->affine)) {
+            // the reference's fp32 scales, the integer zeros as 4-bit codes
+            pack_meta_z4(scales, zeros, rows, G, &meta_u32);
+            out->layout = XQHIP_LAYOUT_TILED64_F32S_Z4;
+            out->meta_bytes = meta_u32.size() * 4;
+        } else if (out->inexact_meta > 0) {  // keep the reference's fp32 values
             pack_meta_f32(scales, zeros, n_meta, &meta_u32);
             out->layout = XQHIP_LAYOUT_TILED64_F32META;
             out->meta_bytes = meta_u32.size() * 4;
@@ -461,10 +491,13 @@ static int validate_w4(const xqhip_w4* w, const char* who) {
     if (!w || !w->nib || !w->meta || w->rows <= 0 || w->cols <= 0)
         return fail(XQHIP_EINVAL, "%s: matrix is not uploaded", who);
     if (w->layout != XQHIP_LAYOUT_TILED64 && w->layout != XQHIP_LAYOUT_GENERIC &&
-        w->layout != XQHIP_LAYOUT_TILED64_F32META && w->layout != XQHIP_LAYOUT_TILED64_SCALE16)
+        w->layout != XQHIP_LAYOUT_TILED64_F32META && w->layout != XQHIP_LAYOUT_TILED64_SCALE16 &&
+        w->layout != XQHIP_LAYOUT_TILED64_F32S_Z4)
         return fail(XQHIP_EINVAL, "%s: unknown layout %d", who, w->layout);
     if (w->layout == XQHIP_LAYOUT_TILED64_SCALE16 && (w->bits != 4 || w->affine || !w->zero_is_8))
         return fail(XQHIP_EINVAL, "%s: the scale-only layout holds 4-bit format-v1 matrices with zero 8", who);
+    if (w->layout == XQHIP_LAYOUT_TILED64_F32S_Z4 && (w->bits != 4 || w->affine))
+        return fail(XQHIP_EINVAL, "%s: the 4-bit-zero layout holds 4-bit format-v1 matrices", who);
     if (w->layout != XQHIP_LAYOUT_GENERIC && (w->group != 64 || w->cols % 64 != 0 || w->cols / 64 > 256))
         return fail(XQHIP_EINVAL, "%s: inconsistent TILED64 matrix %dx%d g%d", who, w->rows, w->cols, w->group);
     if (w->bits != 4 && w->bits != 3 && w->bits != 2)

@@ -50,35 +50,79 @@ __device__ __forceinline__ float half_hi(uint32_t u) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16)));
 }
 
+// a * b rounded to fp32 on its own: never contracted into a later add (the
+// first step of a row sum), so a product's rounding does not depend on how
+// the compiler schedules the code that consumes it
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+
 // Group metadata word of a TILED64 matrix: fp16 (scale, zero) in one u32
 // (META 0), the fp32 (scale, zero) pair in two (META 1, matrices whose values
-// fp16 cannot hold exactly), or the fp16 scale alone with the zero point 8
-// implied (META 2, format-v1 matrices whose zeros are all 8).
+// fp16 cannot hold exactly), the fp16 scale alone with the zero point 8
+// implied (META 2, format-v1 matrices whose zeros are all 8), or the fp32
+// scale with the zero as a 4-bit code (META 3, format-v1 matrices whose zeros
+// are integers 0..15 and whose scales fp16 cannot hold: the reference packer's
+// asymmetric quantiser).  META 3 keeps two arrays in one allocation: the fp32
+// scales [rows][G], then u32 zero words [rows][ceil(G / 8)], nibble k of word
+// j holding the zero of group 8 j + k; a group's word is (scale bits, the zero
+// word that holds its nibble), and meta_zero_at takes the nibble's bit offset.
 struct Scale16 {
     uint32_t v;  // fp16 scale in the low half
 };
+struct ScaleZ4 {
+    uint32_t s;   // fp32 scale bits
+    uint32_t zw;  // zero word of 8 consecutive groups
+};
 template <int META>
-using MetaWord = typename std::conditional<META == 1, u32x2,
-                                           typename std::conditional<META == 2, Scale16, uint32_t>::type>::type;
+using MetaWord = typename std::conditional<
+    META == 1, u32x2,
+    typename std::conditional<META == 2, Scale16,
+                              typename std::conditional<META == 3, ScaleZ4, uint32_t>::type>::type>::type;
+// bytes per group of the (first) metadata array: the offset stride of a group's word
 template <int META>
-constexpr uint32_t kMetaGroupBytes = META == 1 ? 8u : (META == 2 ? 2u : 4u);  // per group
+constexpr uint32_t kMetaGroupBytes = META == 1 ? 8u : (META == 2 ? 2u : 4u);
+// META 3: zero words per row, and the bytes of both arrays of a rows x G matrix
+__host__ __device__ constexpr uint32_t z4_words(uint32_t G) { return (G + 7u) / 8u; }
+template <int META>
+__host__ __device__ constexpr uint32_t meta_total_bytes(uint32_t rows, uint32_t G) {
+    return META == 3 ? rows * G * 4u + rows * z4_words(G) * 4u : rows * G * kMetaGroupBytes<META>;
+}
 __device__ __forceinline__ float meta_scale(uint32_t m) { return half_lo(m); }
 __device__ __forceinline__ float meta_zero(uint32_t m) { return half_hi(m); }
 __device__ __forceinline__ float meta_scale(u32x2 m) { return __uint_as_float(m.x); }
 __device__ __forceinline__ float meta_zero(u32x2 m) { return __uint_as_float(m.y); }
 __device__ __forceinline__ float meta_scale(Scale16 m) { return half_lo(m.v); }
 __device__ __forceinline__ float meta_zero(Scale16) { return 8.0f; }
-// A group's metadata from a buffer resource at byte offset off.
+__device__ __forceinline__ float meta_scale(ScaleZ4 m) { return __uint_as_float(m.s); }
+// The zero of a group; zsh = 4 (g mod 8), the bit offset of group g's nibble
+// in its META 3 zero word (ignored by the other forms).
+template <typename M>
+__device__ __forceinline__ float meta_zero_at(const M& m, uint32_t) { return meta_zero(m); }
+__device__ __forceinline__ float meta_zero_at(const ScaleZ4& m, uint32_t zsh) {
+    return static_cast<float>(__builtin_amdgcn_ubfe(m.zw, zsh, 4));
+}
+// A group's metadata from a buffer resource at byte offset off (META 3: the
+// scale at off, the zero word at zoff).
 // (AUX: the load's cache-policy bits)
 template <int META, int AUX>
-__device__ __forceinline__ MetaWord<META> load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+__device__ __forceinline__ MetaWord<META> load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t zoff = 0) {
     if constexpr (META == 1) {
         return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, AUX);
     } else if constexpr (META == 2) {
         return Scale16{static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, AUX))};
+    } else if constexpr (META == 3) {
+        return ScaleZ4{__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX),
+                       __builtin_amdgcn_raw_buffer_load_b32(r, zoff, 0, AUX)};
     } else {
         return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
     }
+}
+// Byte offset of the zero word of group g of `row` (META 3): past the rows x G
+// scales.  Out-of-range inputs give an offset past the buffer (reads zero).
+__device__ __forceinline__ uint32_t z4_offset(uint32_t rows, uint32_t G, uint32_t row, uint32_t g) {
+    return rows * G * 4u + (__umul24(row, z4_words(G)) + (g >> 3)) * 4u;
 }
 
 // Range-checked buffer loads: an offset at or past the resource's byte range

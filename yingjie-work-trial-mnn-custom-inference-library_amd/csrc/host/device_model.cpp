@@ -100,6 +100,7 @@ bool DeviceModel::upload_matrix(const HostMatrix& m, xqhip_w4* out, std::string*
     matrices_.push_back(out);
     weight_bytes_ += xqhip_w4_weight_bytes(out);
     inexact_meta_ += out->inexact_meta;
+    if (out->layout >= 0 && out->layout < kLayouts) ++layout_count_[out->layout];
     return true;
 }
 
@@ -1149,6 +1150,10 @@ std::string DeviceModel::coverage_summary() const {  // fields of custom_model.c
       << "linear_attention_qk_norm=hip_fused_conv1d;linear_attention_gated_rmsnorm=hip_fused_gemv_prologue;"
       << "sampling=hip_fused_lm_head_argmax;prefill_kv_build=hip_fp16_append;decode_step=hip_graph;"
       << "weight_bytes_per_token=" << weight_bytes_ << ";fp16_meta_inexact=" << inexact_meta_
+      << ";weight_layouts=tiled64:" << layout_count_[XQHIP_LAYOUT_TILED64]
+      << ",generic:" << layout_count_[XQHIP_LAYOUT_GENERIC] << ",f32meta:" << layout_count_[XQHIP_LAYOUT_TILED64_F32META]
+      << ",scale16:" << layout_count_[XQHIP_LAYOUT_TILED64_SCALE16]
+      << ",f32s_z4:" << layout_count_[XQHIP_LAYOUT_TILED64_F32S_Z4]
       << ";kv_capacity=" << max_ctx_ << ";decode_chain=" << chain_note_ << ";kernel_trace=" << trace_note_
       << ";fallback_ops=none";
     return o.str();

@@ -137,6 +137,8 @@ private:
     std::string model_dir_, backend_request_, device_name_;
     uint64_t weight_bytes_ = 0;
     int inexact_meta_ = 0;
+    static constexpr int kLayouts = 5;  // matrices uploaded per XQHIP_LAYOUT_* value
+    int layout_count_[kLayouts] = {};
 
     std::vector<Layer> layers_;
     xqhip_w4 lm_head_{};

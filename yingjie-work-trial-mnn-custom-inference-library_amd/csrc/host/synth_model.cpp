@@ -99,7 +99,7 @@ struct Writer {
         const size_t gpr = static_cast<size_t>((cols + g - 1) / g);
         std::vector<uint8_t> packed(rb * rows);
         std::vector<float> scales(gpr * rows), zeros(gpr * rows, c.zero);
-        const Stream sp(c.seed, name + ":codes"), ss(c.seed, name + ":scales");
+        const Stream sp(c.seed, name + ":codes"), ss(c.seed, name + ":scales"), sz(c.seed, name + ":zeros");
         parallel_for(packed.size() / 8 + 1, c.threads, [&](size_t a, size_t b) {
             for (size_t i = a; i < b; ++i) {
                 const uint64_t v = sp.u64(i);
@@ -110,8 +110,15 @@ struct Writer {
         if (cols & 1)  // keep the unused high nibble of odd-width rows zero
             for (int r = 0; r < rows; ++r) packed[rb * r + rb - 1] &= 0x0f;
         parallel_for(scales.size(), c.threads, [&](size_t a, size_t b) {
-            for (size_t i = a; i < b; ++i)
-                scales[i] = round_f16(static_cast<float>(std::fabs(ss.normal(i)) * c.scale_std));
+            for (size_t i = a; i < b; ++i) {
+                const float s = static_cast<float>(std::fabs(ss.normal(i)) * c.scale_std);
+                if (c.asymmetric) {
+                    scales[i] = s;
+                    zeros[i] = static_cast<float>(std::min(15.0, std::max(0.0, std::nearbyint(7.5 + sz.normal(i)))));
+                } else {
+                    scales[i] = round_f16(s);
+                }
+            }
         });
         char hdr[52] = {};
         std::memcpy(hdr, "XQW4A16", 8);

@@ -21,7 +21,7 @@ F32, F16 = 0, 1
 PRO_NONE, PRO_RMS, PRO_GATED_HEAD, PRO_GATED_HEAD_ACT = 0, 1, 2, 3
 ATTN_PART_STRIDE, ATTN_MAX_SPLITS = 160, 8  # split attention workspace: partials, then counters
 EPI_STORE, EPI_ADD, EPI_SILU_PAIR = 0, 1, 2
-LAYOUT_TILED64, LAYOUT_GENERIC, LAYOUT_TILED64_F32META, LAYOUT_TILED64_SCALE16 = 0, 1, 2, 3
+LAYOUT_TILED64, LAYOUT_GENERIC, LAYOUT_TILED64_F32META, LAYOUT_TILED64_SCALE16, LAYOUT_TILED64_F32S_Z4 = 0, 1, 2, 3, 4
 
 
 class W4(ctypes.Structure):
@@ -301,7 +301,8 @@ class SynthConfig(ctypes.Structure):
                 ("linear_value_head_dim", c_int32), ("linear_num_key_heads", c_int32),
                 ("linear_num_value_heads", c_int32), ("linear_conv_kernel_dim", c_int32), ("group_size", c_int32),
                 ("rms_norm_eps", c_float), ("rope_theta", c_float), ("scale_std", c_float), ("zero", c_float),
-                ("embed_std", c_float), ("norm_std", c_float), ("threads", c_int32)]
+                ("embed_std", c_float), ("norm_std", c_float), ("threads", c_int32),
+                ("asymmetric", c_int32)]
 
 
 _S = c_void_p
