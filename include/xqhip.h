@@ -433,8 +433,9 @@ XQHIP_API int xqhip_lds_fill(float value, void* stream);
  * waits: no kernel boundary and no grid barrier between the ops.  Results are
  * those of xqhip_gemv_w4a16 on the same operands, bit for bit.
  *
- * Every matrix of a chain must be a 4-bit TILED64 matrix and all must share
- * one metadata layout; cols <= 16384. */
+ * Every matrix of a chain must be a 4-bit TILED64 matrix with fp16, fp32-pair
+ * or fp16-scale metadata (layouts TILED64, TILED64_F32META, TILED64_SCALE16,
+ * not TILED64_F32S_Z4), all in one of them; cols <= 16384. */
 typedef struct xqhip_chain_src {
     const float* plain; /* a device fp32 vector complete before the launch, or */
     int32_t op;         /* (plain == NULL) the output of op `op` of the chain */

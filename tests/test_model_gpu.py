@@ -343,7 +343,7 @@ def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch):
     every step is one graph launch timed on its own (decode_step_graph_custom,
     one row entry per untraced step), and the first step after the prefill
     plus every XQ_TRACE_EVERY-th step replay the traced copy of the step graph
-    whose per-op events give the per-op rows (each op one call per traced
+    whose per-op timestamps give the per-op rows (each op one call per traced
     step); the JSON says how many steps the rows were sampled from."""
     monkeypatch.setenv("XQ_TRACE_EVERY", "16")
     s = xb.Session(small_dir, xb.options())
