@@ -301,9 +301,12 @@ PART_CASES = [(32, 8, 128, 32, 0, 64, True), (32, 8, 128, 32, 2, 64, True), (32,
 def test_split_attention_merged_in_kernel(case, splits):
     """xqhip_attn_decode_split (partials merged by the last block of each query
     head) against the oracle and against xqhip_attn_decode_head on its own copy
-    of the caches: bit-identical with one split, within 1e-5 otherwise; three
-    consecutive positions on one workspace, zero-filled once (each call must
-    leave its counters at zero)."""
+    of the caches: bit-identical with one split while the context fits one
+    pass of both kernels (the split kernel's passes are 512 positions, the
+    per-head kernel's 1024: past 512 the running maximum is merged at
+    another point), within 1e-5 otherwise; three consecutive positions on
+    one workspace, zero-filled once (each call must leave its counters at
+    zero)."""
     nq, nkv, hd, rd, pos, max_ctx, gated = case
     theta, eps = 1e7, 1e-6
     print(f"split attention case {case} splits {splits}", flush=True)
@@ -343,7 +346,7 @@ def test_split_attention_merged_in_kernel(case, splits):
         _, want = oracle_attention_step(qsrc, k, gated, qn, kn, nq, nkv, hd, rd, p, theta, eps, kc_got, vc_got)
         got, ref = out.download(np.float32, nq * hd), out2.download(np.float32, nq * hd)
         close(got, want, f"split attention pos {p}")
-        if splits == 1:
+        if splits == 1 and p < 512:
             assert np.array_equal(got, ref), "one split must match the single-block kernel bit for bit"
         else:
             close(got, ref, f"split vs single-block pos {p}", atol=1e-5, rtol=1e-5)

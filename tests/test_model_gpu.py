@@ -337,15 +337,19 @@ def test_decode_chain_matches_per_op_launches(which, small_dir, heads9b_dir, mon
     assert "decode_chain_w4a16" in runs["chain"][2] and "decode_chain_w4a16" not in runs["default"][2]
 
 
-def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch):
+@pytest.mark.parametrize("every", [16, 2])
+def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch, every):
     """Kernel-trace rows of decode (the reference times every op of every step,
     custom_model.cpp:374-417, and exports them through session.cpp:556-566):
     every step is one graph launch timed on its own (decode_step_graph_custom,
     one row entry per untraced step), and the first step after the prefill
     plus every XQ_TRACE_EVERY-th step replay the traced copy of the step graph
     whose per-op timestamps give the per-op rows (each op one call per traced
-    step); the JSON says how many steps the rows were sampled from."""
-    monkeypatch.setenv("XQ_TRACE_EVERY", "16")
+    step); the JSON says how many steps the rows were sampled from.  Every 2:
+    the first traced step after the prefill is followed by another traced
+    step, which must not overwrite its stamps before they are read (every
+    per-op time positive and below the step's).  """
+    monkeypatch.setenv("XQ_TRACE_EVERY", str(every))
     s = xb.Session(small_dir, xb.options())
     assert s.status == xb.XQ_OK
     prompt = [int(t) for t in np.random.default_rng(5).integers(0, 4096, 20)]
@@ -353,9 +357,9 @@ def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch):
     assert st == 0, m.error
     tr = json.loads(s.json("xq_get_kernel_trace_json")[1])
     rows = {r["name"]: r for r in tr["rows"]}
-    traced = 1 + 40 // 16  # the first step after the prefill, then steps 16 and 32
+    traced = 1 + 40 // every  # the first step after the prefill, then every `every`-th graph step
     assert tr["decode_graph_steps"] == 40 and tr["decode_op_traced_graph_steps"] == traced
-    assert tr["decode_op_trace_every"] == 16
+    assert tr["decode_op_trace_every"] == every
     assert rows["decode_step_graph_custom"]["calls"] == 40 - traced
     assert rows["decode_step_graph_traced_custom"]["calls"] == traced
     assert rows["lm_head_custom(fused:rmsnorm_final,argmax)"]["calls"] == traced
@@ -365,6 +369,10 @@ def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch):
     for name in ("linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
                  "attention_score_custom"):
         assert rows[name]["calls"] % traced == 0 and rows[name]["calls"] > 0, name
+    step_max = rows["decode_step_graph_traced_custom"]["max_ms"]
+    for r in tr["rows"]:
+        if "prefill" not in r["name"] and not r["name"].startswith("decode_step_graph"):
+            assert 0 < r["min_ms"] <= r["max_ms"] < step_max, r
     info = s.json("xq_get_backend_info")[1]
-    assert "kernel_trace=per_op_every_16_graph_steps" in info
+    assert f"kernel_trace=per_op_every_{every}_graph_steps" in info
     s.close()

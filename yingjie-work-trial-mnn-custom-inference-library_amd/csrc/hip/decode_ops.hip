@@ -776,17 +776,40 @@ __device__ __forceinline__ uint4 buf_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t 
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Orders one wave's LDS accesses: a wave's LDS instructions execute in issue
+// order, so after this point its lanes see each other's earlier LDS writes
+// (the fences keep the compiler from moving LDS accesses across it); no block
+// barrier is involved.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // One query head over the cached positions [c0, c1) and, when `fresh`, the new
 // token at `pos` (appended to the caches by the first query head of each kv
-// head), with first-pass sub-passes KS (later passes, for ranges past
-// kHeadPass, use all kHeadKSubs).  PART: the unnormalised result goes to
+// head), with first-pass sub-passes KS (later passes, for ranges past one
+// pass, use all the pass's sub-passes).  PART: the unnormalised result goes to
 // part_out (running max, exp sum, sum of exp-weighted values; the consumer
 // merges the ranges and applies 1/l and the gate); otherwise the gated output.
+// A pass is kHeadPass tokens for the per-head kernel and half that for the
+// split kernel (whose ranges are an eighth of the context), which keeps the
+// split kernel's longest body within the register file.
+// kPassSubs(PART): 128-token sub-passes per pass
+template <bool PART>
+constexpr int kPassSubs = PART ? kHeadKSubs / 2 : kHeadKSubs;
+
 template <int HD, int KS, bool PART>
 __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSmem<HD>& sm, int pos, int c0, int c1,
                                                bool fresh, float* part_out) {
     static_assert(HD == 128, "4 score lanes x 32 dims, 16 value lanes x 8 dims");
     constexpr int kWaves = kHeadThreads / kWave;
+    constexpr int kSubs = kPassSubs<PART>;
+    constexpr int kPass = kSubs * kHeadKSub;  // tokens per pass
+    static_assert(KS >= 1 && KS <= kSubs, "first-pass sub-passes");
+    // the first pass's values are requested with its keys when both fit the
+    // register budget beside each other (up to 512 tokens)
+    constexpr bool kVPre = KS <= 4;
     const GqaLaunch& p = a.g;
     const int group = p.nq / p.nkv;
     // blocks b, b + nkv, b + 2 nkv, ... take the query heads of one kv head:
@@ -808,11 +831,11 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
     const float* nw = wid == 0 ? a.q_norm : a.k_norm;
     const float hv0 = src[lane], hv1 = src[lane + kWave];
     const float w0 = nw[lane], w1 = nw[lane + kWave];
-    const int half = a.rotary_dim / 2;
+    const int half = a.rotary_dim / 2;  // <= HD / 2 = kWave: one rotary pair per lane of waves 0 and 1
     const __amdgpu_buffer_rsrc_t r_cs =
         buf_rsrc(a.rope_cs, half > 0 ? static_cast<uint32_t>(pos + 1) * a.rope_pairs * 8u : 0u);
     const uint32_t cs_off =
-        tid < 2 * half ? (static_cast<uint32_t>(pos) * a.rope_pairs + (tid < half ? tid : tid - half)) * 8u : kBufOOB;
+        wid < 2 && lane < half ? (static_cast<uint32_t>(pos) * a.rope_pairs + lane) * 8u : kBufOOB;
     const auto csw = __builtin_amdgcn_raw_buffer_load_b64(r_cs, cs_off, 0, 0);
     // no gate projection: the reference's zero gate, sigmoid(0) (custom_model.cpp:750-753)
     const __amdgpu_buffer_rsrc_t r_gate =
@@ -830,9 +853,26 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
             for (int u = 0; u < 4; ++u)
                 kr[j][u] = buf_load_u4(r, static_cast<uint32_t>(tt + kHeadKSub * j) * row_bytes + sub * 16u + u * 64u);
     };
+    // the values of cached positions [t0, t0 + nc), rows past nc read 0: value
+    // sub-pass jj (32 tokens) of this thread is token ts + 32 jj
+    auto load_v = [&](int t0, int nc, auto& vr) {
+        constexpr int JV = sizeof(vr) / sizeof(vr[0]);
+        const __amdgpu_buffer_rsrc_t r = buf_rsrc(p.v_cache + static_cast<size_t>(t0) * kv_stride + kh * HD,
+                                                  static_cast<uint32_t>(nc) * row_bytes);
+#pragma unroll
+        for (int jj = 0; jj < JV; ++jj)
+            vr[jj] = buf_load_u4(r, static_cast<uint32_t>(ts + kHeadVTok * jj) * row_bytes + dsl * 16u);
+    };
     uint4 kr[KS][4];
-    load_k(c0, min(kHeadPass, c1 - c0), kr);
-    // per-head RMSNorm (custom_model.cpp:301-313) of q and k; v as it is
+    uint4 vpre[kVPre ? KS * kHeadVPerK : 1];
+    load_k(c0, min(kPass, c1 - c0), kr);
+    if constexpr (kVPre) load_v(c0, min(kPass, c1 - c0), vpre);
+    // per-head RMSNorm (custom_model.cpp:301-313) of q (wave 0) and k (wave 1),
+    // then their partial RoPE (custom_model.cpp:351-370), pairs (i, half + i),
+    // each wave on its own LDS row (wave_lds_sync, no block barrier); the new
+    // key (wave 1) and value (wave 2) enter the cache in fp16 and are used
+    // rounded, like every slot, appended by the kv head's first query head
+    const size_t slot = static_cast<size_t>(pos) * kv_stride + static_cast<size_t>(kh) * HD;
     if (wid < 2) {
         float ss = hv0 * hv0 + hv1 * hv1;
         ss = wave_sum(ss);
@@ -840,33 +880,33 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
         float* dst = wid == 0 ? sm.qs : sm.kn;
         dst[lane] = hv0 * (inv * w0);
         dst[lane + kWave] = hv1 * (inv * w1);
+        wave_lds_sync();
+        if (lane < half) {
+            const float cx = __uint_as_float(csw[0]), cy = __uint_as_float(csw[1]);
+            const float x0 = dst[lane], x1 = dst[half + lane];
+            dst[lane] = x0 * cx - x1 * cy;
+            dst[half + lane] = x1 * cx + x0 * cy;
+        }
+        if (wid == 1) {
+            wave_lds_sync();
+            const _Float16 k0 = static_cast<_Float16>(sm.kn[lane]), k1 = static_cast<_Float16>(sm.kn[lane + kWave]);
+            if (owner) {
+                a.k_cache[slot + lane] = k0;
+                a.k_cache[slot + lane + kWave] = k1;
+            }
+            sm.kn[lane] = static_cast<float>(k0);
+            sm.kn[lane + kWave] = static_cast<float>(k1);
+        }
     } else if (wid == 2) {
-        sm.vn[lane] = hv0;
-        sm.vn[lane + kWave] = hv1;
+        const _Float16 v0 = static_cast<_Float16>(hv0), v1 = static_cast<_Float16>(hv1);
+        if (owner) {
+            a.v_cache[slot + lane] = v0;
+            a.v_cache[slot + lane + kWave] = v1;
+        }
+        sm.vn[lane] = static_cast<float>(v0);
+        sm.vn[lane + kWave] = static_cast<float>(v1);
     }
     if (tid < HD) sm.gate[tid] = gv;
-    __syncthreads();
-    // partial RoPE (custom_model.cpp:351-370) of q and the new key, pairs (i, half + i)
-    if (tid < 2 * half) {
-        float* v = tid < half ? sm.qs : sm.kn;
-        const int d = tid < half ? tid : tid - half;
-        const float cx = __uint_as_float(csw[0]), cy = __uint_as_float(csw[1]);
-        const float x0 = v[d], x1 = v[half + d];
-        v[d] = x0 * cx - x1 * cy;
-        v[half + d] = x1 * cx + x0 * cy;
-    }
-    __syncthreads();
-    // the new key / value enter the cache in fp16 and are used rounded, like every slot
-    if (tid < HD) {
-        const _Float16 kq = static_cast<_Float16>(sm.kn[tid]), vq = static_cast<_Float16>(sm.vn[tid]);
-        if (owner) {
-            const size_t slot = static_cast<size_t>(pos) * kv_stride + static_cast<size_t>(kh) * HD + tid;
-            a.k_cache[slot] = kq;
-            a.v_cache[slot] = vq;
-        }
-        sm.kn[tid] = static_cast<float>(kq);
-        sm.vn[tid] = static_cast<float>(vq);
-    }
     __syncthreads();
     // q in registers, in the score lanes' dim order
     float qreg[32];
@@ -883,14 +923,16 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
     // one pass over cached positions [t0, t0 + nc) with their keys in kp (and
     // the new token when it falls in this pass)
-    auto pass = [&](int t0, const auto& kp) {
+    // (vr: the pass's values, already requested when VLOADED, else requested
+    // sub-pass by sub-pass as the keys are consumed)
+    auto pass = [&](int t0, const auto& kp, auto& vr, auto vloaded) {
         constexpr int J = sizeof(kp) / sizeof(kp[0]);
-        const int nc = min(kHeadPass, c1 - t0);
-        const bool last = fresh && c1 - t0 < kHeadPass;
+        constexpr bool kLoaded = decltype(vloaded)::value;
+        const int nc = min(kPass, c1 - t0);
+        const bool last = fresh && c1 - t0 < kPass;
         const __amdgpu_buffer_rsrc_t r_v = buf_rsrc(p.v_cache + static_cast<size_t>(t0) * kv_stride + kh * HD,
                                                     static_cast<uint32_t>(nc) * row_bytes);
         float m = -INFINITY;
-        uint4 vr[J * kHeadVPerK];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int tl = tt + kHeadKSub * j;
@@ -910,10 +952,12 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
                 m = fmaxf(m, dot);
             }
             // the values of these 128 tokens, into the registers the keys held
+            if constexpr (!kLoaded) {
 #pragma unroll
-            for (int r = 0; r < kHeadVPerK; ++r) {
-                const int jj = kHeadVPerK * j + r;
-                vr[jj] = buf_load_u4(r_v, static_cast<uint32_t>(ts + kHeadVTok * jj) * row_bytes + dsl * 16u);
+                for (int r = 0; r < kHeadVPerK; ++r) {
+                    const int jj = kHeadVPerK * j + r;
+                    vr[jj] = buf_load_u4(r_v, static_cast<uint32_t>(ts + kHeadVTok * jj) * row_bytes + dsl * 16u);
+                }
             }
         }
         m = wave_max(m);
@@ -953,14 +997,20 @@ __device__ __forceinline__ void head_attention(const AttnDecodeLaunch& a, HeadSm
         }
         __syncthreads();  // sc and red are rewritten by the next pass
     };
-    pass(c0, kr);
-    // longer ranges: further passes of kHeadKSubs sub-passes, each loading its
+    if constexpr (kVPre) {
+        pass(c0, kr, vpre, std::true_type{});
+    } else {
+        uint4 vr[KS * kHeadVPerK];
+        pass(c0, kr, vr, std::false_type{});
+    }
+    // longer ranges: further passes of kSubs sub-passes, each loading its
     // keys first (kept apart from the first pass so that no key register lives
     // across a value phase); the new token may open a pass of its own
-    for (int t0 = c0 + kHeadPass; fresh ? t0 <= c1 : t0 < c1; t0 += kHeadPass) {
-        uint4 kr2[kHeadKSubs][4];
-        load_k(t0, min(kHeadPass, c1 - t0), kr2);
-        pass(t0, kr2);
+    for (int t0 = c0 + kPass; fresh ? t0 <= c1 : t0 < c1; t0 += kPass) {
+        uint4 kr2[kSubs][4];
+        uint4 vr2[kSubs * kHeadVPerK];
+        load_k(t0, min(kPass, c1 - t0), kr2);
+        pass(t0, kr2, vr2, std::false_type{});
     }
     // lanes with the same dsl: 4 per wave (16 apart), then the waves through LDS;
     // l is the same in every dsl lane of a token group and reduces alongside
@@ -1020,7 +1070,8 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_head_kernel(AttnDeco
 // splits may run on other XCDs), weights exp(m_s - max m), multiplies by 1 / l
 // (custom_model.cpp:901-904) and the sigmoid gate, writes a.g.out and sets the
 // counter back to 0; no block waits for another.  With one split the result is
-// the single-block kernel's, bit for bit.
+// the single-block kernel's, bit for bit, up to 512 cached positions (one pass
+// of this kernel; the single-block kernel's passes are twice as long).
 template <int HD>
 __global__ void __launch_bounds__(kHeadThreads) attn_decode_part_kernel(AttnDecodeLaunch a, float* part,
                                                                         uint32_t* cnt) {
@@ -1041,16 +1092,13 @@ __global__ void __launch_bounds__(kHeadThreads) attn_decode_part_kernel(AttnDeco
             __hip_atomic_store(out + 1, 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     } else {
-        const int ks = max(1, (min(c1 - c0, kHeadPass) + kHeadKSub - 1) / kHeadKSub);
+        constexpr int kSubs = kPassSubs<true>;
+        const int ks = max(1, (min(c1 - c0, kSubs * kHeadKSub) + kHeadKSub - 1) / kHeadKSub);
         switch (ks) {
             case 1: head_attention<HD, 1, true>(a, sm, pos, c0, c1, fresh, out); break;
             case 2: head_attention<HD, 2, true>(a, sm, pos, c0, c1, fresh, out); break;
             case 3: head_attention<HD, 3, true>(a, sm, pos, c0, c1, fresh, out); break;
-            case 4: head_attention<HD, 4, true>(a, sm, pos, c0, c1, fresh, out); break;
-            case 5: head_attention<HD, 5, true>(a, sm, pos, c0, c1, fresh, out); break;
-            case 6: head_attention<HD, 6, true>(a, sm, pos, c0, c1, fresh, out); break;
-            case 7: head_attention<HD, 7, true>(a, sm, pos, c0, c1, fresh, out); break;
-            default: head_attention<HD, 8, true>(a, sm, pos, c0, c1, fresh, out); break;
+            default: head_attention<HD, kSubs, true>(a, sm, pos, c0, c1, fresh, out); break;
         }
     }
     // Ordering without fences: every partial store above is an agent-scope

@@ -762,7 +762,10 @@ bool DeviceModel::ensure_graphs(std::string* error) {
         }))
         return false;
     // the traced step: the same launches with a timestamp kernel after every
-    // op (event-record nodes of a graph give no timings here)
+    // op (event-record nodes of a graph give no timings here).  XQ_TRACE_EVERY=0
+    // leaves it out: the first step after a prefill then runs eagerly with
+    // per-op events, and graph steps are only timed as a whole
+    if (trace_every_ <= 0) return true;
     ops_.clear();
     event_next_ = 0;
     op_chained_ = false;
@@ -1041,6 +1044,16 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
     ++graph_steps_;
     const bool traced = g_step_traced_ &&
                         (detail_decode_ || (trace_every_ > 0 && graph_steps_ % static_cast<uint64_t>(trace_every_) == 0));
+    if (traced) {
+        // every traced step stamps the same host array: a traced step not yet
+        // credited is waited for and credited before the next one overwrites it
+        bool earlier_traced = false;
+        for (const PendingStep& st : pending_) earlier_traced = earlier_traced || st.traced;
+        if (earlier_traced) {
+            XQ_CALL(xqhip_event_synchronize(pending_.back().end), "step event");
+            credit_steps(trace, pending_.size());
+        }
+    }
     void* start = last_end_;
     if (!chained_ || upload || !start) {
         start = next_step_event();
