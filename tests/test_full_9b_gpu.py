@@ -7,7 +7,7 @@ holds the reference's own run through its C ABI on the seeded synthetic model
 vocab 248320, W4A16 g64) with a 512-token seeded prompt: the greedy id of each
 of 16 decode steps, the final-normed hidden state after the prefill and after
 every step, the lm_head top-10 of each of those states, and sha256 digests of
-six model files.  Here the same model is written on the GPU box (checked
+six model files.  Here the same model is written where the test runs (checked
 against the digests) and run through libxqwen35.so: batched MFMA prefill of
 the 512 tokens, then 16 decode steps.
 
