@@ -13,6 +13,9 @@ Prints ONE JSON line.  Workloads (--workload):
   mlp    decode MLP block, hidden 4096 -> 12288 -> 4096, W4A16 g64: fused
          RMSNorm + gate/up GEMV + SiLU*up, then down GEMV + residual add.
          value = algorithmic HBM GB/s of the block (the GEMV bandwidth metric).
+  decode-asym
+         the second run of the decode workload alone (the model written with
+         the asymmetric quantiser's metadata).
   gemv-sweep
          every decode-step projection shape of the 9B-shaped model (with the
          prologue and epilogue it runs with in the model) for 4-, 3- and 2-bit
@@ -591,6 +594,19 @@ def bench_decode_asymmetric(args, prompt, sym_tps, sym_proj):
     return out
 
 
+def bench_decode_asym_only(args):
+    """--workload decode-asym: only the asymmetric-metadata run of the decode
+    workload (for profiling that model on its own)."""
+    prompt = np.random.default_rng(4).integers(0, 248320, 512, dtype=np.int32)
+    a = bench_decode_asymmetric(args, prompt, None, [])
+    return {"metric": METRIC, "value": a["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": a["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u4xf16->f32", "data": "synthetic",
+            "config": {"workload": "batch-1 greedy decode of the 9B-shaped model written with the asymmetric "
+                                   "quantiser's metadata, 512-token prefill and one untimed decode step, then "
+                                   f"{args.steps} timed decode steps", **a}}
+
+
 def cpu_baseline_decode(prompt, gpu_sess, runs=3):
     """The compiled reference customlib (oracle/_ref) on the same model files and
     host cores, timed by its own xq_metrics (decode tokens / decode ms,
@@ -670,7 +686,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "mlp", "gemv-sweep", "pmc-probe"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "decode-asym", "mlp", "gemv-sweep", "pmc-probe"])
     ap.add_argument("--bits", type=int, nargs="+", default=[4, 3, 2], help="gemv-sweep code widths")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
@@ -691,8 +708,8 @@ def main():
     name = ctypes.create_string_buffer(256)
     xb.hip().xqhip_device_name(name, 256)
     log(f"[bench] device: {name.value.decode()}")
-    res = {"decode": bench_decode, "mlp": bench_mlp, "gemv-sweep": bench_gemv_sweep,
-           "pmc-probe": pmc_probe}[args.workload](args)
+    res = {"decode": bench_decode, "decode-asym": bench_decode_asym_only, "mlp": bench_mlp,
+           "gemv-sweep": bench_gemv_sweep, "pmc-probe": pmc_probe}[args.workload](args)
     print(json.dumps(res), flush=True)
 
 
