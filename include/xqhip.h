@@ -29,7 +29,9 @@ enum {
     XQHIP_OK = 0,
     XQHIP_EINVAL = -1,   /* bad argument or unsupported shape */
     XQHIP_EDEVICE = -2,  /* HIP runtime error (message in xqhip_last_error) */
-    XQHIP_ENOMEM = -3
+    XQHIP_ENOMEM = -3,
+    XQHIP_ENOTSUP = -4   /* valid arguments this entry point cannot run on this
+                            matrix or device (the caller uses the separate calls) */
 };
 
 /* Element types of activation vectors. */
@@ -338,6 +340,39 @@ XQHIP_API int xqhip_linear_attn_step_act(const float* mixed, float* conv_state, 
                                          const float* b, const float* a_log, const float* dt_bias, float* state,
                                          int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos,
                                          float* out, float* gate, void* stream);
+
+/* The linear-attention decode step and the output projection that consumes
+ * it, as one launch: the same results, bit for bit, as
+ *   xqhip_linear_attn_step_act(mixed, ..., pos, out, gate, stream);
+ *   xqhip_prologue pro = {XQHIP_PRO_GATED_HEAD_ACT, lv_hd, norm_weight, gate, eps};
+ *   xqhip_gemv_w4a16(w, out, XQHIP_F32, &pro, y, XQHIP_F32, XQHIP_EPI_ADD, stream);
+ * (the step, applyGatedHeadRms, out_proj and addResidual of a linear-attention
+ * layer, customlib/runtime/custom_model.cpp:1074-1135, 1179), with the
+ * projection's weights requested while the step runs instead of after a
+ * kernel boundary.  One 1024-thread block per CU (every block must be resident
+ * at once: each waits, boundedly, for the step's output of all of them).
+ * w: a 4-bit TILED64 matrix (any of its metadata forms) with lv_n * lv_hd <=
+ * 4096 columns; ksize 4.  sync: xqhip_step_outproj_sync_bytes() bytes of
+ * device memory, 128-byte aligned, zero-filled once before the first launch;
+ * every launch leaves it zeroed, launches sharing it must be ordered (one
+ * stream).  Graph-capturable.  Returns XQHIP_ENOTSUP when the matrix or the
+ * device does not allow the combination (xqhip_step_outproj_supported says so
+ * beforehand).  No counterpart in the reference, which runs the two ops one
+ * after the other.  Measured on MI355X (9B shapes) slower than the two calls,
+ * 15.9 against 11.0 us: the hand-off between CUs of different XCDs inside one
+ * launch costs more than a kernel boundary. */
+XQHIP_API size_t xqhip_step_outproj_sync_bytes(void);
+XQHIP_API int xqhip_step_outproj_supported(const xqhip_w4* w, int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
+XQHIP_API int xqhip_linear_attn_step_outproj(const float* mixed, float* conv_state, const float* conv_w,
+                                             const float* a, const float* b, const float* a_log,
+                                             const float* dt_bias, float* state, int lk_n, int lk_hd, int lv_n,
+                                             int lv_hd, int ksize, const int32_t* pos, float* out, float* gate,
+                                             const xqhip_w4* w, const float* norm_weight, float eps, float* y,
+                                             void* sync, void* stream);
+/* Reads the sync block's error word (synchronous copy): 0, or nonzero after a
+ * launch whose wait gave up (its results are then invalid; zero-fill the block
+ * again before the next launch). */
+XQHIP_API int xqhip_step_outproj_error(const void* sync, int* error);
 /* y = x * inv * w (rmsnormReference, ref_rmsnorm.cpp:8-17). */
 XQHIP_API int xqhip_rmsnorm(const float* x, const float* w, int n, float eps, float* y, void* stream);
 

@@ -337,6 +337,43 @@ def test_decode_chain_matches_per_op_launches(which, small_dir, heads9b_dir, mon
     assert "decode_chain_w4a16" in runs["chain"][2] and "decode_chain_w4a16" not in runs["default"][2]
 
 
+@pytest.mark.parametrize("which", ["small", "heads9b"])
+def test_step_outproj_launch_matches_separate_launches(which, small_dir, heads9b_dir, monkeypatch):
+    """XQ_FUSE_STEP=1 runs the linear-attention layers' step and output
+    projection as one launch (xqhip_linear_attn_step_outproj; by default they
+    are two).  Ids and hidden states after the prefill and after every greedy
+    step are equal bit for bit, and both match the oracle."""
+    d = small_dir if which == "small" else heads9b_dir
+    prompt = [int(t) for t in np.random.default_rng(78).integers(0, 4096, 45)]
+    want, margins, hiddens = oracle_run(d, prompt, 6)
+    runs = {}
+    for mode in ("fused", "separate"):
+        monkeypatch.delenv("XQ_FUSE_STEP", raising=False)
+        if mode == "fused":
+            monkeypatch.setenv("XQ_FUSE_STEP", "1")
+        s = xb.Session(d, xb.options())
+        assert s.status == xb.XQ_OK
+        info = s.json("xq_get_backend_info")[1]
+        assert ("linear_step_outproj=on" in info) == (mode == "fused"), info
+        st, _ = s.prefill(prompt)
+        assert st == 0
+        toks, hs = [], [s.hidden()[1]]
+        for _ in range(6):
+            st, tok, m = s.decode_one()
+            assert st == 0, m.error
+            toks.append(tok)
+            hs.append(s.hidden()[1])
+        compare_tokens(toks, want, margins)
+        close(hs[-1], hiddens[-1], f"{mode}: hidden after 6 steps")
+        runs[mode] = (toks, hs, s.json("xq_get_kernel_trace_json")[1])
+        s.close()
+    assert runs["fused"][0] == runs["separate"][0]
+    for a, b in zip(runs["fused"][1], runs["separate"][1]):
+        assert np.array_equal(a, b)
+    assert "linear_attention_state_update_custom+linear_attn_out_proj_w4a16" in runs["fused"][2]
+    assert "linear_attention_state_update_custom+" not in runs["separate"][2]
+
+
 @pytest.mark.parametrize("every", [16, 2])
 def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch, every):
     """Kernel-trace rows of decode (the reference times every op of every step,

@@ -58,8 +58,9 @@ constexpr uint32_t kOutOfRange = 0x80000000u; // beyond every range (matrices < 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t vec_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, kRsrcWord3);
 }
+template <int AUX = 0>
 __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
 }
 __device__ __forceinline__ void as_floats8(const u32x4& a, const u32x4& b, float* v) {
     v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
@@ -75,8 +76,8 @@ __device__ __forceinline__ void decode_act8(const u32x4& a, const u32x4& b, int 
     for (int i = 0; i < 8; ++i) v[i] = x_f16 ? ((i & 1) ? half_hi(h[i >> 1]) : half_lo(h[i >> 1])) : f[i];
 }
 
-// The block stages the whole vector: thread t owns the (group, word) items
-// t, t + THREADS, ... (8 consecutive columns each).  Every wave first issues
+// The block stages the whole vector: thread t (tid, 0 .. THREADS - 1) owns the
+// (group, word) items t, t + THREADS, ... (8 consecutive columns each).  Every wave first issues
 // the 16-byte loads of x and of the prologue vectors, the block then passes a
 // barrier that waits for none of them, and only then calls `prefetch`, which
 // issues the block's first weight loads; the activations thus return first and
@@ -88,9 +89,12 @@ __device__ __forceinline__ void decode_act8(const u32x4& a, const u32x4& b, int 
 // synchronises the block before reading xs.  Prologue vectors are preloaded
 // only for <= 2 items per thread (the 4096-column launches): wider blocks load
 // them after the prefetch, to keep the register budget of the main loop.
-template <int THREADS, int ITEMS, typename Prefetch>
+// XAUX: cache policy of the loads of x and of the gate vector (kAuxAgent when
+// other blocks of the same launch wrote them).
+template <int THREADS, int ITEMS, int XAUX = 0, typename Prefetch>
 __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prologue& pro, int cols,
-                                            uint4* __restrict__ xs, float* red, Prefetch&& prefetch) {
+                                            uint4* __restrict__ xs, float* red, int tid, Prefetch&& prefetch) {
+    __builtin_assume(tid >= 0 && tid < THREADS);
     constexpr bool kPre = ITEMS <= 2;
     constexpr int kW = kPre ? ITEMS : 1;
     const int G = cols >> 6;
@@ -107,15 +111,15 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
     u32x4 xa[ITEMS], xb[ITEMS], wa[kW], wb[kW], za[kW], zb[kW];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t item = static_cast<uint32_t>(min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1));
-        xa[k] = load16(xr, x_f16 ? item * 16u : item * 32u);
-        xb[k] = load16(xr, x_f16 ? kOutOfRange : item * 32u + 16u);
+        const uint32_t item = static_cast<uint32_t>(min(tid + k * THREADS, n_items - 1));
+        xa[k] = load16<XAUX>(xr, x_f16 ? item * 16u : item * 32u);
+        xb[k] = load16<XAUX>(xr, x_f16 ? kOutOfRange : item * 32u + 16u);
         if constexpr (kPre) {
             const uint32_t woff = static_cast<uint32_t>(static_cast<int>(item * 8u) & hmask) * 4u;
             wa[k] = load16(wr, woff);
             wb[k] = load16(wr, woff + 16u);
-            za[k] = load16(zr, item * 32u);
-            zb[k] = load16(zr, item * 32u + 16u);
+            za[k] = load16<XAUX>(zr, item * 32u);
+            zb[k] = load16<XAUX>(zr, item * 32u + 16u);
         }
     }
     // Every wave's activation loads are issued before any wave's weight loads:
@@ -146,7 +150,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
-            const bool in = static_cast<int>(threadIdx.x) + k * THREADS < n_items;
+            const bool in = tid + k * THREADS < n_items;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float a = in ? v[k][i] : 0.0f;
@@ -154,7 +158,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
             }
         }
         ss = wave_sum(ss);
-        if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+        if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
             float wl[8];
@@ -162,7 +166,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
 #pragma unroll
                 for (int i = 0; i < 8; ++i) wl[i] = wv[k][i];
             } else {
-                const uint32_t item = static_cast<uint32_t>(min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1));
+                const uint32_t item = static_cast<uint32_t>(min(tid + k * THREADS, n_items - 1));
                 as_floats8(load16(wr, item * 32u), load16(wr, item * 32u + 16u), wl);
             }
 #pragma unroll
@@ -192,10 +196,10 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
                     zl[i] = zv[k][i];
                 }
             } else {
-                const uint32_t item = static_cast<uint32_t>(min(static_cast<int>(threadIdx.x) + k * THREADS, n_items - 1));
+                const uint32_t item = static_cast<uint32_t>(min(tid + k * THREADS, n_items - 1));
                 const uint32_t woff = static_cast<uint32_t>(static_cast<int>(item * 8u) & hmask) * 4u;
                 as_floats8(load16(wr, woff), load16(wr, woff + 16u), wl);
-                as_floats8(load16(zr, item * 32u), load16(zr, item * 32u + 16u), zl);
+                as_floats8(load16<XAUX>(zr, item * 32u), load16<XAUX>(zr, item * 32u + 16u), zl);
             }
             if (pro.mode == PRO_GATED_ACT) {  // the gate holds silu(gate) already (uniform branch)
 #pragma unroll
@@ -209,7 +213,7 @@ __device__ __forceinline__ void stage_x_lds(const void* x, int x_f16, const Prol
     uint32_t* xw = reinterpret_cast<uint32_t*>(xs);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
-        const int item = threadIdx.x + k * THREADS;
+        const int item = tid + k * THREADS;
         const int g = item >> 3, w = item & 7;
         // group maximum over the 8 items of the group (8 consecutive lanes)
         float mx = 0.0f;
@@ -262,8 +266,8 @@ inline bool stage_supported(int cols, const Prologue& pro) {
 // Greedy argmax in two kernels: every GEMV block stores its best (value, row)
 // key, then argmax_finish_kernel reduces the keys.  The kernel boundary orders
 // the two (no grid-wide fence, no completion counter).
-__device__ __forceinline__ void store_block_key(uint64_t block_best, uint64_t* partial) {
-    if (threadIdx.x == 0) partial[blockIdx.x] = block_best;
+__device__ __forceinline__ void store_block_key(uint64_t block_best, uint64_t* partial, int tid, int block) {
+    if (tid == 0) partial[block] = block_best;
 }
 
 hipError_t launch_argmax_finish(const GemvLaunch& p, int blocks, hipStream_t s);  // gemv_w4a16.hip
@@ -391,19 +395,27 @@ __device__ __forceinline__ void group_words(const uint4& a, const uint4& b, uint
     }
 }
 
-template <int NCH, int RG, int R, int EPI, int BITS, int META>
-__global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
-    // x is not __restrict__: with it the compiler may move the staging loads of
-    // x across the asm barrier of stage_x_lds (it would assume no aliasing)
-    const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
-    const void* x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
-    uint64_t* __restrict__ partial, int grid) {  // grid == gridDim.x (an argument: no late kernarg fetch)
-    extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
-    __shared__ float red[32];
-    __shared__ uint64_t lds_keys[16];
+// The kernel body, for the 64 * NCH * RG threads tid = 0 .. of block `block`
+// out of `grid`; xs / red / lds_keys are the block's LDS areas.
+// EARLY = false (the plain GEMV): the activations are requested first, then
+// the first weight batches, then the staging arithmetic runs while the weights
+// stream in; pre() and wait() are not called.
+// EARLY = true (a GEMV whose input another part of the same launch produces):
+// pre() first, then the first two weight batches (with trips <= 2 every weight
+// the block reads), then wait(), which returns once the input is complete, and
+// only then the activation loads, with cache policy XAUX.
+template <int NCH, int RG, int R, int EPI, int BITS, int META, bool EARLY = false, int XAUX = 0,
+          typename Pre = void (*)(), typename Wait = void (*)()>
+__device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta,
+                                               int rows, int cols, int affine, const void* x, int x_f16,
+                                               const Prologue& pro, void* __restrict__ y, int y_f16,
+                                               uint64_t* __restrict__ partial, int grid, int tid, int block,
+                                               uint4* xs, float* red, uint64_t* lds_keys, Pre&& pre, Wait&& wait) {
+    __builtin_assume(tid >= 0 && tid < 64 * NCH * RG);
+    __builtin_assume(block >= 0 && block < grid);
     const int G = cols >> 6;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = threadIdx.x / kWave;
+    const int lane = tid & (kWave - 1);
+    const int wid = tid / kWave;
     const int c = wid % NCH;
     const int rg = wid / NCH;
     const int g = c * 64 + lane;
@@ -416,17 +428,26 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
     // activations first, then the first weight batches, then the staging
     // arithmetic while the weights stream in
     WBatch<R, META> buf0, buf1;
-    int base = blockIdx.x * RG;
-    // With R >= 2 only the first batch is issued before the staging: a second
-    // one would stall its issue on the CU's in-flight memory requests, and the
-    // staging waits behind it.
-    stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, [&]() {
+    int base = block * RG;
+    if constexpr (EARLY) {
+        pre();
         load_batch<R, BITS, META>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-        if constexpr (R == 1)
-            load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-    });
-    if constexpr (R > 1)
         load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        wait();
+        stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG, XAUX>(x, x_f16, pro, cols, xs, red, tid, []() {});
+    } else {
+        // With R >= 2 only the first batch is issued before the staging: a second
+        // one would stall its issue on the CU's in-flight memory requests, and the
+        // staging waits behind it.
+        stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, tid, [&]() {
+            load_batch<R, BITS, META>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+            if constexpr (R == 1)
+                load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt,
+                                          has_group);
+        });
+        if constexpr (R > 1)
+            load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+    }
     __syncthreads();
     // this lane's group: kDigits x 8 words of digits, then e and G
     uint32_t xd[kDigits][8];
@@ -491,7 +512,7 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         __syncthreads();
         if (c == 0) {
             for (int bi = b0; bi < b0 + n; ++bi) {
-                const int r0 = (static_cast<int>(blockIdx.x) * RG + bi * stride + rg) * R;
+                const int r0 = (block * RG + bi * stride + rg) * R;
                 if (r0 >= rows) continue;
                 float acc[R];
 #pragma unroll
@@ -584,11 +605,26 @@ __global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
         if (lane == 0) lds_keys[wid] = (c == 0) ? best : 0;
         __syncthreads();
         uint64_t b = 0;
-        if (threadIdx.x == 0)
+        if (tid == 0)
             for (int i = 0; i < NCH * RG; ++i) b = u64_max(b, lds_keys[i]);
         __syncthreads();
-        store_block_key(b, partial);
+        store_block_key(b, partial, tid, block);
     }
+}
+
+template <int NCH, int RG, int R, int EPI, int BITS, int META>
+__global__ void __launch_bounds__(64 * NCH * RG) gemv_w4_tiled(
+    // x is not __restrict__: with it the compiler may move the staging loads of
+    // x across the asm barrier of stage_x_lds (it would assume no aliasing)
+    const uint8_t* __restrict__ nib, const uint32_t* __restrict__ meta, int rows, int cols, int affine,
+    const void* x, int x_f16, Prologue pro, void* __restrict__ y, int y_f16,
+    uint64_t* __restrict__ partial, int grid) {  // grid == gridDim.x (an argument: no late kernarg fetch)
+    extern __shared__ uint4 xs[];  // staged activations, kStageRecord uint4 per group
+    __shared__ float red[32];
+    __shared__ uint64_t lds_keys[16];
+    gemv_tiled_run<NCH, RG, R, EPI, BITS, META>(nib, meta, rows, cols, affine, x, x_f16, pro, y, y_f16, partial, grid,
+                                                static_cast<int>(threadIdx.x), static_cast<int>(blockIdx.x), xs, red,
+                                                lds_keys, []() {}, []() {});
 }
 
 // ---------------------------------------------------------------------------

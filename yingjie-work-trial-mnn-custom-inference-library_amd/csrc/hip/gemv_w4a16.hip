@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(256) gemv_w4_generic(const uint8_t* __restrict
         if (threadIdx.x == 0)
             for (int i = 0; i < nw; ++i) b = u64_max(b, lds_keys[i]);
         __syncthreads();
-        store_block_key(b, partial);
+        store_block_key(b, partial, threadIdx.x, blockIdx.x);
     }
 }
 

@@ -869,6 +869,79 @@ int xqhip_linear_attn_step_act(const float* mixed, float* conv_state, const floa
     return check(xqhip::launch_linear_step(p, as_stream(stream)), "linear step launch");
 }
 
+size_t xqhip_step_outproj_sync_bytes(void) { return xqhip::step_outproj_sync_bytes(); }
+
+// The launch descriptors of xqhip_linear_attn_step_outproj, validated as the
+// two separate entry points validate them.
+static int step_outproj_args(const float* mixed, float* conv_state, const float* conv_w, const float* a,
+                             const float* b, const float* a_log, const float* dt_bias, float* state, int lk_n,
+                             int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos, float* out, float* gate,
+                             const xqhip_w4* w, const float* norm_weight, float eps, float* y,
+                             xqhip::LinearStepLaunch* sp, xqhip::GemvLaunch* g, const char* who) {
+    if (!mixed || !conv_state || !conv_w || !a || !b || !a_log || !dt_bias || !state || !pos || !out || !gate ||
+        !norm_weight || !y)
+        return fail(XQHIP_EINVAL, "%s: null argument", who);
+    if (!xqhip::linear_step_supported(lk_n, lk_hd, lv_n, lv_hd, ksize))
+        return fail(XQHIP_EINVAL, "%s: unsupported step shape lk=%dx%d lv=%dx%d k=%d", who, lk_n, lk_hd, lv_n, lv_hd,
+                    ksize);
+    if (int rc = validate_w4(w, who)) return rc;
+    const xqhip_prologue pro{XQHIP_PRO_GATED_HEAD_ACT, lv_hd, norm_weight, gate, eps};
+    if (int rc = validate_prologue(&pro, w->cols, who)) return rc;
+    if (int rc = validate_alignment(w, out, &pro, who)) return rc;
+    if (w->cols != lv_n * lv_hd)
+        return fail(XQHIP_EINVAL, "%s: the projection has %d columns, the step writes %d", who, w->cols, lv_n * lv_hd);
+    *sp = xqhip::LinearStepLaunch{mixed, conv_state, conv_w, a, b, a_log, dt_bias, state,
+                                  lk_n, lk_hd, lv_n, lv_hd, ksize, pos, out, gate};
+    *g = base_launch(w, out, XQHIP_F32, &pro);
+    g->y = y;
+    g->epi = XQHIP_EPI_ADD;
+    return XQHIP_OK;
+}
+
+int xqhip_step_outproj_supported(const xqhip_w4* w, int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize) {
+    if (!w || !w->nib || !w->meta) return 0;
+    // placeholder vectors: only the shapes and the device's residency are checked
+    alignas(16) static float f[4] = {};
+    static int32_t i = 0;
+    xqhip::LinearStepLaunch sp{};
+    xqhip::GemvLaunch g{};
+    if (step_outproj_args(f, f, f, f, f, f, f, f, lk_n, lk_hd, lv_n, lv_hd, ksize, &i, f, f, w, f, 1e-6f, f, &sp, &g,
+                          "xqhip_step_outproj_supported") != XQHIP_OK)
+        return 0;
+    return xqhip::step_outproj_grid(sp, g) > 0 ? 1 : 0;
+}
+
+int xqhip_linear_attn_step_outproj(const float* mixed, float* conv_state, const float* conv_w, const float* a,
+                                   const float* b, const float* a_log, const float* dt_bias, float* state, int lk_n,
+                                   int lk_hd, int lv_n, int lv_hd, int ksize, const int32_t* pos, float* out,
+                                   float* gate, const xqhip_w4* w, const float* norm_weight, float eps, float* y,
+                                   void* sync, void* stream) {
+    static const char* who = "xqhip_linear_attn_step_outproj";
+    xqhip::LinearStepLaunch sp{};
+    xqhip::GemvLaunch g{};
+    if (int rc = step_outproj_args(mixed, conv_state, conv_w, a, b, a_log, dt_bias, state, lk_n, lk_hd, lv_n, lv_hd,
+                                   ksize, pos, out, gate, w, norm_weight, eps, y, &sp, &g, who))
+        return rc;
+    if (!sync || (reinterpret_cast<uintptr_t>(sync) & 127u) != 0)
+        return fail(XQHIP_EINVAL, "%s: sync must be a 128-byte aligned block of xqhip_step_outproj_sync_bytes()", who);
+    if (!xqhip::step_outproj_shape_ok(sp, g) || xqhip::step_outproj_grid(sp, g) == 0)
+        return fail(XQHIP_ENOTSUP, "%s: not available for this matrix (%dx%d layout %d) or device", who, w->rows,
+                    w->cols, w->layout);
+    return check(xqhip::launch_step_outproj(sp, g, static_cast<uint32_t*>(sync), as_stream(stream)),
+                 "step + output projection launch");
+}
+
+int xqhip_step_outproj_error(const void* sync, int* error) {
+    if (!sync || !error) return fail(XQHIP_EINVAL, "xqhip_step_outproj_error: null argument");
+    const size_t words = xqhip::step_outproj_sync_bytes() / sizeof(uint32_t);
+    std::vector<uint32_t> host(words);
+    if (int rc = check(hipMemcpy(host.data(), sync, words * sizeof(uint32_t), hipMemcpyDeviceToHost),
+                       "xqhip_step_outproj_error copy"))
+        return rc;
+    *error = host[xqhip::step_outproj_error_word()] != 0;
+    return XQHIP_OK;
+}
+
 // ---- prefill (multi-token) ---------------------------------------------------
 
 size_t xqhip_gemm_workspace_bytes(int m, int cols, int rows) {

@@ -164,6 +164,15 @@ struct LinearStepLaunch {
 bool linear_step_supported(int lk_n, int lk_hd, int lv_n, int lv_hd, int ksize);
 hipError_t launch_linear_step(const LinearStepLaunch& p, hipStream_t s);
 
+// decode_fused.hip: the step and the output projection g (ADD epilogue, x =
+// p.out) as one launch; sync: step_outproj_sync_bytes(), zeroed before the
+// first launch and left zeroed by every launch.
+size_t step_outproj_sync_bytes();
+int step_outproj_error_word();  // index of the error word (uint32) in sync
+bool step_outproj_shape_ok(const LinearStepLaunch& p, const GemvLaunch& g);
+int step_outproj_grid(const LinearStepLaunch& p, const GemvLaunch& g);  // 0: not runnable on this device
+hipError_t launch_step_outproj(const LinearStepLaunch& p, const GemvLaunch& g, uint32_t* sync, hipStream_t s);
+
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
 hipError_t launch_lds_fill(float value, hipStream_t s);
 hipError_t launch_timestamp(uint64_t* slot, hipStream_t s);

@@ -319,9 +319,43 @@ bool DeviceModel::load(const std::string& model_dir, const std::string& backend_
     if (const char* v = std::getenv("XQ_TRACE_EVERY")) trace_every_ = std::max(0, std::atoi(v));
     trace_note_ = trace_every_ > 0 ? "per_op_every_" + std::to_string(trace_every_) + "_graph_steps"
                                    : std::string("per_op_first_step_after_prefill");
-    if (!build_chains(error)) return false;
+    if (!build_chains(error) || !setup_step_fusion(error)) return false;
     reset_state();
     return xqhip_stream_synchronize(stream_) == 0 || fail_hip(error, "load sync");
+}
+
+// The linear-attention layers' step and output projection as one launch
+// (xqhip_linear_attn_step_outproj, bit-identical to the two) is opt-in,
+// XQ_FUSE_STEP=1: measured on the 9B shapes it takes 15.9 us against 11.0 us
+// for the two kernels, because its in-kernel hand-off between CUs of
+// different XCDs (write-through stores, then polls that bypass the L2) costs
+// 4-5 us where the kernel boundary costs 1.6 us.
+bool DeviceModel::setup_step_fusion(std::string* error) {
+    const char* v = std::getenv("XQ_FUSE_STEP");
+    if (!v || v[0] != '1') {
+        fuse_note_ = "off";
+        return true;
+    }
+    bool any = false;
+    for (const Layer& L : layers_) {
+        if (L.full) continue;
+        any = true;
+        if (!xqhip_step_outproj_supported(&L.out_proj, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_)) {
+            fuse_note_ = "off(unsupported)";
+            return true;
+        }
+    }
+    if (!any) {
+        fuse_note_ = "off(no_linear_layers)";
+        return true;
+    }
+    uint8_t* sync = nullptr;
+    if (!alloc(&sync, xqhip_step_outproj_sync_bytes(), error)) return false;
+    if (xqhip_fill_u8(sync, 0, xqhip_step_outproj_sync_bytes(), stream_) != 0) return fail_hip(error, "fill");
+    fuse_sync_ = sync;
+    fuse_step_ = true;
+    fuse_note_ = "on";
+    return true;
 }
 
 // Decode chains are opt-in (XQ_DECODE_CHAIN=1): measured on the 9B shapes a
@@ -705,18 +739,33 @@ bool DeviceModel::enqueue_layers(bool timed, std::string* error) {
             const float* a = proj_ + conv_dim_;
             const float* b = a + lv_n_;
             float* z = proj_ + conv_dim_ + 2 * lv_n_;
-            // the step also replaces z by silu(z) once, for the output norm's prologue
-            op_begin(timed, "linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
-                     {"linear_attention_conv1d_custom"}, 2);
-            XQ_CALL(xqhip_linear_attn_step_act(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias, L.rec_state,
-                                               lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_, z, stream_),
-                    "linear-attention step");
-            op_end(timed);
-            xqhip_prologue gated{XQHIP_PRO_GATED_HEAD_ACT, lv_hd_, L.lin_norm, z, eps_};
-            op_begin(timed, "linear_attn_out_proj_w4a16(fused:linear_attention_gated_rmsnorm,residual_add_attention)");
-            XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, &gated, resid_, XQHIP_F32, XQHIP_EPI_ADD, stream_),
-                    "out projection");
-            op_end(timed);
+            if (fuse_step_) {  // one launch: the step, then the projection of its output
+                op_begin(timed,
+                         "linear_attention_state_update_custom+linear_attn_out_proj_w4a16(fused:conv1d,qk_l2norm,"
+                         "gated_delta,linear_attention_gated_rmsnorm,residual_add_attention)",
+                         {"linear_attention_conv1d_custom"}, 2);
+                XQ_CALL(xqhip_linear_attn_step_outproj(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias,
+                                                       L.rec_state, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_,
+                                                       z, &L.out_proj, L.lin_norm, eps_, resid_, fuse_sync_, stream_),
+                        "linear-attention step + out projection");
+                op_end(timed);
+            } else {
+                // the step also replaces z by silu(z) once, for the output norm's prologue
+                op_begin(timed, "linear_attention_state_update_custom(fused:conv1d,qk_l2norm,gated_delta)",
+                         {"linear_attention_conv1d_custom"}, 2);
+                XQ_CALL(xqhip_linear_attn_step_act(proj_, L.conv_state, L.conv_w, a, b, L.a_log, L.dt_bias,
+                                                   L.rec_state, lk_n_, lk_hd_, lv_n_, lv_hd_, ksize_, pos, attn_, z,
+                                                   stream_),
+                        "linear-attention step");
+                op_end(timed);
+                xqhip_prologue gated{XQHIP_PRO_GATED_HEAD_ACT, lv_hd_, L.lin_norm, z, eps_};
+                op_begin(timed,
+                         "linear_attn_out_proj_w4a16(fused:linear_attention_gated_rmsnorm,residual_add_attention)");
+                XQ_CALL(xqhip_gemv_w4a16(&L.out_proj, attn_, XQHIP_F32, &gated, resid_, XQHIP_F32, XQHIP_EPI_ADD,
+                                         stream_),
+                        "out projection");
+                op_end(timed);
+            }
         }
         xqhip_prologue rms_post{XQHIP_PRO_RMS, 0, L.post_norm, nullptr, eps_};
         op_begin(timed, "linear_gate_proj_w4a16(fused:up_proj,rmsnorm_post_attention,silu_gate_mul)");
@@ -1148,6 +1197,17 @@ bool DeviceModel::sync(KernelTrace* trace, std::string* error) {
             return false;
         }
     }
+    if (fuse_sync_) {
+        int bad = 0;
+        if (xqhip_step_outproj_error(fuse_sync_, &bad) != 0) return fail_hip(error, "step + projection status");
+        if (bad) {
+            xqhip_fill_u8(fuse_sync_, 0, xqhip_step_outproj_sync_bytes(), stream_);
+            xqhip_stream_synchronize(stream_);
+            *error = "linear-attention step + out projection: a hand-off wait gave up; results since the last check "
+                     "are invalid";
+            return false;
+        }
+    }
     credit_steps(trace, pending_.size());
     return true;
 }
@@ -1167,7 +1227,7 @@ std::string DeviceModel::coverage_summary() const {  // fields of custom_model.c
       << ",generic:" << layout_count_[XQHIP_LAYOUT_GENERIC] << ",f32meta:" << layout_count_[XQHIP_LAYOUT_TILED64_F32META]
       << ",scale16:" << layout_count_[XQHIP_LAYOUT_TILED64_SCALE16]
       << ",f32s_z4:" << layout_count_[XQHIP_LAYOUT_TILED64_F32S_Z4]
-      << ";kv_capacity=" << max_ctx_ << ";decode_chain=" << chain_note_ << ";kernel_trace=" << trace_note_
+      << ";kv_capacity=" << max_ctx_ << ";decode_chain=" << chain_note_ << ";linear_step_outproj=" << fuse_note_ << ";kernel_trace=" << trace_note_
       << ";fallback_ops=none";
     return o.str();
 }

@@ -106,6 +106,7 @@ private:
     void drop_graphs();
     // decode chains: the projections between two non-GEMV ops as one launch
     bool build_chains(std::string* error);
+    bool setup_step_fusion(std::string* error);
     bool enqueue_chain(size_t k, bool timed, std::string* error);
     // batched prefill of prompt chunks (GEMMs on the matrix cores)
     bool prefill_chunk(const int32_t* h_tokens, const int32_t* h_pos, int n, int pos0, bool timed,
@@ -233,6 +234,11 @@ private:
     void* chain_arena_ = nullptr;
     void* chain_sync_ = nullptr;
     std::string chain_note_ = "off";  // why the chains are not used, or "on"
+    // the linear-attention step and its output projection as one launch
+    // (xqhip_linear_attn_step_outproj) in the per-op decode path
+    bool fuse_step_ = false;
+    void* fuse_sync_ = nullptr;
+    std::string fuse_note_ = "off";
 };
 
 }  // namespace xqh

@@ -113,6 +113,12 @@ _HIP_SIGS = {
     "xqhip_linear_attn_step_act": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                            c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                                            c_void_p]),
+    "xqhip_step_outproj_sync_bytes": (c_size_t, []),
+    "xqhip_step_outproj_supported": (c_int, [_P(W4), c_int, c_int, c_int, c_int, c_int]),
+    "xqhip_linear_attn_step_outproj": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                               c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                               c_void_p, _P(W4), c_void_p, c_float, c_void_p, c_void_p, c_void_p]),
+    "xqhip_step_outproj_error": (c_int, [c_void_p, _P(c_int)]),
     "xqhip_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "xqhip_gemm_w4a16": (c_int, [_P(W4), c_void_p, c_int, c_int, _P(Prologue), c_int, c_void_p, c_int, c_int,
                                  c_void_p, c_size_t, c_void_p]),
