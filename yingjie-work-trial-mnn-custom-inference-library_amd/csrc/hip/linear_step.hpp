@@ -14,27 +14,7 @@ constexpr int kDeltaIGroups = 16;   // threads per column
 constexpr int kDeltaMaxKPerThread = 16;  // key dim <= 256
 constexpr int kStepMaxTaps = 8;          // conv kernel size of the fused step
 
-// ---------------------------------------------------------------------------
-// Fused linear-attention step: block (vh, column slice) recomputes the conv1d +
-// SiLU + L2 norm of its key head's q and k channels (cheap: 2 * lk_hd channels
-// of ksize taps), the conv of its own kDeltaCols value channels, then runs the
-// gated delta update of gated_delta_kernel on those columns.  Conv history is
-// double-buffered by position parity (read copy pos & 1, write the other): the
-// q/k history is written by one block per key head (vh % factor == 0, first
-// slice), the value history by the block that owns the channel.
-// ---------------------------------------------------------------------------
-// KS > 0: the conv kernel size as a compile-time constant (the tap loops then
-// issue exactly the loads they need); KS == 0: runtime p.ksize <= kStepMaxTaps.
-// The body of one block of 256 threads (tid 0 .. 255) for value head vh and
-// column slice `slice`.
-// FUSED: the block's four waves run inside a launch whose other waves read
-// the step's output (decode_fused.hip).  The output and the activated gate
-// are then stored through to memory (agent scope: the readers may run on
-// another XCD), the other waves of the block pass two barriers with these
-// four (one right after the step has issued its loads, so their own loads
-// queue behind the step's, and the step's own barrier), and once every store
-// of the four waves is complete the last of them to finish adds 1 to the
-// hand-off counter ho.arrive (ho.lds_cnt: a zeroed LDS word of the block).
+// The block's LDS, and the hand-off words of the FUSED form (below).
 struct StepSmem {
     float qk[2 * 256];
     float vsh[kDeltaCols];
@@ -45,6 +25,27 @@ struct StepHandOff {
     uint32_t* lds_cnt;
 };
 
+// ---------------------------------------------------------------------------
+// Fused linear-attention step, the body of one block of 256 threads (tid
+// 0 .. 255) for value head vh and column slice `slice`: the block recomputes
+// the conv1d + SiLU + L2 norm of its key head's q and k channels (cheap:
+// 2 * lk_hd channels of ksize taps), the conv of its own kDeltaCols value
+// channels, then runs the gated delta update of gated_delta_kernel on those
+// columns.  Conv history is double-buffered by position parity (read copy
+// pos & 1, write the other): the q/k history is written by one block per key
+// head (vh % factor == 0, first slice), the value history by the block that
+// owns the channel.
+// KS > 0: the conv kernel size as a compile-time constant (the tap loops then
+// issue exactly the loads they need); KS == 0: runtime p.ksize <= kStepMaxTaps.
+// FUSED: the block's four waves run inside a launch whose other waves read
+// the step's output (decode_fused.hip).  The output and the activated gate
+// are then stored through to memory (agent scope: the readers may run on
+// another XCD), the other waves of the block pass two barriers with these
+// four (one right after the step has issued its loads, so their own loads
+// queue behind the step's, and the step's own barrier), and once every store
+// of the four waves is complete the last of them to finish adds 1 to the
+// hand-off counter ho.arrive (ho.lds_cnt: a zeroed LDS word of the block).
+// ---------------------------------------------------------------------------
 template <int KS, bool FUSED>
 __device__ __forceinline__ void linear_step_body(const LinearStepLaunch& p, int vh, int slice, uint32_t tid,
                                                  StepSmem& sm, StepHandOff ho) {
