@@ -276,7 +276,7 @@ hipError_t launch_argmax_finish(const GemvLaunch& p, int blocks, hipStream_t s);
 // TILED64 kernel.  NCH = number of 4096-column chunks (the last may be partial);
 // a block has RG row groups x NCH waves, wave (rg, c) owns chunk c for the rows
 // of row group rg; R = rows per wave iteration.  Two register buffers of
-// weights: a buffer is refilled with the batch two strides ahead as soon as it
+// weights: a buffer is refilled with the batch two trips ahead as soon as it
 // is reduced, and the first two batches are requested before the activations
 // are staged.
 //
@@ -424,6 +424,23 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     const uint32_t row_bytes = tiled_row_bytes<BITS>(cols);
     const int stride = grid * RG;
     const WSrc src = make_wsrc<BITS, META>(nib, meta, rows, cols);
+    // First row of this wave's batch (R rows) in trip t (b: block * RG +
+    // t * stride, kept incrementally).  Full trips deal the batches block by
+    // block (block b's waves take batches t stride + b RG + rg).  For the
+    // one-row-batch, one-chunk launches (the 4096-, 10240- and 12352-row
+    // projections, whose rows leave a partial last trip) that trip deals its
+    // batches wave by wave across the blocks (batch t stride + rg grid + b), so
+    // every CU streams within one row of every other instead of a few blocks
+    // taking the whole remainder with all their waves; measured 0.25-0.4 us
+    // off those launches.  (The other instantiations keep the plain mapping:
+    // the extra select cost gate/up and down 0.2-0.3 us.)  Which wave computes
+    // a row does not change its arithmetic.
+    constexpr bool kSpreadTail = R == 1 && NCH == 1 && EPI != EPI_ARGMAX;
+    const int full_trips = ((rows + R - 1) / R) / stride;
+    auto row0 = [&](int t, int b) {
+        if constexpr (kSpreadTail) return (t < full_trips ? b + rg : t * stride + rg * grid + block) * R;
+        return (b + rg) * R;
+    };
 
     // activations first, then the first weight batches, then the staging
     // arithmetic while the weights stream in
@@ -431,8 +448,8 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     int base = block * RG;
     if constexpr (EARLY) {
         pre();
-        load_batch<R, BITS, META>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
-        load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS, META>(buf0, src, row0(0, base), rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS, META>(buf1, src, row0(1, base + stride), rows, row_bytes, G, c, lane, gcnt, has_group);
         wait();
         stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG, XAUX>(x, x_f16, pro, cols, xs, red, tid, []() {});
     } else {
@@ -440,13 +457,13 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
         // one would stall its issue on the CU's in-flight memory requests, and the
         // staging waits behind it.
         stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, tid, [&]() {
-            load_batch<R, BITS, META>(buf0, src, (base + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+            load_batch<R, BITS, META>(buf0, src, row0(0, base), rows, row_bytes, G, c, lane, gcnt, has_group);
             if constexpr (R == 1)
-                load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt,
+                load_batch<R, BITS, META>(buf1, src, row0(1, base + stride), rows, row_bytes, G, c, lane, gcnt,
                                           has_group);
         });
         if constexpr (R > 1)
-            load_batch<R, BITS, META>(buf1, src, (base + stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+            load_batch<R, BITS, META>(buf1, src, row0(1, base + stride), rows, row_bytes, G, c, lane, gcnt, has_group);
     }
     __syncthreads();
     // this lane's group: kDigits x 8 words of digits, then e and G
@@ -512,7 +529,7 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
         __syncthreads();
         if (c == 0) {
             for (int bi = b0; bi < b0 + n; ++bi) {
-                const int r0 = (block * RG + bi * stride + rg) * R;
+                const int r0 = row0(bi, block * RG + bi * stride);
                 if (r0 >= rows) continue;
                 float acc[R];
 #pragma unroll
@@ -529,7 +546,7 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     };
 
     auto process = [&](WBatch<R, META>& cur, int bbase, int bidx) {
-        const int r0 = (bbase + rg) * R;
+        const int r0 = row0(bidx, bbase);
         float acc[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) acc[i] = 0.0f;
@@ -584,15 +601,17 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     };
 
     // two batches per trip so each register buffer has a fixed name; a buffer
-    // is refilled with the batch two strides ahead as soon as it is reduced
+    // is refilled with the batch two trips ahead as soon as it is reduced
     // The trip count is the grid-wide maximum (uniform, so the loop has no
     // early exit between the two buffers): batches past the end load nothing
     // and are skipped by process().
     for (int t = 0; t < trips; t += 2) {
         process(buf0, base, t);
-        load_batch<R, BITS, META>(buf0, src, (base + 2 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS, META>(buf0, src, row0(t + 2, base + 2 * stride), rows, row_bytes, G, c, lane, gcnt,
+                                  has_group);
         process(buf1, base + stride, t + 1);
-        load_batch<R, BITS, META>(buf1, src, (base + 3 * stride + rg) * R, rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_batch<R, BITS, META>(buf1, src, row0(t + 3, base + 3 * stride), rows, row_bytes, G, c, lane, gcnt,
+                                  has_group);
         base += 2 * stride;
     }
     if constexpr (NCH > 1) {
