@@ -9,7 +9,8 @@ Prints ONE JSON line.  Workloads (--workload):
          / decode wall time, as xq_metrics reports it).  A second run on the
          same shape written with the asymmetric quantiser's metadata (fp32
          scales, integer zeros; --no-asymmetric skips it) is reported under
-         "asymmetric_metadata".
+         "asymmetric_metadata", and the prefill's gate/up GEMM over 512 tokens
+         against the fp16 MFMA peak under "prefill_gemm".
   mlp    decode MLP block, hidden 4096 -> 12288 -> 4096, W4A16 g64: fused
          RMSNorm + gate/up GEMV + SiLU*up, then down GEMV + residual add.
          value = algorithmic HBM GB/s of the block (the GEMV bandwidth metric).
@@ -41,6 +42,7 @@ sys.path.insert(0, os.path.join(PKG, "python"))
 import xqbind as xb  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 METRIC = "batch-1 decode tokens/s; W4A16 GEMV achieved HBM GB/s (% of peak)"
 
 
@@ -296,6 +298,48 @@ def time_projection(name, rows, cols, pro_kind, epi, bits=4, n=200, budget=640e6
             "GBps": round(algo / us / 1e3, 1), "frac": round(algo / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
 
 
+def time_prefill_gemm(rows=24576, cols=4096, m=512, n=20):
+    """The prefill's largest GEMM, gate/up (RMSNorm prologue, SiLU pair
+    epilogue) over a 512-token chunk through xqhip_gemm_w4a16: the average of n
+    back-to-back calls (each the activation preparation kernel and the MFMA
+    GEMM), HIP events on the launch stream.  Algorithmic work 2 m rows cols
+    FLOP against the dense fp16 MFMA peak; the kernel issues two fp16 MFMA
+    passes per product (x as fp16 hi + lo), so its MFMA work is twice that."""
+    hip = xb.hip()
+    rng = np.random.default_rng(rows + cols + m)
+    g = rows * (cols // 64)
+    packed = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+    scales = np.abs(rng.normal(0.0, 0.02, g)).astype(np.float16).astype(np.float32)
+    w = xb.DeviceW4(packed, scales, np.full(g, 8.0, np.float32), rows, cols)
+    X = xb.DeviceBuffer.from_array(rng.normal(0, 1, (m, cols)).astype(np.float32))
+    gam = xb.DeviceBuffer.from_array(rng.normal(1.0, 0.1, cols).astype(np.float32))
+    y = xb.DeviceBuffer(m * (rows // 2) * 4)
+    ws = xb.DeviceBuffer(hip.xqhip_gemm_workspace_bytes(m, cols, rows))
+    pro = xb.prologue(xb.PRO_RMS, gam, eps=1e-6)
+
+    def launch():
+        xb.ck(hip.xqhip_gemm_w4a16(w.ref, X.ptr, m, cols, ctypes.byref(pro), 0, y.ptr, rows // 2,
+                                   xb.EPI_SILU_PAIR, ws.ptr, ws.nbytes, None))
+
+    for _ in range(3):
+        launch()
+    ev = Events()
+    ev.start()
+    for _ in range(n):
+        launch()
+    us = ev.stop_ms() * 1e3 / n
+    w.free()
+    flop = 2.0 * m * rows * cols
+    tflops = flop / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "kernel": "prep_x_vec_kernel + gemm_w4_mfma_kernel<4, 1, 2, 4, 2, 2>: prefill gate/up "
+                                       f"{rows}x{cols} W4A16 g64 over {m} tokens, RMSNorm prologue, SiLU*up epilogue",
+            "method": f"HIP events around {n} back-to-back calls of xqhip_gemm_w4a16 (preparation + GEMM); "
+                      "algorithmic FLOP = 2 m rows cols",
+            "avg_us": round(us, 1), "flop": flop, "achieved": round(tflops, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "mfma_passes": 2,
+            "mfma_work_frac": round(2 * tflops / MFMA_FP16_PEAK_TFLOPS, 4)}
+
+
 def projection_table(bits=4, n=200, meta="sym", names=None):
     rows = []
     for name, r, c, pro, epi in PROJECTIONS:
@@ -531,6 +575,11 @@ def bench_decode(args):
                                          "lm_head_argmax": round(lm["mean_ms"] * 1e3, 2) if lm else None},
                      "bytes_per_launch_down_proj": bytes_dn, "bytes_per_launch_lm_head": bytes_lm},
     }
+    if not args.no_projections:
+        pg = time_prefill_gemm()
+        result["prefill_gemm"] = pg
+        log(f"[bench] prefill gate/up GEMM (512 tokens): {pg['avg_us']:.1f} us, {pg['achieved']:.0f} TFLOP/s "
+            f"algorithmic = {pg['frac']:.3f} of the fp16 MFMA peak ({pg['mfma_work_frac']:.3f} counting both passes)")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_decode(prompt, sess)
     sess.close()
