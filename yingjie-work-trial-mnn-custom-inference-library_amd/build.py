@@ -9,8 +9,14 @@
                      $ORIGIN/../lib, so LD_LIBRARY_PATH can put another build of
                      that ABI behind them)
 
-Usage: python build.py [--jobs N] [--only hip|host]
+Usage: python build.py [--jobs N] [--only hip|host|tools] [--sanitize]
 Compiles every time it is called (hipcc cross-compiles for gfx950 without a GPU).
+
+--sanitize builds the host library and the harness programs again with
+AddressSanitizer and UndefinedBehaviorSanitizer (host code only; the kernels
+are lib/libxqhip.so, copied beside them) into sanitize/lib and sanitize/bin,
+for running the harness programs, which link the sanitizer runtime
+themselves, over the whole HIP path.
 """
 import argparse
 import concurrent.futures as cf
@@ -28,6 +34,8 @@ TOOL_SRC = os.path.join(HERE, "csrc", "tools")
 LIB = os.path.join(HERE, "lib")
 BIN = os.path.join(HERE, "bin")
 OBJ = os.path.join(HERE, "_build")
+SAN = os.path.join(HERE, "sanitize")
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
@@ -77,7 +85,7 @@ def build_hip(jobs):
     return out
 
 
-def build_host(jobs):
+def build_host(jobs, lib=LIB, extra=()):
     if not os.path.isdir(HOST_SRC):
         return None
     srcs = sorted(f for f in os.listdir(HOST_SRC) if f.endswith(".cpp"))
@@ -87,12 +95,12 @@ def build_host(jobs):
     for f in srcs:
         o = os.path.join(OBJ, "host", f[:-4] + ".o")
         objs.append(o)
-        tasks.append(["g++", *HOST_FLAGS, "-c", os.path.join(HOST_SRC, f), "-o", o])
+        tasks.append(["g++", *HOST_FLAGS, *extra, "-c", os.path.join(HOST_SRC, f), "-o", o])
     os.makedirs(os.path.join(OBJ, "host"), exist_ok=True)
     _compile_many(jobs, tasks)
-    out = os.path.join(LIB, "libxqwen35.so")
+    out = os.path.join(lib, "libxqwen35.so")
     tmp = out + ".tmp"
-    _run(["g++", "-shared", "-o", tmp, *objs, "-L", LIB, "-lxqhip", "-Wl,-rpath,$ORIGIN",
+    _run(["g++", "-shared", *extra, "-o", tmp, *objs, "-L", lib, "-lxqhip", "-Wl,-rpath,$ORIGIN",
           "-Wl,-soname,libxqwen35.so", "-lpthread"])
     os.replace(tmp, out)
     return out
@@ -102,14 +110,14 @@ def build_host(jobs):
 TOOLS = {"xq_host_quality_runner": [], "xq_benchmark": ["-lxqhip"]}
 
 
-def build_tools(jobs):
-    os.makedirs(BIN, exist_ok=True)
+def build_tools(jobs, lib=LIB, bin_dir=BIN, flags=()):
+    os.makedirs(bin_dir, exist_ok=True)
     tasks, outs = [], []
     for name, extra in TOOLS.items():
-        out = os.path.join(BIN, name)
+        out = os.path.join(bin_dir, name)
         outs.append(out)
-        tasks.append(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", INCLUDE, "-I", TOOL_SRC,
-                      os.path.join(TOOL_SRC, name + ".cpp"), "-o", out, "-L", LIB, "-lxqwen35", *extra,
+        tasks.append(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", *flags, "-I", INCLUDE, "-I", TOOL_SRC,
+                      os.path.join(TOOL_SRC, name + ".cpp"), "-o", out, "-L", lib, "-lxqwen35", *extra,
                       "-Wl,--enable-new-dtags,-rpath,$ORIGIN/../lib"])
     _compile_many(jobs, tasks)
     return outs
@@ -131,10 +139,26 @@ def build(jobs=None, only=None):
     return built
 
 
+def build_sanitized(jobs=None):
+    """The host library and harness programs with ASan + UBSan, beside a copy of
+    the kernel library (built first if it is missing)."""
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    if not os.path.exists(os.path.join(LIB, "libxqhip.so")):
+        build(jobs, "hip")
+    lib, bin_dir = os.path.join(SAN, "lib"), os.path.join(SAN, "bin")
+    os.makedirs(lib, exist_ok=True)
+    shutil.copy2(os.path.join(LIB, "libxqhip.so"), os.path.join(lib, "libxqhip.so"))
+    built = [build_host(jobs, lib, SAN_FLAGS)]
+    built.extend(build_tools(jobs, lib, bin_dir, SAN_FLAGS))
+    shutil.rmtree(OBJ, ignore_errors=True)
+    return built
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--only", choices=["hip", "host", "tools"], default=None)
+    ap.add_argument("--sanitize", action="store_true", help="ASan + UBSan host build into sanitize/")
     a = ap.parse_args()
-    for p in build(a.jobs, a.only):
+    for p in (build_sanitized(a.jobs) if a.sanitize else build(a.jobs, a.only)):
         print(p)
