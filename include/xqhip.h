@@ -215,6 +215,20 @@ XQHIP_API int xqhip_gemv_w4a16_argmax_publish(const xqhip_w4* w, const void* x, 
                                               void* workspace, int32_t* out_index, float* out_value,
                                               int32_t* position, uint64_t* host_slot, void* stream);
 
+/* xqhip_gemv_w4a16_argmax_publish whose finishing kernel also writes the
+ * winner's embedding row, the next position's input: sampleGreedy followed by
+ * loadEmbeddingRow (custom_model.cpp:1281-1338, 569-608) in the same two
+ * launches instead of three.  embed_out[0 .. hidden) = the bf16 row
+ * table[index] widened to fp32, bit for bit what xqhip_embed_bf16 writes for
+ * *out_index (ids past the table wrap to index % vocab).  table: device
+ * [vocab][hidden] bf16; embed_out: device, may be the buffer x points to (the
+ * GEMV has finished reading x when the row is written). */
+XQHIP_API int xqhip_gemv_w4a16_argmax_publish_embed(const xqhip_w4* w, const void* x, int x_type,
+                                                    const xqhip_prologue* pro, void* workspace, int32_t* out_index,
+                                                    float* out_value, int32_t* position, uint64_t* host_slot,
+                                                    const uint16_t* table, int vocab, int hidden, float* embed_out,
+                                                    void* stream);
+
 /* xqhip_gemv_w4a16_argmax without a workspace argument and without any
  * allocation: no counterpart in the reference.  For callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops or

@@ -232,6 +232,70 @@ def test_argmax_publish_advances_position_and_publishes(rows, cols, seed, start)
         xb.ck(xb.hip().xqhip_host_free(slot_p))
 
 
+@pytest.mark.parametrize("rows,cols,vocab,hidden,alias", [(248320, 4096, 1024, 4096, True), (4099, 1024, 3001, 1024, True),
+                                                      (4099, 1024, 5000, 100, False), (700, 64, 7, 4096, False)])
+def test_argmax_publish_embed_matches_publish_then_embed(rows, cols, vocab, hidden, alias):
+    """xqhip_gemv_w4a16_argmax_publish_embed against
+    xqhip_gemv_w4a16_argmax_publish followed by xqhip_embed_bf16 of the
+    published index: index, value, position, host slot and the embedding row
+    bit for bit, on three calls in a row, with the row written over x itself
+    (the decode step's use) or to its own buffer; tables smaller than the
+    matrix (ids wrapping to index % vocab) and a hidden size that is not a
+    multiple of 8 (the scalar copy)."""
+    rng = np.random.default_rng(rows + vocab + hidden)
+    q = w4_matrix(rows, cols, rows + 7)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    table = rng.integers(0, 1 << 16, vocab * hidden, dtype=np.uint16)
+    table[(table & 0x7F80) == 0x7F80] &= 0xBFFF  # finite values only (no bf16 inf / nan patterns)
+    hip = xb.hip()
+    w = xb.DeviceW4(q.packed, q.scales, q.zeros, q.rows, q.cols, q.group, q.affine)
+    td = xb.DeviceBuffer.from_array(table)
+    ws = xb.DeviceBuffer(hip.xqhip_argmax_workspace_bytes(q.rows))
+    slot_p = ctypes.c_void_p()
+    xb.ck(hip.xqhip_host_alloc_coherent(ctypes.byref(slot_p), 8))
+    try:
+        slot = ctypes.cast(slot_p, ctypes.POINTER(ctypes.c_uint64))
+        results = []
+        for fused in (False, True):
+            # x spans max(cols, hidden) floats so that the row can overwrite it
+            xd = xb.DeviceBuffer.from_array(np.concatenate([x, np.zeros(max(0, hidden - cols), np.float32)]))
+            out = xd if alias else xb.DeviceBuffer(hidden * 4)
+            idx, val = xb.DeviceBuffer(4), xb.DeviceBuffer(4)
+            posd = xb.DeviceBuffer.from_array(np.array([40], np.int32))
+            per_call = []
+            for call in range(3):
+                xd.upload(np.concatenate([x * (1 + call), np.zeros(max(0, hidden - cols), np.float32)]))
+                slot[0] = 0xFFFFFFFFFFFFFFFF
+                if fused:
+                    xb.ck(hip.xqhip_gemv_w4a16_argmax_publish_embed(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr,
+                                                                    val.ptr, posd.ptr, slot_p, td.ptr, vocab, hidden,
+                                                                    out.ptr, None))
+                else:
+                    xb.ck(hip.xqhip_gemv_w4a16_argmax_publish(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr, val.ptr,
+                                                              posd.ptr, slot_p, None))
+                    xb.ck(hip.xqhip_embed_bf16(td.ptr, vocab, hidden, idx.ptr, out.ptr, None))
+                xb.ck(hip.xqhip_device_synchronize())
+                i = int(idx.download(np.int32, 1)[0])
+                row = out.download(np.float32, hidden)
+                per_call.append((i, float(val.download(np.float32, 1)[0]), int(posd.download(np.int32, 1)[0]),
+                                 int(slot[0]), row.view(np.uint32).copy()))
+                # the row is the table's, widened exactly
+                want = (table[(i % vocab) * hidden:(i % vocab + 1) * hidden].astype(np.uint32) << 16)
+                assert np.array_equal(row.view(np.uint32), want), (fused, call, i)
+            results.append(per_call)
+        for a, b in zip(*results):
+            assert a[:4] == b[:4]
+            assert np.array_equal(a[4], b[4])
+        rc = hip.xqhip_gemv_w4a16_argmax_publish_embed(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr, val.ptr,
+                                                       posd.ptr, slot_p, None, vocab, hidden, out.ptr, None)
+        assert rc == -1  # XQHIP_EINVAL: no table
+        rc = hip.xqhip_gemv_w4a16_argmax_publish_embed(w.ref, xd.ptr, xb.F32, None, ws.ptr, idx.ptr, val.ptr,
+                                                       posd.ptr, slot_p, td.ptr, 0, hidden, out.ptr, None)
+        assert rc == -1  # XQHIP_EINVAL: empty table
+    finally:
+        xb.ck(hip.xqhip_host_free(slot_p))
+
+
 def test_gemv_gated_head_prologue():
     """out_proj input of the linear-attention layer: per-head gated RMSNorm fused
     into the GEMV prologue (applyGatedHeadRms, custom_model.cpp:329-349)."""

@@ -399,7 +399,9 @@ def test_decode_trace_rows_from_sampled_graph_steps(small_dir, monkeypatch, ever
     assert tr["decode_op_trace_every"] == every
     assert rows["decode_step_graph_custom"]["calls"] == 40 - traced
     assert rows["decode_step_graph_traced_custom"]["calls"] == traced
-    assert rows["lm_head_custom(fused:rmsnorm_final,argmax)"]["calls"] == traced
+    assert rows["lm_head_custom(fused:rmsnorm_final,argmax,embedding)"]["calls"] == traced
+    # the next token's embedding row is written by the lm_head's finishing kernel, whose time its row carries
+    assert rows["embedding_bf16_row_read"]["calls"] >= traced
     assert rows["sampling_greedy_custom"]["calls"] == traced
     step = rows["decode_step_graph_custom"]
     assert 0 < step["min_ms"] < step["max_ms"]  # per-step times, not an average spread over steps

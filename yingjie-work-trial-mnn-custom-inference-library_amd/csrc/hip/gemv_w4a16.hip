@@ -91,10 +91,14 @@ __device__ __forceinline__ float prologue_apply(float v, int c, const Prologue& 
 // position != nullptr: also advances *position by one and publishes
 // (new position << 32 | index) to host_slot (coherent pinned host memory) in
 // one system-scope store, which a host thread polls for.
+// embed_out != nullptr: also writes the bf16 embedding row of the winner as
+// fp32 (the next position's input, as embed_bf16_kernel would from out_idx:
+// the same wrap of ids past the table and the same exact widening).
 __global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __restrict__ partial, int n,
                                                             int32_t* __restrict__ out_idx,
                                                             float* __restrict__ out_val, int32_t* position,
-                                                            uint64_t* host_slot) {
+                                                            uint64_t* host_slot, const uint16_t* __restrict__ table,
+                                                            int vocab, int hidden, float* __restrict__ embed_out) {
     __shared__ uint64_t keys[4];
     uint64_t best = 0;
     for (int i = threadIdx.x; i < n; i += 256) best = u64_max(best, partial[i]);
@@ -102,9 +106,9 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __re
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     if (lane == 0) keys[wid] = best;
     __syncthreads();
+    const uint64_t b = u64_max(u64_max(keys[0], keys[1]), u64_max(keys[2], keys[3]));
+    const uint32_t idx = 0xffffffffu - static_cast<uint32_t>(b);
     if (threadIdx.x == 0) {
-        const uint64_t b = u64_max(u64_max(keys[0], keys[1]), u64_max(keys[2], keys[3]));
-        const uint32_t idx = 0xffffffffu - static_cast<uint32_t>(b);
         *out_idx = static_cast<int32_t>(idx);
         *out_val = float_from_order_key(static_cast<uint32_t>(b >> 32));
         if (position) {
@@ -114,11 +118,31 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __re
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
+    if (embed_out == nullptr) return;
+    // idx is below 2^31 (a row of the matrix), so as an id it is non-negative
+    const uint32_t tok = idx < static_cast<uint32_t>(vocab) ? idx : idx % static_cast<uint32_t>(max(1, vocab));
+    const uint16_t* row = table + static_cast<size_t>(tok) * hidden;
+    const bool vec = (hidden & 7) == 0 && ((reinterpret_cast<uintptr_t>(row) | reinterpret_cast<uintptr_t>(embed_out)) & 15) == 0;
+    if (vec) {  // 8 values per 16-byte load (uniform branch)
+        for (int i = threadIdx.x * 8; i < hidden; i += 256 * 8) {
+            const uint4 w = *reinterpret_cast<const uint4*>(row + i);
+            const uint32_t h[4] = {w.x, w.y, w.z, w.w};
+            float4 lo, hi;
+            lo.x = __uint_as_float(h[0] << 16); lo.y = __uint_as_float(h[0] & 0xffff0000u);
+            lo.z = __uint_as_float(h[1] << 16); lo.w = __uint_as_float(h[1] & 0xffff0000u);
+            hi.x = __uint_as_float(h[2] << 16); hi.y = __uint_as_float(h[2] & 0xffff0000u);
+            hi.z = __uint_as_float(h[3] << 16); hi.w = __uint_as_float(h[3] & 0xffff0000u);
+            *reinterpret_cast<float4*>(embed_out + i) = lo;
+            *reinterpret_cast<float4*>(embed_out + i + 4) = hi;
+        }
+    } else {
+        for (int i = threadIdx.x; i < hidden; i += 256) embed_out[i] = __uint_as_float(static_cast<uint32_t>(row[i]) << 16);
+    }
 }
 
 hipError_t launch_argmax_finish(const GemvLaunch& p, int blocks, hipStream_t s) {
     hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, s, p.partial, blocks, p.out_idx, p.out_val,
-                       p.position, p.host_slot);
+                       p.position, p.host_slot, p.embed_table, p.embed_vocab, p.embed_hidden, p.embed_out);
     return hipGetLastError();
 }
 

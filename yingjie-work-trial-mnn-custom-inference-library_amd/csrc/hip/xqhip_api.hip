@@ -623,6 +623,34 @@ int xqhip_gemv_w4a16_argmax_publish(const xqhip_w4* w, const void* x, int x_type
     return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax_publish launch");
 }
 
+int xqhip_gemv_w4a16_argmax_publish_embed(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
+                                          void* workspace, int32_t* out_index, float* out_value, int32_t* position,
+                                          uint64_t* host_slot, const uint16_t* table, int vocab, int hidden,
+                                          float* embed_out, void* stream) {
+    const char* fn = "xqhip_gemv_w4a16_argmax_publish_embed";
+    if (!position || !host_slot || !table || !embed_out) return fail(XQHIP_EINVAL, "%s: null argument", fn);
+    if (vocab <= 0 || hidden <= 0) return fail(XQHIP_EINVAL, "%s: vocab and hidden must be positive", fn);
+    if (reinterpret_cast<uintptr_t>(host_slot) % alignof(uint64_t) != 0)
+        return fail(XQHIP_EINVAL, "%s: host_slot is not 8-byte aligned", fn);
+    if (int rc = validate_w4(w, fn)) return rc;
+    if (int rc = validate_prologue(pro, w->cols, fn)) return rc;
+    if (!x || !workspace || !out_index || !out_value) return fail(XQHIP_EINVAL, "%s: null argument", fn);
+    if (int rc = validate_alignment(w, x, pro, fn)) return rc;
+    xqhip::GemvLaunch p = base_launch(w, x, x_type, pro);
+    p.epi = 3;
+    p.partial = static_cast<uint64_t*>(workspace);
+    p.out_idx = out_index;
+    p.out_val = out_value;
+    p.position = position;
+    p.host_slot = host_slot;
+    p.embed_table = table;
+    p.embed_vocab = vocab;
+    p.embed_hidden = hidden;
+    p.embed_out = embed_out;
+    p.max_blocks = gemv_block_cap() > 0 ? std::min(kArgmaxMaxBlocks, gemv_block_cap()) : 0;
+    return check(xqhip::launch_gemv(p, as_stream(stream)), "gemv_w4a16_argmax_publish_embed launch");
+}
+
 int xqhip_gemv_w4a16_argmax_static(const xqhip_w4* w, const void* x, int x_type, const xqhip_prologue* pro,
                                    int32_t* out_index, float* out_value, void* stream) {
     const size_t need = xqhip_argmax_workspace_bytes(w ? w->rows : 0);

@@ -41,6 +41,11 @@ struct GemvLaunch {
     float* out_val;
     int32_t* position;    // argmax: advanced by one after the argmax (nullptr: untouched)
     uint64_t* host_slot;  // argmax with position: receives (new position << 32) | index
+    // argmax: when embed_out is set, the winner's bf16 row of embed_table
+    // ([embed_vocab][embed_hidden]) is also written to embed_out as fp32
+    const uint16_t* embed_table;
+    int embed_vocab, embed_hidden;
+    float* embed_out;
     int max_blocks;  // <= 0: as many blocks as are resident on the device at once
 };
 

@@ -643,11 +643,15 @@ bool DeviceModel::enqueue_embed(const int32_t* token_dev, bool timed, std::strin
 
 bool DeviceModel::enqueue_lm_head(bool timed, std::string* error) {
     xqhip_prologue fin{XQHIP_PRO_RMS, 0, final_norm_, nullptr, eps_};
-    op_begin(timed, "lm_head_custom(fused:rmsnorm_final,argmax)", {"sampling_greedy_custom"});
-    // the sampled token is the input of the next position: the kernel advances
-    // d_ctrl_[0] and publishes (position, token) to h_slot_
-    XQ_CALL(xqhip_gemv_w4a16_argmax_publish(&lm_head_, resid_, XQHIP_F32, &fin, argmax_ws_, d_ctrl_ + 2, best_val_,
-                                            d_ctrl_, h_slot_, stream_),
+    op_begin(timed, "lm_head_custom(fused:rmsnorm_final,argmax,embedding)",
+             {"sampling_greedy_custom", "embedding_bf16_row_read"});
+    // the sampled token is the input of the next position: the finishing
+    // kernel advances d_ctrl_[0], publishes (position, token) to h_slot_ and
+    // writes the token's embedding row to resid_ (loadEmbeddingRow,
+    // custom_model.cpp:569-608), which the next layers read
+    XQ_CALL(xqhip_gemv_w4a16_argmax_publish_embed(&lm_head_, resid_, XQHIP_F32, &fin, argmax_ws_, d_ctrl_ + 2,
+                                                  best_val_, d_ctrl_, h_slot_, static_cast<const uint16_t*>(embed_),
+                                                  vocab_, hidden_, resid_, stream_),
             "lm_head argmax");
     op_end(timed);
     return true;
@@ -806,8 +810,7 @@ bool DeviceModel::ensure_graphs(std::string* error) {
     };
     if (!capture(&g_prefill_, [&] { return enqueue_embed(d_ctrl_ + 1, false, error) && enqueue_layers(false, error); }) ||
         !capture(&g_step_, [&] {
-            return enqueue_lm_head(false, error) && enqueue_embed(d_ctrl_ + 2, false, error) &&
-                   enqueue_layers(false, error);
+            return enqueue_lm_head(false, error) && enqueue_layers(false, error);
         }))
         return false;
     // the traced step: the same launches with a timestamp kernel after every
@@ -824,8 +827,7 @@ bool DeviceModel::ensure_graphs(std::string* error) {
     std::string ignored;
     bool ok = xqhip_graph_begin(stream_) == 0;
     if (ok) {
-        const bool enq = enqueue_lm_head(true, &ignored) && enqueue_embed(d_ctrl_ + 2, true, &ignored) &&
-                         enqueue_layers(true, &ignored);
+        const bool enq = enqueue_lm_head(true, &ignored) && enqueue_layers(true, &ignored);
         ok = xqhip_graph_end(stream_, &g) == 0 && enq;
     }
     ts_mode_ = false;
@@ -1075,8 +1077,7 @@ bool DeviceModel::decode_one(int32_t* token_id, size_t position, KernelTrace* tr
         chained_ = false;
         const bool timed = detail_decode_;
         if (!sync(trace, error)) return false;
-        if (!enqueue_lm_head(timed, error)) return false;
-        if (!enqueue_embed(d_ctrl_ + 2, timed, error) || !enqueue_layers(timed, error)) return false;
+        if (!enqueue_lm_head(timed, error) || !enqueue_layers(timed, error)) return false;
         XQ_CALL(xqhip_stream_synchronize(stream_), "decode");
         if (!read_slot(want, token_id, error)) return false;
         dev_pos_ = want;

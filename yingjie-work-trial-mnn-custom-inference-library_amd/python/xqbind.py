@@ -85,6 +85,9 @@ _HIP_SIGS = {
                                         c_void_p]),
     "xqhip_gemv_w4a16_argmax_publish": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p, c_void_p,
                                                 c_void_p, c_void_p, c_void_p]),
+    "xqhip_gemv_w4a16_argmax_publish_embed": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p,
+                                                      c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p,
+                                                      c_void_p]),
     "xqhip_gemv_w4a16_argmax_static": (c_int, [_P(W4), c_void_p, c_int, _P(Prologue), c_void_p, c_void_p,
                                                c_void_p]),
     "xqhip_embed_bf16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
