@@ -204,27 +204,63 @@ __device__ __forceinline__ void linear_step_body(const LinearStepLaunch& p, int 
     const float invq = 1.0f / sqrtf(red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1.0e-6f);
     const float invk = 1.0f / sqrtf(red[1][0] + red[1][1] + red[1][2] + red[1][3] + 1.0e-6f);
     const float vj = active ? vsh[jl] : 0.0f;
-    float pred = 0.0f;
+    // The lane's rows i = ig + 16 r, as straight-line code: every LDS read of
+    // the normalised k_i and q_i issued before the first use (rows past dk
+    // select 0: their state words were read as 0 and are never stored), the
+    // state stores range-checked (kBufOOB for rows past dk and inactive
+    // columns).  Per-row branches had made each row a block of its own with a
+    // full wait for its LDS read.  The second half of the rows exists only for
+    // dk > 128 (a uniform branch).
+    constexpr int kHalf = kDeltaMaxKPerThread / 2;
+    const bool upper = dk > kHalf * kDeltaIGroups;
+    float kn[kDeltaMaxKPerThread], qn[kDeltaMaxKPerThread];
+    auto read_rows = [&](int r0) {
+        // all reads first, unconditionally (i <= 255: both stay inside qk);
+        // the empty asm after them keeps the compiler from moving a read under
+        // the select's branch
+        float kv[kHalf], qv[kHalf];
 #pragma unroll
-    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
-        const int i = ig + r * kDeltaIGroups;
-        if (active && i < dk) {
-            sreg[r] *= decay;
-            pred += sreg[r] * (qk[256 + i] * invk);
+        for (int r = 0; r < kHalf; ++r) {
+            const int i = ig + (r0 + r) * kDeltaIGroups;
+            kv[r] = qk[256 + i];
+            qv[r] = qk[i];
         }
-    }
+#pragma unroll
+        for (int r = 0; r < kHalf; ++r) asm volatile("" : "+v"(kv[r]), "+v"(qv[r]));
+#pragma unroll
+        for (int r = 0; r < kHalf; ++r) {
+            const bool in = ig + (r0 + r) * kDeltaIGroups < dk;
+            kn[r0 + r] = in ? kv[r] * invk : 0.0f;
+            qn[r0 + r] = in ? qv[r] * invq : 0.0f;
+        }
+    };
+    read_rows(0);
+    if (upper) read_rows(kHalf);
+    float pred = 0.0f;
+    auto decay_rows = [&](int r0) {
+#pragma unroll
+        for (int r = r0; r < r0 + kHalf; ++r) {
+            sreg[r] *= decay;
+            pred += sreg[r] * kn[r];
+        }
+    };
+    decay_rows(0);
+    if (upper) decay_rows(kHalf);
     pred = lanes_sum<16>(pred);
     const float delta = active ? beta * (vj - pred) : 0.0f;
     float o = 0.0f;
+    auto update_rows = [&](int r0) {
 #pragma unroll
-    for (int r = 0; r < kDeltaMaxKPerThread; ++r) {
-        const int i = ig + r * kDeltaIGroups;
-        if (active && i < dk) {
-            sreg[r] += (qk[256 + i] * invk) * delta;
-            S[__umul24(i, dv) + j] = sreg[r];
-            o += sreg[r] * (qk[i] * invq);
+        for (int r = r0; r < r0 + kHalf; ++r) {
+            const int i = ig + r * kDeltaIGroups;
+            sreg[r] += kn[r] * delta;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sreg[r]), r_state,
+                                                  active && i < dk ? (__umul24(i, dv) + j) * 4u : kBufOOB, 0, 0);
+            o += sreg[r] * qn[r];
         }
-    }
+    };
+    update_rows(0);
+    if (upper) update_rows(kHalf);
     o = lanes_sum<16>(o);
     if (ig == 0 && active) {
         const float ov = o * (1.0f / sqrtf(static_cast<float>(dk)));
