@@ -442,14 +442,29 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
         return (b + rg) * R;
     };
 
+    // The residual-add epilogue of a one-chunk launch reads y[row] when it
+    // finishes the row: that load is issued with the batch's weights (lane i <
+    // R: row r0 + i), so it returns with them instead of costing a memory
+    // round trip, and a wait for it, after the batch's dot products.  Only the
+    // wave finishing a row writes it, once, so the early read sees the value
+    // the launch started with.
+    constexpr bool kPrefetchY = EPI == EPI_ADD && NCH == 1;
+    const __amdgpu_buffer_rsrc_t y_r = buf_rsrc(y, kPrefetchY ? static_cast<uint32_t>(rows) * 4u : 0u);
+    auto load_b = [&](WBatch<R, META>& wb, float& yv, int r0) {
+        load_batch<R, BITS, META>(wb, src, r0, rows, row_bytes, G, c, lane, gcnt, has_group);
+        if constexpr (kPrefetchY)
+            yv = buf_load_f32(y_r, lane < R && r0 + lane < rows ? static_cast<uint32_t>(r0 + lane) * 4u : kBufOOB);
+    };
+
     // activations first, then the first weight batches, then the staging
     // arithmetic while the weights stream in
     WBatch<R, META> buf0, buf1;
+    float yv0 = 0.0f, yv1 = 0.0f;
     int base = block * RG;
     if constexpr (EARLY) {
         pre();
-        load_batch<R, BITS, META>(buf0, src, row0(0, base), rows, row_bytes, G, c, lane, gcnt, has_group);
-        load_batch<R, BITS, META>(buf1, src, row0(1, base + stride), rows, row_bytes, G, c, lane, gcnt, has_group);
+        load_b(buf0, yv0, row0(0, base));
+        load_b(buf1, yv1, row0(1, base + stride));
         wait();
         stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG, XAUX>(x, x_f16, pro, cols, xs, red, tid, []() {});
     } else {
@@ -457,13 +472,10 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
         // one would stall its issue on the CU's in-flight memory requests, and the
         // staging waits behind it.
         stage_x_lds<64 * NCH * RG, (8 + RG - 1) / RG>(x, x_f16, pro, cols, xs, red, tid, [&]() {
-            load_batch<R, BITS, META>(buf0, src, row0(0, base), rows, row_bytes, G, c, lane, gcnt, has_group);
-            if constexpr (R == 1)
-                load_batch<R, BITS, META>(buf1, src, row0(1, base + stride), rows, row_bytes, G, c, lane, gcnt,
-                                          has_group);
+            load_b(buf0, yv0, row0(0, base));
+            if constexpr (R == 1) load_b(buf1, yv1, row0(1, base + stride));
         });
-        if constexpr (R > 1)
-            load_batch<R, BITS, META>(buf1, src, row0(1, base + stride), rows, row_bytes, G, c, lane, gcnt, has_group);
+        if constexpr (R > 1) load_b(buf1, yv1, row0(1, base + stride));
     }
     __syncthreads();
     // this lane's group: kDigits x 8 words of digits, then e and G
@@ -490,7 +502,7 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     constexpr int kSlots = kDeferredSlots<RG, NCH, R>;
 
     // epilogue of rows r0 .. r0 + R - 1 (chunk-0 waves; every lane holds the sums)
-    auto finish_rows = [&](const float (&acc)[R], int r0) {
+    auto finish_rows = [&](const float (&acc)[R], int r0, float yv) {
         if constexpr (EPI == EPI_ARGMAX) {
 #pragma unroll
             for (int i = 0; i < R; ++i)
@@ -513,7 +525,7 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
             const int row = r0 + lane;
             if (lane < R && row < rows) {
                 if constexpr (EPI == EPI_ADD) {
-                    static_cast<float*>(y)[row] += v;
+                    static_cast<float*>(y)[row] = (kPrefetchY ? yv : static_cast<float*>(y)[row]) + v;
                 } else {
                     if (y_f16)
                         static_cast<_Float16*>(y)[row] = static_cast<_Float16>(v);
@@ -528,24 +540,44 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     auto combine = [&](int b0, int n) {
         __syncthreads();
         if (c == 0) {
-            for (int bi = b0; bi < b0 + n; ++bi) {
-                const int r0 = row0(bi, block * RG + bi * stride);
-                if (r0 >= rows) continue;
-                float acc[R];
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
+            if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
+                // one (batch, row) per lane, so the residual reads of all the
+                // rows are in flight together
+                for (int k = lane; k < n * R; k += kWave) {
+                    const int bi = b0 + k / R, i = k % R;
+                    const int row = row0(bi, block * RG + bi * stride) + i;
+                    if (row >= rows) continue;
                     float t = 0.0f;
 #pragma unroll
                     for (int cc = 0; cc < NCH; ++cc) t += partial_all[(((bi % kSlots) * RG + rg) * NCH + cc) * R + i];
-                    acc[i] = t;
+                    if constexpr (EPI == EPI_ADD)
+                        static_cast<float*>(y)[row] += t;
+                    else if (y_f16)
+                        static_cast<_Float16*>(y)[row] = static_cast<_Float16>(t);
+                    else
+                        static_cast<float*>(y)[row] = t;
                 }
-                finish_rows(acc, r0);
+            } else {
+                for (int bi = b0; bi < b0 + n; ++bi) {
+                    const int r0 = row0(bi, block * RG + bi * stride);
+                    if (r0 >= rows) continue;
+                    float acc[R];
+#pragma unroll
+                    for (int i = 0; i < R; ++i) {
+                        float t = 0.0f;
+#pragma unroll
+                        for (int cc = 0; cc < NCH; ++cc)
+                            t += partial_all[(((bi % kSlots) * RG + rg) * NCH + cc) * R + i];
+                        acc[i] = t;
+                    }
+                    finish_rows(acc, r0, 0.0f);
+                }
             }
         }
         __syncthreads();  // the slots are reused by the next batches
     };
 
-    auto process = [&](WBatch<R, META>& cur, int bbase, int bidx) {
+    auto process = [&](WBatch<R, META>& cur, float yv, int bbase, int bidx) {
         const int r0 = row0(bidx, bbase);
         float acc[R];
 #pragma unroll
@@ -597,7 +629,7 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
             return;
         }
         if (r0 >= rows) return;
-        finish_rows(acc, r0);
+        finish_rows(acc, r0, yv);
     };
 
     // two batches per trip so each register buffer has a fixed name; a buffer
@@ -606,12 +638,10 @@ __device__ __forceinline__ void gemv_tiled_run(const uint8_t* __restrict__ nib, 
     // early exit between the two buffers): batches past the end load nothing
     // and are skipped by process().
     for (int t = 0; t < trips; t += 2) {
-        process(buf0, base, t);
-        load_batch<R, BITS, META>(buf0, src, row0(t + 2, base + 2 * stride), rows, row_bytes, G, c, lane, gcnt,
-                                  has_group);
-        process(buf1, base + stride, t + 1);
-        load_batch<R, BITS, META>(buf1, src, row0(t + 3, base + 3 * stride), rows, row_bytes, G, c, lane, gcnt,
-                                  has_group);
+        process(buf0, yv0, base, t);
+        load_b(buf0, yv0, row0(t + 2, base + 2 * stride));
+        process(buf1, yv1, base + stride, t + 1);
+        load_b(buf1, yv1, row0(t + 3, base + 3 * stride));
         base += 2 * stride;
     }
     if constexpr (NCH > 1) {
