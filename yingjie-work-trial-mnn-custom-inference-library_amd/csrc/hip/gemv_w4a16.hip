@@ -100,8 +100,15 @@ __global__ void __launch_bounds__(256) argmax_finish_kernel(const uint64_t* __re
                                                             uint64_t* host_slot, const uint16_t* __restrict__ table,
                                                             int vocab, int hidden, float* __restrict__ embed_out) {
     __shared__ uint64_t keys[4];
+    // every key of this thread requested at once (range-checked: past n, 0)
+    constexpr int kPer = kArgmaxMaxBlocks / 256;
+    const __amdgpu_buffer_rsrc_t pr = buf_rsrc(partial, static_cast<uint32_t>(n) * 8u);
     uint64_t best = 0;
-    for (int i = threadIdx.x; i < n; i += 256) best = u64_max(best, partial[i]);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(pr, (threadIdx.x + 256u * k) * 8u, 0, 0);
+        best = u64_max(best, (static_cast<uint64_t>(w.y) << 32) | w.x);
+    }
     best = wave_max_u64(best);
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     if (lane == 0) keys[wid] = best;

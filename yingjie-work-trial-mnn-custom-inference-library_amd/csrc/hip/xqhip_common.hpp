@@ -295,9 +295,21 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 
 __device__ __forceinline__ uint64_t u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(dpp_i32<CTRL>(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint32_t hi = static_cast<uint32_t>(dpp_i32<CTRL>(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// maximum over the wave, in every lane: DPP steps inside each row of 16
+// lanes (as the float reductions above), then two lane swaps across rows
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = u64_max(v, dpp_u64<kDppXor1>(v));
+    v = u64_max(v, dpp_u64<kDppXor2>(v));
+    v = u64_max(v, dpp_u64<kDppHalfMirror>(v));
+    v = u64_max(v, dpp_u64<kDppMirror>(v));
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
+    for (int off = 16; off <= 32; off <<= 1) {
         const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
         const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
         v = u64_max(v, (static_cast<uint64_t>(hi) << 32) | lo);
